@@ -1,0 +1,92 @@
+"""ctypes binding of libhipster_qmm.so (the C ABI declared in include/hipster_qmm.h).
+
+The library is built in-tree by ``hipster_amd/csrc/Makefile`` (``__graft_entry__.build()``).  There
+is no fallback: if the shared library is missing or fails to load, every call raises.
+"""
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libhipster_qmm.so")
+
+# status codes and formats (include/hipster_qmm.h)
+QMM_OK = 0
+STATUS = {0: "QMM_OK", -1: "QMM_ERR_FORMAT", -2: "QMM_ERR_SHAPE", -3: "QMM_ERR_NULL",
+          -4: "QMM_ERR_LAUNCH", -5: "QMM_ERR_WORKSPACE", -6: "QMM_ERR_ARG"}
+QMM_Q4_K, QMM_Q5_K, QMM_IQ4_XS, QMM_Q6_K_SOA, QMM_Q8_0_SOA, QMM_Q5_1_SOA, QMM_Q6_K = 0, 1, 2, 3, 4, 5, 6
+
+c_vp = ctypes.c_void_p
+c_int = ctypes.c_int
+
+
+class XQ8(ctypes.Structure):
+    """qmm_xq8 / reference XQ8 (engine/kernels/gemv.h:8)."""
+    _fields_ = [("q", c_vp), ("d", c_vp), ("s", c_vp), ("ds", c_vp)]
+
+
+class GemvSeg(ctypes.Structure):
+    """qmm_gemv_seg / reference GemvSeg (engine/kernels/gemv.h:27)."""
+    _fields_ = [("fmt", ctypes.c_int32), ("w", c_vp), ("y", c_vp), ("N", ctypes.c_int32), ("K", ctypes.c_int32)]
+
+
+class MoeSegs(ctypes.Structure):
+    """qmm_moe_segs / reference MoeSegs (engine/kernels/gemv.h:43)."""
+    _fields_ = [("w", c_vp * 2), ("shared", c_vp * 2), ("y", c_vp * 2), ("ebytes", ctypes.c_size_t), ("slotw", c_vp)]
+
+
+class MoeTile(ctypes.Structure):
+    """qmm_moe_tile / reference MoeTile (engine/kernels/gemv.h:48)."""
+    _fields_ = [("expert", ctypes.c_int32), ("k0", ctypes.c_int32), ("ncols", ctypes.c_int32)]
+
+
+# name -> (restype, argtypes); every symbol the header declares
+SIGNATURES = {
+    "qmm_version": (ctypes.c_char_p, []),
+    "qmm_status_string": (ctypes.c_char_p, [c_int]),
+    "qmm_wfmt_row_bytes": (ctypes.c_size_t, [c_int, c_int]),
+    "qmm_repack_row_q6_K": (c_int, [c_vp, c_vp, c_int]),
+    "qmm_quantize_x_q8": (c_int, [c_vp, XQ8, c_int, c_int, c_vp]),
+    "qmm_gemv_q8": (c_int, [c_int, c_vp, XQ8, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    "qmm_gemv_multi": (c_int, [ctypes.POINTER(GemvSeg), c_int, XQ8, c_int, c_vp]),
+    "qmm_gemv_wmma_ok": (c_int, [ctypes.POINTER(GemvSeg), c_int]),
+    "qmm_gemv_wmma": (c_int, [ctypes.POINTER(GemvSeg), c_int, XQ8, c_int, c_int, c_vp]),
+    "qmm_gemv_q4_K_f32": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
+    "qmm_moe_route": (c_int, [c_vp, c_vp, c_vp, c_int, c_vp]),
+    "qmm_moe_route_n": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
+    "qmm_gemv_moe": (c_int, [c_int, c_int, ctypes.POINTER(MoeSegs), c_int, c_vp, c_int, XQ8, c_int, c_int, c_int, c_int, c_vp]),
+    "qmm_moe_silu_quant": (c_int, [c_vp, c_vp, XQ8, c_int, c_int, c_vp]),
+}
+
+_lib = None
+
+
+class QmmError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libhipster_qmm.so once; raise if it is missing (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise QmmError(f"{LIB_PATH} not built: run __graft_entry__.build() (make -C hipster_amd/csrc)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name, None)
+            if fn is None:
+                continue  # reported by exported_symbols(); calling it raises AttributeError below
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    """Names from SIGNATURES that the loaded library actually exports."""
+    L = lib()
+    return [n for n in SIGNATURES if hasattr(L, n)]
+
+
+def check(status, what=""):
+    if status != QMM_OK:
+        raise QmmError(f"{what}: {STATUS.get(status, status)}")
+    return status

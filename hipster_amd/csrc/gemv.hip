@@ -1,0 +1,503 @@
+// gemv.hip -- decode GEMV for GGUF Q4_K / Q6_K weights on gfx950 (wave64).
+//
+// Entry points (C ABI, include/hipster_qmm.h): qmm_quantize_x_q8, qmm_gemv_q8, qmm_gemv_multi,
+// qmm_gemv_q4_K_f32.  Reference counterparts: engine/kernels/gemv.hip:36-51 (x quantiser),
+// :291-321 + :1225-1242 + :1466-1485 (gemv_q8), :1042-1067 + :1355-1369 (gemv_multi),
+// :1177-1216 + :1486-1489 (gemv_q4_K_f32).
+//
+// Q4_K kernel layout ("chunk-coalesced"): a row of nb superblocks is 9*nb 16-byte chunks
+// (chunk 0 of a block = {d, dmin, scales[12]}, chunks 1..8 = qs).  One wave streams a row with
+// lane l owning chunks l, l+64, l+128, ... so every weight load instruction reads 1 KiB of
+// contiguous HBM.  A qs chunk (p = 1..8) holds 16 low nibbles of sub-block 2j and 16 high
+// nibbles of sub-block 2j+1 (j = (p-1)/2, positions 16h..16h+15, h = (p-1)&1); its lane re-reads
+// the block header from L1 (the same lines the wave just fetched) instead of shuffling it over.
+// Activations are int8 (x quantised per 32), staged once per workgroup in LDS when they fit.
+// The per-lane partial sums are reduced across the wave in a fixed butterfly order, so a
+// column's result does not depend on how many columns the call carries (T-invariance).
+#include "qmm_common.hpp"
+
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+namespace qmm {
+namespace {
+
+constexpr int kBlock = 256;        // threads per workgroup (4 waves)
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr size_t kXLdsBudget = 48 * 1024;   // bytes of LDS a workgroup may use for staged x
+
+int g_cu_count = 0;
+int cu_count() {
+    if (g_cu_count == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_cu_count = n;
+        else
+            g_cu_count = 256;
+    }
+    return g_cu_count;
+}
+
+// ------------------------------------------------------------------------------------------
+// x -> q8 per 32 (gemv.hip:36-51 semantics).  One 32-lane half-wave per 32-block.
+__global__ void __launch_bounds__(256) k_quantize_x_q8(const float* __restrict__ x, int8_t* __restrict__ q,
+                                                       float* __restrict__ d, float* __restrict__ s,
+                                                       float2* __restrict__ ds, int K) {
+    const int col = blockIdx.y;
+    const int sb = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
+    if (sb * 32 >= K) return;
+    const float v = x[(size_t)col * K + sb * 32 + l];
+    float amax = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float dd = amax / 127.f, id = amax > 0.f ? 127.f / amax : 0.f;
+    const int qi = __float2int_rn(v * id);
+    int sum = qi;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 32);
+    q[(size_t)col * K + sb * 32 + l] = (int8_t)qi;
+    if (l == 0) {
+        const size_t o = (size_t)col * (K / 32) + sb;
+        d[o] = dd;
+        s[o] = dd * (float)sum;
+        if (ds) ds[o] = make_float2(dd, dd * (float)sum);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Stage q8 x of NCOL columns into LDS: [xq NCOL*K][xd NCOL*K/32][xs NCOL*K/32].
+template <int NCOL>
+__device__ __forceinline__ void stage_xq8(uint8_t* lds, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                          const float* __restrict__ xs, int K) {
+    const int nq = NCOL * K / 16, ns = NCOL * (K / 32) / 4;
+    uint4* dq = (uint4*)lds;
+    for (int i = threadIdx.x; i < nq; i += blockDim.x) dq[i] = ld16(xq + (size_t)i * 16);
+    float4* dd = (float4*)(lds + (size_t)NCOL * K);
+    float4* dsv = dd + ns;
+    for (int i = threadIdx.x; i < ns; i += blockDim.x) {
+        dd[i] = *(const float4*)(xd + (size_t)i * 4);
+        dsv[i] = *(const float4*)(xs + (size_t)i * 4);
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------------------------------
+// Q4_K x int8 GEMV, chunk-coalesced (see file header).  Persistent grid: the rows are split into
+// gridDim.x contiguous ranges, one per workgroup; the 4 waves of a workgroup take the rows of its
+// range round-robin.
+template <int NCOL, bool XLDS>
+__global__ void __launch_bounds__(kBlock) k_gemv_q4k_q8(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                        const float* __restrict__ xd, const float* __restrict__ xs,
+                                                        float* __restrict__ y, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nb = K >> 8, C = 9 * nb, nsb = K >> 5;
+    const size_t rb = (size_t)nb * 144;
+    const int8_t* xq_s = xq; const float* xd_s = xd; const float* xs_s = xs;
+    if constexpr (XLDS) {
+        stage_xq8<NCOL>(smem, xq, xd, xs, K);
+        xq_s = (const int8_t*)smem;
+        xd_s = (const float*)(smem + (size_t)NCOL * K);
+        xs_s = xd_s + (size_t)NCOL * nsb;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = (int)((long long)N * blockIdx.x / gridDim.x), r1 = (int)((long long)N * (blockIdx.x + 1) / gridDim.x);
+    const int nci = (C + 63) >> 6;
+    for (int row = r0 + wave; row < r1; row += kWavesPerBlock) {
+        const uint8_t* rp = W + (size_t)row * rb;
+        float acc[NCOL];
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+#pragma unroll 2
+        for (int i = 0; i < nci; ++i) {
+            const int cidx = lane + 64 * i;
+            if (cidx >= C) break;
+            const int b = cidx / 9, p = cidx - 9 * b;
+            const uint4 w = ld16(rp + (size_t)cidx * 16);
+            if (p == 0) continue;
+            const uint4 hd = ld16(rp + (size_t)b * 144);
+            const int j = (p - 1) >> 1, h = (p - 1) & 1;
+            const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+            const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
+            const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1);
+            const float mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
+            const uint32_t lo0 = w.x & 0x0f0f0f0fu, lo1 = w.y & 0x0f0f0f0fu, lo2 = w.z & 0x0f0f0f0fu, lo3 = w.w & 0x0f0f0f0fu;
+            const uint32_t hi0 = (w.x >> 4) & 0x0f0f0f0fu, hi1 = (w.y >> 4) & 0x0f0f0f0fu, hi2 = (w.z >> 4) & 0x0f0f0f0fu, hi3 = (w.w >> 4) & 0x0f0f0f0fu;
+            const int kA = 256 * b + 64 * j + 16 * h, sA = 8 * b + 2 * j;
+#pragma unroll
+            for (int c = 0; c < NCOL; ++c) {
+                const uint4 xa = ld16(xq_s + (size_t)c * K + kA), xb = ld16(xq_s + (size_t)c * K + kA + 32);
+                int ia = sdot4(lo0, xa.x, 0); ia = sdot4(lo1, xa.y, ia); ia = sdot4(lo2, xa.z, ia); ia = sdot4(lo3, xa.w, ia);
+                int ib = sdot4(hi0, xb.x, 0); ib = sdot4(hi1, xb.y, ib); ib = sdot4(hi2, xb.z, ib); ib = sdot4(hi3, xb.w, ib);
+                const float2 xdv = *(const float2*)(xd_s + (size_t)c * nsb + sA);
+                float a = dA * xdv.x * (float)ia + dB * xdv.y * (float)ib;
+                if (h == 0) {
+                    const float2 xsv = *(const float2*)(xs_s + (size_t)c * nsb + sA);
+                    a -= mA * xsv.x + mB * xsv.y;
+                }
+                acc[c] += a;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) acc[c] = wave_sum(acc[c]);
+        if (lane == 0) {
+#pragma unroll
+            for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Q6_K x int8 GEMV, one superblock per lane, TPR lanes per row (TPR fixed per tensor shape).
+// F = QMM_Q6_K (GGUF 210-byte blocks, 2-byte aligned) or QMM_Q6_K_SOA (row streams).
+// The 208 bytes {ql, qh, scales} of a GGUF block are read as 13 dword-aligned 16-byte loads
+// starting at the dword below the block and realigned by 0 or 2 bytes; d is read on its own.
+struct Q6Parts { uint32_t ql[32], qh[16], sc[4]; float d; };
+
+template <int F>
+__device__ __forceinline__ void q6k_load(const uint8_t* __restrict__ rp, int b, int nb, Q6Parts& o) {
+    if constexpr (F == QMM_Q6_K) {
+        const uint8_t* blk = rp + (size_t)b * 210;
+        const uintptr_t addr = (uintptr_t)blk;
+        const uint32_t sh = (uint32_t)(addr & 3u);
+        const uint8_t* base = (const uint8_t*)(addr & ~(uintptr_t)3);
+        uint32_t raw[53];
+#pragma unroll
+        for (int i = 0; i < 13; ++i) {
+            const uint4 v = ld16_a4(base + 16 * i);
+            raw[4 * i] = v.x; raw[4 * i + 1] = v.y; raw[4 * i + 2] = v.z; raw[4 * i + 3] = v.w;
+        }
+        // bytes 206..209 of the block when it starts 2 bytes into a dword; else only d at 208
+        raw[52] = sh ? *(const uint32_t*)(base + 208) : (uint32_t)(*(const uint16_t*)(blk + 208)) << 16;
+        uint32_t al[52];
+#pragma unroll
+        for (int i = 0; i < 52; ++i) al[i] = alignbyte(raw[i + 1], raw[i], sh);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) o.ql[i] = al[i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o.qh[i] = al[32 + i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.sc[i] = al[48 + i];
+        // d = bytes 208..209 of the block: the top half of raw[52] in both cases
+        o.d = h2f(raw[52] >> 16);
+    } else {
+        const uint8_t* ql = rp + (size_t)b * 128;
+        const uint8_t* qh = rp + (size_t)nb * 128 + (size_t)b * 64;
+        const uint8_t* sc = rp + (size_t)nb * 192 + (size_t)b * 16;
+        const uint16_t* dp = (const uint16_t*)(rp + (size_t)nb * 208) + b;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { const uint4 v = ld16_a4(ql + 16 * i); o.ql[4 * i] = v.x; o.ql[4 * i + 1] = v.y; o.ql[4 * i + 2] = v.z; o.ql[4 * i + 3] = v.w; }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { const uint4 v = ld16_a4(qh + 16 * i); o.qh[4 * i] = v.x; o.qh[4 * i + 1] = v.y; o.qh[4 * i + 2] = v.z; o.qh[4 * i + 3] = v.w; }
+        const uint4 v = ld16_a4(sc);
+        o.sc[0] = v.x; o.sc[1] = v.y; o.sc[2] = v.z; o.sc[3] = v.w;
+        o.d = h2f(*dp);
+    }
+}
+
+// sum over the 256 weights of a Q6_K block against int8 x (x words xw[64], scales xd[8])
+__device__ __forceinline__ float q6k_dot_q8(const Q6Parts& P, const uint32_t* xw, const float* xdv) {
+    float acc = 0.f;
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            int isum[2] = {0, 0};
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const uint32_t A = P.ql[16 * n + w], B = P.ql[16 * n + 8 + w], Hh = P.qh[8 * n + w];
+                uint32_t q;
+                if (g == 0) q = (A & 0x0f0f0f0fu) | ((Hh << 4) & 0x30303030u);
+                else if (g == 1) q = (B & 0x0f0f0f0fu) | ((Hh << 2) & 0x30303030u);
+                else if (g == 2) q = ((A >> 4) & 0x0f0f0f0fu) | (Hh & 0x30303030u);
+                else q = ((B >> 4) & 0x0f0f0f0fu) | ((Hh >> 2) & 0x30303030u);
+                isum[w >> 2] = sdot4(q6_signed(q), xw[32 * n + 8 * g + w], isum[w >> 2]);
+            }
+            const int s16 = 8 * n + 2 * g;   // scale index of the first 16 of this 32-run
+            const int sa = (int)(int8_t)((P.sc[s16 >> 2] >> (8 * (s16 & 3))) & 0xffu);
+            const int sbv = (int)(int8_t)((P.sc[(s16 + 1) >> 2] >> (8 * ((s16 + 1) & 3))) & 0xffu);
+            acc += P.d * xdv[4 * n + g] * (float)(sa * isum[0] + sbv * isum[1]);
+        }
+    }
+    return acc;
+}
+
+template <int F, int NCOL, int TPR, bool XLDS>
+__global__ void __launch_bounds__(kBlock) k_gemv_q6k_q8(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                        const float* __restrict__ xd, const float* __restrict__ xs,
+                                                        float* __restrict__ y, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int ROWS = kBlock / TPR;
+    const int nb = K >> 8, nsb = K >> 5;
+    const size_t rb = (size_t)nb * 210;
+    const int8_t* xq_s = xq; const float* xd_s = xd;
+    if constexpr (XLDS) {
+        stage_xq8<NCOL>(smem, xq, xd, xs, K);
+        xq_s = (const int8_t*)smem;
+        xd_s = (const float*)(smem + (size_t)NCOL * K);
+    }
+    const int lane = threadIdx.x % TPR, r = threadIdx.x / TPR;
+    const int nrb = (N + ROWS - 1) / ROWS;
+    for (int vb = blockIdx.x; vb < nrb; vb += gridDim.x) {
+        const int row = vb * ROWS + r;
+        float acc[NCOL];
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+        if (row < N) {
+            const uint8_t* rp = W + (size_t)row * rb;
+            for (int b = lane; b < nb; b += TPR) {
+                Q6Parts P;
+                q6k_load<F>(rp, b, nb, P);
+#pragma unroll
+                for (int c = 0; c < NCOL; ++c) {
+                    uint32_t xw[64];
+                    const uint4* xp = (const uint4*)(xq_s + (size_t)c * K + (size_t)b * 256);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) { const uint4 v = xp[i]; xw[4 * i] = v.x; xw[4 * i + 1] = v.y; xw[4 * i + 2] = v.z; xw[4 * i + 3] = v.w; }
+                    float xdv[8];
+                    const float4 d0 = *(const float4*)(xd_s + (size_t)c * nsb + 8 * b), d1 = *(const float4*)(xd_s + (size_t)c * nsb + 8 * b + 4);
+                    xdv[0] = d0.x; xdv[1] = d0.y; xdv[2] = d0.z; xdv[3] = d0.w; xdv[4] = d1.x; xdv[5] = d1.y; xdv[6] = d1.z; xdv[7] = d1.w;
+                    acc[c] += q6k_dot_q8(P, xw, xdv);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) acc[c] = group_sum(acc[c], TPR);
+        if (row < N && lane == 0) {
+#pragma unroll
+            for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Q4_K x f32 GEMV (gemv.hip:1177-1216 semantics): acc += dA*sum(x*qA) + dB*sum(x*qB) - the min
+// terms once per sub-block, with f32 x and per-sub-block sums of x staged in LDS when they fit.
+// Same chunk-coalesced weight stream as k_gemv_q4k_q8.
+template <int NCOL, bool XLDS>
+__global__ void __launch_bounds__(kBlock) k_gemv_q4k_f32(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                         float* __restrict__ y, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nb = K >> 8, C = 9 * nb, nsb = K >> 5;
+    const size_t rb = (size_t)nb * 144;
+    // xsum[c][sb] = sum of the 32 x of sub-block sb (sequential order); x itself from LDS or global
+    float* xsum = (float*)smem;
+    const float* xs_src = x;
+    if constexpr (XLDS) {
+        float* xl = xsum + NCOL * nsb;
+        for (int i = threadIdx.x; i < NCOL * K / 4; i += blockDim.x) ((float4*)xl)[i] = ((const float4*)x)[i];
+        xs_src = xl;
+    }
+    for (int i = threadIdx.x; i < NCOL * nsb; i += blockDim.x) {
+        const float* p = x + (size_t)i * 32;
+        float s = 0.f;
+        for (int l = 0; l < 32; ++l) s += p[l];
+        xsum[i] = s;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = (int)((long long)N * blockIdx.x / gridDim.x), r1 = (int)((long long)N * (blockIdx.x + 1) / gridDim.x);
+    const int nci = (C + 63) >> 6;
+    for (int row = r0 + wave; row < r1; row += kWavesPerBlock) {
+        const uint8_t* rp = W + (size_t)row * rb;
+        float acc[NCOL];
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+        for (int i = 0; i < nci; ++i) {
+            const int cidx = lane + 64 * i;
+            if (cidx >= C) break;
+            const int b = cidx / 9, p = cidx - 9 * b;
+            const uint4 w = ld16(rp + (size_t)cidx * 16);
+            if (p == 0) continue;
+            const uint4 hd = ld16(rp + (size_t)b * 144);
+            const int j = (p - 1) >> 1, h = (p - 1) & 1;
+            const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+            const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
+            const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1);
+            const float mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
+            const uint32_t wq[4] = {w.x, w.y, w.z, w.w};
+            const int kA = 256 * b + 64 * j + 16 * h, sA = 8 * b + 2 * j;
+#pragma unroll
+            for (int c = 0; c < NCOL; ++c) {
+                const float* xa = xs_src + (size_t)c * K + kA;
+                float sa = 0.f, sbv = 0.f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 va = *(const float4*)(xa + 4 * q), vb = *(const float4*)(xa + 32 + 4 * q);
+                    const uint32_t wv = wq[q];
+                    sa += va.x * (float)(wv & 15u) + va.y * (float)((wv >> 8) & 15u) + va.z * (float)((wv >> 16) & 15u) + va.w * (float)((wv >> 24) & 15u);
+                    sbv += vb.x * (float)((wv >> 4) & 15u) + vb.y * (float)((wv >> 12) & 15u) + vb.z * (float)((wv >> 20) & 15u) + vb.w * (float)((wv >> 28) & 15u);
+                }
+                float a = dA * sa + dB * sbv;
+                if (h == 0) a -= mA * xsum[c * nsb + sA] + mB * xsum[c * nsb + sA + 1];
+                acc[c] += a;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) acc[c] = wave_sum(acc[c]);
+        if (lane == 0) {
+#pragma unroll
+            for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// host launchers
+inline size_t xq8_lds_bytes(int ncol, int K) { return (size_t)ncol * K + 2 * (size_t)ncol * (K / 32) * 4; }
+
+// workgroups for the persistent row-range kernels: enough to give every CU several waves, never
+// more than one row per wave
+inline int persistent_grid(int N) {
+    const int want = cu_count() * 4;
+    const int maxg = (N + kWavesPerBlock - 1) / kWavesPerBlock;
+    return want < maxg ? want : maxg;
+}
+
+template <int NCOL>
+int launch_q4k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    const size_t lds = xq8_lds_bytes(NCOL, K);
+    const int grid = persistent_grid(N);
+    if (lds <= kXLdsBudget)
+        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, true>), dim3(grid), dim3(kBlock), lds, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
+    else
+        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, false>), dim3(grid), dim3(kBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+// lanes per row for the Q6_K kernel: a function of K only (never of ncol)
+inline int q6k_tpr(int K) { const int nb = K / 256; return nb >= 32 ? 8 : nb >= 8 ? 4 : nb >= 2 ? 2 : 1; }
+
+template <int F, int NCOL, int TPR>
+int launch_q6k_q8_t(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    constexpr int ROWS = kBlock / TPR;
+    const size_t lds = xq8_lds_bytes(NCOL, K);
+    const int grid = (N + ROWS - 1) / ROWS;
+    if (lds <= kXLdsBudget)
+        hipLaunchKernelGGL((k_gemv_q6k_q8<F, NCOL, TPR, true>), dim3(grid), dim3(kBlock), lds, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
+    else
+        hipLaunchKernelGGL((k_gemv_q6k_q8<F, NCOL, TPR, false>), dim3(grid), dim3(kBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+template <int F, int NCOL>
+int launch_q6k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    switch (q6k_tpr(K)) {
+        case 1: return launch_q6k_q8_t<F, NCOL, 1>(W, x, y, N, K, s);
+        case 2: return launch_q6k_q8_t<F, NCOL, 2>(W, x, y, N, K, s);
+        case 4: return launch_q6k_q8_t<F, NCOL, 4>(W, x, y, N, K, s);
+        default: return launch_q6k_q8_t<F, NCOL, 8>(W, x, y, N, K, s);
+    }
+}
+
+template <int NCOL>
+int launch_gemv_q8_ncol(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    switch (fmt) {
+        case QMM_Q4_K: return launch_q4k_q8<NCOL>(W, x, y, N, K, s);
+        case QMM_Q6_K: return launch_q6k_q8<QMM_Q6_K, NCOL>(W, x, y, N, K, s);
+        case QMM_Q6_K_SOA: return launch_q6k_q8<QMM_Q6_K_SOA, NCOL>(W, x, y, N, K, s);
+        default: return QMM_ERR_FORMAT;
+    }
+}
+
+template <int NCOL>
+int launch_q4k_f32(const void* W, const float* x, float* y, int N, int K, hipStream_t s) {
+    const size_t xsum = (size_t)NCOL * (K / 32) * 4, xf = (size_t)NCOL * K * 4;
+    const int grid = persistent_grid(N);
+    if (xsum + xf <= kXLdsBudget)
+        hipLaunchKernelGGL((k_gemv_q4k_f32<NCOL, true>), dim3(grid), dim3(kBlock), xsum + xf, s, (const uint8_t*)W, x, y, N, K);
+    else
+        hipLaunchKernelGGL((k_gemv_q4k_f32<NCOL, false>), dim3(grid), dim3(kBlock), xsum, s, (const uint8_t*)W, x, y, N, K);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+bool fmt_supported_q8(int fmt) { return fmt == QMM_Q4_K || fmt == QMM_Q6_K || fmt == QMM_Q6_K_SOA; }
+
+int check_gemv_shape(int fmt, int N, int K) {
+    if (N <= 0 || K <= 0 || K % 256 != 0) return QMM_ERR_SHAPE;
+    if (fmt == QMM_Q6_K_SOA && ((K / 256) & 1)) return QMM_ERR_SHAPE;   // streams must stay dword aligned
+    return QMM_OK;
+}
+
+}  // namespace
+
+int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    switch (ncol) {
+        case 1: return launch_gemv_q8_ncol<1>(fmt, W, x, y, N, K, s);
+        case 2: return launch_gemv_q8_ncol<2>(fmt, W, x, y, N, K, s);
+        case 3: return launch_gemv_q8_ncol<3>(fmt, W, x, y, N, K, s);
+        case 4: return launch_gemv_q8_ncol<4>(fmt, W, x, y, N, K, s);
+        case 5: return launch_gemv_q8_ncol<5>(fmt, W, x, y, N, K, s);
+        case 6: return launch_gemv_q8_ncol<6>(fmt, W, x, y, N, K, s);
+        case 7: return launch_gemv_q8_ncol<7>(fmt, W, x, y, N, K, s);
+        case 8: return launch_gemv_q8_ncol<8>(fmt, W, x, y, N, K, s);
+        default: return QMM_ERR_SHAPE;
+    }
+}
+
+}  // namespace qmm
+
+using namespace qmm;
+
+extern "C" {
+
+int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream) {
+    if (!x || !out.q || !out.d || !out.s) return QMM_ERR_NULL;
+    if (ncol <= 0 || K <= 0 || K % 32 != 0) return QMM_ERR_SHAPE;
+    dim3 grid((K / 32 + 7) / 8, ncol);
+    hipLaunchKernelGGL(k_quantize_x_q8, grid, dim3(256), 0, (hipStream_t)stream, x, out.q, out.d, out.s, (float2*)out.ds, K);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, int tpr, int rpt, void* stream) {
+    if (!fmt_supported_q8(fmt)) return QMM_ERR_FORMAT;
+    if (!W || !x.q || !x.d || !x.s || !y) return QMM_ERR_NULL;
+    if (int e = check_gemv_shape(fmt, N, K)) return e;
+    if (ncol < 1 || ncol > 8) return QMM_ERR_SHAPE;
+    if (!(tpr == 0 || tpr == 1 || tpr == 2 || tpr == 4 || tpr == 8 || tpr == 16 || tpr == 32)) return QMM_ERR_ARG;
+    if (rpt < 0 || rpt > 3) return QMM_ERR_ARG;
+    return gemv_q8_dispatch(fmt, W, x, y, N, K, ncol, (hipStream_t)stream);
+}
+
+int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void* stream) {
+    if (!segs || !x.q || !x.d || !x.s) return QMM_ERR_NULL;
+    if (nseg < 1 || nseg > 4 || ncol < 1) return QMM_ERR_SHAPE;
+    for (int i = 0; i < nseg; ++i) {
+        if (!fmt_supported_q8(segs[i].fmt)) return QMM_ERR_FORMAT;
+        if (!segs[i].w || !segs[i].y) return QMM_ERR_NULL;
+        if (int e = check_gemv_shape(segs[i].fmt, segs[i].N, segs[i].K)) return e;
+        if (segs[i].K != segs[0].K) return QMM_ERR_SHAPE;
+    }
+    const int K = segs[0].K;
+    for (int c0 = 0; c0 < ncol; c0 += 8) {
+        const int nc = ncol - c0 < 8 ? ncol - c0 : 8;
+        qmm_xq8 xc = {x.q + (size_t)c0 * K, x.d + (size_t)c0 * (K / 32), x.s + (size_t)c0 * (K / 32), nullptr};
+        for (int i = 0; i < nseg; ++i) {
+            const int e = gemv_q8_dispatch(segs[i].fmt, segs[i].w, xc, segs[i].y + (size_t)c0 * segs[i].N, segs[i].N, K, nc, (hipStream_t)stream);
+            if (e) return e;
+        }
+    }
+    return QMM_OK;
+}
+
+int qmm_gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int ncol, int tpr, void* stream) {
+    if (!W || !x || !y) return QMM_ERR_NULL;
+    if (int e = check_gemv_shape(QMM_Q4_K, N, K)) return e;
+    if (ncol < 1 || ncol > 8) return QMM_ERR_SHAPE;
+    if (!(tpr == 0 || tpr == 4 || tpr == 8 || tpr == 16 || tpr == 32)) return QMM_ERR_ARG;
+    hipStream_t s = (hipStream_t)stream;
+    switch (ncol) {
+        case 1: return launch_q4k_f32<1>(W, x, y, N, K, s);
+        case 2: return launch_q4k_f32<2>(W, x, y, N, K, s);
+        case 3: return launch_q4k_f32<3>(W, x, y, N, K, s);
+        case 4: return launch_q4k_f32<4>(W, x, y, N, K, s);
+        case 5: return launch_q4k_f32<5>(W, x, y, N, K, s);
+        case 6: return launch_q4k_f32<6>(W, x, y, N, K, s);
+        case 7: return launch_q4k_f32<7>(W, x, y, N, K, s);
+        default: return launch_q4k_f32<8>(W, x, y, N, K, s);
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,82 @@
+// qmm_common.hpp -- device helpers shared by the gfx950 kernels of libhipster_qmm.
+// Wave64 throughout (CDNA4).  Nothing here allocates; all state lives in caller buffers.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hipster_qmm.h"
+
+namespace qmm {
+
+constexpr int kWave = 64;
+
+// 16-byte and 8-byte vectors that only promise 4-byte alignment: GGUF Q6_K rows (210-byte
+// blocks) are 2- or 4-byte aligned, and CDNA global loads accept dword-aligned multi-dword
+// accesses, so these still compile to one global_load_dwordx4 / dwordx2.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
+}
+__device__ __forceinline__ uint4 ld16(const void* p) { return *(const uint4*)p; }
+__device__ __forceinline__ uint4 ld16_a4(const void* p) {
+    const u32x4_a4 v = *(const u32x4_a4*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);   // v_dot4_i32_i8
+}
+__device__ __forceinline__ uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t shift_bytes) {
+    return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);     // ({hi,lo} >> 8*shift)[31:0]
+}
+
+// The 12 packed scale bytes of a Q4_K block (engine/src/quant.h:37-40) as four byte-vectors:
+// sc[0..3], sc[4..7], m[0..3], m[4..7].  For j<4 the 6-bit values sit in bytes j / j+4; for j>=4
+// the low nibble of byte j+4 carries the low 4 bits and the top two bits of byte j-4 (scale) or
+// byte j (min) carry bits 4-5.
+struct Q4kScaleBytes { uint32_t sc_lo, sc_hi, m_lo, m_hi; };
+__device__ __forceinline__ Q4kScaleBytes q4k_scale_bytes(uint32_t s0, uint32_t s1, uint32_t s2) {
+    Q4kScaleBytes r;
+    r.sc_lo = s0 & 0x3f3f3f3fu;
+    r.m_lo = s1 & 0x3f3f3f3fu;
+    r.sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+    r.m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+    return r;
+}
+// byte i (0..7) of the 8-byte vector {lo, hi}
+__device__ __forceinline__ uint32_t byte8(uint32_t lo, uint32_t hi, int i) {
+    const uint32_t v = i < 4 ? lo : hi;
+    return (v >> (8 * (i & 3))) & 0xffu;
+}
+
+// Q6_K: 6-bit values (0..63, one per byte) -> signed q-32 per byte without carries between bytes.
+__device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
+
+// ---- wave reductions (wave64) ----
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, width);
+    return v;
+}
+
+// bf16 round-to-nearest-even of the top half (no NaN special case, as engine/kernels/gemm.hip:12)
+__device__ __forceinline__ uint32_t f2bf_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+
+}  // namespace qmm
+
+// Host-side launch check shared by the C-ABI wrappers.
+#define QMM_LAUNCH_CHECK()                                                   \
+    do {                                                                     \
+        if (hipGetLastError() != hipSuccess) return QMM_ERR_LAUNCH;          \
+    } while (0)

@@ -1,0 +1,132 @@
+"""Python mirror of the reference's hot-path call surface (``namespace hip`` in
+engine/kernels/gemv.h, gemm.h and fn.h), over the C ABI of libhipster_qmm.so.
+
+Same function names, argument meaning and output layout as the reference; torch CUDA tensors stand
+in for the device pointers (torch is only the device-memory and stream plumbing here).  Errors that
+the reference turns into ``abort()`` raise ``QmmError`` instead.  Every call launches on the current
+torch stream unless ``stream`` is given.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import GemvSeg, MoeSegs, MoeTile, QmmError, XQ8, check  # noqa: F401
+
+WFmt = type("WFmt", (), {"Q4_K": _lib.QMM_Q4_K, "Q5_K": _lib.QMM_Q5_K, "IQ4_XS": _lib.QMM_IQ4_XS,
+                         "Q6_K_SOA": _lib.QMM_Q6_K_SOA, "Q8_0_SOA": _lib.QMM_Q8_0_SOA,
+                         "Q5_1_SOA": _lib.QMM_Q5_1_SOA, "Q6_K": _lib.QMM_Q6_K})
+
+
+def _p(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream(stream):
+    s = torch.cuda.current_stream() if stream is None else stream
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _dev(t, dtype=None, name="tensor"):
+    if t is None or not t.is_cuda:
+        raise QmmError(f"{name} must be a CUDA tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise QmmError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise QmmError(f"{name} must be contiguous")
+    return t
+
+
+class XQ8Buf:
+    """Device buffers of XQ8 (gemv.h:8): q [ncol][K] int8, d/s [ncol][K/32] f32, optional ds."""
+
+    def __init__(self, ncol, K, device="cuda", with_ds=False):
+        self.ncol, self.K = ncol, K
+        self.q = torch.zeros((ncol, K), dtype=torch.int8, device=device)
+        self.d = torch.zeros((ncol, K // 32), dtype=torch.float32, device=device)
+        self.s = torch.zeros((ncol, K // 32), dtype=torch.float32, device=device)
+        self.ds = torch.zeros((ncol, K // 32, 2), dtype=torch.float32, device=device) if with_ds else None
+
+    def c(self):
+        return XQ8(self.q.data_ptr(), self.d.data_ptr(), self.s.data_ptr(), 0 if self.ds is None else self.ds.data_ptr())
+
+
+def wfmt_row_bytes(fmt, K):
+    return _lib.lib().qmm_wfmt_row_bytes(fmt, K)
+
+
+def repack_row_q6_K(src, K):
+    """Host repack of one GGUF Q6_K row (bytes) to the SoA layout (gemv.hip:1341-1350)."""
+    import numpy as np
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.empty_like(src)
+    check(_lib.lib().qmm_repack_row_q6_K(src.ctypes.data, dst.ctypes.data, K), "repack_row_q6_K")
+    return dst
+
+
+def quantize_x_q8(x, out, ncol, K, stream=None):
+    """gemv.h:10: x f32 [ncol][K] -> out (XQ8Buf)."""
+    _dev(x, torch.float32, "x")
+    check(_lib.lib().qmm_quantize_x_q8(_p(x), out.c(), ncol, K, _stream(stream)), "quantize_x_q8")
+
+
+def gemv_q8(fmt, W, x, y, N, K, ncol, tpr=0, rpt=1, stream=None):
+    """gemv.h:25: y[c][n] = W[n] . x[c] for c < ncol (x an XQ8Buf)."""
+    _dev(W, torch.uint8, "W"); _dev(y, torch.float32, "y")
+    check(_lib.lib().qmm_gemv_q8(fmt, _p(W), x.c(), _p(y), N, K, ncol, tpr, rpt, _stream(stream)), "gemv_q8")
+
+
+def _segs(segs):
+    arr = (GemvSeg * len(segs))()
+    for i, (fmt, w, y, N, K) in enumerate(segs):
+        arr[i] = GemvSeg(fmt, w.data_ptr(), y.data_ptr(), N, K)
+    return arr
+
+
+def gemv_multi(segs, x, ncol, stream=None):
+    """gemv.h:28: segs = [(fmt, W, y, N, K), ...] sharing x."""
+    arr = _segs(segs)
+    check(_lib.lib().qmm_gemv_multi(arr, len(segs), x.c(), ncol, _stream(stream)), "gemv_multi")
+
+
+def gemv_wmma_ok(segs):
+    arr = _segs(segs)
+    return bool(_lib.lib().qmm_gemv_wmma_ok(arr, len(segs)))
+
+
+def gemv_wmma(segs, x, ncol, mode=0, stream=None):
+    """gemv.h:36: matrix-core GEMV, T-invariant, ncol <= 16 per launch."""
+    arr = _segs(segs)
+    check(_lib.lib().qmm_gemv_wmma(arr, len(segs), x.c(), ncol, mode, _stream(stream)), "gemv_wmma")
+
+
+def gemv_q4_K_f32(W, x, y, N, K, ncol, tpr=0, stream=None):
+    """gemv.h:57: f32-activation Q4_K GEMV."""
+    _dev(W, torch.uint8, "W"); _dev(x, torch.float32, "x"); _dev(y, torch.float32, "y")
+    check(_lib.lib().qmm_gemv_q4_K_f32(_p(W), _p(x), _p(y), N, K, ncol, tpr, _stream(stream)), "gemv_q4_K_f32")
+
+
+def moe_route(logits, ids, w, T, stream=None):
+    """fn.h:43: logits [T][513] -> ids/w [T][11] (10 routed + shared)."""
+    check(_lib.lib().qmm_moe_route(_p(logits), _p(ids), _p(w), T, _stream(stream)), "moe_route")
+
+
+def moe_route_n(logits, ids, w, T, nexp, stride, topk, stream=None):
+    check(_lib.lib().qmm_moe_route_n(_p(logits), _p(ids), _p(w), T, nexp, stride, topk, _stream(stream)), "moe_route_n")
+
+
+def gemv_moe(fmt, shared_fmt, w, shared, y, ebytes, ids, nexp, x, N, K, T, xrow_te, slotw=None, stream=None):
+    """gemv.h:44: w/shared/y are lists of 1 or 2 tensors (gate|up share a launch)."""
+    nseg = len(w)
+    a = MoeSegs()
+    for g in range(nseg):
+        a.w[g] = w[g].data_ptr(); a.shared[g] = shared[g].data_ptr(); a.y[g] = y[g].data_ptr()
+    a.ebytes = ebytes
+    a.slotw = 0 if slotw is None else slotw.data_ptr()
+    check(_lib.lib().qmm_gemv_moe(fmt, shared_fmt, ctypes.byref(a), nseg, _p(ids), nexp, x.c(), N, K, T, int(xrow_te),
+                                  _stream(stream)), "gemv_moe")
+
+
+def moe_silu_quant(gate, up, xq, rows, n, stream=None):
+    """fn.h:48: h = silu(g)*u quantised per 32 into xq (XQ8Buf of rows x n)."""
+    check(_lib.lib().qmm_moe_silu_quant(_p(gate), _p(up), xq.c(), rows, n, _stream(stream)), "moe_silu_quant")

@@ -1,0 +1,92 @@
+/*
+ * hipster_qmm.h -- C ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * This is the drop-in boundary for the dzannotti/hipster engine's quantized matmul path.  Every
+ * entry point is the `extern "C"` twin of a reference function (cited per declaration as
+ * file:line in the reference repo); a header-only C++ shim (hipster_amd/csrc/shim/) restores the
+ * reference's `namespace hip` names and signatures on top of it, so the engine's callers compile
+ * unchanged.
+ *
+ * Conventions (same as the reference unless stated):
+ *  - All buffers are device pointers owned by the caller.  The library never allocates on these
+ *    calls; work runs asynchronously on `stream` (a hipStream_t passed as void*, NULL = default).
+ *  - Outputs are column-per-token: y[c*N + row].
+ *  - Every call returns a status (QMM_OK = 0).  Where the reference aborts on an unsupported
+ *    format or silently misbehaves on a bad shape, these return an error code before launching.
+ *  - Numerics: no float atomics; every output element is reduced in a fixed order that does not
+ *    depend on the number of columns/tokens in the call (T-invariance, bitwise).
+ */
+#ifndef HIPSTER_QMM_H
+#define HIPSTER_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+enum {
+    QMM_OK = 0,
+    QMM_ERR_FORMAT = -1,    /* weight format not supported by this entry point */
+    QMM_ERR_SHAPE = -2,     /* N/K/ncol/T out of range (e.g. K % 256 != 0) */
+    QMM_ERR_NULL = -3,      /* a required pointer is NULL */
+    QMM_ERR_LAUNCH = -4,    /* the HIP runtime rejected the launch */
+    QMM_ERR_WORKSPACE = -5, /* workspace missing or too small */
+    QMM_ERR_ARG = -6        /* other invalid argument (mode, tpr, ...) */
+};
+
+/* ---- weight formats: values of the reference's `enum class WFmt` (engine/kernels/gemv.h:13),
+ * plus QMM_Q6_K, the GGUF-native 210-byte Q6_K block read without a repack (this build). ---- */
+enum {
+    QMM_Q4_K = 0,      /* GGUF block_q4_K, 144 B / 256 weights (engine/src/quant.h:22) */
+    QMM_Q5_K = 1,      /* not supported yet */
+    QMM_IQ4_XS = 2,    /* not supported yet */
+    QMM_Q6_K_SOA = 3,  /* Q6_K rows repacked [ql K/2][qh K/4][sc K/16][d K/128] (gemv.h:15) */
+    QMM_Q8_0_SOA = 4,  /* not supported yet */
+    QMM_Q5_1_SOA = 5,  /* not supported yet */
+    QMM_Q6_K = 6       /* GGUF block_q6_K, 210 B / 256 weights (quant.h:24) */
+};
+
+/* ---- POD structs, byte-compatible with the reference's (gemv.h:8,27,43,48) ---- */
+/* x quantised per 32: q [ncol][K] int8, d [ncol][K/32] (scale), s [ncol][K/32] (d*sum q);
+ * ds is an optional packed (d, s) float2 copy (reference: XQ8, gemv.h:8). */
+typedef struct { int8_t* q; float* d; float* s; void* ds; } qmm_xq8;
+/* one weight of a merged launch (reference: GemvSeg, gemv.h:27) */
+typedef struct { int32_t fmt; const void* w; float* y; int32_t N, K; } qmm_gemv_seg;
+/* MoE expert weights of one launch (reference: MoeSegs, gemv.h:43) */
+typedef struct { const void* w[2]; const void* shared[2]; float* y[2]; size_t ebytes; const float* slotw; } qmm_moe_segs;
+/* a tile of <= 16*ct expert-sorted columns (reference: MoeTile, gemv.h:48) */
+typedef struct { int32_t expert, k0, ncols; } qmm_moe_tile;
+
+/* ---- library / host helpers ---- */
+const char* qmm_version(void);
+const char* qmm_status_string(int status);
+/* bytes of one row of K weights (reference: wfmt_row_bytes, gemv.hip:1337-1340); 0 if unknown */
+size_t qmm_wfmt_row_bytes(int fmt, int K);
+/* one GGUF Q6_K row -> the SoA layout of QMM_Q6_K_SOA (reference: repack_row_q6_K, gemv.hip:1341-1350) */
+int qmm_repack_row_q6_K(const uint8_t* src, uint8_t* dst, int K);
+
+/* ---- activation quantiser (reference: quantize_x_q8, gemv.h:10, gemv.hip:36-51,1333-1336) ----
+ * per 32 values: d = amax/127, q = round-half-even(x*127/amax), s = d*sum(q); x f32 [ncol][K]. */
+int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream);
+
+/* ---- decode GEMV, int8 activations (reference: gemv_q8, gemv.h:25, gemv.hip:1466-1485) ----
+ * y[c][n] = sum_k W[n][k] * x[c][k] for c < ncol (1..8), K % 256 == 0.  fmt: Q4_K, Q6_K,
+ * Q6_K_SOA.  tpr/rpt are the reference's tuning knobs; this build picks its own launch shape from
+ * the tensor shape only (never from ncol, which keeps the result T-invariant) and accepts any
+ * tpr in {0,1,2,4,8,16,32} and rpt in {0,1,2,3} for compatibility. */
+int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, int tpr, int rpt, void* stream);
+/* several weights sharing x (reference: gemv_multi, gemv.h:28, gemv.hip:1355-1369); up to 4
+ * segments, all with the same K, any ncol (8 columns per pass).  Results are bitwise those of
+ * qmm_gemv_q8 on each segment. */
+int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void* stream);
+/* f32-activation Q4_K GEMV: acc += (d*sc)*sum(x*q) - (dmin*m)*sum(x) per sub-block
+ * (reference: gemv_q4_K_f32, gemv.h:57, gemv.hip:1177-1216,1486-1489); ncol 1..8. */
+int qmm_gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int ncol, int tpr, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HIPSTER_QMM_H */

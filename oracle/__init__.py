@@ -1,0 +1,243 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so) and of the reference's own quant.h
+(oracle/_ref/libqmm_ref.so, when it was built).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg, as the checker.  The product package (hipster_amd/) never imports it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(_HERE, "liboracle.so")
+REF_LIB = os.path.join(_HERE, "_ref", "libqmm_ref.so")
+
+Q4_K, Q6_K_SOA, Q6_K = 0, 3, 6
+_o = None
+_r = None
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def lib():
+    global _o
+    if _o is None:
+        if not os.path.exists(LIB):
+            raise RuntimeError(f"{LIB} missing: run make -C oracle")
+        L = ctypes.CDLL(LIB)
+        L.qo_f16_to_f32.restype = ctypes.c_float
+        L.qo_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.qo_f32_to_bf16.restype = ctypes.c_uint16
+        L.qo_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.qo_row_bytes.restype = ctypes.c_size_t
+        L.qo_row_bytes.argtypes = [I, I]
+        for name, args in {
+            "qo_scale_min_k4": [I, P, P, P],
+            "qo_dequant_q4_K_block": [P, P], "qo_dequant_q6_K_block": [P, P],
+            "qo_repack_row_q6_K": [P, P, I],
+            "qo_dequant_row": [I, P, P, I],
+            "qo_dequant_matrix": [I, P, I, I, P, I], "qo_dequant_matrix_bf16": [I, P, I, I, P, I],
+            "qo_quantize_x_q8": [P, I, P, P, P], "qo_q8_to_f32": [P, P, I, P],
+            "qo_silu_mul": [P, P, ctypes.c_size_t, P],
+            "qo_gemv_ref": [I, P, I, I, P, I, P, P, I],
+            "qo_gemv_ref_rows": [I, P, I, I, P, I, P, I, P, P],
+            "qo_gemv_f32": [I, P, I, I, P, I, P, I],
+            "qo_moe_route": [P, I, I, I, I, P, P],
+            "qo_moe_sort": [P, I, I, I, P, P, P, P],
+            "qo_moe_decode": [I, P, P, P, ctypes.c_size_t, ctypes.c_size_t, P, P, P, P, P, P, I, I, I, I, P, P, P, P],
+            "qo_moe_down_q8": [I, P, ctypes.c_size_t, P, P, P, P, P, I, I, I, I, P, P],
+            "qo_moe_prefill_tokens": [I, P, P, P, ctypes.c_size_t, ctypes.c_size_t, P, P, P, P, P, P, I, I, I, P, I, P, I],
+            "qo_gemm_wq_ref": [I, P, P, I, I, I, P, P, I, P],
+        }.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = None if name in ("qo_scale_min_k4", "qo_dequant_q4_K_block", "qo_dequant_q6_K_block",
+                                         "qo_repack_row_q6_K", "qo_quantize_x_q8", "qo_q8_to_f32", "qo_silu_mul",
+                                         "qo_moe_route") else I
+        _o = L
+    return _o
+
+
+def ref_lib():
+    """The reference's quant.h compiled by oracle/Makefile, or None when it was not built."""
+    global _r
+    if _r is None and os.path.exists(REF_LIB):
+        L = ctypes.CDLL(REF_LIB)
+        L.ref_f16_to_f32.restype = ctypes.c_float
+        L.ref_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.ref_get_scale_min_k4.argtypes = [I, P, P, P]
+        L.ref_get_scale_min_k4.restype = None
+        L.ref_dequant_row.argtypes = [I, P, P, ctypes.c_uint64]
+        L.ref_dequant_row.restype = None
+        _r = L
+    return _r
+
+
+# ---------------------------------------------------------------- numpy-facing helpers
+def row_bytes(fmt, K):
+    return lib().qo_row_bytes(fmt, K)
+
+
+def dequant_rows(fmt, W, K, nthreads=8):
+    """W uint8 [N][row_bytes] -> f32 [N][K]."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    N = W.shape[0]
+    out = np.empty((N, K), dtype=np.float32)
+    if lib().qo_dequant_matrix(fmt, _ptr(W), N, K, _ptr(out), nthreads) != 0:
+        raise ValueError("dequant_matrix")
+    return out
+
+
+def dequant_rows_bf16(fmt, W, K, nthreads=8):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    N = W.shape[0]
+    out = np.empty((N, K), dtype=np.uint16)
+    if lib().qo_dequant_matrix_bf16(fmt, _ptr(W), N, K, _ptr(out), nthreads) != 0:
+        raise ValueError("dequant_matrix_bf16")
+    return out
+
+
+def quantize_x_q8(x):
+    """x f32 [ncol][K] -> (q int8, d f32 [ncol][K/32], s f32)."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    ncol, K = x.shape
+    q = np.empty((ncol, K), dtype=np.int8)
+    d = np.empty((ncol, K // 32), dtype=np.float32)
+    s = np.empty((ncol, K // 32), dtype=np.float32)
+    for c in range(ncol):
+        lib().qo_quantize_x_q8(_ptr(x[c]), K, _ptr(q[c]), _ptr(d[c]), _ptr(s[c]))
+    return q, d, s
+
+
+def q8_to_f32(q, d):
+    q = np.ascontiguousarray(np.atleast_2d(q), dtype=np.int8)
+    d = np.ascontiguousarray(np.atleast_2d(d), dtype=np.float32)
+    ncol, K = q.shape
+    out = np.empty((ncol, K), dtype=np.float32)
+    for c in range(ncol):
+        lib().qo_q8_to_f32(_ptr(q[c]), _ptr(d[c]), K, _ptr(out[c]))
+    return out
+
+
+def gemv_ref(fmt, W, N, K, x, nthreads=8):
+    """double-precision y [ncol][N] and |w*x| sums (bench_gemv.cpp:95-104)."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    ncol = x.shape[0]
+    y = np.empty((ncol, N), dtype=np.float64)
+    mag = np.empty((ncol, N), dtype=np.float64)
+    if lib().qo_gemv_ref(fmt, _ptr(W), N, K, _ptr(x), ncol, _ptr(y), _ptr(mag), nthreads) != 0:
+        raise ValueError("gemv_ref")
+    return y, mag
+
+
+def gemv_ref_rows(fmt, W, N, K, x, rows):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    ncol = x.shape[0]
+    y = np.empty((ncol, len(rows)), dtype=np.float64)
+    mag = np.empty((ncol, len(rows)), dtype=np.float64)
+    if lib().qo_gemv_ref_rows(fmt, _ptr(W), N, K, _ptr(x), ncol, _ptr(rows), len(rows), _ptr(y), _ptr(mag)) != 0:
+        raise ValueError("gemv_ref_rows")
+    return y, mag
+
+
+def gemv_f32(fmt, W, N, K, x, nthreads=1):
+    """CPU baseline: dequant per row + fp32 dot, nthreads host threads."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    y = np.empty((x.shape[0], N), dtype=np.float32)
+    if lib().qo_gemv_f32(fmt, _ptr(W), N, K, _ptr(x), x.shape[0], _ptr(y), nthreads) != 0:
+        raise ValueError("gemv_f32")
+    return y
+
+
+def moe_route(logits, nexp=512, topk=10):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, stride = logits.shape
+    ids = np.empty((T, topk + 1), dtype=np.int32)
+    w = np.empty((T, topk + 1), dtype=np.float32)
+    lib().qo_moe_route(_ptr(logits), T, nexp, stride, topk, _ptr(ids), _ptr(w))
+    return ids, w
+
+
+def moe_sort(ids, maxc):
+    """ids [T][NE] -> (kpos [T*NE], rowtok [T*NE], tiles [nt][3], stiles [nst][3])."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    T, NE = ids.shape
+    NS = T * NE
+    kpos = np.empty(NS, dtype=np.int32)
+    rowtok = np.empty(NS, dtype=np.int32)
+    tiles = np.empty((NS + 1, 3), dtype=np.int32)
+    nst = ctypes.c_int(0)
+    nt = lib().qo_moe_sort(_ptr(ids), T, NE, maxc, _ptr(kpos), _ptr(rowtok), _ptr(tiles), ctypes.byref(nst))
+    return kpos, rowtok, tiles[:nt].copy(), tiles[nt:nt + nst.value].copy()
+
+
+def moe_decode(fmt, Wg, Wu, Wd, Sg, Su, Sd, x, ids, w, H, F):
+    """Per-token decode MoE (q8 activations): returns g, u [T*NE][F], dn [T*NE][H], y [T][H]."""
+    Wg, Wu, Wd, Sg, Su, Sd = (np.ascontiguousarray(a, dtype=np.uint8) for a in (Wg, Wu, Wd, Sg, Su, Sd))
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    T, NE = ids.shape
+    eb_gu, eb_d = Wg[0].nbytes, Wd[0].nbytes
+    g = np.empty((T * NE, F), dtype=np.float32)
+    u = np.empty((T * NE, F), dtype=np.float32)
+    dn = np.empty((T * NE, H), dtype=np.float32)
+    y = np.empty((T, H), dtype=np.float32)
+    rc = lib().qo_moe_decode(fmt, _ptr(Wg), _ptr(Wu), _ptr(Wd), eb_gu, eb_d, _ptr(Sg), _ptr(Su), _ptr(Sd), _ptr(x),
+                             _ptr(ids), _ptr(w), T, NE, H, F, _ptr(g), _ptr(u), _ptr(dn), _ptr(y))
+    if rc != 0:
+        raise ValueError("moe_decode")
+    return g, u, dn, y
+
+
+def moe_down_q8(fmt, Wd, Sd, hq, hd, ids, w, H, F):
+    Wd, Sd = (np.ascontiguousarray(a, dtype=np.uint8) for a in (Wd, Sd))
+    hq = np.ascontiguousarray(hq, dtype=np.int8)
+    hd = np.ascontiguousarray(hd, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    T, NE = ids.shape
+    dn = np.empty((T * NE, H), dtype=np.float32)
+    y = np.empty((T, H), dtype=np.float32)
+    rc = lib().qo_moe_down_q8(fmt, _ptr(Wd), Wd[0].nbytes, _ptr(Sd), _ptr(hq), _ptr(hd), _ptr(ids), _ptr(w), T, NE, H, F,
+                              _ptr(dn), _ptr(y))
+    if rc != 0:
+        raise ValueError("moe_down_q8")
+    return dn, y
+
+
+def moe_prefill_tokens(fmt, Wg, Wu, Wd, Sg, Su, Sd, xb, ids, w, H, F, toks, nthreads=8):
+    Wg, Wu, Wd, Sg, Su, Sd = (np.ascontiguousarray(a, dtype=np.uint8) for a in (Wg, Wu, Wd, Sg, Su, Sd))
+    xb = np.ascontiguousarray(xb, dtype=np.uint16)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    toks = np.ascontiguousarray(toks, dtype=np.int32)
+    NE = ids.shape[1]
+    y = np.empty((len(toks), H), dtype=np.float32)
+    rc = lib().qo_moe_prefill_tokens(fmt, _ptr(Wg), _ptr(Wu), _ptr(Wd), Wg[0].nbytes, Wd[0].nbytes, _ptr(Sg), _ptr(Su),
+                                     _ptr(Sd), _ptr(xb), _ptr(ids), _ptr(w), NE, H, F, _ptr(toks), len(toks), _ptr(y),
+                                     nthreads)
+    if rc != 0:
+        raise ValueError("moe_prefill_tokens")
+    return y
+
+
+def gemm_wq_ref(fmt, W, A_bf16, M, N, K, ms, ns):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    A = np.ascontiguousarray(A_bf16, dtype=np.uint16)
+    ms = np.ascontiguousarray(ms, dtype=np.int32)
+    ns = np.ascontiguousarray(ns, dtype=np.int32)
+    out = np.empty(len(ms), dtype=np.float64)
+    if lib().qo_gemm_wq_ref(fmt, _ptr(W), _ptr(A), M, N, K, _ptr(ms), _ptr(ns), len(ms), _ptr(out)) != 0:
+        raise ValueError("gemm_wq_ref")
+    return out

@@ -1,0 +1,90 @@
+"""Writes tests/golden/*.npz from the reference's OWN CPU dequantisers.
+
+The reference (dzannotti/hipster) ships no kernel-level golden vectors, so this script builds them:
+it calls engine/src/quant.h (f16_to_f32, get_scale_min_k4, dequant_row for GGUF types 12 = Q4_K and
+14 = Q6_K), compiled unchanged from the reference checkout by oracle/Makefile into
+oracle/_ref/libqmm_ref.so, on seeded random blocks plus hand-made special blocks, and stores the
+inputs and the reference's outputs.  Run from the repo root after `make -C oracle`:
+
+    python tests/golden/make_golden.py
+"""
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.abspath(os.path.join(HERE, "..", "..")))
+
+import oracle  # noqa: E402
+from hipster_amd import synth  # noqa: E402
+
+
+def f16(v):
+    return np.array([v], dtype=np.float16).view(np.uint16)[0]
+
+
+def q4k_special():
+    blocks = []
+    z = np.zeros(144, np.uint8); blocks.append(z)                                     # all zero -> 0
+    b = np.zeros(144, np.uint8); b[0:2] = np.array([f16(1.0)], np.uint16).view(np.uint8)
+    b[4:16] = 0x01; b[16:] = 0x21; blocks.append(b)                                  # known answer: 1.0 / 2.0 runs
+    b = np.full(144, 0xFF, np.uint8); b[0:2] = np.array([f16(0.5)], np.uint16).view(np.uint8)
+    b[2:4] = np.array([f16(0.25)], np.uint16).view(np.uint8); blocks.append(b)       # scales/mins 63, q 15
+    b = synth.q4k_blocks(synth.rng(7), 1)[0].copy(); b[0:2] = [0x01, 0x00]; b[2:4] = [0xff, 0x03]; blocks.append(b)  # subnormal d, dmin
+    b = synth.q4k_blocks(synth.rng(8), 1)[0].copy()
+    b[0:2] = np.array([f16(-0.0123)], np.uint16).view(np.uint8); b[2:4] = np.array([f16(-0.5)], np.uint16).view(np.uint8)
+    blocks.append(b)                                                                  # negative d and dmin
+    b = synth.q4k_blocks(synth.rng(9), 1)[0].copy(); b[4:16] = [0xC0, 0x80, 0x40, 0xFF, 0xC0, 0x3F, 0x00, 0x80, 0xF0, 0x0F, 0xA5, 0x5A]
+    blocks.append(b)                                                                  # top-bit patterns of the packed scales
+    return np.stack(blocks)
+
+
+def q6k_special():
+    blocks = []
+    b = np.zeros(210, np.uint8); b[192:208] = 1; b[208:210] = np.array([f16(1.0)], np.uint16).view(np.uint8)
+    blocks.append(b)                                                                  # q = 0 everywhere -> -32
+    b = np.full(210, 0xFF, np.uint8); b[192:208] = 1; b[208:210] = np.array([f16(1.0)], np.uint16).view(np.uint8)
+    blocks.append(b)                                                                  # q = 63 -> 31
+    b = synth.q6k_blocks(synth.rng(11), 1)[0].copy(); b[192:208] = 0x80; blocks.append(b)   # int8 scale -128
+    b = synth.q6k_blocks(synth.rng(12), 1)[0].copy(); b[208:210] = [0x03, 0x00]; blocks.append(b)  # subnormal d
+    b = synth.q6k_blocks(synth.rng(13), 1)[0].copy(); b[208:210] = np.array([f16(-0.75)], np.uint16).view(np.uint8)
+    blocks.append(b)                                                                  # negative d
+    return np.stack(blocks)
+
+
+def ref_dequant(ref, gtype, blocks):
+    out = np.empty((blocks.shape[0], 256), np.float32)
+    for i in range(blocks.shape[0]):
+        blk = np.ascontiguousarray(blocks[i])
+        ref.ref_dequant_row(gtype, ctypes.c_void_p(blk.ctypes.data), ctypes.c_void_p(out[i].ctypes.data), 256)
+    return out
+
+
+def main():
+    ref = oracle.ref_lib()
+    if ref is None:
+        sys.exit("oracle/_ref/libqmm_ref.so not built (needs the reference checkout): make -C oracle")
+    q4 = np.concatenate([q4k_special(), synth.q4k_blocks(synth.rng(20250), 250)])
+    q6 = np.concatenate([q6k_special(), synth.q6k_blocks(synth.rng(20251), 250)])
+    q4_y = ref_dequant(ref, 12, q4)
+    q6_y = ref_dequant(ref, 14, q6)
+    halfs = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f16_tab = np.array([ref.ref_f16_to_f32(int(h)) for h in halfs], dtype=np.float32)
+    # get_scale_min_k4 over j = 0..7 for 64 seeded 12-byte scale arrays
+    sc_in = synth.rng(20252).integers(0, 256, (64, 12), dtype=np.uint8)
+    sc_out = np.empty((64, 8, 2), np.uint8)
+    for i in range(64):
+        s = np.ascontiguousarray(sc_in[i])
+        for j in range(8):
+            d = ctypes.c_uint8(); m = ctypes.c_uint8()
+            ref.ref_get_scale_min_k4(j, ctypes.c_void_p(s.ctypes.data), ctypes.byref(d), ctypes.byref(m))
+            sc_out[i, j] = (d.value, m.value)
+    np.savez_compressed(os.path.join(HERE, "quant_golden.npz"), q4k_blocks=q4, q4k_y=q4_y, q6k_blocks=q6, q6k_y=q6_y,
+                        f16_bits=halfs, f16_f32=f16_tab, scale_in=sc_in, scale_out=sc_out)
+    print("wrote quant_golden.npz:", q4.shape, q6.shape)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,80 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function include/hipster_qmm.h
+declares, the host helpers match the oracle, and argument validation returns error codes before any
+device work (these calls never reach the GPU)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from hipster_amd import _lib, synth
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "hipster_qmm.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qmm_[a-z0-9_A-Z]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    missing = [n for n in header_functions() if not hasattr(L, n)]
+    assert not missing, missing
+    # and the ctypes signature table covers the header
+    assert set(header_functions()) <= set(_lib.SIGNATURES), set(header_functions()) - set(_lib.SIGNATURES)
+
+
+def test_version_and_status_strings():
+    L = _lib.lib()
+    assert b"gfx950" in L.qmm_version()
+    assert L.qmm_status_string(0) == b"ok"
+    assert L.qmm_status_string(-1) == b"unsupported weight format"
+
+
+def test_row_bytes_and_repack_match_oracle():
+    L = _lib.lib()
+    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q4_K, 5120) == 20 * 144
+    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q6_K, 17408) == 68 * 210
+    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q6_K_SOA, 17408) == 68 * 210
+    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q4_K, 100) == 0
+    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q5_K, 256) == 0
+    W = synth.matrix(5, synth.Q6_K, 4, 2048)
+    soa = synth.repack_q6k_soa(W, 2048)
+    for r in range(4):
+        src = np.ascontiguousarray(W[r]); dst = np.empty_like(src)
+        assert L.qmm_repack_row_q6_K(src.ctypes.data, dst.ctypes.data, 2048) == 0
+        assert np.array_equal(dst, soa[r])
+    assert L.qmm_repack_row_q6_K(None, None, 256) == -3
+
+
+def _xq(p=1):
+    return _lib.XQ8(p, p, p, 0)
+
+
+def test_argument_validation_without_device_work():
+    L = _lib.lib()
+    dummy = ctypes.c_void_p(16)
+    # unsupported formats are refused (the reference aborts here)
+    for fmt in (_lib.QMM_Q5_K, _lib.QMM_IQ4_XS, _lib.QMM_Q8_0_SOA, _lib.QMM_Q5_1_SOA, 99):
+        assert L.qmm_gemv_q8(fmt, dummy, _xq(16), dummy, 16, 256, 1, 0, 1, None) == -1
+    # bad shapes
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 300, 1, 0, 1, None) == -2
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 0, 256, 1, 0, 1, None) == -2
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 256, 9, 0, 1, None) == -2
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 256, 0, 0, 1, None) == -2
+    # odd block count for the SoA layout
+    assert L.qmm_gemv_q8(_lib.QMM_Q6_K_SOA, dummy, _xq(16), dummy, 16, 768, 1, 0, 1, None) == -2
+    # null pointers
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, None, _xq(16), dummy, 16, 256, 1, 0, 1, None) == -3
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _lib.XQ8(0, 0, 0, 0), dummy, 16, 256, 1, 0, 1, None) == -3
+    # knobs
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 256, 1, 3, 1, None) == -6
+    assert L.qmm_quantize_x_q8(None, _xq(16), 1, 256, None) == -3
+    assert L.qmm_quantize_x_q8(dummy, _xq(16), 1, 100, None) == -2
+    assert L.qmm_gemv_q4_K_f32(dummy, dummy, dummy, 16, 200, 1, 0, None) == -2
+    seg = (_lib.GemvSeg * 2)(_lib.GemvSeg(0, 16, 16, 16, 256), _lib.GemvSeg(0, 16, 16, 16, 512))
+    assert L.qmm_gemv_multi(seg, 2, _xq(16), 1, None) == -2          # K differs between segments
+    assert L.qmm_gemv_multi(seg, 5, _xq(16), 1, None) == -2
