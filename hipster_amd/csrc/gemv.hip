@@ -24,7 +24,7 @@ namespace {
 
 constexpr int kBlock = 256;        // threads per workgroup (4 waves)
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr size_t kXLdsBudget = 48 * 1024;   // bytes of LDS a workgroup may use for staged x
+constexpr size_t kXLdsBudget = 64 * 1024;   // bytes of LDS a workgroup may use for staged x
 
 int g_cu_count = 0;
 int cu_count() {
@@ -82,67 +82,161 @@ __device__ __forceinline__ void stage_xq8(uint8_t* lds, const int8_t* __restrict
 }
 
 // ------------------------------------------------------------------------------------------
-// Q4_K x int8 GEMV, chunk-coalesced (see file header).  Persistent grid: the rows are split into
-// gridDim.x contiguous ranges, one per workgroup; the 4 waves of a workgroup take the rows of its
-// range round-robin.
-template <int NCOL, bool XLDS>
+// Q4_K x int8 GEMV ("pair" mapping).
+//
+// A Q4_K block is {d, dmin, scales[12]} + qs[128]; qs bytes 32j..32j+31 carry sub-block 2j in
+// their low nibbles and sub-block 2j+1 in their high nibbles (engine/src/quant.h:43-53).  One
+// lane owns one such 32-byte "pair" (64 weights): it loads the two 16-byte halves plus the
+// 16-byte block header, decodes only the two scales and two mins it needs, and finishes both
+// sub-block dot products itself.  16 lanes cover a row (lane t takes pairs t, t+16, ... of the
+// row, so pair index j = t & 3 is fixed per lane), a wave covers 4 rows, a 256-thread workgroup
+// 16 rows.  Each wave issues the loads of its whole row group (up to 6 pair iterations) before
+// it computes anything; longer rows are streamed in chunks of 4 iterations with the next chunk's
+// loads in flight while the current one is computed.  The loads are unconditional (indices past
+// the row end are clamped and their results masked), which keeps them straight-line code so the
+// compiler waits for one buffer with a partial vmcnt instead of draining all loads.
+//
+// x (int8 per 32, scale d, d*sum) is staged per workgroup in LDS, transposed at 16-byte
+// granularity so that the 16-byte reads of consecutive lanes (consecutive pairs) hit consecutive
+// banks: unit q of pair p (x[64p + 16q .. +15]) sits at ((q * K/64) + p) * 16, and the four
+// scalars {d(2p), d(2p+1), s(2p), s(2p+1)} of pair p at (K + 16p).
+// Per lane the sums accumulate in pair order; the 16 lanes of a row reduce with a fixed butterfly.
+// Neither depends on NCOL, so a column's result is bitwise the same whatever ncol the call has.
+template <int I>
+struct Q4kPairs { uint4 q0[I], q1[I], h[I]; };
+
+template <int I>
+__device__ __forceinline__ void q4k_load_pairs(const uint8_t* __restrict__ rp, int t, int j, int ntask, int it0,
+                                               Q4kPairs<I>& B) {
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+        const int task = min(t + 16 * (it0 + i), ntask - 1);
+        const uint8_t* bp = rp + (size_t)(task >> 2) * 144;
+        B.h[i] = ld16(bp);
+        B.q0[i] = ld16(bp + 16 + 32 * j);
+        B.q1[i] = ld16(bp + 32 + 32 * j);
+    }
+}
+
+// x operand of one column, either from the transposed LDS copy or from global memory
+template <bool XLDS>
+struct XPairSrc {
+    const uint8_t* q;     // LDS: transposed xq of this column; global: xq row of this column
+    const float* d;       // global only
+    const float* s;       // global only
+    int K;
+    __device__ __forceinline__ void get(int task, uint4& u0, uint4& u1, uint4& u2, uint4& u3, float4& ds) const {
+        if constexpr (XLDS) {
+            const int kq = K >> 6;
+            u0 = ld16(q + (size_t)(task) * 16);
+            u1 = ld16(q + (size_t)(kq + task) * 16);
+            u2 = ld16(q + (size_t)(2 * kq + task) * 16);
+            u3 = ld16(q + (size_t)(3 * kq + task) * 16);
+            ds = *(const float4*)(q + (size_t)K + (size_t)task * 16);
+        } else {
+            const uint8_t* p = q + (size_t)task * 64;
+            u0 = ld16(p); u1 = ld16(p + 16); u2 = ld16(p + 32); u3 = ld16(p + 48);
+            const float2 dd = *(const float2*)(d + 2 * task), ss = *(const float2*)(s + 2 * task);
+            ds = make_float4(dd.x, dd.y, ss.x, ss.y);
+        }
+    }
+};
+
+template <int NCOL, int I, bool XLDS>
+__device__ __forceinline__ void q4k_pairs_compute(const Q4kPairs<I>& B, int t, int j, int ntask, int it0,
+                                                  const XPairSrc<XLDS>* xs, float* acc) {
+    const bool jlo = j < 2;
+    const int sh = (j & 1) * 16;
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+        const int task = t + 16 * (it0 + i);
+        if (task >= ntask) continue;
+        const uint4 hd = B.h[i], w0 = B.q0[i], w1 = B.q1[i];
+        const uint32_t scw = jlo ? (hd.y & 0x3f3f3f3fu) : ((hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u));
+        const uint32_t mw = jlo ? (hd.z & 0x3f3f3f3fu) : (((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u));
+        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+        const float dA = d * (float)((scw >> sh) & 0xffu), dB = d * (float)((scw >> (sh + 8)) & 0xffu);
+        const float mA = dmin * (float)((mw >> sh) & 0xffu), mB = dmin * (float)((mw >> (sh + 8)) & 0xffu);
+        const uint32_t a0 = w0.x & 0x0f0f0f0fu, a1 = w0.y & 0x0f0f0f0fu, a2 = w0.z & 0x0f0f0f0fu, a3 = w0.w & 0x0f0f0f0fu;
+        const uint32_t a4 = w1.x & 0x0f0f0f0fu, a5 = w1.y & 0x0f0f0f0fu, a6 = w1.z & 0x0f0f0f0fu, a7 = w1.w & 0x0f0f0f0fu;
+        const uint32_t b0 = (w0.x >> 4) & 0x0f0f0f0fu, b1 = (w0.y >> 4) & 0x0f0f0f0fu, b2 = (w0.z >> 4) & 0x0f0f0f0fu, b3 = (w0.w >> 4) & 0x0f0f0f0fu;
+        const uint32_t b4 = (w1.x >> 4) & 0x0f0f0f0fu, b5 = (w1.y >> 4) & 0x0f0f0f0fu, b6 = (w1.z >> 4) & 0x0f0f0f0fu, b7 = (w1.w >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) {
+            uint4 u0, u1, u2, u3; float4 ds;
+            xs[c].get(task, u0, u1, u2, u3, ds);
+            int ia = sdot4(a0, u0.x, 0); ia = sdot4(a1, u0.y, ia); ia = sdot4(a2, u0.z, ia); ia = sdot4(a3, u0.w, ia);
+            ia = sdot4(a4, u1.x, ia); ia = sdot4(a5, u1.y, ia); ia = sdot4(a6, u1.z, ia); ia = sdot4(a7, u1.w, ia);
+            int ib = sdot4(b0, u2.x, 0); ib = sdot4(b1, u2.y, ib); ib = sdot4(b2, u2.z, ib); ib = sdot4(b3, u2.w, ib);
+            ib = sdot4(b4, u3.x, ib); ib = sdot4(b5, u3.y, ib); ib = sdot4(b6, u3.z, ib); ib = sdot4(b7, u3.w, ib);
+            acc[c] += dA * (ds.x * (float)ia) + dB * (ds.y * (float)ib) - (mA * ds.z + mB * ds.w);
+        }
+    }
+}
+
+// Stage NCOL columns of q8 x into LDS in the transposed pair layout described above; column c
+// occupies [c * 5K/4, (c+1) * 5K/4).
+template <int NCOL>
+__device__ __forceinline__ void stage_xq8_pairs(uint8_t* lds, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                const float* __restrict__ xs, int K) {
+    const int nu = K >> 4, kq = K >> 6, nsb = K >> 5;
+    for (int v = threadIdx.x; v < NCOL * nu; v += blockDim.x) {
+        const int c = v / nu, u = v - c * nu;          // unit u = x[16u .. 16u+15] of column c
+        const int p = u >> 2, q = u & 3;
+        *(uint4*)(lds + (size_t)c * (K + (K >> 2)) + (size_t)(q * kq + p) * 16) = ld16(xq + (size_t)c * K + (size_t)u * 16);
+    }
+    for (int v = threadIdx.x; v < NCOL * kq; v += blockDim.x) {
+        const int c = v / kq, p = v - c * kq;
+        const float2 dd = *(const float2*)(xd + (size_t)c * nsb + 2 * p), ss = *(const float2*)(xs + (size_t)c * nsb + 2 * p);
+        *(float4*)(lds + (size_t)c * (K + (K >> 2)) + (size_t)K + (size_t)p * 16) = make_float4(dd.x, dd.y, ss.x, ss.y);
+    }
+    __syncthreads();
+}
+
+// ILOAD pair iterations per load batch; NITER > 0: the row is exactly NITER iterations and is
+// loaded in one batch; NITER == 0: any length, streamed in double-buffered batches of ILOAD.
+template <int NCOL, int ILOAD, int NITER, bool XLDS>
 __global__ void __launch_bounds__(kBlock) k_gemv_q4k_q8(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                         const float* __restrict__ xd, const float* __restrict__ xs,
                                                         float* __restrict__ y, int N, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int nb = K >> 8, C = 9 * nb, nsb = K >> 5;
-    const size_t rb = (size_t)nb * 144;
-    const int8_t* xq_s = xq; const float* xd_s = xd; const float* xs_s = xs;
-    if constexpr (XLDS) {
-        stage_xq8<NCOL>(smem, xq, xd, xs, K);
-        xq_s = (const int8_t*)smem;
-        xd_s = (const float*)(smem + (size_t)NCOL * K);
-        xs_s = xd_s + (size_t)NCOL * nsb;
-    }
+    const int nb = K >> 8, ntask = 4 * nb, nsb = K >> 5;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r0 = (int)((long long)N * blockIdx.x / gridDim.x), r1 = (int)((long long)N * (blockIdx.x + 1) / gridDim.x);
-    const int nci = (C + 63) >> 6;
-    for (int row = r0 + wave; row < r1; row += kWavesPerBlock) {
-        const uint8_t* rp = W + (size_t)row * rb;
-        float acc[NCOL];
+    const int t = lane & 15, j = t & 3;
+    const int row = (blockIdx.x * kWavesPerBlock + wave) * 4 + (lane >> 4);
+    const uint8_t* rp = W + (size_t)min(row, N - 1) * ((size_t)nb * 144);
+    Q4kPairs<ILOAD> A, B;
+    q4k_load_pairs<ILOAD>(rp, t, j, ntask, 0, A);        // weights first, then x staging
+    XPairSrc<XLDS> xsrc[NCOL];
+    if constexpr (XLDS) {
+        stage_xq8_pairs<NCOL>(smem, xq, xd, xs, K);
 #pragma unroll
-        for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
-#pragma unroll 2
-        for (int i = 0; i < nci; ++i) {
-            const int cidx = lane + 64 * i;
-            if (cidx >= C) break;
-            const int b = cidx / 9, p = cidx - 9 * b;
-            const uint4 w = ld16(rp + (size_t)cidx * 16);
-            if (p == 0) continue;
-            const uint4 hd = ld16(rp + (size_t)b * 144);
-            const int j = (p - 1) >> 1, h = (p - 1) & 1;
-            const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-            const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
-            const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1);
-            const float mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
-            const uint32_t lo0 = w.x & 0x0f0f0f0fu, lo1 = w.y & 0x0f0f0f0fu, lo2 = w.z & 0x0f0f0f0fu, lo3 = w.w & 0x0f0f0f0fu;
-            const uint32_t hi0 = (w.x >> 4) & 0x0f0f0f0fu, hi1 = (w.y >> 4) & 0x0f0f0f0fu, hi2 = (w.z >> 4) & 0x0f0f0f0fu, hi3 = (w.w >> 4) & 0x0f0f0f0fu;
-            const int kA = 256 * b + 64 * j + 16 * h, sA = 8 * b + 2 * j;
+        for (int c = 0; c < NCOL; ++c) xsrc[c] = XPairSrc<XLDS>{smem + (size_t)c * (K + (K >> 2)), nullptr, nullptr, K};
+    } else {
 #pragma unroll
-            for (int c = 0; c < NCOL; ++c) {
-                const uint4 xa = ld16(xq_s + (size_t)c * K + kA), xb = ld16(xq_s + (size_t)c * K + kA + 32);
-                int ia = sdot4(lo0, xa.x, 0); ia = sdot4(lo1, xa.y, ia); ia = sdot4(lo2, xa.z, ia); ia = sdot4(lo3, xa.w, ia);
-                int ib = sdot4(hi0, xb.x, 0); ib = sdot4(hi1, xb.y, ib); ib = sdot4(hi2, xb.z, ib); ib = sdot4(hi3, xb.w, ib);
-                const float2 xdv = *(const float2*)(xd_s + (size_t)c * nsb + sA);
-                float a = dA * xdv.x * (float)ia + dB * xdv.y * (float)ib;
-                if (h == 0) {
-                    const float2 xsv = *(const float2*)(xs_s + (size_t)c * nsb + sA);
-                    a -= mA * xsv.x + mB * xsv.y;
-                }
-                acc[c] += a;
-            }
+        for (int c = 0; c < NCOL; ++c)
+            xsrc[c] = XPairSrc<XLDS>{(const uint8_t*)(xq + (size_t)c * K), xd + (size_t)c * nsb, xs + (size_t)c * nsb, K};
+    }
+    float acc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+    if constexpr (NITER > 0) {
+        q4k_pairs_compute<NCOL, ILOAD, XLDS>(A, t, j, ntask, 0, xsrc, acc);
+    } else {
+        const int niter = (ntask + 15) >> 4, nbatch = (niter + ILOAD - 1) / ILOAD;
+        const int lastb = (nbatch - 1) * ILOAD;
+        for (int bi = 0; bi < nbatch; bi += 2) {
+            q4k_load_pairs<ILOAD>(rp, t, j, ntask, min((bi + 1) * ILOAD, lastb), B);
+            q4k_pairs_compute<NCOL, ILOAD, XLDS>(A, t, j, ntask, bi * ILOAD, xsrc, acc);
+            q4k_load_pairs<ILOAD>(rp, t, j, ntask, min((bi + 2) * ILOAD, lastb), A);
+            if (bi + 1 < nbatch) q4k_pairs_compute<NCOL, ILOAD, XLDS>(B, t, j, ntask, (bi + 1) * ILOAD, xsrc, acc);
         }
+    }
 #pragma unroll
-        for (int c = 0; c < NCOL; ++c) acc[c] = wave_sum(acc[c]);
-        if (lane == 0) {
+    for (int c = 0; c < NCOL; ++c) acc[c] = group_sum(acc[c], 16);
+    if (t == 0 && row < N) {
 #pragma unroll
-            for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
-        }
+        for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
     }
 }
 
@@ -353,16 +447,33 @@ inline int persistent_grid(int N) {
     return want < maxg ? want : maxg;
 }
 
-template <int NCOL>
-int launch_q4k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
-    const size_t lds = xq8_lds_bytes(NCOL, K);
-    const int grid = persistent_grid(N);
+// Launch shape of the Q4_K kernel: 16 rows per workgroup, the row loaded in one batch when it is
+// at most 6 pair iterations (K <= 6144), else streamed in double-buffered batches of 4.  It
+// depends on (N, K) only, never on ncol (T-invariance).  x goes to LDS when NCOL columns fit in
+// kXLdsBudget (5K/4 bytes per column).
+template <int NCOL, int ILOAD, int NITER>
+int launch_q4k_q8_i(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    const size_t lds = (size_t)NCOL * (K + K / 4);
+    const int grid = (N + 4 * kWavesPerBlock - 1) / (4 * kWavesPerBlock);
     if (lds <= kXLdsBudget)
-        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, true>), dim3(grid), dim3(kBlock), lds, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
+        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, ILOAD, NITER, true>), dim3(grid), dim3(kBlock), lds, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
     else
-        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, false>), dim3(grid), dim3(kBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
+        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, ILOAD, NITER, false>), dim3(grid), dim3(kBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
+}
+
+template <int NCOL>
+int launch_q4k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    switch ((K / 256 * 4 + 15) / 16) {   // pair iterations per lane
+        case 1: return launch_q4k_q8_i<NCOL, 1, 1>(W, x, y, N, K, s);
+        case 2: return launch_q4k_q8_i<NCOL, 2, 2>(W, x, y, N, K, s);
+        case 3: return launch_q4k_q8_i<NCOL, 3, 3>(W, x, y, N, K, s);
+        case 4: return launch_q4k_q8_i<NCOL, 4, 4>(W, x, y, N, K, s);
+        case 5: return launch_q4k_q8_i<NCOL, 5, 5>(W, x, y, N, K, s);
+        case 6: return launch_q4k_q8_i<NCOL, 6, 6>(W, x, y, N, K, s);
+        default: return launch_q4k_q8_i<NCOL, 4, 0>(W, x, y, N, K, s);
+    }
 }
 
 // lanes per row for the Q6_K kernel: a function of K only (never of ncol)
