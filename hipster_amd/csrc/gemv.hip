@@ -24,7 +24,14 @@ namespace {
 
 constexpr int kBlock = 256;        // threads per workgroup (4 waves)
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr size_t kXLdsBudget = 64 * 1024;   // bytes of LDS a workgroup may use for staged x
+#ifndef QMM_XLDS_BUDGET
+#define QMM_XLDS_BUDGET (64 * 1024)
+#endif
+constexpr size_t kXLdsBudget = QMM_XLDS_BUDGET;   // bytes of LDS a workgroup may use for staged x
+// x is loaded ahead of the weights (see k_gemv_q4k_q8) for ncol up to this value
+#ifndef QMM_Q4K_XFIRST_NCOL
+#define QMM_Q4K_XFIRST_NCOL 4
+#endif
 
 int g_cu_count = 0;
 int cu_count() {
@@ -142,40 +149,99 @@ struct XPairSrc {
     }
 };
 
-template <int NCOL, int I, bool XLDS>
-__device__ __forceinline__ void q4k_pairs_compute(const Q4kPairs<I>& B, int t, int j, int ntask, int it0,
+// Lane-constant pieces of the scale/min decode for pair j (engine/src/quant.h:37-40).  The 6-bit
+// scales of sub-blocks 2j, 2j+1 are bytes (2j)&3, (2j+1)&3 of
+//   j < 2:  s[0..3] & 63                          (mins: s[4..7] & 63)
+//   j >= 2: (s[8..11] & 15) | ((s[0..3] >> 6) << 4) (mins: (s[8..11] >> 4) | ((s[4..7] >> 6) << 4))
+// written branch-free as ((s0 >> sh0) & m0) | ((s2 >> sh2) & m2).
+struct Q4kPairDecode {
+    uint32_t sh0, m0, m2, bsh;
+    __device__ __forceinline__ explicit Q4kPairDecode(int j) {
+        const bool lo = j < 2;
+        sh0 = lo ? 0u : 2u;
+        m0 = lo ? 0x3f3f3f3fu : 0x30303030u;
+        m2 = lo ? 0u : 0x0f0f0f0fu;
+        bsh = (uint32_t)(j & 1) * 16u;
+    }
+};
+
+template <int NCOL, int I, bool XLDS, bool EXACT>
+__device__ __forceinline__ void q4k_pairs_compute(const Q4kPairs<I>& B, const Q4kPairDecode& dc, int t, int ntask, int it0,
                                                   const XPairSrc<XLDS>* xs, float* acc) {
-    const bool jlo = j < 2;
-    const int sh = (j & 1) * 16;
 #pragma unroll
     for (int i = 0; i < I; ++i) {
         const int task = t + 16 * (it0 + i);
-        if (task >= ntask) continue;
         const uint4 hd = B.h[i], w0 = B.q0[i], w1 = B.q1[i];
-        const uint32_t scw = jlo ? (hd.y & 0x3f3f3f3fu) : ((hd.w & 0x0f0f0f0fu) | ((hd.y >> 2) & 0x30303030u));
-        const uint32_t mw = jlo ? (hd.z & 0x3f3f3f3fu) : (((hd.w >> 4) & 0x0f0f0f0fu) | ((hd.z >> 2) & 0x30303030u));
+        const uint32_t scw = (((hd.y >> dc.sh0) & dc.m0) | (hd.w & dc.m2)) >> dc.bsh;
+        const uint32_t mw = (((hd.z >> dc.sh0) & dc.m0) | ((hd.w >> 4) & dc.m2)) >> dc.bsh;
         const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-        const float dA = d * (float)((scw >> sh) & 0xffu), dB = d * (float)((scw >> (sh + 8)) & 0xffu);
-        const float mA = dmin * (float)((mw >> sh) & 0xffu), mB = dmin * (float)((mw >> (sh + 8)) & 0xffu);
+        const float dA = d * (float)(scw & 0xffu), dB = d * (float)((scw >> 8) & 0xffu);
+        const float mA = dmin * (float)(mw & 0xffu), mB = dmin * (float)((mw >> 8) & 0xffu);
         const uint32_t a0 = w0.x & 0x0f0f0f0fu, a1 = w0.y & 0x0f0f0f0fu, a2 = w0.z & 0x0f0f0f0fu, a3 = w0.w & 0x0f0f0f0fu;
         const uint32_t a4 = w1.x & 0x0f0f0f0fu, a5 = w1.y & 0x0f0f0f0fu, a6 = w1.z & 0x0f0f0f0fu, a7 = w1.w & 0x0f0f0f0fu;
         const uint32_t b0 = (w0.x >> 4) & 0x0f0f0f0fu, b1 = (w0.y >> 4) & 0x0f0f0f0fu, b2 = (w0.z >> 4) & 0x0f0f0f0fu, b3 = (w0.w >> 4) & 0x0f0f0f0fu;
         const uint32_t b4 = (w1.x >> 4) & 0x0f0f0f0fu, b5 = (w1.y >> 4) & 0x0f0f0f0fu, b6 = (w1.z >> 4) & 0x0f0f0f0fu, b7 = (w1.w >> 4) & 0x0f0f0f0fu;
+        const int tk = EXACT ? task : min(task, ntask - 1);
 #pragma unroll
         for (int c = 0; c < NCOL; ++c) {
             uint4 u0, u1, u2, u3; float4 ds;
-            xs[c].get(task, u0, u1, u2, u3, ds);
+            xs[c].get(tk, u0, u1, u2, u3, ds);
             int ia = sdot4(a0, u0.x, 0); ia = sdot4(a1, u0.y, ia); ia = sdot4(a2, u0.z, ia); ia = sdot4(a3, u0.w, ia);
             ia = sdot4(a4, u1.x, ia); ia = sdot4(a5, u1.y, ia); ia = sdot4(a6, u1.z, ia); ia = sdot4(a7, u1.w, ia);
             int ib = sdot4(b0, u2.x, 0); ib = sdot4(b1, u2.y, ib); ib = sdot4(b2, u2.z, ib); ib = sdot4(b3, u2.w, ib);
             ib = sdot4(b4, u3.x, ib); ib = sdot4(b5, u3.y, ib); ib = sdot4(b6, u3.z, ib); ib = sdot4(b7, u3.w, ib);
-            acc[c] += dA * (ds.x * (float)ia) + dB * (ds.y * (float)ib) - (mA * ds.z + mB * ds.w);
+            const float v = dA * (ds.x * (float)ia) + dB * (ds.y * (float)ib) - (mA * ds.z + mB * ds.w);
+            acc[c] += (EXACT || task < ntask) ? v : 0.f;
         }
     }
 }
 
 // Stage NCOL columns of q8 x into LDS in the transposed pair layout described above; column c
-// occupies [c * 5K/4, (c+1) * 5K/4).
+// occupies [c * 5K/4, (c+1) * 5K/4).  The staging is split in two so that a caller can issue the
+// x loads (L2 hits) before its weight loads: vmcnt retires loads in issue order, so x can then be
+// waited for without waiting for the weights.  Unit v < NCOL*K/16 is 16 bytes of xq; unit
+// NCOL*K/16 + w is the {d, d, s, s} quadruple of pair w.  Each thread takes units
+// threadIdx.x + 256*u, u < U (U * 256 >= NCOL * 5K/64).
+template <int NCOL, int U>
+struct XStage { uint4 v[U]; };
+
+template <int NCOL, int U>
+__device__ __forceinline__ void stage_pairs_load(const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                 const float* __restrict__ xs, int K, XStage<NCOL, U>& S) {
+    const int nq = NCOL * (K >> 4), nt = nq + NCOL * (K >> 6), kq = K >> 6, nsb = K >> 5;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int v = min((int)threadIdx.x + kBlock * u, nt - 1);
+        if (v < nq) {
+            S.v[u] = ld16(xq + (size_t)v * 16);
+        } else {
+            const int w = v - nq, c = w / kq, p = w - c * kq;
+            const float2 dd = *(const float2*)(xd + (size_t)c * nsb + 2 * p), ss = *(const float2*)(xs + (size_t)c * nsb + 2 * p);
+            S.v[u] = make_uint4(__float_as_uint(dd.x), __float_as_uint(dd.y), __float_as_uint(ss.x), __float_as_uint(ss.y));
+        }
+    }
+}
+
+template <int NCOL, int U>
+__device__ __forceinline__ void stage_pairs_store(uint8_t* lds, int K, const XStage<NCOL, U>& S) {
+    const int nu = K >> 4, nq = NCOL * nu, nt = nq + NCOL * (K >> 6), kq = K >> 6;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int v = (int)threadIdx.x + kBlock * u;
+        if (v >= nt) continue;
+        size_t off;
+        if (v < nq) {
+            const int c = v / nu, un = v - c * nu;
+            off = (size_t)c * (K + (K >> 2)) + (size_t)((un & 3) * kq + (un >> 2)) * 16;
+        } else {
+            const int w = v - nq, c = w / kq, p = w - c * kq;
+            off = (size_t)c * (K + (K >> 2)) + (size_t)K + (size_t)p * 16;
+        }
+        *(uint4*)(lds + off) = S.v[u];
+    }
+}
+
+// Same layout, loop form for any K (used when the whole x does not fit the register batch).
 template <int NCOL>
 __device__ __forceinline__ void stage_xq8_pairs(uint8_t* lds, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                 const float* __restrict__ xs, int K) {
@@ -194,22 +260,32 @@ __device__ __forceinline__ void stage_xq8_pairs(uint8_t* lds, const int8_t* __re
 }
 
 // ILOAD pair iterations per load batch; NITER > 0: the row is exactly NITER iterations and is
-// loaded in one batch; NITER == 0: any length, streamed in double-buffered batches of ILOAD.
+// loaded in one batch, with x staged from registers loaded ahead of the weights (XU units per
+// thread); NITER == 0: any length, streamed in double-buffered batches of ILOAD.
 template <int NCOL, int ILOAD, int NITER, bool XLDS>
 __global__ void __launch_bounds__(kBlock) k_gemv_q4k_q8(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                         const float* __restrict__ xd, const float* __restrict__ xs,
                                                         float* __restrict__ y, int N, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int XU = (NITER > 0 && XLDS && NCOL <= QMM_Q4K_XFIRST_NCOL) ? 2 * NCOL : 0;
     const int nb = K >> 8, ntask = 4 * nb, nsb = K >> 5;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = lane & 15, j = t & 3;
     const int row = (blockIdx.x * kWavesPerBlock + wave) * 4 + (lane >> 4);
     const uint8_t* rp = W + (size_t)min(row, N - 1) * ((size_t)nb * 144);
     Q4kPairs<ILOAD> A, B;
-    q4k_load_pairs<ILOAD>(rp, t, j, ntask, 0, A);        // weights first, then x staging
     XPairSrc<XLDS> xsrc[NCOL];
+    if constexpr (XU > 0) {
+        XStage<NCOL, (XU > 0 ? XU : 1)> S;
+        stage_pairs_load<NCOL>(xq, xd, xs, K, S);         // x first (older loads) ...
+        q4k_load_pairs<ILOAD>(rp, t, j, ntask, 0, A);     // ... then the weights
+        stage_pairs_store<NCOL>(smem, K, S);              // waits for x only
+        lds_barrier();                                    // not __syncthreads(): keeps the weight loads in flight
+    } else {
+        q4k_load_pairs<ILOAD>(rp, t, j, ntask, 0, A);
+        if constexpr (XLDS) stage_xq8_pairs<NCOL>(smem, xq, xd, xs, K);
+    }
     if constexpr (XLDS) {
-        stage_xq8_pairs<NCOL>(smem, xq, xd, xs, K);
 #pragma unroll
         for (int c = 0; c < NCOL; ++c) xsrc[c] = XPairSrc<XLDS>{smem + (size_t)c * (K + (K >> 2)), nullptr, nullptr, K};
     } else {
@@ -217,19 +293,22 @@ __global__ void __launch_bounds__(kBlock) k_gemv_q4k_q8(const uint8_t* __restric
         for (int c = 0; c < NCOL; ++c)
             xsrc[c] = XPairSrc<XLDS>{(const uint8_t*)(xq + (size_t)c * K), xd + (size_t)c * nsb, xs + (size_t)c * nsb, K};
     }
+    const Q4kPairDecode dc(j);
+    const bool exact = (nb & 3) == 0;
     float acc[NCOL];
 #pragma unroll
     for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
     if constexpr (NITER > 0) {
-        q4k_pairs_compute<NCOL, ILOAD, XLDS>(A, t, j, ntask, 0, xsrc, acc);
+        if (exact) q4k_pairs_compute<NCOL, ILOAD, XLDS, true>(A, dc, t, ntask, 0, xsrc, acc);
+        else q4k_pairs_compute<NCOL, ILOAD, XLDS, false>(A, dc, t, ntask, 0, xsrc, acc);
     } else {
         const int niter = (ntask + 15) >> 4, nbatch = (niter + ILOAD - 1) / ILOAD;
         const int lastb = (nbatch - 1) * ILOAD;
         for (int bi = 0; bi < nbatch; bi += 2) {
             q4k_load_pairs<ILOAD>(rp, t, j, ntask, min((bi + 1) * ILOAD, lastb), B);
-            q4k_pairs_compute<NCOL, ILOAD, XLDS>(A, t, j, ntask, bi * ILOAD, xsrc, acc);
+            q4k_pairs_compute<NCOL, ILOAD, XLDS, false>(A, dc, t, ntask, bi * ILOAD, xsrc, acc);
             q4k_load_pairs<ILOAD>(rp, t, j, ntask, min((bi + 2) * ILOAD, lastb), A);
-            if (bi + 1 < nbatch) q4k_pairs_compute<NCOL, ILOAD, XLDS>(B, t, j, ntask, (bi + 1) * ILOAD, xsrc, acc);
+            if (bi + 1 < nbatch) q4k_pairs_compute<NCOL, ILOAD, XLDS, false>(B, dc, t, ntask, (bi + 1) * ILOAD, xsrc, acc);
         }
     }
 #pragma unroll

@@ -54,6 +54,20 @@ __device__ __forceinline__ uint32_t byte8(uint32_t lo, uint32_t hi, int i) {
 // Q6_K: 6-bit values (0..63, one per byte) -> signed q-32 per byte without carries between bytes.
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() is a release/acquire fence
+// at workgroup scope over all address spaces, which makes every wave wait for all of its
+// outstanding global loads (vmcnt(0)) before the barrier; a kernel that issued its weight loads
+// ahead of the barrier would lose all overlap.  With the fences restricted to LDS ("local") the
+// barrier waits for LDS traffic only.  The scheduling barriers keep the compiler from hoisting
+// work that consumes those loads above the barrier (which would reintroduce the wait).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // ---- wave reductions (wave64) ----
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
