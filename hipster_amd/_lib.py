@@ -54,6 +54,7 @@ SIGNATURES = {
     "qmm_moe_route_n": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
     "qmm_gemv_moe": (c_int, [c_int, c_int, ctypes.POINTER(MoeSegs), c_int, c_vp, c_int, XQ8, c_int, c_int, c_int, c_int, c_vp]),
     "qmm_moe_silu_quant": (c_int, [c_vp, c_vp, XQ8, c_int, c_int, c_vp]),
+    "qmm_moe_combine_sorted": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
 }
 
 _lib = None

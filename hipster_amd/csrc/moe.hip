@@ -1,0 +1,413 @@
+// moe.hip -- MoE decode path on gfx950 (wave64): routing, expert gather GEMV (gate|up), silu*up ->
+// q8, down projection with the weighted combine, and the prefill combine over sorted rows.
+//
+// Entry points (C ABI, include/hipster_qmm.h) and the reference functions they replace:
+//   qmm_moe_route / qmm_moe_route_n   fn::moe_route        engine/kernels/fn.hip:157-205,301
+//   qmm_gemv_moe                      hip::gemv_moe        engine/kernels/gemv.hip:1075-1129,1385-1394
+//   qmm_moe_silu_quant                fn::moe_silu_quant   engine/kernels/fn.hip:206-211,305
+//   qmm_moe_combine_sorted            fn::moe_combine_sorted engine/kernels/fn.hip:126-132,295-297
+//
+// Expert gather (gate|up, or any call without slot weights): the reference launches one thread
+// group per (token, slot, row block), so an expert picked by several tokens, and the shared expert
+// (picked by every token), is streamed once per token.  Here the workgroup of slot te first checks
+// on the device whether an earlier slot routes to the same expert; if so it exits, otherwise it
+// computes every slot of that expert as columns of one weight read (at most 8 columns per pass).
+// Each distinct expert is thus read once per step, with no host sync and no extra launch.  A
+// column's arithmetic is the same whatever the number of columns (T-invariant, bitwise).
+//
+// Down projection with slot weights: y[t][n] = sum_e slotw[t,e] * (W_{ids[t,e]} . x[t*nexp+e]).
+// The 4 waves of a workgroup split the slots of one token; the per-slot row results meet in LDS
+// and one lane per row adds them in slot order (deterministic, no atomics).
+#include "q4k_pair.hpp"
+#include "qmm_common.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace qmm {
+namespace {
+
+constexpr int kMaxCols = 8;        // columns per pass of the gather GEMV
+
+// ------------------------------------------------------------------------------------------
+// Routing (fn.hip:157-205 semantics).  One 512-thread workgroup per token, up to 2 logits per
+// thread (nexp <= 1024).  Top-k is taken on the logits (softmax is monotone, so this is the top-k of
+// the probabilities without their rounding), ties to the lower expert id: each wave takes the top-k
+// of its values with wave argmax rounds, wave 0 merges the 8*k candidates.  Weights are
+// p_i / sum_{selected} p with p = exp(l - max) / sum_all exp(l - max); slot k is the shared
+// expert: id -1, weight sigmoid(logit[nexp]).
+__device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__device__ __forceinline__ void wave_argmax64(float& v, int& i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int oi = __shfl_xor(i, o, 64);
+        if (route_better(ov, oi, v, i)) { v = ov; i = oi; }
+    }
+}
+
+constexpr int kRouteThreads = 512, kRouteWaves = kRouteThreads / 64, kRouteMaxK = 16;
+
+__global__ void __launch_bounds__(kRouteThreads) k_moe_route(const float* __restrict__ logits, int* __restrict__ ids,
+                                                            float* __restrict__ w, int nexp, int stride, int topk) {
+    __shared__ float red[kRouteWaves];
+    __shared__ float cv[kRouteWaves * kRouteMaxK];
+    __shared__ int ci[kRouteWaves * kRouteMaxK];
+    const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const float* l = logits + (size_t)t * stride;
+    const int i0 = tid, i1 = tid + kRouteThreads;
+    float v0 = i0 < nexp ? l[i0] : -INFINITY, v1 = i1 < nexp ? l[i1] : -INFINITY;
+    // max
+    float mx = fmaxf(v0, v1);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int k = 1; k < kRouteWaves; ++k) mx = fmaxf(mx, red[k]);
+    __syncthreads();
+    // sum of exp (fixed tree order)
+    float e = (i0 < nexp ? expf(v0 - mx) : 0.f) + (i1 < nexp ? expf(v1 - mx) : 0.f);
+    e = wave_sum(e);
+    if (lane == 0) red[wave] = e;
+    __syncthreads();
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kRouteWaves; ++k) sum += red[k];
+    // per-wave top-k on the logits
+    bool u0 = i0 >= nexp, u1 = i1 >= nexp;
+    for (int r = 0; r < topk; ++r) {
+        float bv = -INFINITY; int bi = 0x7fffffff;
+        if (!u0) { bv = v0; bi = i0; }
+        if (!u1 && route_better(v1, i1, bv, bi)) { bv = v1; bi = i1; }
+        wave_argmax64(bv, bi);
+        if (lane == 0) { cv[wave * kRouteMaxK + r] = bv; ci[wave * kRouteMaxK + r] = bi; }
+        if (bi == i0) u0 = true;
+        if (bi == i1) u1 = true;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // merge kRouteWaves * topk candidates, two per lane
+        const int nc = kRouteWaves * topk;
+        const int c0 = lane, c1 = lane + 64;
+        float m0 = -INFINITY, m1 = -INFINITY; int j0 = 0x7fffffff, j1 = 0x7fffffff;
+        if (c0 < nc) { m0 = cv[(c0 / topk) * kRouteMaxK + c0 % topk]; j0 = ci[(c0 / topk) * kRouteMaxK + c0 % topk]; }
+        if (c1 < nc) { m1 = cv[(c1 / topk) * kRouteMaxK + c1 % topk]; j1 = ci[(c1 / topk) * kRouteMaxK + c1 % topk]; }
+        bool t0 = c0 >= nc, t1 = c1 >= nc;
+        float psel = 0.f, wsum = 0.f;
+        int* idt = ids + (size_t)t * (topk + 1);
+        float* wt = w + (size_t)t * (topk + 1);
+        for (int r = 0; r < topk; ++r) {
+            float bv = -INFINITY; int bi = 0x7fffffff;
+            if (!t0) { bv = m0; bi = j0; }
+            if (!t1 && route_better(m1, j1, bv, bi)) { bv = m1; bi = j1; }
+            wave_argmax64(bv, bi);
+            if (bi == j0) t0 = true;
+            if (bi == j1) t1 = true;
+            const float p = expf(bv - mx) / sum;     // wave-uniform
+            wsum += p;                                // selection order
+            if (lane == r) psel = p;
+            if (lane == 0) idt[r] = bi;
+        }
+        if (lane < topk) wt[lane] = psel / wsum;
+        if (lane == 0) {
+            idt[topk] = -1;
+            wt[topk] = 1.f / (1.f + expf(-l[nexp]));
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// h = silu(g) * u quantised per 32 (fn.hip:206-211): one 32-lane half-wave per sub-block.
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+
+__device__ __forceinline__ void half_wave_quant32(float v, int8_t* __restrict__ q, float* __restrict__ d,
+                                                  float* __restrict__ s, size_t sb, int l) {
+    float amax = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float dd = amax / 127.f, id = amax > 0.f ? 127.f / amax : 0.f;
+    const int qi = __float2int_rn(v * id);
+    int sum = qi;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 32);
+    q[sb * 32 + l] = (int8_t)qi;
+    if (l == 0) { d[sb] = dd; s[sb] = dd * (float)sum; }
+}
+
+__global__ void __launch_bounds__(256) k_moe_silu_quant(const float* __restrict__ g, const float* __restrict__ u,
+                                                        int8_t* __restrict__ q, float* __restrict__ d, float* __restrict__ s,
+                                                        size_t nsb) {
+    const size_t sb = (size_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int l = threadIdx.x & 31;
+    if (sb >= nsb) return;
+    const size_t i = sb * 32 + l;
+    half_wave_quant32(silu_f(g[i]) * u[i], q, d, s, sb, l);
+}
+
+// ------------------------------------------------------------------------------------------
+// Expert gather GEMV, Q4_K experts and shared expert.  grid = (row blocks, slots, segments).
+// Row block = 4 waves x (64 / LPR) rows.  I = pair iterations per row (ceil(4 K/256 / LPR)).
+template <int LPR, int I, int NC, bool EXACT>
+__device__ __forceinline__ void moe_cols(const uint8_t* rp, int t, int j, int ntask, uint8_t* smem, int K, int N, int row,
+                                         const int* cols, float* __restrict__ y) {
+    Q4kPairs<I> A;
+    q4k_load_pairs<I, LPR>(rp, t, j, ntask, 0, A);
+    XPairSrc<true> xs[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) xs[c] = XPairSrc<true>{smem + (size_t)c * (K + (K >> 2)), nullptr, nullptr, K};
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.f;
+    const Q4kPairDecode dc(j);
+    q4k_pairs_compute<NC, I, true, EXACT, LPR>(A, dc, t, ntask, 0, xs, acc);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = group_sum(acc[c], LPR);
+    if (t == 0 && row < N) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) y[(size_t)cols[c] * N + row] = acc[c];
+    }
+}
+
+// stage the x rows xrow[c] (c < nc) of q8 x into LDS in the pair layout (column c at c * 5K/4)
+__device__ __forceinline__ void stage_gather(uint8_t* lds, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                             const float* __restrict__ xsum, const int* xrow, int nc, int K) {
+    const int nu = K >> 4, kq = K >> 6, nsb = K >> 5;
+    for (int v = threadIdx.x; v < nc * nu; v += blockDim.x) {
+        const int c = v / nu, u = v - c * nu, p = u >> 2, q = u & 3;
+        *(uint4*)(lds + (size_t)c * (K + (K >> 2)) + (size_t)(q * kq + p) * 16) = ld16(xq + (size_t)xrow[c] * K + (size_t)u * 16);
+    }
+    for (int v = threadIdx.x; v < nc * kq; v += blockDim.x) {
+        const int c = v / kq, p = v - c * kq;
+        const float2 dd = *(const float2*)(xd + (size_t)xrow[c] * nsb + 2 * p), ss = *(const float2*)(xsum + (size_t)xrow[c] * nsb + 2 * p);
+        *(float4*)(lds + (size_t)c * (K + (K >> 2)) + (size_t)K + (size_t)p * 16) = make_float4(dd.x, dd.y, ss.x, ss.y);
+    }
+}
+
+template <int LPR, int I>
+__global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
+                                                      const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                      const float* __restrict__ xsum, int N, int K, int nslot, int xrow_te) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_cols[64 + kMaxCols];
+    __shared__ int s_n, s_dup;
+    const int te = blockIdx.y, seg = blockIdx.z, tid = threadIdx.x;
+    const int id = ids[te];
+    if (tid < 64) {
+        // dedup over the slots: leader = the first slot routed to this expert (shared: id < 0)
+        int n = 0, dup = 0;
+        for (int base = 0; base < nslot; base += 64) {
+            const int sl = base + tid;
+            const int sid = sl < nslot ? ids[sl] : 0x7fffffff;
+            const bool m = sl < nslot && (sid == id || (sid < 0 && id < 0));
+            const unsigned long long bal = __ballot(m);
+            // slots before te that match -> duplicate
+            const unsigned long long before = base + 64 <= te ? ~0ull : (te > base ? ((1ull << (te - base)) - 1ull) : 0ull);
+            if (bal & before) dup = 1;
+            // slots >= te that match, in order
+            const unsigned long long from = te <= base ? ~0ull : (te - base >= 64 ? 0ull : ~((1ull << (te - base)) - 1ull));
+            unsigned long long mm = bal & from;
+            while (mm && n < 64) {
+                const int b = __builtin_ctzll(mm);
+                if (tid == 0) s_cols[n] = base + b;
+                ++n;
+                mm &= mm - 1;
+            }
+        }
+        if (tid == 0) { s_n = n; s_dup = dup; }
+    }
+    __syncthreads();
+    if (s_dup) return;
+    const int ncols = s_n;
+    const int nb = K >> 8, ntask = 4 * nb;
+    const int lane = tid & 63, wave = tid >> 6, t = lane & (LPR - 1), j = t & 3;
+    constexpr int RPW = 64 / LPR;
+    const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
+    const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[seg] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[seg];
+    const uint8_t* rp = wbase + (size_t)min(row, N - 1) * ((size_t)nb * 144);
+    float* y = a.y[seg];
+    const bool exact = (ntask % LPR) == 0;
+    for (int c0 = 0; c0 < ncols; c0 += kMaxCols) {
+        const int nc = min(kMaxCols, ncols - c0);
+        int xrow[kMaxCols];
+#pragma unroll
+        for (int c = 0; c < kMaxCols; ++c) {
+            const int sl = s_cols[c0 + min(c, nc - 1)];
+            xrow[c] = xrow_te ? sl : sl / nexp;
+        }
+        if (c0 > 0) __syncthreads();   // previous pass done with the LDS copy
+        stage_gather(smem, xq, xd, xsum, xrow, nc, K);
+        __syncthreads();
+        const int* cols = s_cols + c0;
+#define QMM_MOE_NC(NCV)                                                                                    \
+    case NCV:                                                                                              \
+        if (exact) moe_cols<LPR, I, NCV, true>(rp, t, j, ntask, smem, K, N, row, cols, y);                 \
+        else moe_cols<LPR, I, NCV, false>(rp, t, j, ntask, smem, K, N, row, cols, y);                      \
+        break;
+        switch (nc) {
+            QMM_MOE_NC(1) QMM_MOE_NC(2) QMM_MOE_NC(3) QMM_MOE_NC(4)
+            QMM_MOE_NC(5) QMM_MOE_NC(6) QMM_MOE_NC(7) QMM_MOE_NC(8)
+        }
+#undef QMM_MOE_NC
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Down projection + weighted combine: grid = (row blocks of 64/LPR rows, tokens).  Wave w takes
+// the slots e = w, w+4, ...; per-slot row results go to LDS; lane r of wave 0 sums row r over the
+// slots in order.
+constexpr int kMaxSlots = 16;
+
+template <int LPR, int I>
+__global__ void __launch_bounds__(256) k_gemv_moe_down_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
+                                                           const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                           const float* __restrict__ xsum, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int RPW = 64 / LPR;
+    __shared__ float vres[kMaxSlots][RPW];
+    const int tok = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, t = lane & (LPR - 1), j = t & 3;
+    const int nb = K >> 8, ntask = 4 * nb;
+    const int rloc = lane / LPR, row = blockIdx.x * RPW + rloc;
+    // stage the nexp slot rows of this token
+    int xrow[kMaxSlots];
+#pragma unroll
+    for (int e = 0; e < kMaxSlots; ++e) xrow[e] = tok * nexp + min(e, nexp - 1);
+    stage_gather(smem, xq, xd, xsum, xrow, nexp, K);
+    __syncthreads();
+    const Q4kPairDecode dc(j);
+    const bool exact = (ntask % LPR) == 0;
+    for (int e = wave; e < nexp; e += 4) {
+        const int id = ids[tok * nexp + e];
+        const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[0] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[0];
+        const uint8_t* rp = wbase + (size_t)min(row, N - 1) * ((size_t)nb * 144);
+        Q4kPairs<I> A;
+        q4k_load_pairs<I, LPR>(rp, t, j, ntask, 0, A);
+        XPairSrc<true> xs[1] = {XPairSrc<true>{smem + (size_t)e * (K + (K >> 2)), nullptr, nullptr, K}};
+        float acc[1] = {0.f};
+        if (exact) q4k_pairs_compute<1, I, true, true, LPR>(A, dc, t, ntask, 0, xs, acc);
+        else q4k_pairs_compute<1, I, true, false, LPR>(A, dc, t, ntask, 0, xs, acc);
+        acc[0] = group_sum(acc[0], LPR);
+        if (t == 0) vres[e][rloc] = acc[0];
+    }
+    __syncthreads();
+    if (tid < RPW && blockIdx.x * RPW + tid < N) {
+        float acc = 0.f;
+        for (int e = 0; e < nexp; ++e) acc += a.slotw[tok * nexp + e] * vres[e][tid];
+        a.y[0][(size_t)tok * N + blockIdx.x * RPW + tid] = acc;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// prefill combine over expert-sorted rows (fn.hip:126-132): y[t][d] = sum_e w[t*nexp+e] * down[kpos[t*nexp+e]][d]
+__global__ void __launch_bounds__(256) k_moe_combine_sorted(const float* __restrict__ down, const float* __restrict__ w,
+                                                            const int* __restrict__ kpos, float* __restrict__ y, int nexp, int E) {
+    const int nbk = (E + 255) / 256;
+    const int t = blockIdx.x / nbk, d = (blockIdx.x % nbk) * 256 + threadIdx.x;
+    if (d >= E) return;
+    float acc = 0.f;
+    for (int e = 0; e < nexp; ++e) {
+        const int te = t * nexp + e;
+        acc += w[te] * down[(size_t)kpos[te] * E + d];
+    }
+    y[(size_t)t * E + d] = acc;
+}
+
+// lanes per row for the expert GEMVs: 8 when a row has at most 8 pairs (K <= 512), else 16
+inline int moe_lpr(int K) { return K / 256 * 4 <= 8 ? 8 : 16; }
+
+template <int LPR>
+int launch_gather(const qmm_moe_segs& a, int nseg, const int* ids, int nexp, qmm_xq8 x, int N, int K, int T, int xrow_te,
+                  hipStream_t s) {
+    const int iters = (K / 256 * 4 + LPR - 1) / LPR;
+    const dim3 grid((N + 4 * (64 / LPR) - 1) / (4 * (64 / LPR)), T * nexp, nseg);
+    const size_t lds = (size_t)kMaxCols * (K + K / 4);
+    if (lds > 64 * 1024) return QMM_ERR_SHAPE;
+#define QMM_G(IV) case IV: hipLaunchKernelGGL((k_gemv_moe_q4k<LPR, IV>), grid, dim3(256), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K, T * nexp, xrow_te); break;
+    switch (iters) {
+        QMM_G(1) QMM_G(2) QMM_G(3) QMM_G(4) QMM_G(5) QMM_G(6)
+        default: return QMM_ERR_SHAPE;
+    }
+#undef QMM_G
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+template <int LPR>
+int launch_down(const qmm_moe_segs& a, const int* ids, int nexp, qmm_xq8 x, int N, int K, int T, hipStream_t s) {
+    const int iters = (K / 256 * 4 + LPR - 1) / LPR;
+    const dim3 grid((N + (64 / LPR) - 1) / (64 / LPR), T);
+    const size_t lds = (size_t)nexp * (K + K / 4);
+    if (lds > 64 * 1024) return QMM_ERR_SHAPE;
+#define QMM_D(IV) case IV: hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV>), grid, dim3(256), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K); break;
+    switch (iters) {
+        QMM_D(1) QMM_D(2) QMM_D(3) QMM_D(4) QMM_D(5) QMM_D(6)
+        default: return QMM_ERR_SHAPE;
+    }
+#undef QMM_D
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+}  // namespace
+}  // namespace qmm
+
+using namespace qmm;
+
+extern "C" {
+
+int qmm_moe_route_n(const float* logits, int* ids, float* w, int T, int nexp, int stride, int topk, void* stream) {
+    if (!logits || !ids || !w) return QMM_ERR_NULL;
+    if (T < 0 || nexp < 1 || nexp > 2 * kRouteThreads || topk < 1 || topk > kRouteMaxK || topk > nexp || stride < nexp + 1)
+        return QMM_ERR_SHAPE;
+    if (T == 0) return QMM_OK;
+    hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(kRouteThreads), 0, (hipStream_t)stream, logits, ids, w, nexp, stride, topk);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_moe_route(const float* logits, int* ids, float* w, int T, void* stream) {
+    return qmm_moe_route_n(logits, ids, w, T, 512, 513, 10, stream);
+}
+
+int qmm_moe_silu_quant(const float* gate, const float* up, qmm_xq8 xq, int rows, int n, void* stream) {
+    if (!gate || !up || !xq.q || !xq.d || !xq.s) return QMM_ERR_NULL;
+    if (rows < 0 || n <= 0 || n % 32 != 0) return QMM_ERR_SHAPE;
+    const size_t nsb = (size_t)rows * n / 32;
+    if (nsb == 0) return QMM_OK;
+    hipLaunchKernelGGL(k_moe_silu_quant, dim3((unsigned)((nsb + 7) / 8)), dim3(256), 0, (hipStream_t)stream, gate, up, xq.q, xq.d,
+                       xq.s, nsb);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x, int N, int K,
+                 int T, int xrow_te, void* stream) {
+    if (fmt != QMM_Q4_K || shared_fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+    if (!a || !ids || !x.q || !x.d || !x.s) return QMM_ERR_NULL;
+    if (nseg < 1 || nseg > 2 || N <= 0 || K <= 0 || K % 256 != 0 || T < 0 || nexp < 1 || nexp > kMaxSlots) return QMM_ERR_SHAPE;
+    if (T > 64) return QMM_ERR_SHAPE;   // at most 64 columns (tokens) per expert in the dedup list
+    for (int g = 0; g < nseg; ++g)
+        if (!a->w[g] || !a->shared[g] || !a->y[g]) return QMM_ERR_NULL;
+    if (T == 0) return QMM_OK;
+    hipStream_t s = (hipStream_t)stream;
+    if (a->slotw) {
+        if (nseg != 1) return QMM_ERR_ARG;
+        return moe_lpr(K) == 8 ? launch_down<8>(*a, ids, nexp, x, N, K, T, s) : launch_down<16>(*a, ids, nexp, x, N, K, T, s);
+    }
+    return moe_lpr(K) == 8 ? launch_gather<8>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s)
+                           : launch_gather<16>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s);
+}
+
+int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, float* y, int T, int nexp, int E, void* stream) {
+    if (!down || !w || !kpos || !y) return QMM_ERR_NULL;
+    if (T < 0 || nexp < 1 || E <= 0) return QMM_ERR_SHAPE;
+    if (T == 0) return QMM_OK;
+    const int nbk = (E + 255) / 256;
+    hipLaunchKernelGGL(k_moe_combine_sorted, dim3(T * nbk), dim3(256), 0, (hipStream_t)stream, down, w, kpos, y, nexp, E);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+}  // extern "C"

@@ -127,6 +127,12 @@ def gemv_moe(fmt, shared_fmt, w, shared, y, ebytes, ids, nexp, x, N, K, T, xrow_
                                   _stream(stream)), "gemv_moe")
 
 
+def moe_combine_sorted(down, w, kpos, y, T, nexp, E, stream=None):
+    """fn.h:38: y[t][d] = sum_e w[t*nexp+e] * down[kpos[t*nexp+e]][d] (E is an argument here)."""
+    check(_lib.lib().qmm_moe_combine_sorted(_p(down), _p(w), _p(kpos), _p(y), T, nexp, E, _stream(stream)),
+          "moe_combine_sorted")
+
+
 def moe_silu_quant(gate, up, xq, rows, n, stream=None):
     """fn.h:48: h = silu(g)*u quantised per 32 into xq (XQ8Buf of rows x n)."""
     check(_lib.lib().qmm_moe_silu_quant(_p(gate), _p(up), xq.c(), rows, n, _stream(stream)), "moe_silu_quant")

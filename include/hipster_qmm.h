@@ -86,6 +86,31 @@ int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void
  * (reference: gemv_q4_K_f32, gemv.h:57, gemv.hip:1177-1216,1486-1489); ncol 1..8. */
 int qmm_gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int ncol, int tpr, void* stream);
 
+/* ---- MoE decode ---- */
+/* routing (reference: fn::moe_route, fn.h:43, fn.hip:160-205,301): logits [T][513] f32 -> softmax over
+ * 512 experts -> top-10 (ties to the lower id) -> weights renormalised over the 10; slot 10 is the
+ * shared expert (id -1, weight sigmoid(logits[t][512])).  ids [T][11] int32, w [T][11] f32. */
+int qmm_moe_route(const float* logits, int* ids, float* w, int T, void* stream);
+/* the same for nexp <= 1024 experts, row stride >= nexp+1 (logit nexp = shared gate), topk <= 16:
+ * ids/w [T][topk+1].  No reference counterpart (the reference fixes 512/513/10 at compile time). */
+int qmm_moe_route_n(const float* logits, int* ids, float* w, int T, int nexp, int stride, int topk, void* stream);
+/* expert GEMV (reference: gemv_moe, gemv.h:44, gemv.hip:1075-1129,1385-1394).  Slot te = t*nexp+e
+ * uses expert ids[te] (ids < 0: the shared matrices a->shared[g]); x row = te if xrow_te else t.
+ * Without a->slotw: y[g][te][N] = W[g][ids[te]] . x[row] for g < nseg (gate|up share the launch);
+ * each distinct expert is read once for all the slots routed to it.  With a->slotw (nseg = 1):
+ * y[t][N] = sum_e slotw[te] * (W[ids[te]] . x[te]) summed in slot order (down + combine).
+ * fmt = shared_fmt = QMM_Q4_K; K % 256 == 0, K <= 6144; nexp <= 16; T <= 64. */
+int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x,
+                 int N, int K, int T, int xrow_te, void* stream);
+/* h = silu(gate) * up quantised per 32 into xq, rows x n (reference: fn::moe_silu_quant, fn.h:48,
+ * fn.hip:206-211,305) */
+int qmm_moe_silu_quant(const float* gate, const float* up, qmm_xq8 xq, int rows, int n, void* stream);
+/* prefill combine (reference: fn::moe_combine_sorted, fn.h:38, fn.hip:126-132,295-297):
+ * y[t][d] = sum_e w[t*nexp+e] * down[kpos[t*nexp+e]][d], slot order; the row width E is an argument
+ * here (the reference fixes E = 2560 at compile time). */
+int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, float* y, int T, int nexp, int E,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,3 +78,26 @@ def test_argument_validation_without_device_work():
     seg = (_lib.GemvSeg * 2)(_lib.GemvSeg(0, 16, 16, 16, 256), _lib.GemvSeg(0, 16, 16, 16, 512))
     assert L.qmm_gemv_multi(seg, 2, _xq(16), 1, None) == -2          # K differs between segments
     assert L.qmm_gemv_multi(seg, 5, _xq(16), 1, None) == -2
+
+
+def test_moe_argument_validation_without_device_work():
+    L = _lib.lib()
+    d = ctypes.c_void_p(16)
+    assert L.qmm_moe_route(None, d, d, 1, None) == -3
+    assert L.qmm_moe_route_n(d, d, d, 1, 512, 512, 10, None) == -2        # stride must hold the shared gate logit
+    assert L.qmm_moe_route_n(d, d, d, 1, 2048, 2049, 10, None) == -2      # too many experts
+    assert L.qmm_moe_route_n(d, d, d, 1, 64, 65, 17, None) == -2          # top-k above 16
+    assert L.qmm_moe_route_n(d, d, d, 0, 64, 65, 4, None) == 0            # empty batch: nothing to do
+    segs = _lib.MoeSegs()
+    for g in range(2):
+        segs.w[g] = 16; segs.shared[g] = 16; segs.y[g] = 16
+    segs.ebytes = 1024
+    assert L.qmm_gemv_moe(_lib.QMM_Q6_K, _lib.QMM_Q4_K, ctypes.byref(segs), 2, d, 11, _xq(16), 512, 2048, 1, 0, None) == -1
+    assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, ctypes.byref(segs), 2, d, 11, _xq(16), 512, 2000, 1, 0, None) == -2
+    assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, ctypes.byref(segs), 2, d, 17, _xq(16), 512, 2048, 1, 0, None) == -2
+    assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, ctypes.byref(segs), 2, d, 11, _xq(16), 512, 2048, 65, 0, None) == -2
+    assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, None, 2, d, 11, _xq(16), 512, 2048, 1, 0, None) == -3
+    segs.slotw = 16
+    assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, ctypes.byref(segs), 2, d, 11, _xq(16), 512, 2048, 1, 1, None) == -6
+    assert L.qmm_moe_silu_quant(d, d, _xq(16), 4, 100, None) == -2
+    assert L.qmm_moe_combine_sorted(d, d, None, d, 4, 11, 2048, None) == -3

@@ -1,0 +1,197 @@
+"""GPU parity of the MoE decode path (routing, expert gather GEMV, silu*up -> q8, down + combine,
+prefill combine) against the CPU oracle, through the C ABI.
+
+Bars: routing ids bit-exact; weights and outputs within rel 1e-5 of the
+oracle fed with the same stage inputs; per-slot expert outputs bitwise equal to the plain decode GEMV
+of that expert (so the device-side expert dedup changes nothing); a token's result bitwise the same
+alone and inside a batch (T-invariance).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hipster_amd import qmm, synth
+from tests.gpu_util import dev, host, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+H, F = 2048, 512          # hidden 2048, expert FF 512
+
+
+def experts(seed, n_exp, N, K):
+    return synth.experts(seed, synth.Q4_K, n_exp, N, K)
+
+
+@pytest.mark.parametrize("T,zipf", [(1, None), (4, None), (8, None), (2048, 1.1)])
+def test_route_matches_oracle(gpu, T, zipf):
+    logits = synth.router_logits(1200 + T, T, 512, zipf)
+    ids_ref, w_ref = oracle.moe_route(logits, 512, 10)
+    ids = torch.zeros((T, 11), dtype=torch.int32, device="cuda")
+    w = torch.zeros((T, 11), dtype=torch.float32, device="cuda")
+    qmm.moe_route(dev(logits), ids, w, T)
+    assert np.array_equal(host(ids), ids_ref)
+    np.testing.assert_allclose(host(w), w_ref, rtol=1e-5, atol=1e-7)
+
+
+def test_route_ties_and_small_expert_counts(gpu):
+    logits = synth.router_logits(7, 6, 64)
+    logits[0, [3, 9, 40]] = 5.0          # exact ties: lower ids first
+    logits[1, :64] = 1.0                 # all equal
+    logits[2, 60:64] = 9.0
+    for nexp, topk in ((64, 4), (64, 10), (33, 16)):
+        lg = np.ascontiguousarray(logits[:, :nexp + 1] if nexp + 1 <= 65 else logits)
+        ids_ref, w_ref = oracle.moe_route(lg, nexp, topk)
+        ids = torch.zeros((6, topk + 1), dtype=torch.int32, device="cuda")
+        w = torch.zeros((6, topk + 1), dtype=torch.float32, device="cuda")
+        qmm.moe_route_n(dev(lg), ids, w, 6, nexp, lg.shape[1], topk)
+        assert np.array_equal(host(ids), ids_ref), (nexp, topk)
+        np.testing.assert_allclose(host(w), w_ref, rtol=1e-5, atol=1e-7)
+
+
+def test_moe_silu_quant(gpu):
+    rows, n = 88, 512
+    g = synth.normal_f32(30, (rows, n)) * 3
+    u = synth.normal_f32(31, (rows, n))
+    g[0, :32] = 0.0
+    xq = qmm.XQ8Buf(rows, n)
+    qmm.moe_silu_quant(dev(g), dev(u), xq, rows, n)
+    h = np.empty_like(g)
+    oracle.lib().qo_silu_mul(oracle._ptr(g), oracle._ptr(u), g.size, oracle._ptr(h))
+    q, d, s = oracle.quantize_x_q8(h)
+    gq, gd = host(xq.q), host(xq.d)
+    # silu's exp may differ from the host libm by an ulp, which can move a value across a rounding
+    # boundary of the quantiser: allow a difference of one quantum on at most 0.1% of the values
+    assert np.max(np.abs(gq.astype(int) - q.astype(int))) <= 1
+    assert np.mean(gq != q) < 1e-3
+    np.testing.assert_allclose(gd, d, rtol=1e-5)
+    np.testing.assert_allclose(oracle.q8_to_f32(gq, gd), oracle.q8_to_f32(q, d), rtol=0, atol=float(d.max()) * 1.01)
+
+
+def gather(ids, nexp, Wg, Wu, Sg, Su, x, T):
+    """GPU gate|up for all slots: returns g, u [T*nexp][F] and the x quantised on the GPU."""
+    xb = qmm.XQ8Buf(T, H)
+    qmm.quantize_x_q8(dev(x), xb, T, H)
+    g = torch.full((T * nexp, F), float("nan"), device="cuda")
+    u = torch.full((T * nexp, F), float("nan"), device="cuda")
+    eb = Wg[0].nbytes
+    qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [Wg, Wu], [Sg, Su], [g, u], eb, ids, nexp, xb, F, H, T, False)
+    return g, u, xb
+
+
+@pytest.mark.parametrize("T", [1, 4, 8])
+def test_gemv_moe_gate_up_equals_per_expert_gemv(gpu, T):
+    n_exp = 64
+    Wg_h, Wu_h = experts(1210, n_exp, F, H), experts(1211, n_exp, F, H)
+    Sg_h, Su_h = synth.matrix(1212, synth.Q4_K, F, H), synth.matrix(1213, synth.Q4_K, F, H)
+    x = synth.normal_f32(1214, (T, H))
+    logits = synth.router_logits(1215, T, n_exp)
+    ids_h, _ = oracle.moe_route(logits, n_exp, 10)
+    if T >= 4:                      # force experts shared between tokens (exercise the dedup)
+        ids_h[1, 3] = ids_h[0, 5]
+        ids_h[2, 0] = ids_h[0, 5]
+        ids_h[3, 9] = ids_h[1, 1]
+    nexp = 11
+    Wg, Wu, Sg, Su = dev(Wg_h), dev(Wu_h), dev(Sg_h), dev(Su_h)
+    ids = dev(ids_h)
+    g, u, xb = gather(ids, nexp, Wg, Wu, Sg, Su, x, T)
+    gh, uh = host(g), host(u)
+    q, d, _ = oracle.quantize_x_q8(x)
+    xr = oracle.q8_to_f32(q, d)
+    for t in range(T):
+        for e in range(nexp):
+            te, eid = t * nexp + e, ids_h[t, e]
+            for seg, (Wx, Sx, out) in enumerate(((Wg, Sg, gh), (Wu, Su, uh))):
+                Wm = Wx[eid] if eid >= 0 else Sx
+                y1 = torch.zeros((1, F), device="cuda")
+                xb1 = qmm.XQ8Buf(1, H)
+                qmm.quantize_x_q8(dev(x[t:t + 1]), xb1, 1, H)
+                qmm.gemv_q8(synth.Q4_K, Wm.contiguous(), xb1, y1, F, H, 1)
+                assert np.array_equal(out[te].view(np.uint32), host(y1)[0].view(np.uint32)), (t, e, seg)
+        # and against the oracle (same-math q8 x, double dot)
+        for e in (0, 7, 10):
+            eid = ids_h[t, e]
+            Wm = Wg_h[eid] if eid >= 0 else Sg_h
+            ref, _ = oracle.gemv_ref(synth.Q4_K, Wm, F, H, xr[t:t + 1])
+            assert rel_l2(gh[t * nexp + e], ref[0]) <= 1e-5
+
+
+def test_gemv_moe_down_combine_matches_oracle(gpu):
+    T, nexp, n_exp = 8, 11, 64
+    Wd_h = experts(1220, n_exp, H, F)
+    Sd_h = synth.matrix(1221, synth.Q4_K, H, F)
+    logits = synth.router_logits(1222, T, n_exp)
+    ids_h, w_h = oracle.moe_route(logits, n_exp, 10)
+    ids_h[5, 2] = ids_h[4, 2]
+    hrows = synth.normal_f32(1223, (T * nexp, F))
+    hq = qmm.XQ8Buf(T * nexp, F)
+    qmm.quantize_x_q8(dev(hrows), hq, T * nexp, F)
+    y = torch.full((T, H), float("nan"), device="cuda")
+    qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [dev(Wd_h)], [dev(Sd_h)], [y], Wd_h[0].nbytes, dev(ids_h), nexp, hq, H, F, T,
+                 True, slotw=dev(w_h))
+    dn_ref, y_ref = oracle.moe_down_q8(synth.Q4_K, Wd_h, Sd_h, host(hq.q), host(hq.d), ids_h, w_h, H, F)
+    yh = host(y)
+    for t in range(T):
+        assert rel_l2(yh[t], y_ref[t]) <= 1e-5, t
+
+
+def test_moe_decode_t_invariant_and_end_to_end(gpu):
+    """Full decode MoE on device (route -> gate|up -> silu q8 -> down+combine) for T = 8, and each
+    token again alone: bitwise equal.  End to end against the oracle's own pipeline within 1e-3
+    (its silu uses the host libm exp, which can flip a q8 rounding of h)."""
+    n_exp, T, nexp = 64, 8, 11
+    Wg_h, Wu_h, Wd_h = experts(1230, n_exp, F, H), experts(1231, n_exp, F, H), experts(1232, n_exp, H, F)
+    Sg_h, Su_h, Sd_h = (synth.matrix(1233 + i, synth.Q4_K, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
+    W = [dev(a) for a in (Wg_h, Wu_h, Wd_h, Sg_h, Su_h, Sd_h)]
+    x = synth.normal_f32(1236, (T, H))
+    logits = synth.router_logits(1237, T, n_exp)
+
+    def run(xs, lg):
+        Tn = xs.shape[0]
+        ids = torch.zeros((Tn, nexp), dtype=torch.int32, device="cuda")
+        w = torch.zeros((Tn, nexp), dtype=torch.float32, device="cuda")
+        qmm.moe_route_n(dev(lg), ids, w, Tn, n_exp, lg.shape[1], 10)
+        g, u, _ = gather(ids, nexp, W[0], W[1], W[3], W[4], xs, Tn)
+        hq = qmm.XQ8Buf(Tn * nexp, F)
+        qmm.moe_silu_quant(g, u, hq, Tn * nexp, F)
+        y = torch.zeros((Tn, H), device="cuda")
+        qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [W[2]], [W[5]], [y], Wd_h[0].nbytes, ids, nexp, hq, H, F, Tn, True, slotw=w)
+        return host(y), host(ids), host(w)
+
+    yT, idsT, wT = run(x, logits)
+    for t in range(T):
+        y1, _, _ = run(x[t:t + 1], logits[t:t + 1])
+        assert np.array_equal(y1[0].view(np.uint32), yT[t].view(np.uint32)), t
+    _, _, _, y_ref = oracle.moe_decode(synth.Q4_K, Wg_h, Wu_h, Wd_h, Sg_h, Su_h, Sd_h, x, idsT, wT, H, F)
+    assert rel_l2(yT, y_ref) <= 1e-3
+
+
+def test_moe_full_512_experts_gate_up(gpu):
+    """The BASELINE config-2 expert table (512 Q4_K experts + shared) at T = 8."""
+    n_exp, T, nexp = 512, 8, 11
+    Wg_h, Wu_h = experts(1240, n_exp, F, H), experts(1241, n_exp, F, H)
+    Sg_h, Su_h = synth.matrix(1242, synth.Q4_K, F, H), synth.matrix(1243, synth.Q4_K, F, H)
+    x = synth.normal_f32(1244, (T, H))
+    ids_h, _ = oracle.moe_route(synth.router_logits(1245, T, n_exp), n_exp, 10)
+    g, u, _ = gather(dev(ids_h), nexp, dev(Wg_h), dev(Wu_h), dev(Sg_h), dev(Su_h), x, T)
+    q, d, _ = oracle.quantize_x_q8(x)
+    xr = oracle.q8_to_f32(q, d)
+    gh, uh = host(g), host(u)
+    for t in (0, 7):
+        for e in range(nexp):
+            eid = ids_h[t, e]
+            for W_h, S_h, out in ((Wg_h, Sg_h, gh), (Wu_h, Su_h, uh)):
+                ref, _ = oracle.gemv_ref(synth.Q4_K, W_h[eid] if eid >= 0 else S_h, F, H, xr[t:t + 1])
+                assert rel_l2(out[t * nexp + e], ref[0]) <= 1e-5
+
+
+def test_moe_combine_sorted(gpu):
+    T, nexp, E = 64, 11, 2048
+    NS = T * nexp
+    down = synth.normal_f32(1250, (NS, E))
+    w = np.abs(synth.normal_f32(1251, (T, nexp)))
+    kpos = synth.rng(1252).permutation(NS).astype(np.int32)
+    y = torch.zeros((T, E), device="cuda")
+    qmm.moe_combine_sorted(dev(down), dev(w), dev(kpos), y, T, nexp, E)
+    ref = np.einsum("te,ted->td", w.astype(np.float64), down[kpos.reshape(T, nexp)].astype(np.float64))
+    assert rel_l2(host(y), ref) <= 1e-6
