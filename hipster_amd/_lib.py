@@ -55,6 +55,13 @@ SIGNATURES = {
     "qmm_gemv_moe": (c_int, [c_int, c_int, ctypes.POINTER(MoeSegs), c_int, c_vp, c_int, XQ8, c_int, c_int, c_int, c_int, c_vp]),
     "qmm_moe_silu_quant": (c_int, [c_vp, c_vp, XQ8, c_int, c_int, c_vp]),
     "qmm_moe_combine_sorted": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    "qmm_dequant_bf16": (c_int, [c_int, c_vp, c_vp, c_int, c_int, c_vp]),
+    "qmm_gemm_wq": (c_int, [c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    "qmm_gemm_bf16": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    "qmm_f32_to_bf16": (c_int, [c_vp, c_vp, ctypes.c_size_t, c_vp]),
+    "qmm_bf16_to_f32": (c_int, [c_vp, c_vp, ctypes.c_size_t, c_vp]),
+    "qmm_bf16_to_f32_seg": (c_int, [c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp]),
+    "qmm_bf16_to_f32_seg2": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp]),
 }
 
 _lib = None

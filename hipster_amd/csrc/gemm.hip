@@ -1,0 +1,372 @@
+// gemm.hip -- prefill-sized matrix products on gfx950: dequantisation to bf16, a Q4_K-weight GEMM
+// with the dequantisation fused into the LDS staging of the weight tile, a plain bf16 GEMM and the
+// bf16 <-> f32 helpers of the reference's engine/kernels/gemm.h.
+//
+// Entry points (C ABI, include/hipster_qmm.h) and the reference functions they replace:
+//   qmm_dequant_bf16        hip::dequant_bf16     engine/kernels/gemm.hip:16-76,96-107
+//   qmm_gemm_wq             (new) dequant_bf16 + BlasLt::gemm fused; engine/src/qwen35.cpp:204-239,
+//                           engine/src/qwen4exp.cpp:513-527 are the callers it serves
+//   qmm_gemm_bf16           hip::BlasLt::gemm     engine/kernels/gemm.hip:125-160 (own MFMA kernel, no hipBLASLt)
+//   qmm_f32_to_bf16, qmm_bf16_to_f32, qmm_bf16_to_f32_seg, qmm_bf16_to_f32_seg2   gemm.hip:77-95
+//
+// GEMM tiling (MFMA v_mfma_f32_16x16x32_bf16, wave64): a 256-thread workgroup computes a
+// 256 (M, activation rows) x 128 (N, weight rows) tile of D = A . W^T, stepping K by 64.  Wave w owns
+// rows 64w..64w+63 of the tile and all 128 columns: 4 x 8 MFMA tiles of 16 x 16, 128 f32
+// accumulators per lane.  Per K step the A tile (256 x 64 bf16, 32 KiB) and the W tile (128 x 64)
+// sit in LDS with rows padded to 72 elements (144 B) to spread the 16-byte fragment reads over the
+// banks.  For Q4_K weights a K step of 64 is exactly one 32-byte qs "pair" of each row's block,
+// so two threads per weight row decode one 32-weight sub-block each (header + 32 qs bytes ->
+// 32 bf16) straight into LDS.  The next step's global loads (A: 8 x 16 B per thread, W: 48 B or
+// 64 B) are issued before the MFMAs of the current step and land in registers while they run.
+// Workgroups are mapped XCD-aware: consecutive workgroup ids go to different XCDs, so tile ids are
+// assigned so that the 8 M tiles of one weight tile run on the same XCD and share its L2.
+#include "qmm_common.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace qmm {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------------------------------
+// Bit-exact dequantisation to bf16 (engine/src/quant.h:43-53,65-80 arithmetic, then RNE to bf16 as
+// engine/kernels/gemm.hip:12).  Contraction is off: (d*sc)*q and dmin*m are rounded on their own,
+// exactly as the host reference computes them.
+#pragma clang fp contract(off)
+
+// Q4_K: one thread per 32-weight sub-block (8 per block); writes 32 bf16 (64 B)
+__global__ void __launch_bounds__(256) k_dequant_q4k_bf16(const uint8_t* __restrict__ W, uint16_t* __restrict__ out,
+                                                          size_t nsub, int K) {
+    const size_t g = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= nsub) return;
+    const size_t blk = g >> 3;
+    const int s = (int)(g & 7), j = s >> 1, h = s & 1;
+    const uint8_t* bp = W + blk * 144;
+    const uint4 hd = ld16(bp);
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
+    const float dl = d * (float)byte8(sb.sc_lo, sb.sc_hi, s), ml = dmin * (float)byte8(sb.m_lo, sb.m_hi, s);
+    const uint4 q0 = ld16(bp + 16 + 32 * j), q1 = ld16(bp + 32 + 32 * j);
+    const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    uint32_t o[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t v = h ? (qw[i] >> 4) : qw[i];
+        uint32_t bf[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) bf[b] = f2bf_bits(dl * (float)((v >> (8 * b)) & 15u) - ml);
+        o[2 * i] = bf[0] | (bf[1] << 16);
+        o[2 * i + 1] = bf[2] | (bf[3] << 16);
+    }
+    // element index of this sub-block: row-major [N][K] with K = nb * 256 -> block blk holds elements blk*256..
+    uint4* dst = (uint4*)(out + blk * 256 + 32 * s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
+// Q6_K (GGUF 210-byte blocks, or the row-SoA repack): one thread per 16 weights sharing one scale
+template <int F>
+__global__ void __launch_bounds__(256) k_dequant_q6k_bf16(const uint8_t* __restrict__ W, uint16_t* __restrict__ out,
+                                                          size_t ngrp, int K) {
+    const size_t gi = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (gi >= ngrp) return;
+    const int nb = K >> 8;
+    const size_t blkg = gi >> 4;                       // global block index (row * nb + b)
+    const int grp = (int)(gi & 15);                    // 16-weight group within the block
+    const size_t row = blkg / nb;
+    const int b = (int)(blkg - row * nb);
+    const uint8_t *ql, *qh, *sc, *dp;
+    if constexpr (F == QMM_Q6_K) {
+        const uint8_t* bp = W + blkg * 210;
+        ql = bp; qh = bp + 128; sc = bp + 192; dp = bp + 208;
+    } else {
+        const uint8_t* rp = W + row * ((size_t)nb * 210);
+        ql = rp + (size_t)b * 128; qh = rp + (size_t)nb * 128 + (size_t)b * 64;
+        sc = rp + (size_t)nb * 192 + (size_t)b * 16; dp = rp + (size_t)nb * 208 + (size_t)b * 2;
+    }
+    const float d = h2f((uint32_t)dp[0] | ((uint32_t)dp[1] << 8));
+    // element e = 16 * grp + i: half n = e / 128, r = e % 128, quarter g = r / 32, l = r % 32
+    const int e0 = 16 * grp, n = e0 >> 7, r0 = e0 & 127, g = r0 >> 5, l0 = r0 & 31;
+    const float ds = d * (float)(int8_t)sc[8 * n + (l0 >> 4) + 2 * g];
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+        uint32_t bf[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int l = l0 + i + k;
+            const uint32_t lo = ql[64 * n + l + 32 * (g & 1)], hi = qh[32 * n + l];
+            const int q = (int)((g < 2 ? (lo & 15u) : (lo >> 4)) | (((hi >> (2 * g)) & 3u) << 4)) - 32;
+            bf[k] = f2bf_bits(ds * (float)q);
+        }
+        o[i >> 1] = bf[0] | (bf[1] << 16);
+    }
+    uint4* dst = (uint4*)(out + row * (size_t)K + (size_t)b * 256 + e0);
+    dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+#pragma clang fp contract(on)
+
+// ------------------------------------------------------------------------------------------
+// bf16 <-> f32 helpers (gemm.hip:77-95 semantics; bf16 from f32 by RNE without a NaN case)
+__global__ void k_f32_to_bf16(const float* __restrict__ x, uint16_t* __restrict__ o, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) o[i] = (uint16_t)f2bf_bits(x[i]);
+}
+__global__ void k_bf16_to_f32(const uint16_t* __restrict__ x, float* __restrict__ o, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) o[i] = bf2f(x[i]);
+}
+// rows m < M of a [M][Nt] bf16 matrix, columns off..off+N (plus a second matrix when x2) -> f32 [M][N]
+__global__ void k_bf16_to_f32_seg2(const uint16_t* __restrict__ x, const uint16_t* __restrict__ x2, int Nt, int off, int N,
+                                   float* __restrict__ o, int M) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)M * N) return;
+    const int m = (int)(i / N), c = (int)(i % N);
+    const size_t idx = (size_t)m * Nt + off + c;
+    float v = bf2f(x[idx]);
+    if (x2) v += bf2f(x2[idx]);
+    o[i] = v;
+}
+
+// ------------------------------------------------------------------------------------------
+// MFMA GEMM core
+constexpr int GBM = 256, GBN = 128, GBK = 64, GLD = GBK + 8;
+
+struct GemmLds {
+    __bf16 a[GBM * GLD];
+    __bf16 b[GBN * GLD];
+};
+
+// A tile loader: bf16 [M][K] row-major; thread t owns 16-byte column t%8 of rows t/8 + 32p
+struct ALoad {
+    uint4 r[8];
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ A, int M, int K, int m0, int k0) {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int m = min(m0 + 32 * p + (t >> 3), M - 1);
+            r[p] = ld16(A + (size_t)m * K + k0 + 8 * (t & 7));
+        }
+    }
+    __device__ __forceinline__ void store(GemmLds& L) const {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) *(uint4*)&L.a[(32 * p + (t >> 3)) * GLD + 8 * (t & 7)] = r[p];
+    }
+};
+
+// W tile loader, Q4_K: thread t decodes sub-block (2j + (t&1)) of weight row t/2 for the K step at k0
+// (block k0/256, pair j = (k0/64)&3).  The GEMM tolerance path: w = fma(d*sc, q, -dmin*m), RNE to bf16.
+struct BLoadQ4K {
+    uint4 hd, q0, q1;
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
+        const int t = threadIdx.x;
+        const int n = min(n0 + (t >> 1), N - 1);
+        const uint8_t* bp = W + (size_t)n * ((size_t)(K >> 8) * 144) + (size_t)(k0 >> 8) * 144;
+        const int j = (k0 >> 6) & 3;
+        hd = ld16(bp);
+        q0 = ld16(bp + 16 + 32 * j);
+        q1 = ld16(bp + 32 + 32 * j);
+    }
+    __device__ __forceinline__ void store(GemmLds& L, int k0) const {
+        const int t = threadIdx.x, h = t & 1;
+        const int s = 2 * ((k0 >> 6) & 3) + h;
+        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+        const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
+        const float dl = d * (float)byte8(sb.sc_lo, sb.sc_hi, s), ml = dmin * (float)byte8(sb.m_lo, sb.m_hi, s);
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        __bf16 v[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t u = (h ? (qw[i] >> 4) : qw[i]) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) v[4 * i + b] = (__bf16)(dl * (float)((u >> (8 * b)) & 0xffu) - ml);
+        }
+        __bf16* dst = &L.b[(t >> 1) * GLD + 32 * h];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *(bf16x8*)(dst + 8 * i) = *(const bf16x8*)(v + 8 * i);
+    }
+};
+
+// W tile loader, bf16 [N][K]: thread t copies 32 elements (k0 + 32*(t&1) ..) of row t/2
+struct BLoadBf16 {
+    uint4 r[4];
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ W, int N, int K, int n0, int k0) {
+        const int t = threadIdx.x;
+        const int n = min(n0 + (t >> 1), N - 1);
+        const uint16_t* p = W + (size_t)n * K + k0 + 32 * (t & 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = ld16(p + 8 * i);
+    }
+    __device__ __forceinline__ void store(GemmLds& L, int) const {
+        const int t = threadIdx.x;
+        uint4* dst = (uint4*)&L.b[(t >> 1) * GLD + 32 * (t & 1)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = r[i];
+    }
+};
+
+// tile id -> (m tile, n tile), XCD-aware: workgroup id i runs on XCD i % 8; give XCD x the
+// contiguous tile range [x * ntiles/8, (x+1) * ntiles/8) with M tiles fastest, so the M tiles that
+// share a weight tile share one L2.  Falls back to the plain order when the count is not a multiple of 8.
+__device__ __forceinline__ void tile_of(int bid, int mt, int nt, int& tm, int& tn) {
+    const int ntiles = mt * nt;
+    int id = bid;
+    if ((ntiles & 7) == 0) id = (bid & 7) * (ntiles >> 3) + (bid >> 3);
+    tm = id % mt;
+    tn = id / mt;
+}
+
+template <class BL, class WT, bool OUT_BF16>
+__global__ void __launch_bounds__(256) k_gemm(const uint16_t* __restrict__ A, const WT* __restrict__ W, void* __restrict__ D,
+                                              int M, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem_raw[];
+    GemmLds& L = *(GemmLds*)smem_raw;
+    const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
+    int tm, tn;
+    tile_of(blockIdx.x, mt, nt, tm, tn);
+    const int m0 = tm * GBM, n0 = tn * GBN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nk = K / GBK;
+    ALoad al;
+    BL bl;
+    al.load(A, M, K, m0, 0);
+    bl.load(W, N, K, n0, 0);
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jn = 0; jn < 8; ++jn) acc[i][jn] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int fr = lane & 15, fk = 8 * (lane >> 4);
+    for (int s = 0; s < nk; ++s) {
+        const int k0 = s * GBK;
+        if (s > 0) lds_barrier();                 // everyone is done reading the previous tiles
+        al.store(L);
+        bl.store(L, k0);
+        lds_barrier();
+        const int kn = min(s + 1, nk - 1) * GBK;  // prefetch (the last step re-reads its own tile)
+        al.load(A, M, K, m0, kn);
+        bl.load(W, N, K, n0, kn);
+#pragma unroll
+        for (int ks = 0; ks < GBK / 32; ++ks) {
+            bf16x8 af[4], bf[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *(const bf16x8*)&L.a[(64 * wave + 16 * i + fr) * GLD + 32 * ks + fk];
+#pragma unroll
+            for (int jn = 0; jn < 8; ++jn) bf[jn] = *(const bf16x8*)&L.b[(16 * jn + fr) * GLD + 32 * ks + fk];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jn = 0; jn < 8; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
+        }
+    }
+    // epilogue: acc[i][jn][r] = D[m0 + 64w + 16i + 4*(lane/16) + r][n0 + 16jn + lane%16]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 64 * wave + 16 * i + 4 * (lane >> 4) + r;
+            if (m >= M) continue;
+#pragma unroll
+            for (int jn = 0; jn < 8; ++jn) {
+                const int n = n0 + 16 * jn + fr;
+                if (n >= N) continue;
+                if constexpr (OUT_BF16) ((uint16_t*)D)[(size_t)m * N + n] = (uint16_t)f2bf_bits(acc[i][jn][r]);
+                else ((float*)D)[(size_t)m * N + n] = acc[i][jn][r];
+            }
+        }
+    }
+}
+
+int launch_gemm_q4k(const void* W, const uint16_t* A, float* D, int M, int N, int K, hipStream_t s) {
+    const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
+    hipLaunchKernelGGL((k_gemm<BLoadQ4K, uint8_t, false>), dim3(grid), dim3(256), sizeof(GemmLds), s, A, (const uint8_t*)W,
+                       (void*)D, M, N, K);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+}  // namespace
+}  // namespace qmm
+
+using namespace qmm;
+
+extern "C" {
+
+int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* stream) {
+    if (!W || !out) return QMM_ERR_NULL;
+    if (N <= 0 || K <= 0 || K % 256 != 0) return QMM_ERR_SHAPE;
+    hipStream_t s = (hipStream_t)stream;
+    const size_t nb = (size_t)N * (K / 256);
+    switch (fmt) {
+        case QMM_Q4_K:
+            hipLaunchKernelGGL(k_dequant_q4k_bf16, dim3((unsigned)((nb * 8 + 255) / 256)), dim3(256), 0, s, (const uint8_t*)W, out,
+                               nb * 8, K);
+            break;
+        case QMM_Q6_K:
+            hipLaunchKernelGGL(k_dequant_q6k_bf16<QMM_Q6_K>, dim3((unsigned)((nb * 16 + 255) / 256)), dim3(256), 0, s,
+                               (const uint8_t*)W, out, nb * 16, K);
+            break;
+        case QMM_Q6_K_SOA:
+            hipLaunchKernelGGL(k_dequant_q6k_bf16<QMM_Q6_K_SOA>, dim3((unsigned)((nb * 16 + 255) / 256)), dim3(256), 0, s,
+                               (const uint8_t*)W, out, nb * 16, K);
+            break;
+        default: return QMM_ERR_FORMAT;
+    }
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int N, int K, void* stream) {
+    if (fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+    if (!W || !A || !D) return QMM_ERR_NULL;
+    if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0) return QMM_ERR_SHAPE;
+    return launch_gemm_q4k(W, A, D, M, N, K, (hipStream_t)stream);
+}
+
+int qmm_gemm_bf16(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, void* stream) {
+    if (!A || !W || !D) return QMM_ERR_NULL;
+    if (M <= 0 || N <= 0 || K <= 0 || K % GBK != 0) return QMM_ERR_SHAPE;
+    const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
+    hipLaunchKernelGGL((k_gemm<BLoadBf16, uint16_t, true>), dim3(grid), dim3(256), sizeof(GemmLds), (hipStream_t)stream, A, W,
+                       (void*)D, M, N, K);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_f32_to_bf16(const float* x, uint16_t* out, size_t n, void* stream) {
+    if (!x || !out) return QMM_ERR_NULL;
+    if (n == 0) return QMM_OK;
+    hipLaunchKernelGGL(k_f32_to_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, out, n);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_bf16_to_f32(const uint16_t* x, float* out, size_t n, void* stream) {
+    if (!x || !out) return QMM_ERR_NULL;
+    if (n == 0) return QMM_OK;
+    hipLaunchKernelGGL(k_bf16_to_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, out, n);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_bf16_to_f32_seg2(const uint16_t* x, const uint16_t* x2, int Nt, int off, int N, float* out, int M, void* stream) {
+    if (!x || !out) return QMM_ERR_NULL;
+    if (M < 0 || N < 0 || off < 0 || off + N > Nt) return QMM_ERR_SHAPE;
+    const size_t n = (size_t)M * N;
+    if (n == 0) return QMM_OK;
+    hipLaunchKernelGGL(k_bf16_to_f32_seg2, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, x2, Nt, off,
+                       N, out, M);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_bf16_to_f32_seg(const uint16_t* x, int Nt, int off, int N, float* out, int M, void* stream) {
+    return qmm_bf16_to_f32_seg2(x, nullptr, Nt, off, N, out, M, stream);
+}
+
+}  // extern "C"

@@ -136,3 +136,38 @@ def moe_combine_sorted(down, w, kpos, y, T, nexp, E, stream=None):
 def moe_silu_quant(gate, up, xq, rows, n, stream=None):
     """fn.h:48: h = silu(g)*u quantised per 32 into xq (XQ8Buf of rows x n)."""
     check(_lib.lib().qmm_moe_silu_quant(_p(gate), _p(up), xq.c(), rows, n, _stream(stream)), "moe_silu_quant")
+
+
+# ---- prefill GEMM (engine/kernels/gemm.h) ----
+def dequant_bf16(fmt, W, out, N, K, stream=None):
+    """gemm.h:12: W -> bf16 [N][K] (out: int16/uint16-sized tensor of N*K elements), bit-exact."""
+    _dev(W, torch.uint8, "W")
+    check(_lib.lib().qmm_dequant_bf16(fmt, _p(W), _p(out), N, K, _stream(stream)), "dequant_bf16")
+
+
+def gemm_wq(fmt, W, A, D, M, N, K, stream=None):
+    """D[M][N] f32 = A[M][K] bf16 . dequant(W)[N][K]^T, dequantisation fused into the GEMM."""
+    _dev(W, torch.uint8, "W"); _dev(A, torch.bfloat16, "A"); _dev(D, torch.float32, "D")
+    check(_lib.lib().qmm_gemm_wq(fmt, _p(W), _p(A), _p(D), M, N, K, _stream(stream)), "gemm_wq")
+
+
+def gemm_bf16(A, W, D, M, N, K, stream=None):
+    """BlasLt::gemm (gemm.h:27): D[M][N] bf16 = A[M][K] bf16 . W[N][K]^T bf16, f32 accumulate."""
+    _dev(A, torch.bfloat16, "A"); _dev(W, torch.bfloat16, "W"); _dev(D, torch.bfloat16, "D")
+    check(_lib.lib().qmm_gemm_bf16(_p(A), _p(W), _p(D), M, N, K, _stream(stream)), "gemm_bf16")
+
+
+def f32_to_bf16(x, out, n, stream=None):
+    check(_lib.lib().qmm_f32_to_bf16(_p(x), _p(out), n, _stream(stream)), "f32_to_bf16")
+
+
+def bf16_to_f32(x, out, n, stream=None):
+    check(_lib.lib().qmm_bf16_to_f32(_p(x), _p(out), n, _stream(stream)), "bf16_to_f32")
+
+
+def bf16_to_f32_seg(x, Nt, off, N, out, M, stream=None):
+    check(_lib.lib().qmm_bf16_to_f32_seg(_p(x), Nt, off, N, _p(out), M, _stream(stream)), "bf16_to_f32_seg")
+
+
+def bf16_to_f32_seg2(x, x2, Nt, off, N, out, M, stream=None):
+    check(_lib.lib().qmm_bf16_to_f32_seg2(_p(x), _p(x2), Nt, off, N, _p(out), M, _stream(stream)), "bf16_to_f32_seg2")

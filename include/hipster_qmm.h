@@ -111,6 +111,25 @@ int qmm_moe_silu_quant(const float* gate, const float* up, qmm_xq8 xq, int rows,
 int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, float* y, int T, int nexp, int E,
                            void* stream);
 
+/* ---- prefill GEMM ---- */
+/* whole weight -> bf16 [N][K], bit-exact: quant.h arithmetic ((d*sc)*q - dmin*m, no contraction) then
+ * round-to-nearest-even (reference: dequant_bf16, gemm.h:12, gemm.hip:16-76,96-107).  fmt: Q4_K, Q6_K,
+ * Q6_K_SOA; K % 256 == 0. */
+int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* stream);
+/* D[M][N] f32 = A[M][K] bf16 . W[N][K]^T with W in Q4_K, dequantised to bf16 inside the kernel
+ * (bf16 MFMA, f32 accumulate).  Replaces the reference's dequant_bf16 + BlasLt::gemm pair
+ * (engine/src/qwen35.cpp:204-239, engine/src/qwen4exp.cpp:513-527) with one launch and no scratch. */
+int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int N, int K, void* stream);
+/* D[M][N] bf16 = A[M][K] bf16 . W[N][K]^T bf16, f32 accumulate, RNE to bf16 (reference: BlasLt::gemm,
+ * gemm.h:27, gemm.hip:125-160; here an own MFMA kernel, no hipBLASLt).  K % 64 == 0. */
+int qmm_gemm_bf16(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, void* stream);
+/* bf16 helpers (reference: gemm.h:14-20, gemm.hip:77-95) */
+int qmm_f32_to_bf16(const float* x, uint16_t* out, size_t n, void* stream);
+int qmm_bf16_to_f32(const uint16_t* x, float* out, size_t n, void* stream);
+/* rows m < M of a [M][Nt] bf16 matrix, columns off..off+N -> f32 [M][N] (plus x2 when not NULL) */
+int qmm_bf16_to_f32_seg(const uint16_t* x, int Nt, int off, int N, float* out, int M, void* stream);
+int qmm_bf16_to_f32_seg2(const uint16_t* x, const uint16_t* x2, int Nt, int off, int N, float* out, int M, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

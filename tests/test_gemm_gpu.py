@@ -1,0 +1,110 @@
+"""GPU parity of the prefill path: bit-exact dequantisation to bf16, the fused Q4_K GEMM and the
+plain bf16 GEMM, through the C ABI.
+
+Bars: dequant_bf16 bit-exact against the oracle (quant.h arithmetic, RNE to bf16), the golden
+special blocks included; GEMM outputs within rel-L2 2e-3 (north star, bf16 MFMA path) of the
+oracle's double-precision product of the same bf16 operands, checked on sampled (m, n) pairs at the
+full BASELINE config-3 shape and on the whole matrix against a torch float32 reference."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hipster_amd import qmm, synth
+from tests.gpu_util import dev, host, rel_l2
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "quant_golden.npz"))
+TOL = 2e-3
+
+
+def bf16_dev(a_bits):
+    return torch.from_numpy(np.ascontiguousarray(a_bits).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("fmt,N,K", [(synth.Q4_K, 333, 5120), (synth.Q6_K, 129, 2048), (synth.Q6_K_SOA, 64, 4096),
+                                     (synth.Q4_K, 17408, 5120)])
+def test_dequant_bf16_bit_exact(gpu, fmt, N, K):
+    W = synth.matrix(900 + N, fmt, N, K)
+    out = torch.zeros((N, K), dtype=torch.int16, device="cuda")
+    qmm.dequant_bf16(fmt, dev(W), out, N, K)
+    ref = oracle.dequant_rows_bf16(fmt, W, K)
+    assert np.array_equal(host(out).view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("fmt,key", [(synth.Q4_K, "q4k"), (synth.Q6_K, "q6k")])
+def test_dequant_bf16_golden_blocks(gpu, fmt, key):
+    blocks = GOLD[key + "_blocks"]
+    out = torch.zeros((blocks.shape[0], 256), dtype=torch.int16, device="cuda")
+    qmm.dequant_bf16(fmt, dev(blocks), out, blocks.shape[0], 256)
+    assert np.array_equal(host(out).view(np.uint16), synth.to_bf16_bits(GOLD[key + "_y"]))
+
+
+def gemm_check(M, N, K, seed, npairs=0):
+    W = synth.matrix(seed, synth.Q4_K, N, K)
+    A = synth.to_bf16_bits(synth.normal_f32(seed + 1, (M, K)))
+    D = torch.full((M, N), float("nan"), device="cuda")
+    Wd, Ad = dev(W), bf16_dev(A)
+    qmm.gemm_wq(synth.Q4_K, Wd, Ad, D, M, N, K)
+    Dh = host(D)
+    assert np.isfinite(Dh).all()
+    # full matrix against torch float32 on the exactly dequantised bf16 weights
+    Wb = torch.zeros((N, K), dtype=torch.int16, device="cuda")
+    qmm.dequant_bf16(synth.Q4_K, Wd, Wb, N, K)
+    ref = torch.matmul(Ad.float(), Wb.view(torch.bfloat16).float().t().contiguous())
+    err = rel_l2(Dh, host(ref))
+    print(f"gemm_wq M={M} N={N} K={K} rel-L2 vs torch fp32 {err:.2e}", flush=True)
+    assert err <= TOL
+    if npairs:
+        g = synth.rng(seed + 2)
+        ms, ns = g.integers(0, M, npairs).astype(np.int32), g.integers(0, N, npairs).astype(np.int32)
+        o = np.argsort(ns, kind="stable")
+        ms, ns = ms[o], ns[o]
+        r = oracle.gemm_wq_ref(synth.Q4_K, W, A, M, N, K, ms, ns)
+        e2 = rel_l2(Dh[ms, ns], r)
+        print(f"  sampled vs oracle rel-L2 {e2:.2e}", flush=True)
+        assert e2 <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 128, 256), (300, 200, 512), (37, 1000, 2048), (513, 129, 5120)])
+def test_gemm_wq_small_and_ragged(gpu, M, N, K):
+    gemm_check(M, N, K, 1300 + M, npairs=64)
+
+
+def test_gemm_wq_config3_full_shape(gpu):
+    gemm_check(2048, 17408, 5120, synth.SEEDS["cfg3"], npairs=256)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 515, 640), (2048, 2048, 2048)])
+def test_gemm_bf16(gpu, M, N, K):
+    A = synth.to_bf16_bits(synth.normal_f32(70 + M, (M, K)))
+    W = synth.to_bf16_bits(synth.normal_f32(71 + N, (N, K)))
+    D = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
+    Ad, Wd = bf16_dev(A), bf16_dev(W)
+    qmm.gemm_bf16(Ad, Wd, D, M, N, K)
+    ref = torch.matmul(Ad.float(), Wd.float().t().contiguous())
+    assert rel_l2(host(D.float()), host(ref)) <= 4e-3      # bf16 output rounding (2^-9) dominates
+
+
+def test_gemm_deterministic(gpu):
+    M, N, K = 512, 384, 1024
+    W = dev(synth.matrix(1400, synth.Q4_K, N, K))
+    A = bf16_dev(synth.to_bf16_bits(synth.normal_f32(1401, (M, K))))
+    D1 = torch.zeros((M, N), device="cuda"); D2 = torch.zeros((M, N), device="cuda")
+    qmm.gemm_wq(synth.Q4_K, W, A, D1, M, N, K)
+    qmm.gemm_wq(synth.Q4_K, W, A, D2, M, N, K)
+    assert torch.equal(D1, D2)
+
+
+def test_bf16_helpers(gpu):
+    x = synth.normal_f32(80, (33, 70))
+    xb = torch.zeros(x.size, dtype=torch.int16, device="cuda")
+    qmm.f32_to_bf16(dev(x), xb, x.size)
+    assert np.array_equal(host(xb).view(np.uint16), synth.to_bf16_bits(x).ravel())
+    back = torch.zeros(x.size, device="cuda")
+    qmm.bf16_to_f32(xb, back, x.size)
+    assert np.array_equal(host(back), synth.bf16_bits_to_f32(synth.to_bf16_bits(x)).ravel())
+    seg = torch.zeros((33, 20), device="cuda")
+    qmm.bf16_to_f32_seg2(xb, xb, 70, 30, 20, seg, 33)
+    want = 2 * synth.bf16_bits_to_f32(synth.to_bf16_bits(x))[:, 30:50]
+    assert np.array_equal(host(seg), want)
