@@ -10,14 +10,11 @@
 //   qmm_f32_to_bf16, qmm_bf16_to_f32, qmm_bf16_to_f32_seg, qmm_bf16_to_f32_seg2   gemm.hip:77-95
 //
 // GEMM tiling (MFMA v_mfma_f32_16x16x32_bf16, wave64): a 256-thread workgroup computes a
-// 256 (M, activation rows) x 128 (N, weight rows) tile of D = A . W^T, stepping K by 64.  Wave w owns
-// rows 64w..64w+63 of the tile and all 128 columns: 4 x 8 MFMA tiles of 16 x 16, 128 f32
-// accumulators per lane.  Per K step the A tile (256 x 64 bf16, 32 KiB) and the W tile (128 x 64)
-// sit in LDS with rows padded to 72 elements (144 B) to spread the 16-byte fragment reads over the
-// banks.  For Q4_K weights a K step of 64 is exactly one 32-byte qs "pair" of each row's block,
-// so two threads per weight row decode one 32-weight sub-block each (header + 32 qs bytes ->
-// 32 bf16) straight into LDS.  The next step's global loads (A: 8 x 16 B per thread, W: 48 B or
-// 64 B) are issued before the MFMAs of the current step and land in registers while they run.
+// 256 (M, activation rows) x 256 (N, weight rows) tile of D = A . W^T, stepping K by 64 through a
+// two-stage LDS ring (see the core below).  For Q4_K weights a K step of 64 is exactly one 32-byte
+// qs "pair" of each row's block, so one thread per weight row decodes it (header + 32 qs bytes ->
+// 64 bf16) straight into LDS.  The next step's global loads (A: 8 x 16 B per thread, W: 48 B or
+// 128 B) are issued before the MFMAs of the current step and land in registers while they run.
 // Workgroups are mapped XCD-aware: consecutive workgroup ids go to different XCDs, so tile ids are
 // assigned so that the 8 M tiles of one weight tile run on the same XCD and share its L2.
 #include "qmm_common.hpp"
@@ -133,13 +130,15 @@ __global__ void k_bf16_to_f32_seg2(const uint16_t* __restrict__ x, const uint16_
 }
 
 // ------------------------------------------------------------------------------------------
-// MFMA GEMM core
-constexpr int GBM = 256, GBN = 128, GBK = 64, GLD = GBK + 8;
-
-struct GemmLds {
-    __bf16 a[GBM * GLD];
-    __bf16 b[GBN * GLD];
-};
+// MFMA GEMM core.  Macro tile GBM x GBN = 256 x 256, K step 64, 4 waves as 2 x 2, each wave a
+// 128 x 128 tile = 8 x 8 MFMA tiles of 16 x 16 (256 f32 accumulators per lane, held in AGPRs).
+// LDS holds two stages of {A 256 x 64, W 256 x 64} bf16 with rows padded to 72 elements (144 B):
+// the 16-byte fragment reads of 16 consecutive rows then fall on 16 distinct 4-bank groups.
+// Step s: issue the global loads of step s+1 into registers, run the 128 MFMAs of step s from
+// stage s&1, write step s+1's registers (A copied, W dequantised) into the other stage, barrier.
+constexpr int GBM = 256, GBN = 256, GBK = 64, GLD = GBK + 8;
+constexpr int kStageElems = (GBM + GBN) * GLD;                 // bf16 elements per stage
+constexpr size_t kGemmLds = 2 * (size_t)kStageElems * 2;     // bytes (147,456)
 
 // A tile loader: bf16 [M][K] row-major; thread t owns 16-byte column t%8 of rows t/8 + 32p
 struct ALoad {
@@ -152,61 +151,65 @@ struct ALoad {
             r[p] = ld16(A + (size_t)m * K + k0 + 8 * (t & 7));
         }
     }
-    __device__ __forceinline__ void store(GemmLds& L) const {
+    __device__ __forceinline__ void store(__bf16* La) const {
         const int t = threadIdx.x;
 #pragma unroll
-        for (int p = 0; p < 8; ++p) *(uint4*)&L.a[(32 * p + (t >> 3)) * GLD + 8 * (t & 7)] = r[p];
+        for (int p = 0; p < 8; ++p) *(uint4*)&La[(32 * p + (t >> 3)) * GLD + 8 * (t & 7)] = r[p];
     }
 };
 
-// W tile loader, Q4_K: thread t decodes sub-block (2j + (t&1)) of weight row t/2 for the K step at k0
-// (block k0/256, pair j = (k0/64)&3).  The GEMM tolerance path: w = fma(d*sc, q, -dmin*m), RNE to bf16.
+// W tile loader, Q4_K: thread t decodes weight row n0+t for the K step at k0, i.e. qs pair
+// j = (k0/64)&3 of block k0/256: low nibbles -> k 0..31 (sub-block 2j), high -> k 32..63 (2j+1).
+// This is the GEMM's tolerance path: w = fma(d*sc, q, -dmin*m), RNE to bf16 in hardware.
 struct BLoadQ4K {
     uint4 hd, q0, q1;
     __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
-        const int t = threadIdx.x;
-        const int n = min(n0 + (t >> 1), N - 1);
+        const int n = min(n0 + (int)threadIdx.x, N - 1);
         const uint8_t* bp = W + (size_t)n * ((size_t)(K >> 8) * 144) + (size_t)(k0 >> 8) * 144;
         const int j = (k0 >> 6) & 3;
         hd = ld16(bp);
         q0 = ld16(bp + 16 + 32 * j);
         q1 = ld16(bp + 32 + 32 * j);
     }
-    __device__ __forceinline__ void store(GemmLds& L, int k0) const {
-        const int t = threadIdx.x, h = t & 1;
-        const int s = 2 * ((k0 >> 6) & 3) + h;
+    __device__ __forceinline__ void store(__bf16* Lb, int k0) const {
+        const int j = (k0 >> 6) & 3;
         const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
         const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
-        const float dl = d * (float)byte8(sb.sc_lo, sb.sc_hi, s), ml = dmin * (float)byte8(sb.m_lo, sb.m_hi, s);
+        const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
+        const float dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
         const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        __bf16 v[32];
+        __bf16* dst = &Lb[threadIdx.x * GLD];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t u = (h ? (qw[i] >> 4) : qw[i]) & 0x0f0f0f0fu;
+        for (int hh = 0; hh < 2; ++hh) {
+            const float dl = hh ? dB : dA, ml = hh ? mB : mA;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) v[4 * i + b] = (__bf16)(dl * (float)((u >> (8 * b)) & 0xffu) - ml);
+            for (int c = 0; c < 4; ++c) {           // 8 weights per 16-byte store
+                __bf16 v[8];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const uint32_t u = (hh ? (qw[2 * c + e] >> 4) : qw[2 * c + e]) & 0x0f0f0f0fu;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) v[4 * e + b] = (__bf16)(dl * (float)((u >> (8 * b)) & 0xffu) - ml);
+                }
+                *(bf16x8*)(dst + 32 * hh + 8 * c) = *(const bf16x8*)v;
+            }
         }
-        __bf16* dst = &L.b[(t >> 1) * GLD + 32 * h];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *(bf16x8*)(dst + 8 * i) = *(const bf16x8*)(v + 8 * i);
     }
 };
 
-// W tile loader, bf16 [N][K]: thread t copies 32 elements (k0 + 32*(t&1) ..) of row t/2
+// W tile loader, bf16 [N][K]: thread t copies the 64 elements of row n0+t
 struct BLoadBf16 {
-    uint4 r[4];
+    uint4 r[8];
     __device__ __forceinline__ void load(const uint16_t* __restrict__ W, int N, int K, int n0, int k0) {
-        const int t = threadIdx.x;
-        const int n = min(n0 + (t >> 1), N - 1);
-        const uint16_t* p = W + (size_t)n * K + k0 + 32 * (t & 1);
+        const int n = min(n0 + (int)threadIdx.x, N - 1);
+        const uint16_t* p = W + (size_t)n * K + k0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = ld16(p + 8 * i);
+        for (int i = 0; i < 8; ++i) r[i] = ld16(p + 8 * i);
     }
-    __device__ __forceinline__ void store(GemmLds& L, int) const {
-        const int t = threadIdx.x;
-        uint4* dst = (uint4*)&L.b[(t >> 1) * GLD + 32 * (t & 1)];
+    __device__ __forceinline__ void store(__bf16* Lb, int) const {
+        uint4* dst = (uint4*)&Lb[threadIdx.x * GLD];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i] = r[i];
+        for (int i = 0; i < 8; ++i) dst[i] = r[i];
     }
 };
 
@@ -221,59 +224,73 @@ __device__ __forceinline__ void tile_of(int bid, int mt, int nt, int& tm, int& t
     tn = id / mt;
 }
 
+// 128 MFMAs of one K step from one LDS stage
+__device__ __forceinline__ void mfma_step(const __bf16* La, const __bf16* Lb, int wm, int wn, int fr, int fk, f32x4 (&acc)[8][8]) {
+#pragma unroll
+    for (int ks = 0; ks < GBK / 32; ++ks) {
+        bf16x8 af[8], bf[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) af[i] = *(const bf16x8*)&La[(128 * wm + 16 * i + fr) * GLD + 32 * ks + fk];
+#pragma unroll
+        for (int jn = 0; jn < 8; ++jn) bf[jn] = *(const bf16x8*)&Lb[(128 * wn + 16 * jn + fr) * GLD + 32 * ks + fk];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int jn = 0; jn < 8; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
+    }
+}
+
+// Step s: the global loads of step s+1 go out first, then the MFMAs of step s from LDS stage s&1,
+// then step s+1's registers are written (A copied, W dequantised) into the other stage.
 template <class BL, class WT, bool OUT_BF16>
 __global__ void __launch_bounds__(256) k_gemm(const uint16_t* __restrict__ A, const WT* __restrict__ W, void* __restrict__ D,
                                               int M, int N, int K) {
     extern __shared__ __align__(16) uint8_t smem_raw[];
-    GemmLds& L = *(GemmLds*)smem_raw;
+    __bf16* const lds = (__bf16*)smem_raw;
     const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
     int tm, tn;
     tile_of(blockIdx.x, mt, nt, tm, tn);
     const int m0 = tm * GBM, n0 = tn * GBN;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave & 1, wn = wave >> 1;
     const int nk = K / GBK;
     ALoad al;
     BL bl;
     al.load(A, M, K, m0, 0);
     bl.load(W, N, K, n0, 0);
-    f32x4 acc[4][8];
+    al.store(lds);
+    bl.store(lds + GBM * GLD, 0);
+    lds_barrier();
+    f32x4 acc[8][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int jn = 0; jn < 8; ++jn) acc[i][jn] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int fr = lane & 15, fk = 8 * (lane >> 4);
     for (int s = 0; s < nk; ++s) {
-        const int k0 = s * GBK;
-        if (s > 0) lds_barrier();                 // everyone is done reading the previous tiles
-        al.store(L);
-        bl.store(L, k0);
-        lds_barrier();
-        const int kn = min(s + 1, nk - 1) * GBK;  // prefetch (the last step re-reads its own tile)
-        al.load(A, M, K, m0, kn);
-        bl.load(W, N, K, n0, kn);
-#pragma unroll
-        for (int ks = 0; ks < GBK / 32; ++ks) {
-            bf16x8 af[4], bf[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *(const bf16x8*)&L.a[(64 * wave + 16 * i + fr) * GLD + 32 * ks + fk];
-#pragma unroll
-            for (int jn = 0; jn < 8; ++jn) bf[jn] = *(const bf16x8*)&L.b[(16 * jn + fr) * GLD + 32 * ks + fk];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int jn = 0; jn < 8; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
+        const __bf16* La = lds + (size_t)(s & 1) * kStageElems;
+        const bool more = s + 1 < nk;
+        if (more) {
+            al.load(A, M, K, m0, (s + 1) * GBK);
+            bl.load(W, N, K, n0, (s + 1) * GBK);
         }
+        mfma_step(La, La + GBM * GLD, wm, wn, fr, fk, acc);
+        if (more) {
+            __bf16* Sa = lds + (size_t)((s + 1) & 1) * kStageElems;
+            al.store(Sa);
+            bl.store(Sa + GBM * GLD, (s + 1) * GBK);
+        }
+        lds_barrier();
     }
-    // epilogue: acc[i][jn][r] = D[m0 + 64w + 16i + 4*(lane/16) + r][n0 + 16jn + lane%16]
+    // epilogue: acc[i][jn][r] = D[m0 + 128wm + 16i + 4*(lane/16) + r][n0 + 128wn + 16jn + lane%16]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int m = m0 + 64 * wave + 16 * i + 4 * (lane >> 4) + r;
+            const int m = m0 + 128 * wm + 16 * i + 4 * (lane >> 4) + r;
             if (m >= M) continue;
 #pragma unroll
             for (int jn = 0; jn < 8; ++jn) {
-                const int n = n0 + 16 * jn + fr;
+                const int n = n0 + 128 * wn + 16 * jn + fr;
                 if (n >= N) continue;
                 if constexpr (OUT_BF16) ((uint16_t*)D)[(size_t)m * N + n] = (uint16_t)f2bf_bits(acc[i][jn][r]);
                 else ((float*)D)[(size_t)m * N + n] = acc[i][jn][r];
@@ -284,7 +301,7 @@ __global__ void __launch_bounds__(256) k_gemm(const uint16_t* __restrict__ A, co
 
 int launch_gemm_q4k(const void* W, const uint16_t* A, float* D, int M, int N, int K, hipStream_t s) {
     const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-    hipLaunchKernelGGL((k_gemm<BLoadQ4K, uint8_t, false>), dim3(grid), dim3(256), sizeof(GemmLds), s, A, (const uint8_t*)W,
+    hipLaunchKernelGGL((k_gemm<BLoadQ4K, uint8_t, false>), dim3(grid), dim3(256), kGemmLds, s, A, (const uint8_t*)W,
                        (void*)D, M, N, K);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
@@ -332,7 +349,7 @@ int qmm_gemm_bf16(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int 
     if (!A || !W || !D) return QMM_ERR_NULL;
     if (M <= 0 || N <= 0 || K <= 0 || K % GBK != 0) return QMM_ERR_SHAPE;
     const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-    hipLaunchKernelGGL((k_gemm<BLoadBf16, uint16_t, true>), dim3(grid), dim3(256), sizeof(GemmLds), (hipStream_t)stream, A, W,
+    hipLaunchKernelGGL((k_gemm<BLoadBf16, uint16_t, true>), dim3(grid), dim3(256), kGemmLds, (hipStream_t)stream, A, W,
                        (void*)D, M, N, K);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
