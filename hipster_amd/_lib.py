@@ -56,6 +56,9 @@ SIGNATURES = {
     "qmm_moe_silu_quant": (c_int, [c_vp, c_vp, XQ8, c_int, c_int, c_vp]),
     "qmm_moe_combine_sorted": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "qmm_dequant_bf16": (c_int, [c_int, c_vp, c_vp, c_int, c_int, c_vp]),
+    "qmm_moe_sort": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "qmm_moe_gemm_bf16": (c_int, [c_int, c_int, c_vp, c_vp, ctypes.c_size_t, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_vp]),
+    "qmm_moe_silu_bf16": (c_int, [c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp]),
     "qmm_gemm_wq": (c_int, [c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "qmm_gemm_bf16": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "qmm_f32_to_bf16": (c_int, [c_vp, c_vp, ctypes.c_size_t, c_vp]),

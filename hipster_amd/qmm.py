@@ -171,3 +171,27 @@ def bf16_to_f32_seg(x, Nt, off, N, out, M, stream=None):
 
 def bf16_to_f32_seg2(x, x2, Nt, off, N, out, M, stream=None):
     check(_lib.lib().qmm_bf16_to_f32_seg2(_p(x), _p(x2), Nt, off, N, _p(out), M, _stream(stream)), "bf16_to_f32_seg2")
+
+
+# ---- MoE prefill ----
+MOE_TILE_ROWS = 64     # rows per tile of qmm_moe_gemm_bf16
+
+
+def moe_tiles_capacity(T, nslot, nexperts, maxc=MOE_TILE_ROWS):
+    return -(-(T * nslot) // maxc) + nexperts + 1
+
+
+def moe_sort(ids, T, nslot, nexperts, maxc, kpos, rowtok, tiles, counts, stream=None):
+    """Device expert sort (replaces the host path of qwen4exp.cpp:628-645).  tiles: int32 [cap][3]."""
+    check(_lib.lib().qmm_moe_sort(_p(ids), T, nslot, nexperts, maxc, _p(kpos), _p(rowtok), _p(tiles), _p(counts),
+                                  _stream(stream)), "moe_sort")
+
+
+def moe_gemm_bf16(fmt, shared_fmt, W, Wsh, ebytes, tiles, counts, max_tiles, rowtab, A, D, N, K, stream=None):
+    """Grouped expert GEMM over sorted rows, bf16 activations (moe_gemm, gemv.h:49-50)."""
+    check(_lib.lib().qmm_moe_gemm_bf16(fmt, shared_fmt, _p(W), _p(Wsh), ebytes, _p(tiles), _p(counts), max_tiles,
+                                       _p(rowtab), _p(A), _p(D), N, K, _stream(stream)), "moe_gemm_bf16")
+
+
+def moe_silu_bf16(gate, up, h, n, stream=None):
+    check(_lib.lib().qmm_moe_silu_bf16(_p(gate), _p(up), _p(h), n, _stream(stream)), "moe_silu_bf16")

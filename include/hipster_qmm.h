@@ -130,6 +130,26 @@ int qmm_bf16_to_f32(const uint16_t* x, float* out, size_t n, void* stream);
 int qmm_bf16_to_f32_seg(const uint16_t* x, int Nt, int off, int N, float* out, int M, void* stream);
 int qmm_bf16_to_f32_seg2(const uint16_t* x, const uint16_t* x2, int Nt, int off, int N, float* out, int M, void* stream);
 
+/* ---- MoE prefill ---- */
+/* Device-side replacement of the host sort of engine/src/qwen4exp.cpp:628-645: slots te = t*nslot + e
+ * of ids [T][nslot] (id -1 = shared expert, else 0..nexperts-1) ordered by (id, te), stable.
+ * kpos[te] = sorted position, rowtok[k] = token of sorted position k, tiles = tiles of <= maxc
+ * consecutive positions of one expert, routed experts first (ascending id) then the shared expert
+ * (expert -1); counts[0] = routed tiles, counts[1] = shared tiles (both written on the device: no
+ * host sync).  tiles needs room for ceil(T*nslot/maxc) + nexperts + 1 entries.  nexperts <= 1024. */
+int qmm_moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* kpos, int* rowtok, qmm_moe_tile* tiles,
+                 int* counts, void* stream);
+/* Grouped expert GEMM over sorted rows (reference: moe_gemm, gemv.h:49-50, gemv.hip:909-969,1377-1381,
+ * with bf16 activations and the bf16 MFMA path): for tile i < counts[0] + counts[1] (read on the device)
+ * and r < ncols: D[k0 + r][n] = A[rowtab ? rowtab[k0 + r] : k0 + r] . W_e[n] (f32), W_e the Q4_K
+ * expert matrix at W + expert * ebytes, or Wsh for expert -1.  Tiles of at most 64 rows; max_tiles
+ * bounds the grid (the capacity of tiles). */
+int qmm_moe_gemm_bf16(int fmt, int shared_fmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles,
+                      const int* counts, int max_tiles, const int* rowtab, const uint16_t* A, float* D, int N, int K,
+                      void* stream);
+/* h = bf16(silu(gate) * up), n elements (the bf16-path counterpart of fn::moe_silu_quant, fn.hip:206-211) */
+int qmm_moe_silu_bf16(const float* gate, const float* up, uint16_t* h, size_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
