@@ -18,7 +18,12 @@ Prints ONE JSON line:
   cpu_baseline -- the oracle's restatement of the reference host path (per-row dequant_q4_K + fp32 dot),
                   threaded over rows on this host, timed over a bounded sample (--cpu-seconds)
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--cpu-seconds 10]
+The other BASELINE configurations are measured too and reported under "extra" (parity-test
+shapes, not the headline): the dense decode layer at M = 1, 4, 8 (config 1), the MoE decode step at
+T = 1, 4, 8 (config 2), the dense prefill GEMM and the M = 3..6 verify GEMVs (config 3) and the MoE
+prefill pipeline at 2048 tokens (config 4).  --no-extra skips them.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--cpu-seconds 10] [--no-extra]
 """
 import argparse
 import json
@@ -40,6 +45,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
     return p.parse_args()
 
 
@@ -100,6 +106,143 @@ def q4k_gemv_m1(args):
     return dict(N=N, K=K, W=W, x=x, ncopy=ncopy, algo_bytes=algo_bytes, ms_step=ms_step, ms_kernel=ms_kernel)
 
 
+def graph_us(torch, fns, reps=5):
+    """Average microseconds of one pass over fns (a list of launch closures), graph replay."""
+    g = capture(torch, [f for _ in range(reps) for f in fns])
+    timed_replay(torch, g)
+    return timed_replay(torch, g) / reps * 1e3
+
+
+def extra_cfg1(torch):
+    """one dense decode layer (gate+up Q4_K 2x17408x5120, down Q6_K 5120x17408,
+    QKV Q4_K 8192x5120, O Q4_K 5120x6144) at M = 1, 4, 8, weights rotated over >= 1 GiB."""
+    from hipster_amd import qmm, synth
+    sh = dict(gate=(synth.Q4_K, 17408, 5120), up=(synth.Q4_K, 17408, 5120), down=(synth.Q6_K, 5120, 17408),
+              qkv=(synth.Q4_K, 8192, 5120), o=(synth.Q4_K, 5120, 6144))
+    host = {k: synth.matrix(synth.SEEDS["cfg1"] + i, *v) for i, (k, v) in enumerate(sh.items())}
+    layer_bytes = sum(a.nbytes for a in host.values())
+    ncopy = max(2, -(-ROTATE_BYTES // layer_bytes))
+    copies = [{k: torch.from_numpy(a).cuda() for k, a in host.items()} for _ in range(ncopy)]
+    out = {"layer_weight_bytes": layer_bytes}
+    for M in (1, 4, 8):
+        xs = {K: qmm.XQ8Buf(M, K) for K in (5120, 17408, 6144)}
+        for K, xb in xs.items():
+            qmm.quantize_x_q8(torch.randn((M, K), device="cuda"), xb, M, K)
+        ys = {k: torch.zeros((M, v[1]), device="cuda") for k, v in sh.items()}
+
+        def layer(c):
+            def f():
+                W = copies[c]
+                qmm.gemv_multi([(synth.Q4_K, W["gate"], ys["gate"], 17408, 5120), (synth.Q4_K, W["up"], ys["up"], 17408, 5120)],
+                               xs[5120], M)
+                qmm.gemv_q8(synth.Q6_K, W["down"], xs[17408], ys["down"], 5120, 17408, M)
+                qmm.gemv_q8(synth.Q4_K, W["qkv"], xs[5120], ys["qkv"], 8192, 5120, M)
+                qmm.gemv_q8(synth.Q4_K, W["o"], xs[6144], ys["o"], 5120, 6144, M)
+            return f
+        us = graph_us(torch, [layer(c) for c in range(ncopy)], reps=2) / ncopy
+        out[f"M{M}"] = {"us_per_layer": round(us, 1), "GB_s": round(layer_bytes / us / 1e3, 1)}
+    return out
+
+
+def moe_tables(torch):
+    from hipster_amd import synth
+    H, F, n_exp = 2048, 512, 512
+    gen = lambda i, N, K: torch.from_numpy(synth.experts(synth.SEEDS["cfg4"] + i, synth.Q4_K, n_exp, N, K)).cuda()
+    one = lambda i, N, K: torch.from_numpy(synth.matrix(synth.SEEDS["cfg4"] + 10 + i, synth.Q4_K, N, K)).cuda()
+    return dict(Wg=gen(0, F, H), Wu=gen(1, F, H), Wd=gen(2, H, F), Sg=one(0, F, H), Su=one(1, F, H), Sd=one(2, H, F))
+
+
+def extra_cfg2(torch, tb):
+    """MoE decode step (route, gate|up gather GEMV, silu*up q8, down + combine)
+    at T = 1, 4, 8 over 512 Q4_K experts + shared; each replayed step routes different logits."""
+    import numpy as np
+    from hipster_amd import qmm, synth
+    H, F, NE = 2048, 512, 11
+    per_expert = 3 * tb["Wg"][0].numel()
+    out = {"bytes_per_expert": per_expert}
+    for T in (1, 4, 8):
+        R = 16
+        lg = [torch.from_numpy(synth.router_logits(synth.SEEDS["cfg2"] + 100 * T + r, T, 512)).cuda() for r in range(R)]
+        xb = qmm.XQ8Buf(T, H)
+        qmm.quantize_x_q8(torch.randn((T, H), device="cuda"), xb, T, H)
+        ids = [torch.zeros((T, NE), dtype=torch.int32, device="cuda") for _ in range(R)]
+        w = [torch.zeros((T, NE), device="cuda") for _ in range(R)]
+        g = torch.zeros((T * NE, F), device="cuda"); u = torch.zeros((T * NE, F), device="cuda")
+        hq = qmm.XQ8Buf(T * NE, F)
+        y = torch.zeros((T, H), device="cuda")
+
+        def step(r):
+            def f():
+                qmm.moe_route(lg[r], ids[r], w[r], T)
+                qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [tb["Wg"], tb["Wu"]], [tb["Sg"], tb["Su"]], [g, u], tb["Wg"][0].numel(),
+                             ids[r], NE, xb, F, H, T, False)
+                qmm.moe_silu_quant(g, u, hq, T * NE, F)
+                qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [tb["Wd"]], [tb["Sd"]], [y], tb["Wd"][0].numel(), ids[r], NE, hq, H, F, T,
+                             True, slotw=w[r])
+            return f
+        us = graph_us(torch, [step(r) for r in range(R)], reps=2) / R
+        distinct = float(np.mean([len(np.unique(i.cpu().numpy())) for i in ids]))   # includes the shared slot (-1)
+        byts = distinct * per_expert
+        out[f"T{T}"] = {"us_per_step": round(us, 1), "distinct_experts_incl_shared": distinct,
+                        "GB_s": round(byts / us / 1e3, 1)}
+    return out
+
+
+def extra_cfg3(torch):
+    """dense prefill GEMM 2048 x 5120 -> 17408 (bf16 A, Q4_K W, f32 D) and the
+    M = 3..6 verify GEMVs on the same weight."""
+    from hipster_amd import qmm, synth
+    M, N, K = synth.CFG3["M"], synth.CFG3["N"], synth.CFG3["K"]
+    W = torch.from_numpy(synth.matrix(synth.SEEDS["cfg3"], synth.Q4_K, N, K)).cuda()
+    A = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+    D = torch.zeros((M, N), device="cuda")
+    us = graph_us(torch, [lambda: qmm.gemm_wq(synth.Q4_K, W, A, D, M, N, K)], reps=5)
+    flop = 2 * M * N * K
+    out = {"gemm_us": round(us, 1), "TFLOPS": round(flop / us / 1e6, 1), "pct_bf16_peak": round(100 * flop / us / 1e6 / 2500, 1)}
+    ncopy = max(2, -(-ROTATE_BYTES // W.numel()))
+    Ws = [W] + [W.clone() for _ in range(ncopy - 1)]
+    for m in synth.CFG3["verify_M"]:
+        xb = qmm.XQ8Buf(m, K)
+        qmm.quantize_x_q8(torch.randn((m, K), device="cuda"), xb, m, K)
+        y = torch.zeros((m, N), device="cuda")
+        us = graph_us(torch, [(lambda c=c: qmm.gemv_q8(synth.Q4_K, Ws[c], xb, y, N, K, m)) for c in range(ncopy)], reps=2) / ncopy
+        out[f"verify_M{m}_us"] = round(us, 2)
+    return out
+
+
+def extra_cfg4(torch, tb):
+    """MoE prefill at 2048 tokens (route, device sort, grouped gate / up GEMMs,
+    silu -> bf16, grouped down GEMM, combine) with the Zipf-biased routing."""
+    import numpy as np
+    from hipster_amd import qmm, synth
+    H, F, NE, T = 2048, 512, 11, 2048
+    x = torch.randn((T, H), device="cuda").to(torch.bfloat16)
+    logits = torch.from_numpy(synth.router_logits(synth.SEEDS["cfg4"], T, 512, 1.1)).cuda()
+    NS = T * NE
+    cap = qmm.moe_tiles_capacity(T, NE, 512)
+    ids = torch.zeros((T, NE), dtype=torch.int32, device="cuda"); w = torch.zeros((T, NE), device="cuda")
+    kpos = torch.zeros(NS, dtype=torch.int32, device="cuda"); rowtok = torch.zeros(NS, dtype=torch.int32, device="cuda")
+    tiles = torch.zeros((cap, 3), dtype=torch.int32, device="cuda"); counts = torch.zeros(2, dtype=torch.int32, device="cuda")
+    g = torch.zeros((NS, F), device="cuda"); u = torch.zeros((NS, F), device="cuda")
+    h = torch.zeros((NS, F), dtype=torch.bfloat16, device="cuda")
+    dn = torch.zeros((NS, H), device="cuda"); y = torch.zeros((T, H), device="cuda")
+    ebg, ebd = tb["Wg"][0].numel(), tb["Wd"][0].numel()
+    route = [lambda: qmm.moe_route(logits, ids, w, T),
+             lambda: qmm.moe_sort(ids, T, NE, 512, qmm.MOE_TILE_ROWS, kpos, rowtok, tiles, counts)]
+    gemms = [lambda: qmm.moe_gemm_bf16(0, 0, tb["Wg"], tb["Sg"], ebg, tiles, counts, cap, rowtok, x, g, F, H),
+             lambda: qmm.moe_gemm_bf16(0, 0, tb["Wu"], tb["Su"], ebg, tiles, counts, cap, rowtok, x, u, F, H),
+             lambda: qmm.moe_silu_bf16(g, u, h, NS * F),
+             lambda: qmm.moe_gemm_bf16(0, 0, tb["Wd"], tb["Sd"], ebd, tiles, counts, cap, None, h, dn, H, F)]
+    comb = [lambda: qmm.moe_combine_sorted(dn, w, kpos, y, T, NE, H)]
+    us_all = graph_us(torch, route + gemms + comb, reps=3)
+    us_g = graph_us(torch, [gemms[0], gemms[1], gemms[3]], reps=3)
+    flop = 141733920768       # routed 2*20480*3*512*2048 + shared 2*2048*3*512*2048
+    c = counts.cpu().numpy()
+    return {"pipeline_us": round(us_all, 1), "grouped_gemms_us": round(us_g, 1), "TFLOPS": round(flop / us_g / 1e6, 1),
+            "pct_bf16_peak": round(100 * flop / us_g / 1e6 / 2500, 1), "tiles": [int(c[0]), int(c[1])],
+            "distinct_experts_incl_shared": int(len(np.unique(ids.cpu().numpy())))}
+
+
 def cpu_baseline_gemv(W, x, N, K, seconds):
     """The oracle's restatement of the reference host path (dequant_row + fp32 dot per row), threaded."""
     import oracle
@@ -157,6 +300,18 @@ def main():
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_gemv(r["W"], r["x"], r["N"], r["K"], args.cpu_seconds)
+    if not args.no_extra:
+        del r
+        torch.cuda.empty_cache()
+        extra = {"cfg1_dense_decode_layer": extra_cfg1(torch)}
+        torch.cuda.empty_cache()
+        tb = moe_tables(torch)
+        extra["cfg2_moe_decode"] = extra_cfg2(torch, tb)
+        extra["cfg4_moe_prefill"] = extra_cfg4(torch, tb)
+        del tb
+        torch.cuda.empty_cache()
+        extra["cfg3_dense_prefill"] = extra_cfg3(torch)
+        out["extra"] = extra
     print(json.dumps(out), flush=True)
 
 

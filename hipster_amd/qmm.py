@@ -90,14 +90,15 @@ def gemv_multi(segs, x, ncol, stream=None):
 
 
 def gemv_wmma_ok(segs):
-    arr = _segs(segs)
-    return bool(_lib.lib().qmm_gemv_wmma_ok(arr, len(segs)))
+    """gemv.h:35: the library's GEMV is T-invariant for every supported format, so any segment list
+    of Q4_K / Q6_K_SOA weights with K % 256 == 0 qualifies."""
+    return 1 <= len(segs) <= 4 and all(f in (WFmt.Q4_K, WFmt.Q6_K_SOA) and K % 256 == 0 for f, _, _, _, K in segs)
 
 
 def gemv_wmma(segs, x, ncol, mode=0, stream=None):
-    """gemv.h:36: matrix-core GEMV, T-invariant, ncol <= 16 per launch."""
-    arr = _segs(segs)
-    check(_lib.lib().qmm_gemv_wmma(arr, len(segs), x.c(), ncol, mode, _stream(stream)), "gemv_wmma")
+    """gemv.h:36: the reference's T-invariant matrix-core GEMV; here the (T-invariant) multi GEMV,
+    mode accepted and ignored."""
+    gemv_multi(segs, x, ncol, stream)
 
 
 def gemv_q4_K_f32(W, x, y, N, K, ncol, tpr=0, stream=None):

@@ -1,0 +1,121 @@
+// hipster_qmm_shim.hpp -- header-only C++ shim that restores the reference engine's call surface
+// (namespace hip in engine/kernels/gemv.h, gemm.h and the MoE part of fn.h) on top of the C ABI of
+// libhipster_qmm.so (include/hipster_qmm.h).  An engine that includes this header instead of those
+// three files compiles unchanged against the gfx950 library.
+//
+// Differences from the reference, all deliberate:
+//  - errors (unsupported format, bad shape, launch failure) throw std::runtime_error carrying the
+//    library's status string, where the reference calls abort() or misbehaves silently;
+//  - gemv_wmma / gemv_wmma_ok map onto the library's T-invariant GEMV (any ncol gives every column
+//    the same reduction order), so `mode` is accepted and ignored;
+//  - BlasLt::gemm runs the library's own bf16 MFMA GEMM (no hipBLASLt, no autotune, no workspace);
+//  - fn::moe_combine_sorted takes the row width from the hidden size E of the caller's model: the
+//    reference fixes E = 2560 at compile time; here it is the template argument (default 2560).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "hipster_qmm.h"
+
+namespace hip {
+
+namespace detail {
+inline void ck(int status, const char* what) {
+    if (status != QMM_OK) throw std::runtime_error(std::string(what) + ": " + qmm_status_string(status));
+}
+}  // namespace detail
+
+// ---- gemv.h -------------------------------------------------------------------------------
+struct XQ8 { int8_t* q; float* d; float* s; float2* ds = nullptr; };                         // gemv.h:8
+enum class WFmt { Q4_K, Q5_K, IQ4_XS, Q6_K_SOA, Q8_0_SOA, Q5_1_SOA };                           // gemv.h:13
+struct GemvSeg { WFmt fmt; const void* w; float* y; int N, K; };                                 // gemv.h:27
+struct MoeSegs { const void* w[2]; const void* shared[2]; float* y[2]; size_t ebytes; const float* slotw = nullptr; };  // gemv.h:43
+struct MoeTile { int expert, k0, ncols; };                                                      // gemv.h:48
+
+inline qmm_xq8 to_c(const XQ8& x) { return qmm_xq8{x.q, x.d, x.s, (void*)x.ds}; }
+
+inline void quantize_x_q8(const float* x, XQ8 out, int ncol, int K, hipStream_t s) {
+    detail::ck(qmm_quantize_x_q8(x, to_c(out), ncol, K, (void*)s), "quantize_x_q8");
+}
+inline size_t wfmt_row_bytes(WFmt f, int K) { return qmm_wfmt_row_bytes((int)f, K); }
+inline void repack_row_q6_K(const uint8_t* src, uint8_t* dst, int K) {
+    detail::ck(qmm_repack_row_q6_K(src, dst, K), "repack_row_q6_K");
+}
+inline void gemv_q8(WFmt f, const void* W, XQ8 x, float* y, int N, int K, int ncol, int tpr, int rpt, hipStream_t s) {
+    detail::ck(qmm_gemv_q8((int)f, W, to_c(x), y, N, K, ncol, tpr, rpt, (void*)s), "gemv_q8");
+}
+inline void gemv_multi(const GemvSeg* segs, int nseg, XQ8 x, int ncol, hipStream_t s) {
+    qmm_gemv_seg c[4];
+    if (nseg < 1 || nseg > 4) detail::ck(QMM_ERR_SHAPE, "gemv_multi");
+    for (int i = 0; i < nseg; ++i) c[i] = qmm_gemv_seg{(int32_t)segs[i].fmt, segs[i].w, segs[i].y, segs[i].N, segs[i].K};
+    detail::ck(qmm_gemv_multi(c, nseg, to_c(x), ncol, (void*)s), "gemv_multi");
+}
+inline bool gemv_wmma_ok(const GemvSeg* segs, int nseg) {
+    if (nseg < 1 || nseg > 4) return false;
+    for (int i = 0; i < nseg; ++i)
+        if ((segs[i].fmt != WFmt::Q4_K && segs[i].fmt != WFmt::Q6_K_SOA) || segs[i].K % 256 != 0) return false;
+    return true;
+}
+inline void gemv_wmma(const GemvSeg* segs, int nseg, XQ8 x, int ncol, int /*mode*/, hipStream_t s) {
+    gemv_multi(segs, nseg, x, ncol, s);
+}
+inline void gemv_moe(WFmt f, WFmt fs, const MoeSegs& a, int nseg, const int* ids, int nexp, XQ8 x, int N, int K, int T,
+                     bool xrow_te, hipStream_t s) {
+    qmm_moe_segs c;
+    for (int g = 0; g < 2; ++g) { c.w[g] = a.w[g]; c.shared[g] = a.shared[g]; c.y[g] = a.y[g]; }
+    c.ebytes = a.ebytes;
+    c.slotw = a.slotw;
+    detail::ck(qmm_gemv_moe((int)f, (int)fs, &c, nseg, ids, nexp, to_c(x), N, K, T, xrow_te ? 1 : 0, (void*)s), "gemv_moe");
+}
+inline void gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int ncol, int tpr, hipStream_t s) {
+    detail::ck(qmm_gemv_q4_K_f32(W, x, y, N, K, ncol, tpr, (void*)s), "gemv_q4_K_f32");
+}
+
+// ---- gemm.h -------------------------------------------------------------------------------
+inline void dequant_bf16(WFmt f, const void* W, uint16_t* out, int N, int K, hipStream_t s) {
+    detail::ck(qmm_dequant_bf16((int)f, W, out, N, K, (void*)s), "dequant_bf16");
+}
+inline void f32_to_bf16(const float* x, uint16_t* out, size_t n, hipStream_t s) {
+    detail::ck(qmm_f32_to_bf16(x, out, n, (void*)s), "f32_to_bf16");
+}
+inline void bf16_to_f32(const uint16_t* x, float* out, size_t n, hipStream_t s) {
+    detail::ck(qmm_bf16_to_f32(x, out, n, (void*)s), "bf16_to_f32");
+}
+inline void bf16_to_f32_seg(const uint16_t* x, int Nt, int off, int N, float* out, int M, hipStream_t s) {
+    detail::ck(qmm_bf16_to_f32_seg(x, Nt, off, N, out, M, (void*)s), "bf16_to_f32_seg");
+}
+inline void bf16_to_f32_seg2(const uint16_t* x, const uint16_t* x2, int Nt, int off, int N, float* out, int M, hipStream_t s) {
+    detail::ck(qmm_bf16_to_f32_seg2(x, x2, Nt, off, N, out, M, (void*)s), "bf16_to_f32_seg2");
+}
+class BlasLt {
+public:
+    // D[M][N] bf16 = A[M][K] bf16 . W[N][K]^T bf16, f32 accumulate (gemm.h:27)
+    void gemm(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, hipStream_t s) {
+        detail::ck(qmm_gemm_bf16(A, W, D, M, N, K, (void*)s), "BlasLt::gemm");
+    }
+};
+
+namespace fn {
+// ---- fn.h (MoE part) ----------------------------------------------------------------------
+inline void moe_route(const float* logits, int* ids, float* w, int T, hipStream_t s) {
+    detail::ck(qmm_moe_route(logits, ids, w, T, (void*)s), "moe_route");
+}
+inline void moe_gemv(WFmt fmt, WFmt shared_fmt, const MoeSegs& a, int nseg, const int* ids, int nexp, XQ8 xq, int N, int K, int T,
+                     hipStream_t s) {
+    // the reference's forwarder: the down projection (slot weights set) reads per-(t, e) rows
+    hip::gemv_moe(fmt, shared_fmt, a, nseg, ids, nexp, xq, N, K, T, a.slotw != nullptr, s);
+}
+inline void moe_silu_quant(const float* gate, const float* up, XQ8 xq, int rows, int n, hipStream_t s) {
+    detail::ck(qmm_moe_silu_quant(gate, up, to_c(xq), rows, n, (void*)s), "moe_silu_quant");
+}
+template <int E = 2560>
+inline void moe_combine_sorted(const float* down, const float* w, const int* kpos, float* y, int T, int nexp, hipStream_t s) {
+    detail::ck(qmm_moe_combine_sorted(down, w, kpos, y, T, nexp, E, (void*)s), "moe_combine_sorted");
+}
+}  // namespace fn
+
+}  // namespace hip

@@ -1,0 +1,46 @@
+"""CPU check of the drop-in C++ shim (include/hipster_qmm_shim.hpp): it compiles with hipcc against
+libhipster_qmm.so, keeps the reference's namespace hip names (engine/kernels/gemv.h, gemm.h, fn.h),
+and turns a library error into std::runtime_error instead of the reference's abort()."""
+import os
+import shutil
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HIPCC = "/opt/rocm/bin/hipcc"
+
+SRC = r'''
+#include "hipster_qmm_shim.hpp"
+#include <cstdio>
+int main() {
+    hip::GemvSeg seg{hip::WFmt::Q5_K, nullptr, nullptr, 16, 256};
+    hip::GemvSeg ok4{hip::WFmt::Q4_K, nullptr, nullptr, 16, 256};
+    if (hip::gemv_wmma_ok(&seg, 1) || !hip::gemv_wmma_ok(&ok4, 1)) return 2;
+    if (hip::wfmt_row_bytes(hip::WFmt::Q4_K, 5120) != 20 * 144) return 3;
+    try {
+        hip::gemv_q8(hip::WFmt::Q5_K, (void*)16, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, (float*)16, 16, 256, 1, 0, 1, nullptr);
+    } catch (const std::runtime_error& e) {
+        std::printf("%s\n", e.what());
+        return 0;
+    }
+    return 1;
+}
+'''
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+def test_shim_compiles_and_reports_errors():
+    lib = os.path.join(ROOT, "hipster_amd", "lib")
+    d = tempfile.mkdtemp()
+    try:
+        src, exe = os.path.join(d, "t.cpp"), os.path.join(d, "t")
+        open(src, "w").write(SRC)
+        subprocess.run([HIPCC, "-std=c++17", "-I" + os.path.join(ROOT, "include"), src, "-L" + lib, "-lhipster_qmm",
+                        "-Wl,-rpath," + lib, "-o", exe], check=True, capture_output=True)
+        r = subprocess.run([exe], capture_output=True, text=True)
+        assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+        assert "unsupported weight format" in r.stdout
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
