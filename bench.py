@@ -46,7 +46,22 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
+    p.add_argument("--calib-copy", action="store_true",
+                   help="only run 10 plain device copies of 256 MiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
+
+
+def calib_copy():
+    """A plain copy kernel of known size: 10 x 256 MiB read + 256 MiB written (torch's copy kernel).
+    The counter reads of these dispatches scale the ones of the measured kernels."""
+    import torch
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_()
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib_copy_bytes_read": n, "calib_copy_bytes_written": n, "dispatches": 10}), flush=True)
 
 
 def capture(torch, launches):
@@ -271,10 +286,17 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.calib_copy:
+        calib_copy()
+        return
     from hipster_amd import _lib
     _lib.lib()   # fails loudly if the HIP library is missing
 
     r = q4k_gemv_m1(args)
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "q4k_gemv_m1_traffic.json")
+    if os.path.exists(tfile):   # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+        traffic = json.load(open(tfile)).get("traffic_bytes")
     gbs_step = r["algo_bytes"] / (r["ms_step"] * 1e-3) / 1e9
     gbs_kernel = r["algo_bytes"] / (r["ms_kernel"] * 1e-3) / 1e9
     out = {
@@ -295,7 +317,7 @@ def main():
                    "N": r["N"], "K": r["K"], "M": 1, "algo_bytes_per_step": r["algo_bytes"],
                    "pct_of_hbm_peak": round(100 * gbs_step / HBM_PEAK_GBS, 1)},
         "roofline": {"bound": "hbm", "achieved": round(gbs_kernel, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs_kernel / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs_kernel / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_gemv_q4k_q8<1,5,5,true>", "us_per_launch": round(r["ms_kernel"] * 1e3, 3)},
     }
     if not args.no_cpu:
