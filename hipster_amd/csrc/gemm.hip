@@ -130,18 +130,12 @@ __global__ void k_bf16_to_f32_seg2(const uint16_t* __restrict__ x, const uint16_
 }
 
 // ------------------------------------------------------------------------------------------
-// MFMA GEMM core.  Macro tile GBM x GBN = 256 x 256, K step 64, 4 waves as 2 x 2, each wave a
+// bf16 x bf16 MFMA GEMM (the BlasLt::gemm twin).  Macro tile GBM x GBN = 256 x 256, K step 64, 4 waves as 2 x 2, each wave a
 // 128 x 128 tile = 8 x 8 MFMA tiles of 16 x 16 (256 f32 accumulators per lane, held in AGPRs).
 // LDS holds two stages of {A 256 x 64, W 256 x 64} bf16 with rows padded to 72 elements (144 B):
 // the 16-byte fragment reads of 16 consecutive rows then fall on 16 distinct 4-bank groups.
 // Step s: issue the global loads of step s+1 into registers, run the 128 MFMAs of step s from
-// stage s&1, write step s+1's registers (A copied, W dequantised) into the other stage, barrier.
-#ifndef QMM_GEMM_DMA
-#define QMM_GEMM_DMA 2
-#endif
-#ifndef QMM_GEMM_SCHED
-#define QMM_GEMM_SCHED 1
-#endif
+// stage s&1, write step s+1's registers into the other stage, barrier.
 constexpr int GBM = 256, GBN = 256, GBK = 64, GLD = GBK + 8;
 constexpr int kStageElems = (GBM + GBN) * GLD;                 // bf16 elements per stage
 constexpr size_t kGemmLds = 2 * (size_t)kStageElems * 2;     // bytes (147,456)
@@ -161,45 +155,6 @@ struct ALoad {
         const int t = threadIdx.x;
 #pragma unroll
         for (int p = 0; p < 8; ++p) *(uint4*)&La[(32 * p + (t >> 3)) * GLD + 8 * (t & 7)] = r[p];
-    }
-};
-
-// W tile loader, Q4_K: thread t decodes weight row n0+t for the K step at k0, i.e. qs pair
-// j = (k0/64)&3 of block k0/256: low nibbles -> k 0..31 (sub-block 2j), high -> k 32..63 (2j+1).
-// This is the GEMM's tolerance path: w = fma(d*sc, q, -dmin*m), RNE to bf16 in hardware.
-struct BLoadQ4K {
-    uint4 hd, q0, q1;
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
-        const int n = min(n0 + (int)threadIdx.x, N - 1);
-        const uint8_t* bp = W + (size_t)n * ((size_t)(K >> 8) * 144) + (size_t)(k0 >> 8) * 144;
-        const int j = (k0 >> 6) & 3;
-        hd = ld16(bp);
-        q0 = ld16(bp + 16 + 32 * j);
-        q1 = ld16(bp + 32 + 32 * j);
-    }
-    __device__ __forceinline__ void store(__bf16* Lb, int k0) const {
-        const int j = (k0 >> 6) & 3;
-        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-        const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
-        const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
-        const float dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
-        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        __bf16* dst = &Lb[threadIdx.x * GLD];
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            const float dl = hh ? dB : dA, ml = hh ? mB : mA;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {           // 8 weights per 16-byte store
-                __bf16 v[8];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint32_t u = (hh ? (qw[2 * c + e] >> 4) : qw[2 * c + e]) & 0x0f0f0f0fu;
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) v[4 * e + b] = (__bf16)(dl * (float)((u >> (8 * b)) & 0xffu) - ml);
-                }
-                *(bf16x8*)(dst + 32 * hh + 8 * c) = *(const bf16x8*)v;
-            }
-        }
     }
 };
 
@@ -306,192 +261,32 @@ __global__ void __launch_bounds__(256) k_gemm(const uint16_t* __restrict__ A, co
 }
 
 // ------------------------------------------------------------------------------------------
-// DMA-staged variant.  The A tile goes global -> LDS with global_load_lds_dwordx4 (no registers),
-// three stages deep; the bf16 W tile (dequantised from Q4_K registers, or DMA-copied) two stages.
+// Fused Q4_K GEMM with DMA-staged A.  The A tile goes global -> LDS with global_load_lds_dwordx4 (no
+// registers), three stages deep; the bf16 W tile, dequantised from Q4_K registers, two stages.
 // Stage layout: 256 rows x 8 chunks of 16 B, unpadded, chunk c of row r stored in slot
 // r*8 + (c ^ ((r >> 1) & 7)): a DMA instruction writes 1 KiB of consecutive slots (lane i -> slot
 // base + i, so the swizzle is applied to the global address each lane fetches), and the 16
 // consecutive rows of an MFMA fragment read land on 16 distinct 4-bank groups.
-// Step s: DMA A tile s+2 -> A stage (s+2)%3 and load W tile s+2 into register set s%2; MFMAs of
-// tile s (A stage s%3, W stage s%2); tile s+1's W registers -> W stage (s+1)%2; barrier.  Waiting
-// for W tile s+1's registers (issued before A tile s+2's DMA) also retires A tile s+1's DMA, since
-// vmcnt retires in issue order.  The A tile thus has two steps of MFMA time to land.
+// Step s: DMA A tile s+2 -> A stage (s+2)%3; MFMAs of tile s (A stage s%3, W stage s%2); tile s+1's
+// W registers -> W stage (s+1)%2; W tile s+2 -> registers; wait; barrier.  The A tile thus has two
+// steps of MFMA time to land.
 constexpr int kChunks = GBM * GBK / 8;                         // 16-byte chunks per stage (2048)
 constexpr size_t kGemmDmaLds = (3 + 2) * (size_t)kChunks * 16;  // 163,840 B
 
 __device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
 
-// A tile (rows m0.., k0..k0+63) -> stage at La (chunk units): wave w issues chunk positions
-// (8w + i) * 64 + lane, i < 8
-__device__ __forceinline__ void dma_a(const uint16_t* __restrict__ A, int M, int K, int m0, int k0, uint4* La) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        // chunk slot p = (8w + i) * 64 + lane: row r = 64w + 8i + lane/8, slot column lane%8,
-        // data column (lane%8) ^ ((r >> 1) & 7) = (lane%8) ^ ((4i + lane/16) & 7)
-        const int r = 64 * wave + 8 * i + (lane >> 3), c = (lane & 7) ^ ((4 * i + (lane >> 4)) & 7);
-        const uint32_t off = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)(k0 + 8 * c);
-        __builtin_amdgcn_global_load_lds(A + off, La + (8 * wave + i) * 64, 16, 0, 0);
-    }
-}
-
-struct WRawQ4K {
-    uint4 hd, q0, q1;
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
-        const int n = min(n0 + (int)threadIdx.x, N - 1);
-        const uint8_t* bp = W + (size_t)n * ((size_t)(K >> 8) * 144) + (size_t)(k0 >> 8) * 144;
-        const int j = (k0 >> 6) & 3;
-        hd = ld16(bp);
-        q0 = ld16(bp + 16 + 32 * j);
-        q1 = ld16(bp + 32 + 32 * j);
-    }
-    // row threadIdx.x of the W stage at Lb: 64 bf16 (low nibbles -> chunks 0..3, high -> 4..7)
-    __device__ __forceinline__ void store(uint4* Lb, int k0) const {
-        const int j = (k0 >> 6) & 3, t = threadIdx.x;
-        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-        const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
-        const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
-        const float dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
-        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            const float dl = hh ? dB : dA, ml = hh ? mB : mA;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                __bf16 v[8];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint32_t u = (hh ? (qw[2 * c + e] >> 4) : qw[2 * c + e]) & 0x0f0f0f0fu;
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) v[4 * e + b] = (__bf16)(dl * (float)((u >> (8 * b)) & 0xffu) - ml);
-                }
-                Lb[swz(t, 4 * hh + c)] = *(const uint4*)v;
-            }
-        }
-    }
-};
-
-// Fragment reads of a swizzled stage.  Row R = 128*wm + 16*i + fr has (R >> 1) & 7 == (fr >> 1) & 7
-// for every i, so fragment i of K half ks sits at lane base fo[ks] + 128*i chunks: one VGPR base per
-// K half and compile-time offsets (the ds_read immediate) for the 8 fragments.
-__device__ __forceinline__ void mfma_step_swz(const uint4* La, const uint4* Lb, const int (&foa)[2], const int (&fob)[2],
-                                              f32x4 (&acc)[8][8]) {
-#pragma unroll
-    for (int ks = 0; ks < GBK / 32; ++ks) {
-        bf16x8 af[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint4 v = La[foa[ks] + 128 * i];
-            af[i] = *(const bf16x8*)&v;
-        }
-#pragma unroll
-        for (int jn = 0; jn < 8; ++jn) {
-            const uint4 v = Lb[fob[ks] + 128 * jn];
-            const bf16x8 bf = *(const bf16x8*)&v;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf, acc[i][jn], 0, 0, 0);
-        }
-    }
-}
-
-// 32 x 32 x 16 MFMA variant of the wave tile: 4 x 4 MFMA tiles of 32 x 32 (16 f32 per lane each).
-// Operand layout (v_mfma_f32_32x32x16_bf16): lane l supplies row (or column) l%32 and the 8
-// consecutive k values 8*(l/32)..+7 of the 16-wide K slice; output element i of lane l is
-// row 8*(i/4) + 4*(l/32) + i%4, column l%32.  Fragment row R = base + 32*t + l%32 keeps
+// 32 x 32 x 16 MFMA tiles.  Operand layout (v_mfma_f32_32x32x16_bf16): lane l supplies row (or
+// column) l%32 and the 8 consecutive k values 8*(l/32)..+7 of the 16-wide K slice; output element i
+// of lane l is row 8*(i/4) + 4*(l/32) + i%4, column l%32.  Fragment row R = base + 32*t + l%32 keeps
 // (R >> 1) & 7 == ((l%32) >> 1) & 7, so fragment t of slice ks sits at lane base + 256*t chunks.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-__global__ void __launch_bounds__(256) k_gemm_q4k_dma(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
-                                                      float* __restrict__ D, int M, int N, int K) {
-    extern __shared__ __align__(16) uint8_t smem_raw[];
-    uint4* const As = (uint4*)smem_raw;                 // 3 stages
-    uint4* const Bs = As + 3 * kChunks;                 // 2 stages
-    const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
-    int tm, tn;
-    tile_of(blockIdx.x, mt, nt, tm, tn);
-    const int m0 = tm * GBM, n0 = tn * GBN;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave & 1, wn = wave >> 1;
-    const int nk = K / GBK, lastk = (nk - 1) * GBK;
-    WRawQ4K wr;
-    wr.load(W, N, K, n0, 0);
-    dma_a(A, M, K, m0, 0, As);
-    dma_a(A, M, K, m0, min(GBK, lastk), As + kChunks);
-    wr.store(Bs, 0);
-    wr.load(W, N, K, n0, min(GBK, lastk));
-    __builtin_amdgcn_s_waitcnt(0);       // A tiles 0, 1 in LDS, W tile 1 in registers
-    lds_barrier();
-    f32x16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int jn = 0; jn < 4; ++jn)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][jn][e] = 0.f;
-    const int fr = lane & 31, fc = lane >> 5, fx = (fr >> 1) & 7;
-    int foa[4], fob[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        foa[ks] = (128 * wm + fr) * 8 + ((2 * ks + fc) ^ fx);
-        fob[ks] = (128 * wn + fr) * 8 + ((2 * ks + fc) ^ fx);
-    }
-    int sa = 0;                          // A stage of tile s
-    for (int s = 0; s < nk; ++s) {
-        // A tile s+2 -> LDS by DMA (two steps of lead); MFMAs of tile s; W tile s+1 (registers
-        // loaded a step ago) dequantised into the other W stage; W tile s+2 -> registers.  Tiles
-        // past the end are clamped re-reads into stages nobody reads again.
-        const int sa2 = sa >= 1 ? sa - 1 : 2;                         // (s + 2) % 3
-        const uint4* La = As + sa * kChunks;
-        const uint4* Lb = Bs + (s & 1) * kChunks;
-#if !EXP_NODMA
-        dma_a(A, M, K, m0, min((s + 2) * GBK, lastk), As + sa2 * kChunks);
-#endif
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            bf16x8 af[4], bf[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) { const uint4 v = La[foa[ks] + 256 * t]; af[t] = *(const bf16x8*)&v; }
-#pragma unroll
-            for (int t = 0; t < 4; ++t) { const uint4 v = Lb[fob[ks] + 256 * t]; bf[t] = *(const bf16x8*)&v; }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int jn = 0; jn < 4; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
-#if !EXP_NODEQ
-            if (ks == 1) wr.store(Bs + ((s + 1) & 1) * kChunks, min((s + 1) * GBK, lastk));
-#endif
-        }
-#if !EXP_NOWLOAD
-        wr.load(W, N, K, n0, min((s + 2) * GBK, lastk));
-#endif
-        // A tile s+1's DMA (issued a step ago, before W tile s+1's loads) must have landed: everything
-        // but this step's 8 DMAs and 3 W loads
-        __builtin_amdgcn_s_waitcnt(0x0F7B);   // vmcnt <= 11
-        lds_barrier();
-        sa = sa == 2 ? 0 : sa + 1;
-    }
-    __builtin_amdgcn_s_waitcnt(0);            // drain the clamped trailing DMAs
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int m = m0 + 128 * wm + 32 * i + 8 * (e >> 2) + 4 * fc + (e & 3);
-            if (m >= M) continue;
-#pragma unroll
-            for (int jn = 0; jn < 4; ++jn) {
-                const int n = n0 + 128 * wn + 32 * jn + fr;
-                if (n < N) D[(size_t)m * N + n] = acc[i][jn][e];
-            }
-        }
-    }
-}
 
 // ------------------------------------------------------------------------------------------
 // Two waves per SIMD ("ping-pong"): 512 threads, 8 waves as 2 (M) x 4 (N), wave tile 128 x 64 =
 // 4 x 2 MFMA tiles of 32 x 32 (128 accumulators per lane).  The two waves of a SIMD interleave in
 // hardware: while one issues MFMAs the other runs its W dequantisation, DMA issue and fragment
-// reads, so the non-MFMA work of a step hides under the other wave's MFMAs.  LDS stages, swizzle
-// and the DMA lead are those of k_gemm_q4k_dma; each W row is dequantised by two threads, one
-// sub-block (32 weights) each.
+// reads, so the non-MFMA work of a step hides under the other wave's MFMAs.  Each W row is
+// dequantised by two threads, one sub-block (32 weights) each.
 constexpr int kPPThreads = 512;
 
 __device__ __forceinline__ void dma_a_pp(const uint16_t* __restrict__ A, int M, int K, int m0, int k0, uint4* La) {
@@ -614,14 +409,7 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __re
 
 int launch_gemm_q4k(const void* W, const uint16_t* A, float* D, int M, int N, int K, hipStream_t s) {
     const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-#if QMM_GEMM_DMA == 2
     hipLaunchKernelGGL(k_gemm_q4k_pp, dim3(grid), dim3(kPPThreads), kGemmDmaLds, s, A, (const uint8_t*)W, D, M, N, K);
-#elif QMM_GEMM_DMA
-    hipLaunchKernelGGL(k_gemm_q4k_dma, dim3(grid), dim3(256), kGemmDmaLds, s, A, (const uint8_t*)W, D, M, N, K);
-#else
-    hipLaunchKernelGGL((k_gemm<BLoadQ4K, uint8_t, false>), dim3(grid), dim3(256), kGemmLds, s, A, (const uint8_t*)W,
-                       (void*)D, M, N, K);
-#endif
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }

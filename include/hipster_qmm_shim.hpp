@@ -99,6 +99,32 @@ public:
     }
 };
 
+// ---- additions with no reference counterpart (the calls the engine's prefill moves to) ----------
+// D[M][N] f32 = A[M][K] bf16 . dequant(W)[N][K]^T in one launch: replaces dequant_bf16 + BlasLt::gemm
+// + bf16_to_f32_seg of Qwen4Exp::lin_gemm / Qwen35::lin_multi without the bf16 weight scratch.
+inline void gemm_wq(WFmt f, const void* W, const uint16_t* A, float* D, int M, int N, int K, hipStream_t s) {
+    detail::ck(qmm_gemm_wq((int)f, W, A, D, M, N, K, (void*)s), "gemm_wq");
+}
+// device sort of the routed slots (replaces the host block of qwen4exp.cpp:628-645; no host sync)
+inline void moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* kpos, int* rowtok, MoeTile* tiles,
+                     int* counts, hipStream_t s) {
+    static_assert(sizeof(MoeTile) == sizeof(qmm_moe_tile), "MoeTile layout");
+    detail::ck(qmm_moe_sort(ids, T, nslot, nexperts, maxc, kpos, rowtok, reinterpret_cast<qmm_moe_tile*>(tiles), counts,
+                            (void*)s),
+               "moe_sort");
+}
+// grouped expert GEMM over sorted bf16 rows; the tile count is read from counts on the device
+inline void moe_gemm_bf16(WFmt f, WFmt fs, const void* W, const void* Wsh, size_t ebytes, const MoeTile* tiles,
+                          const int* counts, int max_tiles, const int* rowtab, const uint16_t* A, float* D, int N, int K,
+                          hipStream_t s) {
+    detail::ck(qmm_moe_gemm_bf16((int)f, (int)fs, W, Wsh, ebytes, reinterpret_cast<const qmm_moe_tile*>(tiles), counts,
+                                 max_tiles, rowtab, A, D, N, K, (void*)s),
+               "moe_gemm_bf16");
+}
+inline void moe_silu_bf16(const float* gate, const float* up, uint16_t* h, size_t n, hipStream_t s) {
+    detail::ck(qmm_moe_silu_bf16(gate, up, h, n, (void*)s), "moe_silu_bf16");
+}
+
 namespace fn {
 // ---- fn.h (MoE part) ----------------------------------------------------------------------
 inline void moe_route(const float* logits, int* ids, float* w, int T, hipStream_t s) {

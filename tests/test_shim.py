@@ -19,6 +19,14 @@ int main() {
     hip::GemvSeg ok4{hip::WFmt::Q4_K, nullptr, nullptr, 16, 256};
     if (hip::gemv_wmma_ok(&seg, 1) || !hip::gemv_wmma_ok(&ok4, 1)) return 2;
     if (hip::wfmt_row_bytes(hip::WFmt::Q4_K, 5120) != 20 * 144) return 3;
+    int caught = 0;
+    try {
+        hip::gemm_wq(hip::WFmt::Q6_K_SOA, (void*)16, (const uint16_t*)16, (float*)16, 16, 16, 256, nullptr);
+    } catch (const std::runtime_error&) { ++caught; }
+    try {
+        hip::moe_sort((const int*)16, 4, 11, 4096, 64, (int*)16, (int*)16, (hip::MoeTile*)16, (int*)16, nullptr);
+    } catch (const std::runtime_error&) { ++caught; }
+    if (caught != 2) return 4;
     try {
         hip::gemv_q8(hip::WFmt::Q5_K, (void*)16, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, (float*)16, 16, 256, 1, 0, 1, nullptr);
     } catch (const std::runtime_error& e) {
