@@ -56,6 +56,8 @@ SIGNATURES = {
     "qmm_dequant_bf16": (c_int, [c_int, c_vp, c_vp, c_int, c_int, c_vp]),
     "qmm_moe_sort": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "qmm_moe_gemm_bf16": (c_int, [c_int, c_int, c_vp, c_vp, ctypes.c_size_t, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_vp]),
+    "qmm_moe_gemm_gate_up_bf16": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp, c_vp, c_int, c_vp, c_vp,
+                                          c_vp, c_int, c_int, c_vp]),
     "qmm_moe_silu_bf16": (c_int, [c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp]),
     "qmm_gemm_wq": (c_int, [c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "qmm_gemm_bf16": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),

@@ -9,14 +9,13 @@
 //   qmm_gemm_bf16           hip::BlasLt::gemm     engine/kernels/gemm.hip:125-160 (own MFMA kernel, no hipBLASLt)
 //   qmm_f32_to_bf16, qmm_bf16_to_f32, qmm_bf16_to_f32_seg, qmm_bf16_to_f32_seg2   gemm.hip:77-95
 //
-// GEMM tiling (MFMA v_mfma_f32_16x16x32_bf16, wave64): a 256-thread workgroup computes a
-// 256 (M, activation rows) x 256 (N, weight rows) tile of D = A . W^T, stepping K by 64 through a
-// two-stage LDS ring (see the core below).  For Q4_K weights a K step of 64 is exactly one 32-byte
-// qs "pair" of each row's block, so one thread per weight row decodes it (header + 32 qs bytes ->
-// 64 bf16) straight into LDS.  The next step's global loads (A: 8 x 16 B per thread, W: 48 B or
-// 128 B) are issued before the MFMAs of the current step and land in registers while they run.
-// Workgroups are mapped XCD-aware: consecutive workgroup ids go to different XCDs, so tile ids are
-// assigned so that the 8 M tiles of one weight tile run on the same XCD and share its L2.
+// Q4_K GEMM (qmm_gemm_wq): 256 x 256 output tiles, K step 64, 512 threads (two waves per SIMD, so
+// one wave's MFMAs hide the other's dequantisation), v_mfma_f32_32x32x16_bf16.  A streams
+// global -> LDS by DMA three stages ahead; a K step of 64 is exactly one 32-byte qs "pair" of each
+// weight row's block, dequantised from registers into a two-stage bf16 W ring.  bf16 GEMM
+// (qmm_gemm_bf16): 256 x 256 tiles, 4 waves, v_mfma_f32_16x16x32_bf16, register-staged two-stage
+// LDS ring.  Both map workgroups XCD-aware: consecutive workgroup ids go to different XCDs, so tile
+// ids are assigned so that the M tiles of one weight tile run on the same XCD and share its L2.
 #include "qmm_common.hpp"
 
 #include <hip/hip_runtime.h>

@@ -8,6 +8,8 @@
 //                       host->device copies) -- here one workgroup on the device, no host sync
 //   qmm_moe_gemm_bf16   moe_gemm (engine/kernels/gemv.h:49-50, gemv.hip:909-969,1377-1381) with
 //                       bf16 activations; the tile count is read on the device
+//   qmm_moe_gemm_gate_up_bf16  the gate and up moe_gemm calls plus moe_silu_quant of
+//                       qwen4exp.cpp:646-648 in one launch, writing h = bf16(silu(g) * u)
 //   qmm_moe_silu_bf16   moe_silu_quant (fn.hip:206-211) for the bf16 path: h = bf16(silu(g) * u)
 #include "qmm_common.hpp"
 
@@ -146,146 +148,240 @@ __global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict
 }
 
 // ------------------------------------------------------------------------------------------
-// Grouped expert GEMM.  Work unit = (tile, 256-row block of the expert's weight): D[k0 + r][n] =
-// sum_k A[row(r)][k] * W_e[n][k] for r < ncols, row(r) = rowtab[k0 + r] (or k0 + r), W_e the expert's
-// Q4_K matrix (the shared matrix when expert < 0).  Tiles hold up to 64 sorted rows: the MFMA tile
-// is 64 (rows) x 256 (weight rows), K step 64; 4 waves, wave w the weight rows 64w..64w+63, 2 x 2
-// MFMA tiles of 32 x 32.  LDS: two A stages (64 x 64 bf16, DMA-gathered by row) and two W stages
-// (256 x 64 bf16 dequantised from registers), 80 KiB, so two workgroups share a CU and their waves
-// interleave on each SIMD.  Stage layout and swizzle as in gemm.hip (chunk c of row r in slot
-// r*8 + (c ^ ((r >> 1) & 7))).
-constexpr int MBM = 64, MBN = 256, MBK = 64;
-constexpr int kAChunks = MBM * MBK / 8, kBChunks = MBN * MBK / 8;        // 512, 2048 chunks of 16 B
-constexpr size_t kMoeGemmLds = 2 * (size_t)(kAChunks + kBChunks) * 16;   // 81,920 B
+// Grouped expert GEMM.  Work unit = (tile, block of the expert's weight rows).  A tile holds up to
+// 128 sorted rows: D[k0 + r][n] = sum_k A[row(r)][k] * W_e[n][k] for r < ncols, row(r) =
+// rowtab[k0 + r] (or k0 + r), W_e the expert's Q4_K matrix (the shared matrix when expert < 0).
+//
+// 256 threads, 4 waves side by side along the weight rows: wave w owns two 32-wide MFMA column
+// blocks and all NRB = ceil(ncols / 32) row blocks of the tile, so every weight is dequantised
+// once per workgroup, by the wave that multiplies it, straight into MFMA operand registers.
+// v_mfma_f32_32x32x16_bf16 takes from lane l weight row l%32 and k = 8(l/32)..+7 of a 16-wide K
+// slice; for a 64-wide K step (one qs pair j of a block) these are the low nibbles of qs bytes
+// 8h..8h+7 (slice 0) and 16+8h..16+8h+7 (slice 1) and the high nibbles of the same bytes (slices
+// 2, 3), h = l/32.  A (gathered bf16 rows) and the raw weight bytes (16-byte block header and the two
+// 16-byte halves of the step's qs pair, per weight row) stream global -> LDS with
+// global_load_lds_dwordx4 through a ring of XST = 5 stages issued four steps ahead; the raw bytes of
+// step t+1 are dequantised while the MFMAs of step t run.  A stage: 128 rows x 8 chunks of 16 B,
+// chunk c of row r in slot r*8 + (c ^ ((r >> 1) & 7)) (conflict-free fragment reads); weight stage:
+// slots [part][256 rows], part 0 = header, 1 = qs bytes 32j..32j+15, 2 = qs bytes 32j+16..32j+31.
+// Gate/up mode: the 256 weight rows of a workgroup are 128 gate rows and the same 128 up rows; wave
+// w's column block 0 is gate rows n0+32w.., block 1 the same up rows, so a lane holds g and u of the
+// same output element and writes h = bf16(silu(g) * u) directly.
+constexpr int XBM = 128, XBW = 256, XBK = 64, XST = 5;
+constexpr int kXA = XBM * XBK / 8;                          // 16-byte chunks per A stage (1024)
+constexpr int kXW = 3 * XBW;                                // chunks per weight stage (768)
+constexpr size_t kXLds = (size_t)XST * (kXA + kXW) * 16;    // 143,360 B
 
-__device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
+// s_waitcnt immediate for "vmcnt <= v" (expcnt, lgkmcnt unconstrained)
+constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >> 4) << 14); }
 
-struct MoeWRaw {
-    uint4 hd, q0, q1;
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ We, int N, int K, int n0, int k0) {
-        const int n = min(n0 + (int)threadIdx.x, N - 1);
-        const uint8_t* bp = We + (size_t)n * ((size_t)(K >> 8) * 144) + (size_t)(k0 >> 8) * 144;
-        const int j = (k0 >> 6) & 3;
-        hd = ld16(bp);
-        q0 = ld16(bp + 16 + 32 * j);
-        q1 = ld16(bp + 32 + 32 * j);
-    }
-    __device__ __forceinline__ void store(uint4* Lb, int k0) const {
-        const int j = (k0 >> 6) & 3, t = threadIdx.x;
-        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-        const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
-        const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
-        const float dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
-        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            const float dl = hh ? dB : dA, ml = hh ? mB : mA;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                __bf16 v[8];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint32_t u = (hh ? (qw[2 * c + e] >> 4) : qw[2 * c + e]) & 0x0f0f0f0fu;
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) v[4 * e + b] = (__bf16)(dl * (float)((u >> (8 * b)) & 0xffu) - ml);
-                }
-                Lb[swz(t, 4 * hh + c)] = *(const uint4*)v;
-            }
-        }
-    }
+struct XArgs {
+    const uint8_t* w0;     // expert matrices (gate in gate/up mode), expert e at w0 + e * ebytes
+    const uint8_t* w0sh;   // shared-expert matrix
+    const uint8_t* w1;     // up experts (gate/up mode only)
+    const uint8_t* w1sh;
+    size_t ebytes;
+    const qmm_moe_tile* tiles;
+    const int* counts;
+    const int* rowtab;
+    const uint16_t* A;
+    void* D;               // f32 [k][N], or bf16 h [k][N] in gate/up mode
+    int N, K, nb;          // nb = weight-row blocks per tile
 };
 
-// A tile (64 gathered rows, k0..k0+63) -> stage La: wave w issues chunk slots (2w + i) * 64 + lane
-__device__ __forceinline__ void dma_a_rows(const uint16_t* __restrict__ A, const int* rows, int K, int k0, uint4* La) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// 8 nibbles (one per byte of {u0, u1}) -> bf16 dl * q - ml, k order = byte order
+__device__ __forceinline__ bf16x8 q4_bf16x8(uint32_t u0, uint32_t u1, float dl, float ml) {
+    __bf16 v[8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = 16 * wave + 8 * i + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-        const uint32_t off = (uint32_t)rows[r] * (uint32_t)K + (uint32_t)(k0 + 8 * c);
-        __builtin_amdgcn_global_load_lds(A + off, La + (2 * wave + i) * 64, 16, 0, 0);
-    }
+    for (int b = 0; b < 4; ++b) v[b] = (__bf16)(dl * (float)((u0 >> (8 * b)) & 0xffu) - ml);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) v[4 + b] = (__bf16)(dl * (float)((u1 >> (8 * b)) & 0xffu) - ml);
+    return *(const bf16x8*)v;
 }
 
-__global__ void __launch_bounds__(256) k_moe_gemm_bf16(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Wsh,
-                                                       size_t ebytes, const qmm_moe_tile* __restrict__ tiles,
-                                                       const int* __restrict__ counts, const int* __restrict__ rowtab,
-                                                       const uint16_t* __restrict__ A, float* __restrict__ D, int N, int K) {
-    extern __shared__ __align__(16) uint8_t smem_raw[];
-    __shared__ int rows[MBM];
-    const int ntl = counts[0] + counts[1];
-    const int tix = blockIdx.x;
-    if (tix >= ntl) return;
-    const qmm_moe_tile tl = tiles[tix];
-    const int n0 = blockIdx.y * MBN;
-    uint4* const As = (uint4*)smem_raw;                  // 2 stages of kAChunks
-    uint4* const Bs = As + 2 * kAChunks;                 // 2 stages of kBChunks
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (threadIdx.x < MBM) {
-        const int k = tl.k0 + min((int)threadIdx.x, tl.ncols - 1);
-        rows[threadIdx.x] = rowtab ? rowtab[k] : k;
-    }
-    __syncthreads();
-    const uint8_t* We = tl.expert >= 0 ? W + (size_t)tl.expert * ebytes : Wsh;
-    const int nk = K / MBK, lastk = (nk - 1) * MBK;
-    MoeWRaw wr;
-    wr.load(We, N, K, n0, 0);
-    dma_a_rows(A, rows, K, 0, As);
-    wr.store(Bs, 0);
-    wr.load(We, N, K, n0, min(MBK, lastk));
-    __builtin_amdgcn_s_waitcnt(0);
-    lds_barrier();
-    f32x16 acc[2][2];
+template <bool GU, int NRB>
+__device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile tl, int n0, uint4* As, uint4* Ws,
+                                              const int* rows) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, fr = lane & 31, h = lane >> 5, fx = (fr >> 1) & 7;
+    const int K = a.K, N = a.N, nk = K / XBK;
+    const size_t rowbytes = (size_t)(K >> 8) * 144;
+    const uint8_t* w0 = tl.expert >= 0 ? a.w0 + (size_t)tl.expert * a.ebytes : a.w0sh;
+    const uint8_t* w1 = GU ? (tl.expert >= 0 ? a.w1 + (size_t)tl.expert * a.ebytes : a.w1sh) : w0;
+    // A DMA: instruction q of wave w fills slots (w + 4q) * 64 + lane = row block q
+    uint32_t aoff[NRB];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int q = 0; q < NRB; ++q) {
+        const int r = 8 * (wave + 4 * q) + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+        aoff[q] = (uint32_t)rows[r] * (uint32_t)K + (uint32_t)(8 * c);
+    }
+    // weight DMA: instruction q (0..2) of wave w fills slots i * 64 + lane, i = 3w + q: part i / 4,
+    // weight row (i % 4) * 64 + lane of the workgroup's 256
+    const uint8_t* wsrc[3];
+    int wpart[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const int i = 3 * wave + q, col = ((i & 3) << 6) + lane;
+        wpart[q] = i >> 2;
+        const uint8_t* base = GU && col >= 128 ? w1 : w0;
+        const int n = min(n0 + (GU ? (col & 127) : col), N - 1);
+        wsrc[q] = base + (size_t)n * rowbytes;
+    }
+    auto issue = [&](int p, int st) {
+        uint4* la = As + st * kXA;
+        uint4* lw = Ws + st * kXW;
+        const uint32_t k0 = (uint32_t)(p * XBK);
+#pragma unroll
+        for (int q = 0; q < NRB; ++q) __builtin_amdgcn_global_load_lds(a.A + aoff[q] + k0, la + (wave + 4 * q) * 64, 16, 0, 0);
+        const int boff = (p >> 2) * 144, j = p & 3;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+            const int off = boff + (wpart[q] == 0 ? 0 : wpart[q] == 1 ? 16 + 32 * j : 32 + 32 * j);
+            __builtin_amdgcn_global_load_lds(wsrc[q] + off, lw + (3 * wave + q) * 64, 16, 0, 0);
+        }
+    };
+    auto dequant = [&](int p, int st, bf16x8 (&wb)[2][4]) {
+        const uint4* lw = Ws + st * kXW;
+        const int j = p & 3;
+#pragma unroll
+        for (int jn = 0; jn < 2; ++jn) {
+            const int c = GU ? jn * 128 + 32 * wave + fr : 64 * wave + 32 * jn + fr;
+            const uint4 hd = lw[c];
+            const uint2 q0 = *(const uint2*)((const uint8_t*)(lw + 256 + c) + 8 * h);
+            const uint2 q1 = *(const uint2*)((const uint8_t*)(lw + 512 + c) + 8 * h);
+            const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+            const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
+            const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
+            const float dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
+            wb[jn][0] = q4_bf16x8(q0.x & 0x0f0f0f0fu, q0.y & 0x0f0f0f0fu, dA, mA);
+            wb[jn][1] = q4_bf16x8(q1.x & 0x0f0f0f0fu, q1.y & 0x0f0f0f0fu, dA, mA);
+            wb[jn][2] = q4_bf16x8((q0.x >> 4) & 0x0f0f0f0fu, (q0.y >> 4) & 0x0f0f0f0fu, dB, mB);
+            wb[jn][3] = q4_bf16x8((q1.x >> 4) & 0x0f0f0f0fu, (q1.y >> 4) & 0x0f0f0f0fu, dB, mB);
+        }
+    };
+    f32x16 acc[NRB][2];
+#pragma unroll
+    for (int i = 0; i < NRB; ++i)
 #pragma unroll
         for (int jn = 0; jn < 2; ++jn)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][jn][e] = 0.f;
-    const int fr = lane & 31, fc = lane >> 5, fx = (fr >> 1) & 7;
-    int foa[4], fob[4];
+    auto mfmas = [&](int st, const bf16x8 (&wb)[2][4]) {
+        const uint4* la = As + st * kXA;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        foa[ks] = fr * 8 + ((2 * ks + fc) ^ fx);
-        fob[ks] = (64 * wave + fr) * 8 + ((2 * ks + fc) ^ fx);
-    }
-    for (int s = 0; s < nk; ++s) {
-        // A tile s+1 -> the other A stage by DMA; MFMAs of tile s; W tile s+1 (registers) -> the
-        // other W stage; W tile s+2 -> registers
-        const uint4* La = As + (s & 1) * kAChunks;
-        const uint4* Lb = Bs + (s & 1) * kBChunks;
-        dma_a_rows(A, rows, K, min((s + 1) * MBK, lastk), As + ((s + 1) & 1) * kAChunks);
+        for (int s = 0; s < 4; ++s) {
+            bf16x8 af[NRB];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            bf16x8 af[2], bf[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) { const uint4 v = La[foa[ks] + 256 * t]; af[t] = *(const bf16x8*)&v; }
-#pragma unroll
-            for (int t = 0; t < 2; ++t) { const uint4 v = Lb[fob[ks] + 256 * t]; bf[t] = *(const bf16x8*)&v; }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int jn = 0; jn < 2; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
-        }
-        wr.store(Bs + ((s + 1) & 1) * kBChunks, min((s + 1) * MBK, lastk));
-        wr.load(We, N, K, n0, min((s + 2) * MBK, lastk));
-        __builtin_amdgcn_s_waitcnt(0x0F73);   // vmcnt <= 3: this step's A DMA has landed
-        lds_barrier();
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    // acc[i][jn][e] = D[k0 + 32i + 8*(e/4) + 4*(lane/32) + e%4][n0 + 64w + 32jn + lane%32]
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int r = 32 * i + 8 * (e >> 2) + 4 * fc + (e & 3);
-            if (r >= tl.ncols) continue;
-#pragma unroll
-            for (int jn = 0; jn < 2; ++jn) {
-                const int n = n0 + 64 * wave + 32 * jn + fr;
-                if (n < N) D[(size_t)(tl.k0 + r) * N + n] = acc[i][jn][e];
+            for (int i = 0; i < NRB; ++i) {
+                const uint4 v = la[(32 * i + fr) * 8 + ((2 * s + h) ^ fx)];
+                af[i] = *(const bf16x8*)&v;
             }
+#pragma unroll
+            for (int i = 0; i < NRB; ++i)
+#pragma unroll
+                for (int jn = 0; jn < 2; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], wb[jn][s], acc[i][jn], 0, 0, 0);
         }
+    };
+    constexpr int L = NRB + 3;        // loads per step per wave
+    // prologue (K % 256 == 0, so nk >= 4): steps 0..3 in flight, wait for 0 and 1
+    issue(0, 0);
+    issue(1, 1);
+    issue(2, 2);
+    issue(3, 3);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * L));
+    lds_barrier();
+    bf16x8 wa[2][4], wb[2][4];
+    dequant(0, 0, wa);
+    // step t: (t > 0) wait for step t+1's loads, barrier; issue step t+4 into the stage step t-1
+    // used; dequantise step t+1 while running step t's MFMAs
+    auto step = [&](int t, int st, int st1, int st4, const bf16x8 (&cur)[2][4], bf16x8 (&nxt)[2][4]) {
+        if (t > 0) {
+            const int rem = min(nk - 1, t + 3) - (t + 1);
+            if (rem >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * L));
+            else if (rem == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(L));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            lds_barrier();
+        }
+        if (t + 4 < nk) issue(t + 4, st4);
+        dequant(t + 1, st1, nxt);
+        mfmas(st, cur);
+    };
+    int st = 0;
+    for (int t = 0; t < nk - 2; t += 2) {     // nk is a multiple of 4
+        const int s1 = st == XST - 1 ? 0 : st + 1, s2 = s1 == XST - 1 ? 0 : s1 + 1;
+        const int s3 = s2 == XST - 1 ? 0 : s2 + 1, s4 = s3 == XST - 1 ? 0 : s3 + 1, s5 = s4 == XST - 1 ? 0 : s4 + 1;
+        step(t, st, s1, s4, wa, wb);
+        step(t + 1, s1, s2, s5, wb, wa);
+        st = s2;
     }
+    {   // steps nk-2 and nk-1
+        const int s1 = st == XST - 1 ? 0 : st + 1;
+        step(nk - 2, st, s1, 0, wa, wb);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        mfmas(s1, wb);
+    }
+    // acc[i][jn][e] = output row 32i + 8(e/4) + 4h + e%4 of the tile, column block jn, column fr
+    if constexpr (GU) {
+        uint16_t* H = (uint16_t*)a.D;
+        const int n = n0 + 32 * wave + fr;
+#pragma unroll
+        for (int i = 0; i < NRB; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int r = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (r >= tl.ncols || n >= N) continue;
+                const float g = acc[i][0][e], u = acc[i][1][e];
+                H[(size_t)(tl.k0 + r) * N + n] = (uint16_t)f2bf_bits(g / (1.f + expf(-g)) * u);
+            }
+    } else {
+        float* D = (float*)a.D;
+#pragma unroll
+        for (int i = 0; i < NRB; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int r = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (r >= tl.ncols) continue;
+#pragma unroll
+                for (int jn = 0; jn < 2; ++jn) {
+                    const int n = n0 + 64 * wave + 32 * jn + fr;
+                    if (n < N) D[(size_t)(tl.k0 + r) * N + n] = acc[i][jn][e];
+                }
+            }
+    }
+}
+
+// One workgroup per (tile, weight-row block).  Workgroup id i runs on XCD i % 8; XCD x takes tiles
+// x, x+8, x+16, ... with all their row blocks, so the blocks of one tile share its A rows in one L2.
+template <bool GU>
+__global__ void __launch_bounds__(256) k_moe_gemm_x(XArgs a) {
+    extern __shared__ __align__(16) uint8_t smem_raw[];
+    __shared__ int rows[XBM];
+    const int id = blockIdx.x, sid = id >> 3;
+    const int tix = 8 * (sid / a.nb) + (id & 7), nbi = sid % a.nb;
+    if (tix >= a.counts[0] + a.counts[1]) return;
+    qmm_moe_tile tl = a.tiles[tix];
+    tl.ncols = max(1, min(tl.ncols, XBM));
+    if (threadIdx.x < XBM) {
+        const int k = tl.k0 + min((int)threadIdx.x, tl.ncols - 1);
+        rows[threadIdx.x] = a.rowtab ? a.rowtab[k] : k;
+    }
+    __syncthreads();
+    uint4* const As = (uint4*)smem_raw;
+    uint4* const Ws = As + XST * kXA;
+    const int n0 = nbi * (GU ? XBW / 2 : XBW);
+    switch ((tl.ncols + 31) >> 5) {
+        case 1: moe_gemm_tile<GU, 1>(a, tl, n0, As, Ws, rows); break;
+        case 2: moe_gemm_tile<GU, 2>(a, tl, n0, As, Ws, rows); break;
+        case 3: moe_gemm_tile<GU, 3>(a, tl, n0, As, Ws, rows); break;
+        default: moe_gemm_tile<GU, 4>(a, tl, n0, As, Ws, rows); break;
+    }
+}
+
+int launch_moe_gemm_x(bool gu, const XArgs& a, int max_tiles, hipStream_t s) {
+    const int grid = 8 * ((max_tiles + 7) / 8) * a.nb;
+    if (gu) hipLaunchKernelGGL(k_moe_gemm_x<true>, dim3(grid), dim3(256), kXLds, s, a);
+    else hipLaunchKernelGGL(k_moe_gemm_x<false>, dim3(grid), dim3(256), kXLds, s, a);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -324,11 +420,21 @@ int qmm_moe_gemm_bf16(int fmt, int shared_fmt, const void* W, const void* Wsh, s
     if (!W || !Wsh || !tiles || !counts || !A || !D) return QMM_ERR_NULL;
     if (N <= 0 || K <= 0 || K % 256 != 0 || max_tiles < 0) return QMM_ERR_SHAPE;
     if (max_tiles == 0) return QMM_OK;
-    const dim3 grid(max_tiles, (N + MBN - 1) / MBN);
-    hipLaunchKernelGGL(k_moe_gemm_bf16, grid, dim3(256), kMoeGemmLds, (hipStream_t)stream, (const uint8_t*)W, (const uint8_t*)Wsh,
-                       ebytes, tiles, counts, rowtab, A, D, N, K);
-    QMM_LAUNCH_CHECK();
-    return QMM_OK;
+    XArgs a{(const uint8_t*)W, (const uint8_t*)Wsh, nullptr, nullptr, ebytes, tiles, counts, rowtab, A, D, N, K,
+            (N + XBW - 1) / XBW};
+    return launch_moe_gemm_x(false, a, max_tiles, (hipStream_t)stream);
+}
+
+int qmm_moe_gemm_gate_up_bf16(int fmt, int shared_fmt, const void* Wg, const void* Wgsh, const void* Wu, const void* Wush,
+                              size_t ebytes, const qmm_moe_tile* tiles, const int* counts, int max_tiles, const int* rowtab,
+                              const uint16_t* A, uint16_t* H, int N, int K, void* stream) {
+    if (fmt != QMM_Q4_K || shared_fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+    if (!Wg || !Wgsh || !Wu || !Wush || !tiles || !counts || !A || !H) return QMM_ERR_NULL;
+    if (N <= 0 || K <= 0 || K % 256 != 0 || max_tiles < 0) return QMM_ERR_SHAPE;
+    if (max_tiles == 0) return QMM_OK;
+    XArgs a{(const uint8_t*)Wg, (const uint8_t*)Wgsh, (const uint8_t*)Wu, (const uint8_t*)Wush, ebytes, tiles, counts,
+            rowtab, A, H, N, K, (N + XBW / 2 - 1) / (XBW / 2)};
+    return launch_moe_gemm_x(true, a, max_tiles, (hipStream_t)stream);
 }
 
 int qmm_moe_silu_bf16(const float* gate, const float* up, uint16_t* h, size_t n, void* stream) {

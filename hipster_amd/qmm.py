@@ -175,7 +175,7 @@ def bf16_to_f32_seg2(x, x2, Nt, off, N, out, M, stream=None):
 
 
 # ---- MoE prefill ----
-MOE_TILE_ROWS = 64     # rows per tile of qmm_moe_gemm_bf16
+MOE_TILE_ROWS = 128    # rows per tile of qmm_moe_gemm_bf16 / qmm_moe_gemm_gate_up_bf16 (at most 128)
 
 
 def moe_tiles_capacity(T, nslot, nexperts, maxc=MOE_TILE_ROWS):
@@ -192,6 +192,14 @@ def moe_gemm_bf16(fmt, shared_fmt, W, Wsh, ebytes, tiles, counts, max_tiles, row
     """Grouped expert GEMM over sorted rows, bf16 activations (moe_gemm, gemv.h:49-50)."""
     check(_lib.lib().qmm_moe_gemm_bf16(fmt, shared_fmt, _p(W), _p(Wsh), ebytes, _p(tiles), _p(counts), max_tiles,
                                        _p(rowtab), _p(A), _p(D), N, K, _stream(stream)), "moe_gemm_bf16")
+
+
+def moe_gemm_gate_up_bf16(fmt, shared_fmt, Wg, Wgsh, Wu, Wush, ebytes, tiles, counts, max_tiles, rowtab, A, H, N, K,
+                          stream=None):
+    """h = bf16(silu(A . Wg^T) * (A . Wu^T)) over the sorted rows, one launch (gate, up and silu)."""
+    check(_lib.lib().qmm_moe_gemm_gate_up_bf16(fmt, shared_fmt, _p(Wg), _p(Wgsh), _p(Wu), _p(Wush), ebytes, _p(tiles),
+                                               _p(counts), max_tiles, _p(rowtab), _p(A), _p(H), N, K, _stream(stream)),
+          "moe_gemm_gate_up_bf16")
 
 
 def moe_silu_bf16(gate, up, h, n, stream=None):

@@ -142,11 +142,18 @@ int qmm_moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* 
 /* Grouped expert GEMM over sorted rows (reference: moe_gemm, gemv.h:49-50, gemv.hip:909-969,1377-1381,
  * with bf16 activations and the bf16 MFMA path): for tile i < counts[0] + counts[1] (read on the device)
  * and r < ncols: D[k0 + r][n] = A[rowtab ? rowtab[k0 + r] : k0 + r] . W_e[n] (f32), W_e the Q4_K
- * expert matrix at W + expert * ebytes, or Wsh for expert -1.  Tiles of at most 64 rows; max_tiles
- * bounds the grid (the capacity of tiles). */
+ * expert matrix at W + expert * ebytes, or Wsh for expert -1.  Tiles of at most 128 rows (qmm_moe_sort
+ * with maxc <= 128); max_tiles bounds the grid (the capacity of tiles). */
 int qmm_moe_gemm_bf16(int fmt, int shared_fmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles,
                       const int* counts, int max_tiles, const int* rowtab, const uint16_t* A, float* D, int N, int K,
                       void* stream);
+/* The gate and up grouped GEMMs and the silu of the reference's prefill MoE (moe_gemm twice and
+ * fn::moe_silu_quant, engine/src/qwen4exp.cpp:646-648) in one launch: for the tiles as above,
+ * H[k0 + r][n] = bf16(silu(g) * u), g = A[row] . Wg_e[n], u = A[row] . Wu_e[n] (f32, each bitwise equal
+ * to qmm_moe_gemm_bf16's output; silu(x) = x / (1 + exp(-x)) as in qmm_moe_silu_bf16).  N = ffn rows. */
+int qmm_moe_gemm_gate_up_bf16(int fmt, int shared_fmt, const void* Wg, const void* Wgsh, const void* Wu, const void* Wush,
+                              size_t ebytes, const qmm_moe_tile* tiles, const int* counts, int max_tiles, const int* rowtab,
+                              const uint16_t* A, uint16_t* H, int N, int K, void* stream);
 /* h = bf16(silu(gate) * up), n elements (the bf16-path counterpart of fn::moe_silu_quant, fn.hip:206-211) */
 int qmm_moe_silu_bf16(const float* gate, const float* up, uint16_t* h, size_t n, void* stream);
 

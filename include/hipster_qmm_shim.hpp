@@ -121,6 +121,15 @@ inline void moe_gemm_bf16(WFmt f, WFmt fs, const void* W, const void* Wsh, size_
                                  max_tiles, rowtab, A, D, N, K, (void*)s),
                "moe_gemm_bf16");
 }
+// gate and up grouped GEMMs and silu in one launch: h = bf16(silu(A . Wg^T) * (A . Wu^T)), sorted rows
+inline void moe_gemm_gate_up_bf16(WFmt f, WFmt fs, const void* Wg, const void* Wgsh, const void* Wu, const void* Wush,
+                                  size_t ebytes, const MoeTile* tiles, const int* counts, int max_tiles, const int* rowtab,
+                                  const uint16_t* A, uint16_t* H, int N, int K, hipStream_t s) {
+    detail::ck(qmm_moe_gemm_gate_up_bf16((int)f, (int)fs, Wg, Wgsh, Wu, Wush, ebytes,
+                                         reinterpret_cast<const qmm_moe_tile*>(tiles), counts, max_tiles, rowtab, A, H, N, K,
+                                         (void*)s),
+               "moe_gemm_gate_up_bf16");
+}
 inline void moe_silu_bf16(const float* gate, const float* up, uint16_t* h, size_t n, hipStream_t s) {
     detail::ck(qmm_moe_silu_bf16(gate, up, h, n, (void*)s), "moe_silu_bf16");
 }

@@ -101,3 +101,27 @@ def test_moe_argument_validation_without_device_work():
     assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, ctypes.byref(segs), 2, d, 11, _xq(16), 512, 2048, 1, 1, None) == -6
     assert L.qmm_moe_silu_quant(d, d, _xq(16), 4, 100, None) == -2
     assert L.qmm_moe_combine_sorted(d, d, None, d, 4, 11, 2048, None) == -3
+
+
+def test_prefill_argument_validation_without_device_work():
+    L = _lib.lib()
+    d = ctypes.c_void_p(16)
+    q4, q6 = _lib.QMM_Q4_K, _lib.QMM_Q6_K
+    assert L.qmm_moe_sort(None, 4, 11, 512, 128, d, d, d, d, None) == -3
+    assert L.qmm_moe_sort(d, 4, 11, 4096, 128, d, d, d, d, None) == -2       # more experts than the sort holds
+    assert L.qmm_moe_sort(d, 4, 11, 512, 0, d, d, d, d, None) == -2
+    args = (d, d, 1024, d, d, 8, d, d, d)
+    assert L.qmm_moe_gemm_bf16(q6, q4, *args, 512, 2048, None) == -1
+    assert L.qmm_moe_gemm_bf16(q4, q4, None, d, 1024, d, d, 8, d, d, d, 512, 2048, None) == -3
+    assert L.qmm_moe_gemm_bf16(q4, q4, *args, 512, 2000, None) == -2
+    assert L.qmm_moe_gemm_bf16(q4, q4, d, d, 1024, d, d, 0, d, d, d, 512, 2048, None) == 0   # no tiles: nothing to do
+    gu = (d, d, d, d, 1024, d, d, 8, d, d, d)
+    assert L.qmm_moe_gemm_gate_up_bf16(q4, q6, *gu, 512, 2048, None) == -1
+    assert L.qmm_moe_gemm_gate_up_bf16(q4, q4, d, d, None, d, 1024, d, d, 8, d, d, d, 512, 2048, None) == -3
+    assert L.qmm_moe_gemm_gate_up_bf16(q4, q4, *gu, 0, 2048, None) == -2
+    assert L.qmm_gemm_wq(q6, d, d, d, 16, 16, 256, None) == -1
+    assert L.qmm_gemm_wq(q4, d, d, d, 16, 16, 300, None) == -2
+    assert L.qmm_gemm_wq(q4, d, None, d, 16, 16, 256, None) == -3
+    assert L.qmm_gemm_bf16(d, d, d, 16, 16, 100, None) == -2
+    assert L.qmm_dequant_bf16(q4, d, d, 16, 100, None) == -2
+    assert L.qmm_dequant_bf16(_lib.QMM_Q5_K, d, d, 16, 256, None) == -1

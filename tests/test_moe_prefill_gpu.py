@@ -59,13 +59,17 @@ def dequant_experts_f32(Wd, n_exp, N, K):
     return out.view(torch.bfloat16).float()
 
 
-@pytest.mark.parametrize("T,N,K,gather", [(96, F, H, True), (300, H, F, False), (64, 512, 768, True)])
-def test_moe_gemm_bf16_matches_torch(gpu, T, N, K, gather):
+@pytest.mark.parametrize("T,N,K,gather,maxc", [(96, F, H, True, 128), (300, H, F, False, 128), (64, 512, 768, True, 128),
+                                                (200, 384, 512, True, 64), (150, F, 1024, True, 16),
+                                                (120, 256, 512, False, 96)])
+def test_moe_gemm_bf16_matches_torch(gpu, T, N, K, gather, maxc):
+    """tiles of 128, 96, 64 and 16 rows (one to four 32-row MFMA blocks, ragged last tiles), weight
+    row counts that are not a multiple of the 256-row workgroup block"""
     n_exp = 32
     W_h = synth.experts(1410 + N, synth.Q4_K, n_exp, N, K)
     S_h = synth.matrix(1411 + N, synth.Q4_K, N, K)
     ids_h, _ = oracle.moe_route(synth.router_logits(1412 + T, T, n_exp, 1.1), n_exp, 10)
-    kpos, rowtok, tiles, counts, cap = sort_on_gpu(ids_h, n_exp)
+    kpos, rowtok, tiles, counts, cap = sort_on_gpu(ids_h, n_exp, maxc)
     NS = T * NE
     rows_a = T if gather else NS
     A = bf16_dev(synth.to_bf16_bits(synth.normal_f32(1413, (rows_a, K))))
@@ -84,13 +88,36 @@ def test_moe_gemm_bf16_matches_torch(gpu, T, N, K, gather):
         arow = Af[rt[k]] if gather else Af[k]
         ref[k] = torch.mv((Wf[e] if e >= 0 else Sf), arow)
     err = rel_l2(host(D), host(ref))
-    print(f"moe_gemm_bf16 T={T} N={N} K={K} rel-L2 {err:.2e}", flush=True)
+    print(f"moe_gemm_bf16 T={T} N={N} K={K} maxc={maxc} rel-L2 {err:.2e}", flush=True)
     assert err <= 2e-3
+
+
+@pytest.mark.parametrize("T,N,K,maxc", [(300, F, H, 128), (77, 384, 512, 32), (2048, F, H, 128)])
+def test_moe_gate_up_fused_equals_unfused(gpu, T, N, K, maxc):
+    """qmm_moe_gemm_gate_up_bf16 == moe_gemm_bf16(gate), moe_gemm_bf16(up), moe_silu_bf16, bit for bit"""
+    n_exp = 64
+    Wg_h, Wu_h = synth.experts(1440, synth.Q4_K, n_exp, N, K), synth.experts(1441, synth.Q4_K, n_exp, N, K)
+    Sg_h, Su_h = synth.matrix(1442, synth.Q4_K, N, K), synth.matrix(1443, synth.Q4_K, N, K)
+    ids_h, _ = oracle.moe_route(synth.router_logits(1444 + T, T, n_exp, 1.1), n_exp, 10)
+    kpos, rowtok, tiles, counts, cap = sort_on_gpu(ids_h, n_exp, maxc)
+    NS = T * NE
+    A = bf16_dev(synth.to_bf16_bits(synth.normal_f32(1445, (T, K))))
+    Wg, Wu, Sg, Su = (dev(a) for a in (Wg_h, Wu_h, Sg_h, Su_h))
+    g = torch.zeros((NS, N), device="cuda"); u = torch.zeros((NS, N), device="cuda")
+    qmm.moe_gemm_bf16(synth.Q4_K, synth.Q4_K, Wg, Sg, Wg_h[0].nbytes, tiles, counts, cap, rowtok, A, g, N, K)
+    qmm.moe_gemm_bf16(synth.Q4_K, synth.Q4_K, Wu, Su, Wu_h[0].nbytes, tiles, counts, cap, rowtok, A, u, N, K)
+    h_ref = torch.zeros((NS, N), dtype=torch.bfloat16, device="cuda")
+    qmm.moe_silu_bf16(g, u, h_ref, NS * N)
+    h = torch.full((NS, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    qmm.moe_gemm_gate_up_bf16(synth.Q4_K, synth.Q4_K, Wg, Sg, Wu, Su, Wg_h[0].nbytes, tiles, counts, cap, rowtok, A, h, N, K)
+    a, b = host(h.view(torch.int16)), host(h_ref.view(torch.int16))
+    print(f"gate/up fused T={T} N={N} K={K} maxc={maxc}: {int((a != b).sum())} differing of {a.size}", flush=True)
+    assert np.array_equal(a, b)
 
 
 def test_moe_prefill_config4_pipeline(gpu):
     """2048 tokens, hidden 2048, 512 Q4_K experts + shared, top-10 with the Zipf
-    bias.  Device pipeline: route -> sort -> gate, up -> silu -> down -> combine; 12 sampled tokens
+    bias.  Device pipeline: route -> sort -> gate/up/silu (one launch) -> down -> combine; 12 sampled tokens
     against the oracle's bf16 path (bf16 weights and activations, double accumulation)."""
     T, n_exp = 2048, 512
     Wg_h, Wu_h, Wd_h = (synth.experts(1420 + i, synth.Q4_K, n_exp, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
@@ -107,11 +134,8 @@ def test_moe_prefill_config4_pipeline(gpu):
     kpos = torch.zeros(NS, dtype=torch.int32, device="cuda"); rowtok = torch.zeros(NS, dtype=torch.int32, device="cuda")
     tiles = torch.zeros((cap, 3), dtype=torch.int32, device="cuda"); counts = torch.zeros(2, dtype=torch.int32, device="cuda")
     qmm.moe_sort(ids, T, NE, n_exp, qmm.MOE_TILE_ROWS, kpos, rowtok, tiles, counts)
-    g = torch.zeros((NS, F), device="cuda"); u = torch.zeros((NS, F), device="cuda")
-    qmm.moe_gemm_bf16(synth.Q4_K, synth.Q4_K, Wg, Sg, Wg_h[0].nbytes, tiles, counts, cap, rowtok, x, g, F, H)
-    qmm.moe_gemm_bf16(synth.Q4_K, synth.Q4_K, Wu, Su, Wu_h[0].nbytes, tiles, counts, cap, rowtok, x, u, F, H)
     h = torch.zeros((NS, F), dtype=torch.bfloat16, device="cuda")
-    qmm.moe_silu_bf16(g, u, h, NS * F)
+    qmm.moe_gemm_gate_up_bf16(synth.Q4_K, synth.Q4_K, Wg, Sg, Wu, Su, Wg_h[0].nbytes, tiles, counts, cap, rowtok, x, h, F, H)
     dn = torch.zeros((NS, H), device="cuda")
     qmm.moe_gemm_bf16(synth.Q4_K, synth.Q4_K, Wd, Sd, Wd_h[0].nbytes, tiles, counts, cap, None, h, dn, H, F)
     y = torch.zeros((T, H), device="cuda")
