@@ -226,8 +226,8 @@ def extra_cfg3(torch):
 
 
 def extra_cfg4(torch, tb):
-    """MoE prefill at 2048 tokens (route, device sort, grouped gate / up GEMMs,
-    silu -> bf16, grouped down GEMM, combine) with the Zipf-biased routing."""
+    """MoE prefill at 2048 tokens (route, device sort, grouped gate/up GEMM with the
+    silu -> bf16 epilogue, grouped down GEMM, combine) with the Zipf-biased routing."""
     import numpy as np
     from hipster_amd import qmm, synth
     H, F, NE, T = 2048, 512, 11, 2048
@@ -238,22 +238,22 @@ def extra_cfg4(torch, tb):
     ids = torch.zeros((T, NE), dtype=torch.int32, device="cuda"); w = torch.zeros((T, NE), device="cuda")
     kpos = torch.zeros(NS, dtype=torch.int32, device="cuda"); rowtok = torch.zeros(NS, dtype=torch.int32, device="cuda")
     tiles = torch.zeros((cap, 3), dtype=torch.int32, device="cuda"); counts = torch.zeros(2, dtype=torch.int32, device="cuda")
-    g = torch.zeros((NS, F), device="cuda"); u = torch.zeros((NS, F), device="cuda")
     h = torch.zeros((NS, F), dtype=torch.bfloat16, device="cuda")
     dn = torch.zeros((NS, H), device="cuda"); y = torch.zeros((T, H), device="cuda")
     ebg, ebd = tb["Wg"][0].numel(), tb["Wd"][0].numel()
     route = [lambda: qmm.moe_route(logits, ids, w, T),
              lambda: qmm.moe_sort(ids, T, NE, 512, qmm.MOE_TILE_ROWS, kpos, rowtok, tiles, counts)]
-    gemms = [lambda: qmm.moe_gemm_bf16(0, 0, tb["Wg"], tb["Sg"], ebg, tiles, counts, cap, rowtok, x, g, F, H),
-             lambda: qmm.moe_gemm_bf16(0, 0, tb["Wu"], tb["Su"], ebg, tiles, counts, cap, rowtok, x, u, F, H),
-             lambda: qmm.moe_silu_bf16(g, u, h, NS * F),
+    gemms = [lambda: qmm.moe_gemm_gate_up_bf16(0, 0, tb["Wg"], tb["Sg"], tb["Wu"], tb["Su"], ebg, tiles, counts, cap, rowtok,
+                                               x, h, F, H),
              lambda: qmm.moe_gemm_bf16(0, 0, tb["Wd"], tb["Sd"], ebd, tiles, counts, cap, None, h, dn, H, F)]
     comb = [lambda: qmm.moe_combine_sorted(dn, w, kpos, y, T, NE, H)]
     us_all = graph_us(torch, route + gemms + comb, reps=3)
-    us_g = graph_us(torch, [gemms[0], gemms[1], gemms[3]], reps=3)
+    us_g = graph_us(torch, gemms, reps=3)
+    us_gu = graph_us(torch, gemms[:1], reps=3)
     flop = 141733920768       # routed 2*20480*3*512*2048 + shared 2*2048*3*512*2048
     c = counts.cpu().numpy()
-    return {"pipeline_us": round(us_all, 1), "grouped_gemms_us": round(us_g, 1), "TFLOPS": round(flop / us_g / 1e6, 1),
+    return {"pipeline_us": round(us_all, 1), "grouped_gemms_us": round(us_g, 1), "gate_up_silu_us": round(us_gu, 1),
+            "down_us": round(us_g - us_gu, 1), "TFLOPS": round(flop / us_g / 1e6, 1),
             "pct_bf16_peak": round(100 * flop / us_g / 1e6 / 2500, 1), "tiles": [int(c[0]), int(c[1])],
             "distinct_experts_incl_shared": int(len(np.unique(ids.cpu().numpy())))}
 

@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(kRouteThreads) k_moe_route(const float* __rest
     for (int k = 1; k < kRouteWaves; ++k) mx = fmaxf(mx, red[k]);
     __syncthreads();
     // sum of exp (fixed tree order)
-    float e = (i0 < nexp ? expf(v0 - mx) : 0.f) + (i1 < nexp ? expf(v1 - mx) : 0.f);
+    float e = (i0 < nexp ? __expf(v0 - mx) : 0.f) + (i1 < nexp ? __expf(v1 - mx) : 0.f);
     e = wave_sum(e);
     if (lane == 0) red[wave] = e;
     __syncthreads();
@@ -105,7 +105,7 @@ __global__ void __launch_bounds__(kRouteThreads) k_moe_route(const float* __rest
             wave_argmax64(bv, bi);
             if (bi == j0) t0 = true;
             if (bi == j1) t1 = true;
-            const float p = expf(bv - mx) / sum;     // wave-uniform
+            const float p = __expf(bv - mx) / sum;     // wave-uniform
             wsum += p;                                // selection order
             if (lane == r) psel = p;
             if (lane == 0) idt[r] = bi;
@@ -113,14 +113,14 @@ __global__ void __launch_bounds__(kRouteThreads) k_moe_route(const float* __rest
         if (lane < topk) wt[lane] = psel / wsum;
         if (lane == 0) {
             idt[topk] = -1;
-            wt[topk] = 1.f / (1.f + expf(-l[nexp]));
+            wt[topk] = 1.f / (1.f + __expf(-l[nexp]));
         }
     }
 }
 
 // ------------------------------------------------------------------------------------------
 // h = silu(g) * u quantised per 32 (fn.hip:206-211): one 32-lane half-wave per sub-block.
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
 
 __device__ __forceinline__ void half_wave_quant32(float v, int8_t* __restrict__ q, float* __restrict__ d,
                                                   float* __restrict__ s, size_t sb, int l) {

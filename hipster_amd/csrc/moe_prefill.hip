@@ -189,75 +189,57 @@ struct XArgs {
     int N, K, nb;          // nb = weight-row blocks per tile
 };
 
-// 8 nibbles (one per byte of {u0, u1}) -> bf16 dl * q - ml, k order = byte order
+// 8 values (one per byte of {u0, u1}, already masked to one nibble) -> bf16 fma(dl, q, -ml), k order
+// = byte order
 __device__ __forceinline__ bf16x8 q4_bf16x8(uint32_t u0, uint32_t u1, float dl, float ml) {
     __bf16 v[8];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) v[b] = (__bf16)(dl * (float)((u0 >> (8 * b)) & 0xffu) - ml);
+    for (int b = 0; b < 4; ++b) v[b] = (__bf16)__builtin_fmaf(dl, (float)((u0 >> (8 * b)) & 0xffu), -ml);
 #pragma unroll
-    for (int b = 0; b < 4; ++b) v[4 + b] = (__bf16)(dl * (float)((u1 >> (8 * b)) & 0xffu) - ml);
+    for (int b = 0; b < 4; ++b) v[4 + b] = (__bf16)__builtin_fmaf(dl, (float)((u1 >> (8 * b)) & 0xffu), -ml);
     return *(const bf16x8*)v;
 }
 
 template <bool GU, int NRB>
 __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile tl, int n0, uint4* As, uint4* Ws,
                                               const int* rows) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, fr = lane & 31, h = lane >> 5, fx = (fr >> 1) & 7;
+    const int lane = threadIdx.x & 63, fr = lane & 31, h = lane >> 5, fx = (fr >> 1) & 7;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, N = a.N, nk = K / XBK;
-    const size_t rowbytes = (size_t)(K >> 8) * 144;
+    const uint32_t rowbytes = (uint32_t)(K >> 8) * 144u;
     const uint8_t* w0 = tl.expert >= 0 ? a.w0 + (size_t)tl.expert * a.ebytes : a.w0sh;
     const uint8_t* w1 = GU ? (tl.expert >= 0 ? a.w1 + (size_t)tl.expert * a.ebytes : a.w1sh) : w0;
-    // A DMA: instruction q of wave w fills slots (w + 4q) * 64 + lane = row block q
+    const uint32_t lA = lds_addr(As), lW = lds_addr(Ws);
+    // A DMA: instruction q of wave w fills slots (w + 4q) * 64 + lane = row block q; byte offsets
     uint32_t aoff[NRB];
 #pragma unroll
     for (int q = 0; q < NRB; ++q) {
         const int r = 8 * (wave + 4 * q) + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-        aoff[q] = (uint32_t)rows[r] * (uint32_t)K + (uint32_t)(8 * c);
+        aoff[q] = ((uint32_t)rows[r] * (uint32_t)K + (uint32_t)(8 * c)) * 2u;
     }
     // weight DMA: instruction q (0..2) of wave w fills slots i * 64 + lane, i = 3w + q: part i / 4,
     // weight row (i % 4) * 64 + lane of the workgroup's 256
-    const uint8_t* wsrc[3];
-    int wpart[3];
+    uint32_t woff[3];
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
         const int i = 3 * wave + q, col = ((i & 3) << 6) + lane;
-        wpart[q] = i >> 2;
-        const uint8_t* base = GU && col >= 128 ? w1 : w0;
-        const int n = min(n0 + (GU ? (col & 127) : col), N - 1);
-        wsrc[q] = base + (size_t)n * rowbytes;
+        woff[q] = (uint32_t)min(n0 + (GU ? (col & 127) : col), N - 1) * rowbytes;
     }
     auto issue = [&](int p, int st) {
-        uint4* la = As + st * kXA;
-        uint4* lw = Ws + st * kXW;
-        const uint32_t k0 = (uint32_t)(p * XBK);
+        const uint8_t* abase = (const uint8_t*)a.A + (size_t)p * (XBK * 2);
+        const uint32_t la = lA + (uint32_t)(st * kXA * 16), lw = lW + (uint32_t)(st * kXW * 16);
 #pragma unroll
-        for (int q = 0; q < NRB; ++q) __builtin_amdgcn_global_load_lds(a.A + aoff[q] + k0, la + (wave + 4 * q) * 64, 16, 0, 0);
+        for (int q = 0; q < NRB; ++q) dma16s(abase, aoff[q], la + (uint32_t)((wave + 4 * q) * 1024));
         const int boff = (p >> 2) * 144, j = p & 3;
 #pragma unroll
         for (int q = 0; q < 3; ++q) {
-            const int off = boff + (wpart[q] == 0 ? 0 : wpart[q] == 1 ? 16 + 32 * j : 32 + 32 * j);
-            __builtin_amdgcn_global_load_lds(wsrc[q] + off, lw + (3 * wave + q) * 64, 16, 0, 0);
+            const int i = 3 * wave + q, part = i >> 2;
+            const uint8_t* wb = (GU && (i & 3) >= 2 ? w1 : w0) + boff + (part == 0 ? 0 : part == 1 ? 16 + 32 * j : 32 + 32 * j);
+            dma16s(wb, woff[q], lw + (uint32_t)(i * 1024));
         }
     };
-    auto dequant = [&](int p, int st, bf16x8 (&wb)[2][4]) {
-        const uint4* lw = Ws + st * kXW;
-        const int j = p & 3;
-#pragma unroll
-        for (int jn = 0; jn < 2; ++jn) {
-            const int c = GU ? jn * 128 + 32 * wave + fr : 64 * wave + 32 * jn + fr;
-            const uint4 hd = lw[c];
-            const uint2 q0 = *(const uint2*)((const uint8_t*)(lw + 256 + c) + 8 * h);
-            const uint2 q1 = *(const uint2*)((const uint8_t*)(lw + 512 + c) + 8 * h);
-            const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-            const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
-            const float dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j), mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
-            const float dB = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1), mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
-            wb[jn][0] = q4_bf16x8(q0.x & 0x0f0f0f0fu, q0.y & 0x0f0f0f0fu, dA, mA);
-            wb[jn][1] = q4_bf16x8(q1.x & 0x0f0f0f0fu, q1.y & 0x0f0f0f0fu, dA, mA);
-            wb[jn][2] = q4_bf16x8((q0.x >> 4) & 0x0f0f0f0fu, (q0.y >> 4) & 0x0f0f0f0fu, dB, mB);
-            wb[jn][3] = q4_bf16x8((q1.x >> 4) & 0x0f0f0f0fu, (q1.y >> 4) & 0x0f0f0f0fu, dB, mB);
-        }
-    };
+    // lane's weight rows (column slots of the stage) for its two MFMA column blocks
+    const int c0 = GU ? 32 * wave + fr : 64 * wave + fr, c1 = GU ? 128 + 32 * wave + fr : 64 * wave + 32 + fr;
     f32x16 acc[NRB][2];
 #pragma unroll
     for (int i = 0; i < NRB; ++i)
@@ -265,21 +247,44 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
         for (int jn = 0; jn < 2; ++jn)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][jn][e] = 0.f;
-    auto mfmas = [&](int st, const bf16x8 (&wb)[2][4]) {
-        const uint4* la = As + st * kXA;
+    // A fragments of K slice s (16 wide) of the stage at la, row blocks 0..NRB-1
+    auto afrag = [&](const uint4* la, int s, bf16x8 (&af)[NRB]) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            bf16x8 af[NRB];
-#pragma unroll
-            for (int i = 0; i < NRB; ++i) {
-                const uint4 v = la[(32 * i + fr) * 8 + ((2 * s + h) ^ fx)];
-                af[i] = *(const bf16x8*)&v;
-            }
-#pragma unroll
-            for (int i = 0; i < NRB; ++i)
-#pragma unroll
-                for (int jn = 0; jn < 2; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], wb[jn][s], acc[i][jn], 0, 0, 0);
+        for (int i = 0; i < NRB; ++i) {
+            const uint4 v = la[(32 * i + fr) * 8 + ((2 * s + h) ^ fx)];
+            af[i] = *(const bf16x8*)&v;
         }
+    };
+    // raw weight bytes of one step for the lane's two weight rows, and their decode
+    struct Raw { uint4 hd[2]; uint2 q0[2], q1[2]; };
+    auto rawread = [&](int st, Raw& r) {
+        const uint4* lw = Ws + st * kXW;
+#pragma unroll
+        for (int jn = 0; jn < 2; ++jn) {
+            const int c = jn ? c1 : c0;
+            r.hd[jn] = lw[c];
+            r.q0[jn] = *(const uint2*)((const uint8_t*)(lw + 256 + c) + 8 * h);
+            r.q1[jn] = *(const uint2*)((const uint8_t*)(lw + 512 + c) + 8 * h);
+        }
+    };
+    struct Scl { float dA, mA, dB16, mB; };
+    auto decode = [&](const uint4 hd, int j) {
+        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+        const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
+        Scl c;
+        c.dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j);
+        c.mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
+        // high nibbles stay in place (16 q): the exact factor 1/16 moves into the scale
+        c.dB16 = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1) * 0.0625f;
+        c.mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
+        return c;
+    };
+    // slice s of K (16 wide) of the step for one weight row: s 0, 1 = low nibbles of the two qs
+    // halves (sub-block 2j), s 2, 3 = their high nibbles (sub-block 2j+1)
+    auto deq = [&](const Raw& r, const Scl& c, int jn, int s) {
+        const uint2 q = (s & 1) ? r.q1[jn] : r.q0[jn];
+        const uint32_t m = s < 2 ? 0x0f0f0f0fu : 0xf0f0f0f0u;
+        return q4_bf16x8(opaque(q.x & m), opaque(q.y & m), s < 2 ? c.dA : c.dB16, s < 2 ? c.mA : c.mB);
     };
     constexpr int L = NRB + 3;        // loads per step per wave
     // prologue (K % 256 == 0, so nk >= 4): steps 0..3 in flight, wait for 0 and 1
@@ -289,10 +294,23 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
     issue(3, 3);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * L));
     lds_barrier();
-    bf16x8 wa[2][4], wb[2][4];
-    dequant(0, 0, wa);
-    // step t: (t > 0) wait for step t+1's loads, barrier; issue step t+4 into the stage step t-1
-    // used; dequantise step t+1 while running step t's MFMAs
+    bf16x8 wa[2][4], wb[2][4], af0[NRB];
+    {
+        Raw r;
+        rawread(0, r);
+#pragma unroll
+        for (int jn = 0; jn < 2; ++jn) {
+            const Scl c = decode(r.hd[jn], 0);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) wa[jn][s] = deq(r, c, jn, s);
+        }
+        afrag(As, 0, af0);
+    }
+    // Step t (t < nk-1): wait for step t+1's loads and barrier (t > 0); issue step t+4 into the
+    // stage step t-1 used; then 8 chunks (K slice s, column block jn), each the NRB MFMAs of step t
+    // for (s, jn) and the dequantisation of one bf16x8 of step t+1, fenced so that every MFMA has
+    // VALU work of its own wave to overlap with.  A fragments are read one slice ahead, slice 0 of
+    // step t+1 during step t.
     auto step = [&](int t, int st, int st1, int st4, const bf16x8 (&cur)[2][4], bf16x8 (&nxt)[2][4]) {
         if (t > 0) {
             const int rem = min(nk - 1, t + 3) - (t + 1);
@@ -302,8 +320,45 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
             lds_barrier();
         }
         if (t + 4 < nk) issue(t + 4, st4);
-        dequant(t + 1, st1, nxt);
-        mfmas(st, cur);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint4* la = As + st * kXA;
+        Raw r;
+        rawread(st1, r);
+        Scl c[2];
+        bf16x8 af[NRB], afn[NRB];
+#pragma unroll
+        for (int i = 0; i < NRB; ++i) af[i] = af0[i];
+        const int j = (t + 1) & 3;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+            for (int jn = 0; jn < 2; ++jn) {
+                if (jn == 0) afrag(s < 3 ? la : As + st1 * kXA, s < 3 ? s + 1 : 0, afn);
+                if (s == 0) c[jn] = decode(r.hd[jn], j);
+                nxt[jn][s] = deq(r, c[jn], jn, s);
+                asm volatile("" : : "v"(nxt[jn][s]));   // keeps the dequantisation inside this chunk
+#pragma unroll
+                for (int i = 0; i < NRB; ++i) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], cur[jn][s], acc[i][jn], 0, 0, 0);
+                if (s == 0) {
+#pragma unroll
+                    for (int k = 0; k < NRB; ++k) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 40 / NRB + 1, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < NRB; ++k) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 22 / NRB + 1, 0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int i = 0; i < NRB; ++i) af[i] = afn[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NRB; ++i) af0[i] = af[i];
     };
     int st = 0;
     for (int t = 0; t < nk - 2; t += 2) {     // nk is a multiple of 4
@@ -316,8 +371,21 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
     {   // steps nk-2 and nk-1
         const int s1 = st == XST - 1 ? 0 : st + 1;
         step(nk - 2, st, s1, 0, wa, wb);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        mfmas(s1, wb);
+        const uint4* la = As + s1 * kXA;
+        bf16x8 af[NRB];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s == 0) {
+#pragma unroll
+                for (int i = 0; i < NRB; ++i) af[i] = af0[i];
+            } else {
+                afrag(la, s, af);
+            }
+#pragma unroll
+            for (int i = 0; i < NRB; ++i)
+#pragma unroll
+                for (int jn = 0; jn < 2; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], wb[jn][s], acc[i][jn], 0, 0, 0);
+        }
     }
     // acc[i][jn][e] = output row 32i + 8(e/4) + 4h + e%4 of the tile, column block jn, column fr
     if constexpr (GU) {
@@ -330,7 +398,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
                 const int r = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
                 if (r >= tl.ncols || n >= N) continue;
                 const float g = acc[i][0][e], u = acc[i][1][e];
-                H[(size_t)(tl.k0 + r) * N + n] = (uint16_t)f2bf_bits(g / (1.f + expf(-g)) * u);
+                H[(size_t)(tl.k0 + r) * N + n] = (uint16_t)f2bf_bits(g / (1.f + __expf(-g)) * u);
             }
     } else {
         float* D = (float*)a.D;
@@ -385,13 +453,13 @@ int launch_moe_gemm_x(bool gu, const XArgs& a, int max_tiles, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------------------------------
-// h = bf16(silu(g) * u), RNE; silu(x) = x / (1 + exp(-x)) (fn.hip:8)
+// h = bf16(silu(g) * u), RNE; silu(x) = x / (1 + __expf(-x)) as the reference (fn.hip:8)
 __global__ void __launch_bounds__(256) k_moe_silu_bf16(const float* __restrict__ g, const float* __restrict__ u,
                                                        uint16_t* __restrict__ h, size_t n) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     const float x = g[i];
-    h[i] = (uint16_t)f2bf_bits(x / (1.f + expf(-x)) * u[i]);
+    h[i] = (uint16_t)f2bf_bits(x / (1.f + __expf(-x)) * u[i]);
 }
 
 }  // namespace

@@ -54,6 +54,33 @@ __device__ __forceinline__ uint32_t byte8(uint32_t lo, uint32_t hi, int i) {
 // Q6_K: 6-bit values (0..63, one per byte) -> signed q-32 per byte without carries between bytes.
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
+// LDS byte address of a pointer into __shared__ memory
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Global -> LDS DMA of 16 bytes per lane (global_load_lds_dwordx4): lane i writes lds + 16*i, lds
+// wave-uniform.  Issued as inline assembly on purpose: the compiler tracks the builtin form as an
+// LDS store and, unable to tell the stages of a ring apart, puts s_waitcnt vmcnt(0) before the next
+// LDS read, which waits for the DMA just issued for a later step and serialises the prefetch.  The
+// callers order DMA and LDS reads themselves (s_waitcnt vmcnt(n), then a barrier).  Loads the
+// compiler issues itself stay correct: a vmcnt it computes without counting these only waits longer.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+// The same with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset: per-step
+// address changes then cost scalar adds only.  base and lds must be wave-uniform.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
+}
+
+// A value the optimiser cannot see through (keeps a byte mask from being folded into the
+// byte-select of v_cvt_f32_ubyte{1,2,3}, which would turn each conversion into bfe + cvt)
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() is a release/acquire fence
 // at workgroup scope over all address spaces, which makes every wave wait for all of its
 // outstanding global loads (vmcnt(0)) before the barrier; a kernel that issued its weight loads
