@@ -152,28 +152,38 @@ __global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict
 // 128 sorted rows: D[k0 + r][n] = sum_k A[row(r)][k] * W_e[n][k] for r < ncols, row(r) =
 // rowtab[k0 + r] (or k0 + r), W_e the expert's Q4_K matrix (the shared matrix when expert < 0).
 //
-// 256 threads, 4 waves side by side along the weight rows: wave w owns two 32-wide MFMA column
-// blocks and all NRB = ceil(ncols / 32) row blocks of the tile, so every weight is dequantised
-// once per workgroup, by the wave that multiplies it, straight into MFMA operand registers.
+// 512 threads = 8 waves, two per SIMD, side by side along the weight rows: wave w owns one 32-wide
+// MFMA column block (256 weight rows per workgroup) and all NRB = ceil(ncols / 32) row blocks of
+// the tile, so every weight is dequantised once per workgroup, by the wave that multiplies it,
+// straight into MFMA operand registers; the two waves of a SIMD hide each other's waits.
 // v_mfma_f32_32x32x16_bf16 takes from lane l weight row l%32 and k = 8(l/32)..+7 of a 16-wide K
 // slice; for a 64-wide K step (one qs pair j of a block) these are the low nibbles of qs bytes
 // 8h..8h+7 (slice 0) and 16+8h..16+8h+7 (slice 1) and the high nibbles of the same bytes (slices
-// 2, 3), h = l/32.  A (gathered bf16 rows) and the raw weight bytes (16-byte block header and the two
-// 16-byte halves of the step's qs pair, per weight row) stream global -> LDS with
-// global_load_lds_dwordx4 through a ring of XST = 5 stages issued four steps ahead; the raw bytes of
-// step t+1 are dequantised while the MFMAs of step t run.  A stage: 128 rows x 8 chunks of 16 B,
-// chunk c of row r in slot r*8 + (c ^ ((r >> 1) & 7)) (conflict-free fragment reads); weight stage:
-// slots [part][256 rows], part 0 = header, 1 = qs bytes 32j..32j+15, 2 = qs bytes 32j+16..32j+31.
-// Gate/up mode: the 256 weight rows of a workgroup are 128 gate rows and the same 128 up rows; wave
-// w's column block 0 is gate rows n0+32w.., block 1 the same up rows, so a lane holds g and u of the
-// same output element and writes h = bf16(silu(g) * u) directly.
-constexpr int XBM = 128, XBW = 256, XBK = 64, XST = 5;
+// 2, 3), h = l/32.  A (gathered bf16 rows, DMA issued by waves 0-3) streams global -> LDS with
+// global_load_lds_dwordx4 through a ring of XST = 5 stages issued four steps ahead; the weight rows'
+// Q4_K blocks (144 contiguous bytes per row, so one DMA instruction covers about 7 rows: coalesced)
+// stream through a ring of two block stages, one block (4 K steps) ahead, DMA issued by waves 4-7.
+// The raw bytes of step t+1 are dequantised while the MFMAs of step t run.  A stage: 128 rows x 8
+// chunks of 16 B, chunk c of row r in slot r*8 + (c ^ ((r >> 1) & 7)) (conflict-free fragment
+// reads); block stage: 256 rows x 144 B, row-major.
+// Gate/up mode: the 256 weight rows of a workgroup are 128 gate rows (waves 0-3) and the same 128
+// up rows (waves 4-7); the up waves hand their results over through LDS and the gate waves write
+// h = bf16(silu(g) * u).
+constexpr int XBM = 128, XBW = 256, XBK = 64, XST = 5, XTHREADS = 512;
 constexpr int kXA = XBM * XBK / 8;                          // 16-byte chunks per A stage (1024)
-constexpr int kXW = 3 * XBW;                                // chunks per weight stage (768)
-constexpr size_t kXLds = (size_t)XST * (kXA + kXW) * 16;    // 143,360 B
+constexpr int kXW = 9 * XBW;                                // chunks per weight block stage (2304)
+constexpr size_t kXLds = ((size_t)XST * kXA + 2 * (size_t)kXW) * 16;   // 155,648 B
 
 // s_waitcnt immediate for "vmcnt <= v" (expcnt, lgkmcnt unconstrained)
 constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >> 4) << 14); }
+
+// wait until at most `rem` steps of L loads each are outstanding (rem = 0, 1 or 2)
+template <int L>
+__device__ __forceinline__ void wait_steps(int rem) {
+    if (rem >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * L));
+    else if (rem == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(L));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+}
 
 struct XArgs {
     const uint8_t* w0;     // expert matrices (gate in gate/up mode), expert e at w0 + e * ebytes
@@ -204,49 +214,53 @@ template <bool GU, int NRB>
 __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile tl, int n0, uint4* As, uint4* Ws,
                                               const int* rows) {
     const int lane = threadIdx.x & 63, fr = lane & 31, h = lane >> 5, fx = (fr >> 1) & 7;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), team = wave >> 2, wq = wave & 3;
     const int K = a.K, N = a.N, nk = K / XBK;
     const uint32_t rowbytes = (uint32_t)(K >> 8) * 144u;
     const uint8_t* w0 = tl.expert >= 0 ? a.w0 + (size_t)tl.expert * a.ebytes : a.w0sh;
     const uint8_t* w1 = GU ? (tl.expert >= 0 ? a.w1 + (size_t)tl.expert * a.ebytes : a.w1sh) : w0;
     const uint32_t lA = lds_addr(As), lW = lds_addr(Ws);
-    // A DMA: instruction q of wave w fills slots (w + 4q) * 64 + lane = row block q; byte offsets
+    // A DMA (waves 0-3): instruction q of wave wq fills slots (wq + 4q) * 64 + lane = row block q
     uint32_t aoff[NRB];
 #pragma unroll
     for (int q = 0; q < NRB; ++q) {
-        const int r = 8 * (wave + 4 * q) + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+        const int r = 8 * (wq + 4 * q) + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
         aoff[q] = ((uint32_t)rows[r] * (uint32_t)K + (uint32_t)(8 * c)) * 2u;
     }
-    // weight DMA: instruction q (0..2) of wave w fills slots i * 64 + lane, i = 3w + q: part i / 4,
-    // weight row (i % 4) * 64 + lane of the workgroup's 256
-    uint32_t woff[3];
+    // weight DMA (waves 4-7), one Q4_K block (144 B) of each of the 256 weight rows per 4 K steps:
+    // instruction k = 9 wq + q (0..35) fills chunks 64k + lane = row (64k + lane) / 9, 16-byte part
+    // (64k + lane) % 9.  In gate/up mode instructions 0-17 are exactly the 128 gate rows.
+    uint32_t woff[9];
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-        const int i = 3 * wave + q, col = ((i & 3) << 6) + lane;
-        woff[q] = (uint32_t)min(n0 + (GU ? (col & 127) : col), N - 1) * rowbytes;
+    for (int q = 0; q < 9; ++q) {
+        const int k = 9 * wq + q, p = 64 * k + lane, row = p / 9, part = p - 9 * row;
+        woff[q] = (uint32_t)min(n0 + (GU ? (row & 127) : row), N - 1) * rowbytes + (uint32_t)(16 * part);
     }
-    auto issue = [&](int p, int st) {
-        const uint8_t* abase = (const uint8_t*)a.A + (size_t)p * (XBK * 2);
-        const uint32_t la = lA + (uint32_t)(st * kXA * 16), lw = lW + (uint32_t)(st * kXW * 16);
+    auto issue = [&](int p, int st) {       // A of step p (waves 0-3)
+        if (team == 0) {
+            const uint8_t* abase = (const uint8_t*)a.A + (size_t)p * (XBK * 2);
+            const uint32_t la = lA + (uint32_t)(st * kXA * 16);
 #pragma unroll
-        for (int q = 0; q < NRB; ++q) dma16s(abase, aoff[q], la + (uint32_t)((wave + 4 * q) * 1024));
-        const int boff = (p >> 2) * 144, j = p & 3;
-#pragma unroll
-        for (int q = 0; q < 3; ++q) {
-            const int i = 3 * wave + q, part = i >> 2;
-            const uint8_t* wb = (GU && (i & 3) >= 2 ? w1 : w0) + boff + (part == 0 ? 0 : part == 1 ? 16 + 32 * j : 32 + 32 * j);
-            dma16s(wb, woff[q], lw + (uint32_t)(i * 1024));
+            for (int q = 0; q < NRB; ++q) dma16s(abase, aoff[q], la + (uint32_t)((wq + 4 * q) * 1024));
         }
     };
-    // lane's weight rows (column slots of the stage) for its two MFMA column blocks
-    const int c0 = GU ? 32 * wave + fr : 64 * wave + fr, c1 = GU ? 128 + 32 * wave + fr : 64 * wave + 32 + fr;
-    f32x16 acc[NRB][2];
+    auto issue_w = [&](int b) {             // weight block b into block stage b & 1 (waves 4-7)
+        if (team == 1) {
+            const uint32_t lw = lW + (uint32_t)((b & 1) * kXW * 16);
+#pragma unroll
+            for (int q = 0; q < 9; ++q) {
+                const int k = 9 * wq + q;
+                dma16s((GU && k >= 18 ? w1 : w0) + b * 144, woff[q], lw + (uint32_t)(k * 1024));
+            }
+        }
+    };
+    // the lane's weight row (column slot of the stage) for its MFMA column block
+    const int c0 = GU ? 128 * team + 32 * wq + fr : 32 * wave + fr;
+    f32x16 acc[NRB];
 #pragma unroll
     for (int i = 0; i < NRB; ++i)
 #pragma unroll
-        for (int jn = 0; jn < 2; ++jn)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][jn][e] = 0.f;
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
     // A fragments of K slice s (16 wide) of the stage at la, row blocks 0..NRB-1
     auto afrag = [&](const uint4* la, int s, bf16x8 (&af)[NRB]) {
 #pragma unroll
@@ -255,17 +269,14 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
             af[i] = *(const bf16x8*)&v;
         }
     };
-    // raw weight bytes of one step for the lane's two weight rows, and their decode
-    struct Raw { uint4 hd[2]; uint2 q0[2], q1[2]; };
-    auto rawread = [&](int st, Raw& r) {
-        const uint4* lw = Ws + st * kXW;
-#pragma unroll
-        for (int jn = 0; jn < 2; ++jn) {
-            const int c = jn ? c1 : c0;
-            r.hd[jn] = lw[c];
-            r.q0[jn] = *(const uint2*)((const uint8_t*)(lw + 256 + c) + 8 * h);
-            r.q1[jn] = *(const uint2*)((const uint8_t*)(lw + 512 + c) + 8 * h);
-        }
+    // raw weight bytes of one step for the lane's weight row, and their decode
+    struct Raw { uint4 hd; uint2 q0, q1; };
+    auto rawread = [&](int p, Raw& r) {     // step p: block p / 4, qs pair p % 4
+        const uint8_t* rp = (const uint8_t*)(Ws + ((p >> 2) & 1) * kXW) + c0 * 144;
+        const int j = p & 3;
+        r.hd = *(const uint4*)rp;
+        r.q0 = *(const uint2*)(rp + 16 + 32 * j + 8 * h);
+        r.q1 = *(const uint2*)(rp + 32 + 32 * j + 8 * h);
     };
     struct Scl { float dA, mA, dB16, mB; };
     auto decode = [&](const uint4 hd, int j) {
@@ -279,81 +290,78 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
         c.mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
         return c;
     };
-    // slice s of K (16 wide) of the step for one weight row: s 0, 1 = low nibbles of the two qs
-    // halves (sub-block 2j), s 2, 3 = their high nibbles (sub-block 2j+1)
-    auto deq = [&](const Raw& r, const Scl& c, int jn, int s) {
-        const uint2 q = (s & 1) ? r.q1[jn] : r.q0[jn];
+    // K slice s (16 wide) of the step: s 0, 1 = low nibbles of the two qs halves (sub-block 2j),
+    // s 2, 3 = their high nibbles (sub-block 2j+1)
+    auto deq = [&](const Raw& r, const Scl& c, int s) {
+        const uint2 q = (s & 1) ? r.q1 : r.q0;
         const uint32_t m = s < 2 ? 0x0f0f0f0fu : 0xf0f0f0f0u;
         return q4_bf16x8(opaque(q.x & m), opaque(q.y & m), s < 2 ? c.dA : c.dB16, s < 2 ? c.mA : c.mB);
     };
-    constexpr int L = NRB + 3;        // loads per step per wave
-    // prologue (K % 256 == 0, so nk >= 4): steps 0..3 in flight, wait for 0 and 1
+    // before dequantising step p (waves 4-7 hold at most one block in flight: the next one is
+    // issued at the first step of the current block, after this wait)
+    auto wait_rem = [&](int rem, int p) {
+        if (team == 0) wait_steps<NRB>(rem);
+        else if ((p & 3) == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    };
+    // prologue (K % 256 == 0, so nk >= 4): A steps 0..3 and weight block 0 in flight, wait for A
+    // steps 0, 1 and block 0
     issue(0, 0);
     issue(1, 1);
     issue(2, 2);
     issue(3, 3);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * L));
+    issue_w(0);
+    wait_rem(2, 0);
     lds_barrier();
-    bf16x8 wa[2][4], wb[2][4], af0[NRB];
+    bf16x8 wa[4], wb[4], af0[NRB];
     {
         Raw r;
         rawread(0, r);
+        const Scl c = decode(r.hd, 0);
 #pragma unroll
-        for (int jn = 0; jn < 2; ++jn) {
-            const Scl c = decode(r.hd[jn], 0);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) wa[jn][s] = deq(r, c, jn, s);
-        }
+        for (int s = 0; s < 4; ++s) wa[s] = deq(r, c, s);
         afrag(As, 0, af0);
     }
     // Step t (t < nk-1): wait for step t+1's loads and barrier (t > 0); issue step t+4 into the
-    // stage step t-1 used; then 8 chunks (K slice s, column block jn), each the NRB MFMAs of step t
-    // for (s, jn) and the dequantisation of one bf16x8 of step t+1, fenced so that every MFMA has
-    // VALU work of its own wave to overlap with.  A fragments are read one slice ahead, slice 0 of
-    // step t+1 during step t.
-    auto step = [&](int t, int st, int st1, int st4, const bf16x8 (&cur)[2][4], bf16x8 (&nxt)[2][4]) {
+    // stage step t-1 used; then 4 chunks (K slice s), each the NRB MFMAs of step t for slice s and
+    // the dequantisation of slice s of step t+1, fenced so that the MFMAs have VALU work of the same
+    // wave to overlap with.  A fragments are read one slice ahead, slice 0 of step t+1 during step t.
+    auto step = [&](int t, int st, int st1, int st4, const bf16x8 (&cur)[4], bf16x8 (&nxt)[4]) {
         if (t > 0) {
-            const int rem = min(nk - 1, t + 3) - (t + 1);
-            if (rem >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * L));
-            else if (rem == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(L));
-            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            wait_rem(min(nk - 1, t + 3) - (t + 1), t + 1);
             lds_barrier();
         }
         if (t + 4 < nk) issue(t + 4, st4);
+        if ((t & 3) == 0 && t + 4 < nk) issue_w((t >> 2) + 1);
         __builtin_amdgcn_sched_barrier(0);
         const uint4* la = As + st * kXA;
         Raw r;
-        rawread(st1, r);
-        Scl c[2];
+        rawread(t + 1, r);
+        Scl c;
         bf16x8 af[NRB], afn[NRB];
 #pragma unroll
         for (int i = 0; i < NRB; ++i) af[i] = af0[i];
-        const int j = (t + 1) & 3;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
+            afrag(s < 3 ? la : As + st1 * kXA, s < 3 ? s + 1 : 0, afn);
+            if (s == 0) c = decode(r.hd, (t + 1) & 3);
+            nxt[s] = deq(r, c, s);
+            asm volatile("" : : "v"(nxt[s]));   // keeps the dequantisation inside this chunk
 #pragma unroll
-            for (int jn = 0; jn < 2; ++jn) {
-                if (jn == 0) afrag(s < 3 ? la : As + st1 * kXA, s < 3 ? s + 1 : 0, afn);
-                if (s == 0) c[jn] = decode(r.hd[jn], j);
-                nxt[jn][s] = deq(r, c[jn], jn, s);
-                asm volatile("" : : "v"(nxt[jn][s]));   // keeps the dequantisation inside this chunk
+            for (int i = 0; i < NRB; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], cur[s], acc[i], 0, 0, 0);
+            if (s == 0) {
 #pragma unroll
-                for (int i = 0; i < NRB; ++i) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], cur[jn][s], acc[i][jn], 0, 0, 0);
-                if (s == 0) {
-#pragma unroll
-                    for (int k = 0; k < NRB; ++k) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x002, 40 / NRB + 1, 0);
-                    }
-                } else {
-#pragma unroll
-                    for (int k = 0; k < NRB; ++k) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x002, 22 / NRB + 1, 0);
-                    }
+                for (int k = 0; k < NRB; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 44 / NRB + 1, 0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
+            } else {
+#pragma unroll
+                for (int k = 0; k < NRB; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 24 / NRB + 1, 0);
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < NRB; ++i) af[i] = afn[i];
         }
@@ -382,37 +390,43 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
                 afrag(la, s, af);
             }
 #pragma unroll
-            for (int i = 0; i < NRB; ++i)
-#pragma unroll
-                for (int jn = 0; jn < 2; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], wb[jn][s], acc[i][jn], 0, 0, 0);
+            for (int i = 0; i < NRB; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], wb[s], acc[i], 0, 0, 0);
         }
     }
-    // acc[i][jn][e] = output row 32i + 8(e/4) + 4h + e%4 of the tile, column block jn, column fr
+    // acc[i][e] = output row 32i + 8(e/4) + 4h + e%4 of the tile, weight row n0 + (column block) + fr
     if constexpr (GU) {
-        uint16_t* H = (uint16_t*)a.D;
+        // up waves (4-7) hand their accumulators to the gate waves of the same SIMD through LDS
+        float* xch = (float*)As;                        // ring no longer needed: 4 x NRB x 16 x 64 floats
+        lds_barrier();
+        if (team == 1) {
+#pragma unroll
+            for (int i = 0; i < NRB; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) xch[((wq * NRB + i) * 16 + e) * 64 + lane] = acc[i][e];
+        }
+        lds_barrier();
+        if (team == 0) {
+            uint16_t* H = (uint16_t*)a.D;
+            const int n = n0 + 32 * wq + fr;
+#pragma unroll
+            for (int i = 0; i < NRB; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int r = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+                    if (r >= tl.ncols || n >= N) continue;
+                    const float g = acc[i][e], u = xch[((wq * NRB + i) * 16 + e) * 64 + lane];
+                    H[(size_t)(tl.k0 + r) * N + n] = (uint16_t)f2bf_bits(g / (1.f + __expf(-g)) * u);
+                }
+        }
+    } else {
+        float* D = (float*)a.D;
         const int n = n0 + 32 * wave + fr;
 #pragma unroll
         for (int i = 0; i < NRB; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int r = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (r >= tl.ncols || n >= N) continue;
-                const float g = acc[i][0][e], u = acc[i][1][e];
-                H[(size_t)(tl.k0 + r) * N + n] = (uint16_t)f2bf_bits(g / (1.f + __expf(-g)) * u);
-            }
-    } else {
-        float* D = (float*)a.D;
-#pragma unroll
-        for (int i = 0; i < NRB; ++i)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int r = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (r >= tl.ncols) continue;
-#pragma unroll
-                for (int jn = 0; jn < 2; ++jn) {
-                    const int n = n0 + 64 * wave + 32 * jn + fr;
-                    if (n < N) D[(size_t)(tl.k0 + r) * N + n] = acc[i][jn][e];
-                }
+                if (r < tl.ncols && n < N) D[(size_t)(tl.k0 + r) * N + n] = acc[i][e];
             }
     }
 }
@@ -420,7 +434,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
 // One workgroup per (tile, weight-row block).  Workgroup id i runs on XCD i % 8; XCD x takes tiles
 // x, x+8, x+16, ... with all their row blocks, so the blocks of one tile share its A rows in one L2.
 template <bool GU>
-__global__ void __launch_bounds__(256) k_moe_gemm_x(XArgs a) {
+__global__ void __launch_bounds__(XTHREADS) k_moe_gemm_x(XArgs a) {
     extern __shared__ __align__(16) uint8_t smem_raw[];
     __shared__ int rows[XBM];
     const int id = blockIdx.x, sid = id >> 3;
@@ -446,8 +460,8 @@ __global__ void __launch_bounds__(256) k_moe_gemm_x(XArgs a) {
 
 int launch_moe_gemm_x(bool gu, const XArgs& a, int max_tiles, hipStream_t s) {
     const int grid = 8 * ((max_tiles + 7) / 8) * a.nb;
-    if (gu) hipLaunchKernelGGL(k_moe_gemm_x<true>, dim3(grid), dim3(256), kXLds, s, a);
-    else hipLaunchKernelGGL(k_moe_gemm_x<false>, dim3(grid), dim3(256), kXLds, s, a);
+    if (gu) hipLaunchKernelGGL(k_moe_gemm_x<true>, dim3(grid), dim3(XTHREADS), kXLds, s, a);
+    else hipLaunchKernelGGL(k_moe_gemm_x<false>, dim3(grid), dim3(XTHREADS), kXLds, s, a);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }
