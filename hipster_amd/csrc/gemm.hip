@@ -20,6 +20,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 namespace qmm {
 namespace {
 
@@ -270,7 +272,39 @@ __global__ void __launch_bounds__(256) k_gemm(const uint16_t* __restrict__ A, co
 // W registers -> W stage (s+1)%2; W tile s+2 -> registers; wait; barrier.  The A tile thus has two
 // steps of MFMA time to land.
 constexpr int kChunks = GBM * GBK / 8;                         // 16-byte chunks per stage (2048)
-constexpr size_t kGemmDmaLds = (3 + 2) * (size_t)kChunks * 16;  // 163,840 B
+
+// The five stages are separate LDS variables and every access names its stage at compile time (the
+// K loop is unrolled by 6 = 3 A stages x 2 W stages).  The compiler then knows which stage each DMA
+// writes, so an LDS read waits only for DMA into its own stage, and its count of the W register
+// loads stays exact (with one LDS array it would wait for every DMA in flight before each read).
+__shared__ uint4 gA0[kChunks], gA1[kChunks], gA2[kChunks], gB0[kChunks], gB1[kChunks];
+template <int S>
+__device__ __forceinline__ uint4* ga() {
+    if constexpr (S == 0) return gA0;
+    else if constexpr (S == 1) return gA1;
+    else return gA2;
+}
+template <int S>
+__device__ __forceinline__ uint4* gb() {
+    if constexpr (S == 0) return gB0;
+    else return gB1;
+}
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+// Workgroup barrier for a kernel whose DMA into LDS is still in flight on purpose.  A workgroup
+// release fence on LDS would wait for every outstanding DMA (vmcnt(0)); here the release is at wave
+// scope (it only keeps the compiler from moving LDS accesses across it), this wave's own LDS stores
+// are retired with lgkmcnt(0), and the DMA a reader depends on has been waited for explicitly with
+// vmcnt(n) before the barrier.
+__device__ __forceinline__ void lds_barrier_dma() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_sched_barrier(0);
+}
 
 __device__ __forceinline__ int swz(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
 
@@ -333,9 +367,6 @@ struct WRawQ4KHalf {
 
 __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
                                                            float* __restrict__ D, int M, int N, int K) {
-    extern __shared__ __align__(16) uint8_t smem_raw[];
-    uint4* const As = (uint4*)smem_raw;                 // 3 stages
-    uint4* const Bs = As + 3 * kChunks;                 // 2 stages
     const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
     int tm, tn;
     tile_of(blockIdx.x, mt, nt, tm, tn);
@@ -344,9 +375,9 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __re
     const int nk = K / GBK, lastk = (nk - 1) * GBK;
     WRawQ4KHalf wr;
     wr.load(W, N, K, n0, 0);
-    dma_a_pp(A, M, K, m0, 0, As);
-    dma_a_pp(A, M, K, m0, min(GBK, lastk), As + kChunks);
-    wr.store(Bs, 0);
+    dma_a_pp(A, M, K, m0, 0, ga<0>());
+    dma_a_pp(A, M, K, m0, min(GBK, lastk), ga<1>());
+    wr.store(gb<0>(), 0);
     wr.load(W, N, K, n0, min(GBK, lastk));
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
@@ -364,12 +395,12 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __re
         foa[ks] = (128 * wm + fr) * 8 + ((2 * ks + fc) ^ fx);
         fob[ks] = (64 * wn + fr) * 8 + ((2 * ks + fc) ^ fx);
     }
-    int sa = 0;
-    for (int s = 0; s < nk; ++s) {
-        const int sa2 = sa >= 1 ? sa - 1 : 2;                         // (s + 2) % 3
-        const uint4* La = As + sa * kChunks;
-        const uint4* Lb = Bs + (s & 1) * kChunks;
-        dma_a_pp(A, M, K, m0, min((s + 2) * GBK, lastk), As + sa2 * kChunks);
+    // step s with A stage SA = s % 3 and W stage SB = s % 2
+    auto body = [&](auto sa_c, auto sb_c, int s) {
+        constexpr int SA = decltype(sa_c)::value, SB = decltype(sb_c)::value;
+        const uint4* La = ga<SA>();
+        const uint4* Lb = gb<SB>();
+        dma_a_pp(A, M, K, m0, min((s + 2) * GBK, lastk), ga<(SA + 2) % 3>());
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             bf16x8 af[4], bf[2];
@@ -382,13 +413,29 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __re
 #pragma unroll
                 for (int jn = 0; jn < 2; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
         }
-        wr.store(Bs + ((s + 1) & 1) * kChunks, min((s + 1) * GBK, lastk));
+        wr.store(gb<1 - SB>(), min((s + 1) * GBK, lastk));
         wr.load(W, N, K, n0, min((s + 2) * GBK, lastk));
         // A tile s+1 (DMA'd a step ago, before W tile s+1's loads) has landed once at most this
         // step's 4 DMAs and 3 W loads are outstanding
         __builtin_amdgcn_s_waitcnt(0x0F77);   // vmcnt <= 7
-        lds_barrier();
-        sa = sa == 2 ? 0 : sa + 1;
+        lds_barrier_dma();
+    };
+    int s = 0;
+    for (; s + 6 <= nk; s += 6) {
+        body(IC<0>(), IC<0>(), s);
+        body(IC<1>(), IC<1>(), s + 1);
+        body(IC<2>(), IC<0>(), s + 2);
+        body(IC<0>(), IC<1>(), s + 3);
+        body(IC<1>(), IC<0>(), s + 4);
+        body(IC<2>(), IC<1>(), s + 5);
+    }
+    if (s < nk) {                              // nk % 4 == 0, so 2 or 4 steps remain
+        body(IC<0>(), IC<0>(), s);
+        body(IC<1>(), IC<1>(), s + 1);
+        if (s + 2 < nk) {
+            body(IC<2>(), IC<0>(), s + 2);
+            body(IC<0>(), IC<1>(), s + 3);
+        }
     }
     __builtin_amdgcn_s_waitcnt(0);            // drain the clamped trailing DMAs
 #pragma unroll
@@ -408,7 +455,7 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __re
 
 int launch_gemm_q4k(const void* W, const uint16_t* A, float* D, int M, int N, int K, hipStream_t s) {
     const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-    hipLaunchKernelGGL(k_gemm_q4k_pp, dim3(grid), dim3(kPPThreads), kGemmDmaLds, s, A, (const uint8_t*)W, D, M, N, K);
+    hipLaunchKernelGGL(k_gemm_q4k_pp, dim3(grid), dim3(kPPThreads), 0, s, A, (const uint8_t*)W, D, M, N, K);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }
