@@ -29,92 +29,83 @@ namespace {
 constexpr int kMaxCols = 8;        // columns per pass of the gather GEMV
 
 // ------------------------------------------------------------------------------------------
-// Routing (fn.hip:157-205 semantics).  One 512-thread workgroup per token, up to 2 logits per
-// thread (nexp <= 1024).  Top-k is taken on the logits (softmax is monotone, so this is the top-k of
-// the probabilities without their rounding), ties to the lower expert id: each wave takes the top-k
-// of its values with wave argmax rounds, wave 0 merges the 8*k candidates.  Weights are
-// p_i / sum_{selected} p with p = exp(l - max) / sum_all exp(l - max); slot k is the shared
-// expert: id -1, weight sigmoid(logit[nexp]).
+// Routing (fn.hip:157-205 semantics).  One wave per token (4 tokens per workgroup), VPL logits per
+// lane (expert lane + 64 j).  Top-k is taken on the logits (softmax is monotone, so this is the
+// top-k of the probabilities without their rounding), ties to the lower expert id, by k rounds of
+// wave argmax over the lanes' best untaken values.  Weights are p_i / sum_{selected} p with
+// p = exp(l - max) / sum_all exp(l - max), the selected sum in selection order; slot k is the
+// shared expert: id -1, weight sigmoid(logit[nexp]).
 __device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
+// one DPP step of the (value, id) argmax: combine with the lane the DPP control names (lanes
+// without a source see (-inf, INT_MAX))
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
+    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), CTRL, ROWS, 0xf, false));
+    const int oi = __builtin_amdgcn_update_dpp(0x7fffffff, i, CTRL, ROWS, 0xf, false);
+    if (route_better(ov, oi, v, i)) { v = ov; i = oi; }
+}
+// argmax over the wave (larger value, then lower id), result in every lane: DPP row_shr 1/2/4/8
+// leaves each row's best in its lane 15, row_bcast15 / row_bcast31 carry them into lane 63
 __device__ __forceinline__ void wave_argmax64(float& v, int& i) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o, 64);
-        const int oi = __shfl_xor(i, o, 64);
-        if (route_better(ov, oi, v, i)) { v = ov; i = oi; }
-    }
+    argmax_dpp<0x111, 0xf>(v, i);
+    argmax_dpp<0x112, 0xf>(v, i);
+    argmax_dpp<0x114, 0xf>(v, i);
+    argmax_dpp<0x118, 0xf>(v, i);
+    argmax_dpp<0x142, 0xa>(v, i);
+    argmax_dpp<0x143, 0xc>(v, i);
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    i = __builtin_amdgcn_readlane(i, 63);
 }
 
-constexpr int kRouteThreads = 512, kRouteWaves = kRouteThreads / 64, kRouteMaxK = 16;
+constexpr int kRouteMaxK = 16, kRouteMaxExp = 1024;
 
-__global__ void __launch_bounds__(kRouteThreads) k_moe_route(const float* __restrict__ logits, int* __restrict__ ids,
-                                                            float* __restrict__ w, int nexp, int stride, int topk) {
-    __shared__ float red[kRouteWaves];
-    __shared__ float cv[kRouteWaves * kRouteMaxK];
-    __shared__ int ci[kRouteWaves * kRouteMaxK];
-    const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+template <int VPL>
+__global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ logits, int* __restrict__ ids,
+                                                   float* __restrict__ w, int T, int nexp, int stride, int topk) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;                                  // wave-uniform
     const float* l = logits + (size_t)t * stride;
-    const int i0 = tid, i1 = tid + kRouteThreads;
-    float v0 = i0 < nexp ? l[i0] : -INFINITY, v1 = i1 < nexp ? l[i1] : -INFINITY;
-    // max
-    float mx = fmaxf(v0, v1);
+    float v[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {                      // unconditional (clamped) loads: no wait per load
+        const float x = l[min(lane + 64 * j, nexp - 1)];
+        v[j] = lane + 64 * j < nexp ? x : -INFINITY;
+    }
+    float mx = v[0];
+#pragma unroll
+    for (int j = 1; j < VPL; ++j) mx = fmaxf(mx, v[j]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = red[0];
+    float e = 0.f;
 #pragma unroll
-    for (int k = 1; k < kRouteWaves; ++k) mx = fmaxf(mx, red[k]);
-    __syncthreads();
-    // sum of exp (fixed tree order)
-    float e = (i0 < nexp ? __expf(v0 - mx) : 0.f) + (i1 < nexp ? __expf(v1 - mx) : 0.f);
-    e = wave_sum(e);
-    if (lane == 0) red[wave] = e;
-    __syncthreads();
-    float sum = 0.f;
+    for (int j = 0; j < VPL; ++j)
+        if (lane + 64 * j < nexp) e += __expf(v[j] - mx);
+    const float sum = wave_sum(e);
+    uint32_t taken = 0;
 #pragma unroll
-    for (int k = 0; k < kRouteWaves; ++k) sum += red[k];
-    // per-wave top-k on the logits
-    bool u0 = i0 >= nexp, u1 = i1 >= nexp;
+    for (int j = 0; j < VPL; ++j)
+        if (lane + 64 * j >= nexp) taken |= 1u << j;
+    float psel = 0.f, wsum = 0.f;
+    int* idt = ids + (size_t)t * (topk + 1);
+    float* wt = w + (size_t)t * (topk + 1);
     for (int r = 0; r < topk; ++r) {
-        float bv = -INFINITY; int bi = 0x7fffffff;
-        if (!u0) { bv = v0; bi = i0; }
-        if (!u1 && route_better(v1, i1, bv, bi)) { bv = v1; bi = i1; }
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+            if (!((taken >> j) & 1u) && route_better(v[j], lane + 64 * j, bv, bi)) { bv = v[j]; bi = lane + 64 * j; }
         wave_argmax64(bv, bi);
-        if (lane == 0) { cv[wave * kRouteMaxK + r] = bv; ci[wave * kRouteMaxK + r] = bi; }
-        if (bi == i0) u0 = true;
-        if (bi == i1) u1 = true;
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        const float p = __expf(bv - mx) / sum;          // wave-uniform
+        wsum += p;                                       // selection order
+        if (lane == r) psel = p;
+        if (lane == 0) idt[r] = bi;
     }
-    __syncthreads();
-    if (wave == 0) {
-        // merge kRouteWaves * topk candidates, two per lane
-        const int nc = kRouteWaves * topk;
-        const int c0 = lane, c1 = lane + 64;
-        float m0 = -INFINITY, m1 = -INFINITY; int j0 = 0x7fffffff, j1 = 0x7fffffff;
-        if (c0 < nc) { m0 = cv[(c0 / topk) * kRouteMaxK + c0 % topk]; j0 = ci[(c0 / topk) * kRouteMaxK + c0 % topk]; }
-        if (c1 < nc) { m1 = cv[(c1 / topk) * kRouteMaxK + c1 % topk]; j1 = ci[(c1 / topk) * kRouteMaxK + c1 % topk]; }
-        bool t0 = c0 >= nc, t1 = c1 >= nc;
-        float psel = 0.f, wsum = 0.f;
-        int* idt = ids + (size_t)t * (topk + 1);
-        float* wt = w + (size_t)t * (topk + 1);
-        for (int r = 0; r < topk; ++r) {
-            float bv = -INFINITY; int bi = 0x7fffffff;
-            if (!t0) { bv = m0; bi = j0; }
-            if (!t1 && route_better(m1, j1, bv, bi)) { bv = m1; bi = j1; }
-            wave_argmax64(bv, bi);
-            if (bi == j0) t0 = true;
-            if (bi == j1) t1 = true;
-            const float p = __expf(bv - mx) / sum;     // wave-uniform
-            wsum += p;                                // selection order
-            if (lane == r) psel = p;
-            if (lane == 0) idt[r] = bi;
-        }
-        if (lane < topk) wt[lane] = psel / wsum;
-        if (lane == 0) {
-            idt[topk] = -1;
-            wt[topk] = 1.f / (1.f + __expf(-l[nexp]));
-        }
+    if (lane < topk) wt[lane] = psel / wsum;
+    if (lane == 0) {
+        idt[topk] = -1;
+        wt[topk] = 1.f / (1.f + __expf(-l[nexp]));
     }
 }
 
@@ -199,7 +190,8 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
         int n = 0, dup = 0;
         for (int base = 0; base < nslot; base += 64) {
             const int sl = base + tid;
-            const int sid = sl < nslot ? ids[sl] : 0x7fffffff;
+            const int sid0 = ids[min(sl, nslot - 1)];
+            const int sid = sl < nslot ? sid0 : 0x7fffffff;
             const bool m = sl < nslot && (sid == id || (sid < 0 && id < 0));
             const unsigned long long bal = __ballot(m);
             // slots before te that match -> duplicate
@@ -301,17 +293,33 @@ __global__ void __launch_bounds__(256) k_gemv_moe_down_q4k(qmm_moe_segs a, const
 
 // ------------------------------------------------------------------------------------------
 // prefill combine over expert-sorted rows (fn.hip:126-132): y[t][d] = sum_e w[t*nexp+e] * down[kpos[t*nexp+e]][d]
+// one workgroup per token; thread i sums float4 columns i, i+256, ... in slot order
 __global__ void __launch_bounds__(256) k_moe_combine_sorted(const float* __restrict__ down, const float* __restrict__ w,
                                                             const int* __restrict__ kpos, float* __restrict__ y, int nexp, int E) {
-    const int nbk = (E + 255) / 256;
-    const int t = blockIdx.x / nbk, d = (blockIdx.x % nbk) * 256 + threadIdx.x;
-    if (d >= E) return;
-    float acc = 0.f;
-    for (int e = 0; e < nexp; ++e) {
-        const int te = t * nexp + e;
-        acc += w[te] * down[(size_t)kpos[te] * E + d];
+    const int t = blockIdx.x;
+    const int* kp = kpos + (size_t)t * nexp;
+    const float* wt = w + (size_t)t * nexp;
+    if ((E & 3) == 0) {
+        const int E4 = E >> 2;
+        for (int d4 = threadIdx.x; d4 < E4; d4 += 256) {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int e = 0; e < nexp; ++e) {
+                const float we = wt[e];
+                const float4 v = ((const float4*)(down + (size_t)kp[e] * E))[d4];
+                acc.x += we * v.x;
+                acc.y += we * v.y;
+                acc.z += we * v.z;
+                acc.w += we * v.w;
+            }
+            ((float4*)(y + (size_t)t * E))[d4] = acc;
+        }
+    } else {
+        for (int d = threadIdx.x; d < E; d += 256) {
+            float acc = 0.f;
+            for (int e = 0; e < nexp; ++e) acc += wt[e] * down[(size_t)kp[e] * E + d];
+            y[(size_t)t * E + d] = acc;
+        }
     }
-    y[(size_t)t * E + d] = acc;
 }
 
 // lanes per row for the expert GEMVs: 8 when a row has at most 8 pairs (K <= 512), else 16
@@ -359,10 +367,15 @@ extern "C" {
 
 int qmm_moe_route_n(const float* logits, int* ids, float* w, int T, int nexp, int stride, int topk, void* stream) {
     if (!logits || !ids || !w) return QMM_ERR_NULL;
-    if (T < 0 || nexp < 1 || nexp > 2 * kRouteThreads || topk < 1 || topk > kRouteMaxK || topk > nexp || stride < nexp + 1)
+    if (T < 0 || nexp < 1 || nexp > kRouteMaxExp || topk < 1 || topk > kRouteMaxK || topk > nexp || stride < nexp + 1)
         return QMM_ERR_SHAPE;
     if (T == 0) return QMM_OK;
-    hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(kRouteThreads), 0, (hipStream_t)stream, logits, ids, w, nexp, stride, topk);
+    const dim3 grid((T + 3) / 4);
+    hipStream_t s = (hipStream_t)stream;
+    if (nexp <= 128) hipLaunchKernelGGL(k_moe_route<2>, grid, dim3(256), 0, s, logits, ids, w, T, nexp, stride, topk);
+    else if (nexp <= 256) hipLaunchKernelGGL(k_moe_route<4>, grid, dim3(256), 0, s, logits, ids, w, T, nexp, stride, topk);
+    else if (nexp <= 512) hipLaunchKernelGGL(k_moe_route<8>, grid, dim3(256), 0, s, logits, ids, w, T, nexp, stride, topk);
+    else hipLaunchKernelGGL(k_moe_route<16>, grid, dim3(256), 0, s, logits, ids, w, T, nexp, stride, topk);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }
@@ -404,8 +417,7 @@ int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, f
     if (!down || !w || !kpos || !y) return QMM_ERR_NULL;
     if (T < 0 || nexp < 1 || E <= 0) return QMM_ERR_SHAPE;
     if (T == 0) return QMM_OK;
-    const int nbk = (E + 255) / 256;
-    hipLaunchKernelGGL(k_moe_combine_sorted, dim3(T * nbk), dim3(256), 0, (hipStream_t)stream, down, w, kpos, y, nexp, E);
+    hipLaunchKernelGGL(k_moe_combine_sorted, dim3(T), dim3(256), 0, (hipStream_t)stream, down, w, kpos, y, nexp, E);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }

@@ -31,7 +31,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // Tiles: per key, ceil(count / maxc) tiles of consecutive sorted positions (the reference cuts a
 // tile at each expert change and every maxc positions, qwen4exp.cpp:636-641); routed-expert tiles
 // first in expert order, then the shared-expert tiles.  counts = {routed tiles, shared tiles}.
-constexpr int kSortThreads = 1024, kSortWaves = kSortThreads / 64, kMaxKeys = 1025;
+constexpr int kSortThreads = 1024, kSortWaves = kSortThreads / 64, kMaxKeys = 1025, kSortBatch = 16;
 
 // exclusive scan over the workgroup of one int per thread; *total gets the sum
 __device__ __forceinline__ int block_exscan(int v, int* wsum, int* total) {
@@ -60,8 +60,8 @@ __device__ __forceinline__ int block_exscan(int v, int* wsum, int* total) {
 }
 
 __global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict__ ids, int ns, int nslot, int nkeys, int maxc,
-                                                           int* __restrict__ kpos, int* __restrict__ rowtok,
-                                                           qmm_moe_tile* __restrict__ tiles, int* __restrict__ counts) {
+                                                           int* __restrict__ kpos, qmm_moe_tile* __restrict__ tiles,
+                                                           int* __restrict__ counts) {
     extern __shared__ int sm[];
     int* cnt = sm;                                   // [kSortWaves][nkeys]: per-wave counts, then running offsets
     int* tot = cnt + kSortWaves * nkeys;             // [nkeys]
@@ -72,8 +72,20 @@ __global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict
     const int per = ((ns + kSortWaves - 1) / kSortWaves + 63) & ~63;
     const int lo = min(ns, wave * per), hi = min(ns, lo + per);
     // pass 1: per-wave key counts (ids outside [-1, nkeys-2] are clamped into range by the host
-    // check; the kernel trusts them)
-    for (int i = lo + lane; i < hi; i += 64) atomicAdd(&cnt[wave * nkeys + ids[i] + 1], 1);
+    // check; the kernel trusts them).  The ids of a wave's range are loaded kSortBatch per lane at a
+    // time, so the loads overlap instead of each waiting behind the previous LDS atomic.
+    for (int c0 = lo; c0 < hi; c0 += 64 * kSortBatch) {
+        int kk[kSortBatch];
+#pragma unroll
+        for (int u = 0; u < kSortBatch; ++u) {      // unconditional (clamped) loads: no wait per load
+            const int i = c0 + 64 * u + lane;
+            const int v = ids[min(i, hi - 1)] + 1;
+            kk[u] = i < hi ? v : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kSortBatch; ++u)
+            if (kk[u] >= 0) atomicAdd(&cnt[wave * nkeys + kk[u]], 1);
+    }
     __syncthreads();
     // each thread owns a contiguous key range [k0, k1)
     const int kper = (nkeys + kSortThreads - 1) / kSortThreads;
@@ -98,26 +110,37 @@ __global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict
     __syncthreads();
     // pass 3: stable scatter, each wave over its own range in order
     const unsigned long long lt = (1ull << lane) - 1ull;
-    for (int c0 = lo; c0 < hi; c0 += 64) {
-        const int i = c0 + lane;
-        const bool valid = i < hi;
-        const int key = valid ? ids[i] + 1 : 0;
-        unsigned long long peers = __ballot(valid);
-        for (int b = 0; b < 11; ++b) {
-            const bool bit = (key >> b) & 1;
-            const unsigned long long m = __ballot(bit);
-            peers &= bit ? m : ~m;
+    for (int b0 = lo; b0 < hi; b0 += 64 * kSortBatch) {
+        int kk[kSortBatch];
+#pragma unroll
+        for (int u = 0; u < kSortBatch; ++u) {
+            const int i = b0 + 64 * u + lane;
+            const int v = ids[min(i, hi - 1)] + 1;
+            kk[u] = i < hi ? v : 0;
         }
-        const int rank = __popcll(peers & lt);
-        int pos = 0;
-        if (valid) pos = cnt[wave * nkeys + key] + rank;
-        __builtin_amdgcn_wave_barrier();
-        if (valid) {
-            kpos[i] = pos;
-            rowtok[pos] = i / nslot;
-            if (rank == 0) cnt[wave * nkeys + key] += __popcll(peers);
+#pragma unroll
+        for (int u = 0; u < kSortBatch; ++u) {
+            const int c0 = b0 + 64 * u;
+            if (c0 >= hi) break;
+            const int i = c0 + lane;
+            const bool valid = i < hi;
+            const int key = kk[u];
+            unsigned long long peers = __ballot(valid);
+            for (int b = 0; b < 11; ++b) {
+                const bool bit = (key >> b) & 1;
+                const unsigned long long m = __ballot(bit);
+                peers &= bit ? m : ~m;
+            }
+            const int rank = __popcll(peers & lt);
+            int pos = 0;
+            if (valid) pos = cnt[wave * nkeys + key] + rank;
+            __builtin_amdgcn_wave_barrier();
+            if (valid) {
+                kpos[i] = pos;
+                if (rank == 0) cnt[wave * nkeys + key] += __popcll(peers);
+            }
+            __builtin_amdgcn_wave_barrier();
         }
-        __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
     // tiles.  After pass 3 the running offset of the last wave for key k is the end of key k's run
@@ -145,6 +168,13 @@ __global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict
         counts[0] = nrouted;
         counts[1] = n;
     }
+}
+
+// rowtok[kpos[i]] = token of slot i: the inverse permutation, written by the whole grid (scattered
+// 4-byte stores issued from the one sorting workgroup would all queue on a single CU)
+__global__ void __launch_bounds__(256) k_moe_rowtok(const int* __restrict__ kpos, int* __restrict__ rowtok, int ns, int nslot) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < ns) rowtok[kpos[i]] = i / nslot;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -490,8 +520,13 @@ int qmm_moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* 
     const int nkeys = nexperts + 1;
     const size_t lds = (size_t)(kSortWaves + 1) * nkeys * 4;
     hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(kSortThreads), lds, (hipStream_t)stream, ids, T * nslot, nslot, nkeys, maxc, kpos,
-                       rowtok, tiles, counts);
+                       tiles, counts);
     QMM_LAUNCH_CHECK();
+    const int ns = T * nslot;
+    if (ns > 0) {
+        hipLaunchKernelGGL(k_moe_rowtok, dim3((ns + 255) / 256), dim3(256), 0, (hipStream_t)stream, kpos, rowtok, ns, nslot);
+        QMM_LAUNCH_CHECK();
+    }
     return QMM_OK;
 }
 
