@@ -47,6 +47,7 @@ SIGNATURES = {
     "qmm_quantize_x_q8": (c_int, [c_vp, XQ8, c_int, c_int, c_vp]),
     "qmm_gemv_q8": (c_int, [c_int, c_vp, XQ8, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
     "qmm_gemv_multi": (c_int, [ctypes.POINTER(GemvSeg), c_int, XQ8, c_int, c_vp]),
+    "qmm_gemv_q8_f32x": (c_int, [c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "qmm_gemv_q4_K_f32": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
     "qmm_moe_route": (c_int, [c_vp, c_vp, c_vp, c_int, c_vp]),
     "qmm_moe_route_n": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),

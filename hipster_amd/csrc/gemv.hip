@@ -149,6 +149,43 @@ __global__ void __launch_bounds__(kBlock) k_gemv_q4k_q8(const uint8_t* __restric
     }
 }
 
+// f32 x in, q8 arithmetic: the q8 quantisation of x fused into the staging of k_gemv_q4k_q8 (x
+// loaded ahead of the weights and quantised while they stream in), so quantize_x_q8 + gemv_q8 is
+// one launch with bit-identical results.  Rows of NITER pair iterations (K <= 1024 * NITER).
+template <int NCOL, int NITER>
+__global__ void __launch_bounds__(kBlock) k_gemv_q4k_fx(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                        float* __restrict__ y, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nb = K >> 8, ntask = 4 * nb;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = lane & 15, j = t & 3;
+    const int row = (blockIdx.x * kWavesPerBlock + wave) * 4 + (lane >> 4);
+    const uint8_t* rp = W + (size_t)min(row, N - 1) * ((size_t)nb * 144);
+    Q4kPairs<NITER> A;
+    {
+        XStageF<NCOL, (NCOL * NITER + 1) / 2> S;          // NCOL * K/8 <= 256 * NCOL * NITER / 2
+        stagef_load<NCOL>(x, K, S);                       // x first (older loads) ...
+        q4k_load_pairs<NITER>(rp, t, j, ntask, 0, A);     // ... then the weights
+        stagef_store<NCOL>(smem, K, S);                   // quantise while the weights stream in
+        lds_barrier();
+    }
+    XPairSrc<true> xsrc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) xsrc[c] = XPairSrc<true>{smem + (size_t)c * (K + (K >> 2)), nullptr, nullptr, K};
+    const Q4kPairDecode dc(j);
+    float acc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+    if ((nb & 3) == 0) q4k_pairs_compute<NCOL, NITER, true, true>(A, dc, t, ntask, 0, xsrc, acc);
+    else q4k_pairs_compute<NCOL, NITER, true, false>(A, dc, t, ntask, 0, xsrc, acc);
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = group_sum(acc[c], 16);
+    if (t == 0 && row < N) {
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // Q6_K x int8 GEMV, one superblock per lane, TPR lanes per row (TPR fixed per tensor shape).
 // F = QMM_Q6_K (GGUF 210-byte blocks, 2-byte aligned) or QMM_Q6_K_SOA (row streams).
@@ -385,6 +422,20 @@ int launch_q4k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t 
     }
 }
 
+template <int NCOL>
+int launch_q4k_fx(const void* W, const float* x, float* y, int N, int K, hipStream_t s) {
+    const size_t lds = (size_t)NCOL * (K + K / 4);
+    const int grid = (N + 4 * kWavesPerBlock - 1) / (4 * kWavesPerBlock);
+#define QMM_FX(IV) case IV: hipLaunchKernelGGL((k_gemv_q4k_fx<NCOL, IV>), dim3(grid), dim3(kBlock), lds, s, (const uint8_t*)W, x, y, N, K); break;
+    switch ((K / 256 * 4 + 15) / 16) {
+        QMM_FX(1) QMM_FX(2) QMM_FX(3) QMM_FX(4) QMM_FX(5) QMM_FX(6)
+        default: return QMM_ERR_SHAPE;
+    }
+#undef QMM_FX
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
 // lanes per row for the Q6_K kernel: a function of K only (never of ncol)
 inline int q6k_tpr(int K) { const int nb = K / 256; return nb >= 32 ? 8 : nb >= 8 ? 4 : nb >= 2 ? 2 : 1; }
 
@@ -418,6 +469,114 @@ int launch_gemv_q8_ncol(int fmt, const void* W, qmm_xq8 x, float* y, int N, int 
         case QMM_Q6_K_SOA: return launch_q6k_q8<QMM_Q6_K_SOA, NCOL>(W, x, y, N, K, s);
         default: return QMM_ERR_FORMAT;
     }
+}
+
+// ------------------------------------------------------------------------------------------
+// Q4_K x f32 GEMV on the pair mapping of k_gemv_q4k_q8 (16 lanes per row, a lane owns one 32-byte
+// qs pair = 64 weights per iteration, all of a row's loads in flight at once).  x is staged per
+// workgroup in LDS as f32, transposed at 16-byte granularity (float4 unit u of pair p at
+// (u * K/64 + p) * 16, so consecutive lanes read consecutive banks), followed by the 32-element
+// sums of x per sub-block (pair p: {xs(2p), xs(2p+1)} at 4K + 8p).  Per pair and column:
+// sA = sum x * qA, sB = sum x * qB (one cvt_f32_ubyte and one fma per weight; the high nibbles stay
+// in place as 16 q and the exact 1/16 moves into dB) and acc += dA sA + dB sB - (mA xsA + mB xsB),
+// the reference's arithmetic (gemv.hip:1177-1216) in another summation order.
+template <int NCOL, int U>
+__device__ __forceinline__ void stage_f32_pairs(uint8_t* lds, int K, const XStageF<NCOL, U>& S) {
+    const int k8 = K >> 3, n8 = NCOL * k8, kp = K >> 6;
+    const size_t cs = (size_t)K * 4 + (size_t)(K >> 3);      // bytes per column
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int e = (int)threadIdx.x + kPairBlock * u;      // floats 8e..8e+7 (quads share e < n8)
+        const float4 a = S.v[u][0], b = S.v[u][1];
+        float sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+        sum += __int_as_float(quad_xor<1>(__float_as_int(sum)));
+        sum += __int_as_float(quad_xor<2>(__float_as_int(sum)));
+        if (e < n8) {
+            const int c = e / k8, f8 = e - c * k8, g = 2 * f8;   // float4 units g, g+1 of the column
+            uint8_t* base = lds + (size_t)c * cs;
+            const int p = g >> 4, uu = g & 15;
+            *(float4*)(base + (size_t)(uu * kp + p) * 16) = a;
+            *(float4*)(base + (size_t)((uu + 1) * kp + p) * 16) = b;
+            if ((f8 & 3) == 0) *(float*)(base + (size_t)K * 4 + (size_t)(f8 >> 2) * 4) = sum;
+        }
+    }
+}
+
+template <int NCOL, int NITER>
+__global__ void __launch_bounds__(kBlock) k_gemv_q4k_f32p(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                          float* __restrict__ y, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nb = K >> 8, ntask = 4 * nb, kp = K >> 6;
+    const size_t cs = (size_t)K * 4 + (size_t)(K >> 3);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = lane & 15, j = t & 3;
+    const int row = (blockIdx.x * kWavesPerBlock + wave) * 4 + (lane >> 4);
+    const uint8_t* rp = W + (size_t)min(row, N - 1) * ((size_t)nb * 144);
+    Q4kPairs<NITER> A;
+    {
+        XStageF<NCOL, (NCOL * NITER + 1) / 2> S;
+        stagef_load<NCOL>(x, K, S);                       // x first (older loads) ...
+        q4k_load_pairs<NITER>(rp, t, j, ntask, 0, A);     // ... then the weights
+        stage_f32_pairs<NCOL>(smem, K, S);
+        lds_barrier();
+    }
+    const Q4kPairDecode dc(j);
+    float acc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NITER; ++i) {
+        const int task = t + 16 * i, tk = min(task, ntask - 1);
+        const uint4 hd = A.h[i], w0 = A.q0[i], w1 = A.q1[i];
+        const uint32_t scw = (((hd.y >> dc.sh0) & dc.m0) | (hd.w & dc.m2)) >> dc.bsh;
+        const uint32_t mw = (((hd.z >> dc.sh0) & dc.m0) | ((hd.w >> 4) & dc.m2)) >> dc.bsh;
+        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+        const float dA = d * (float)(scw & 0xffu), dB16 = d * (float)((scw >> 8) & 0xffu) * 0.0625f;
+        const float mA = dmin * (float)(mw & 0xffu), mB = dmin * (float)((mw >> 8) & 0xffu);
+        const uint32_t wq[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) {
+            const uint8_t* xc = smem + (size_t)c * cs;
+            float sa = 0.f, sb = 0.f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint32_t lo = opaque(wq[q] & 0x0f0f0f0fu), hi = opaque(wq[q] & 0xf0f0f0f0u);
+                const float4 xa = *(const float4*)(xc + (size_t)(q * kp + tk) * 16);
+                const float4 xb = *(const float4*)(xc + (size_t)((8 + q) * kp + tk) * 16);
+                sa = __builtin_fmaf(xa.x, (float)(lo & 0xffu), sa);
+                sa = __builtin_fmaf(xa.y, (float)((lo >> 8) & 0xffu), sa);
+                sa = __builtin_fmaf(xa.z, (float)((lo >> 16) & 0xffu), sa);
+                sa = __builtin_fmaf(xa.w, (float)(lo >> 24), sa);
+                sb = __builtin_fmaf(xb.x, (float)(hi & 0xffu), sb);
+                sb = __builtin_fmaf(xb.y, (float)((hi >> 8) & 0xffu), sb);
+                sb = __builtin_fmaf(xb.z, (float)((hi >> 16) & 0xffu), sb);
+                sb = __builtin_fmaf(xb.w, (float)(hi >> 24), sb);
+            }
+            const float2 xs = *(const float2*)(xc + (size_t)K * 4 + (size_t)tk * 8);
+            const float v = dA * sa + dB16 * sb - (mA * xs.x + mB * xs.y);
+            acc[c] += task < ntask ? v : 0.f;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = group_sum(acc[c], 16);
+    if (t == 0 && row < N) {
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+    }
+}
+
+template <int NCOL>
+int launch_q4k_f32p(const void* W, const float* x, float* y, int N, int K, hipStream_t s) {
+    const size_t lds = (size_t)NCOL * ((size_t)K * 4 + (size_t)(K >> 3));
+    const int grid = (N + 4 * kWavesPerBlock - 1) / (4 * kWavesPerBlock);
+#define QMM_FP(IV) case IV: hipLaunchKernelGGL((k_gemv_q4k_f32p<NCOL, IV>), dim3(grid), dim3(kBlock), lds, s, (const uint8_t*)W, x, y, N, K); break;
+    switch ((K / 256 * 4 + 15) / 16) {
+        QMM_FP(1) QMM_FP(2) QMM_FP(3) QMM_FP(4) QMM_FP(5) QMM_FP(6)
+        default: return QMM_ERR_SHAPE;
+    }
+#undef QMM_FP
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
 }
 
 template <int NCOL>
@@ -471,6 +630,20 @@ int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream
     return QMM_OK;
 }
 
+int qmm_gemv_q8_f32x(int fmt, const void* W, const float* x, float* y, int N, int K, int ncol, void* stream) {
+    if (fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+    if (!W || !x || !y) return QMM_ERR_NULL;
+    if (int e = check_gemv_shape(fmt, N, K)) return e;
+    if (ncol < 1 || ncol > 4 || K > 6144) return QMM_ERR_SHAPE;
+    hipStream_t s = (hipStream_t)stream;
+    switch (ncol) {
+        case 1: return launch_q4k_fx<1>(W, x, y, N, K, s);
+        case 2: return launch_q4k_fx<2>(W, x, y, N, K, s);
+        case 3: return launch_q4k_fx<3>(W, x, y, N, K, s);
+        default: return launch_q4k_fx<4>(W, x, y, N, K, s);
+    }
+}
+
 int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, int tpr, int rpt, void* stream) {
     if (!fmt_supported_q8(fmt)) return QMM_ERR_FORMAT;
     if (!W || !x.q || !x.d || !x.s || !y) return QMM_ERR_NULL;
@@ -508,6 +681,22 @@ int qmm_gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int
     if (ncol < 1 || ncol > 8) return QMM_ERR_SHAPE;
     if (!(tpr == 0 || tpr == 4 || tpr == 8 || tpr == 16 || tpr == 32)) return QMM_ERR_ARG;
     hipStream_t s = (hipStream_t)stream;
+    // pair kernel: columns in launches of at most g (what fits the LDS budget); every column gets
+    // the same arithmetic whatever ncol is
+    const size_t per_col = (size_t)K * 4 + (size_t)(K >> 3);
+    const int g = (int)min((size_t)3, kXLdsBudget / per_col);
+    if (K <= 6144 && g >= 1) {
+        for (int c0 = 0; c0 < ncol; c0 += g) {
+            const int nc = min(g, ncol - c0);
+            const float* xc = x + (size_t)c0 * K;
+            float* yc = y + (size_t)c0 * N;
+            const int e = nc == 1 ? launch_q4k_f32p<1>(W, xc, yc, N, K, s)
+                        : nc == 2 ? launch_q4k_f32p<2>(W, xc, yc, N, K, s)
+                                  : launch_q4k_f32p<3>(W, xc, yc, N, K, s);
+            if (e != QMM_OK) return e;
+        }
+        return QMM_OK;
+    }
     switch (ncol) {
         case 1: return launch_q4k_f32<1>(W, x, y, N, K, s);
         case 2: return launch_q4k_f32<2>(W, x, y, N, K, s);

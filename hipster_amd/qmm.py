@@ -101,6 +101,11 @@ def gemv_wmma(segs, x, ncol, mode=0, stream=None):
     gemv_multi(segs, x, ncol, stream)
 
 
+def gemv_q8_f32x(fmt, W, x, y, N, K, ncol, stream=None):
+    """quantize_x_q8 + gemv_q8 in one launch (f32 x in), bit for bit the same y."""
+    check(_lib.lib().qmm_gemv_q8_f32x(fmt, _p(W), _p(x), _p(y), N, K, ncol, _stream(stream)), "gemv_q8_f32x")
+
+
 def gemv_q4_K_f32(W, x, y, N, K, ncol, tpr=0, stream=None):
     """gemv.h:57: f32-activation Q4_K GEMV."""
     _dev(W, torch.uint8, "W"); _dev(x, torch.float32, "x"); _dev(y, torch.float32, "y")

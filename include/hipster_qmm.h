@@ -82,6 +82,11 @@ int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int n
  * segments, all with the same K, any ncol (8 columns per pass).  Results are bitwise those of
  * qmm_gemv_q8 on each segment. */
 int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void* stream);
+/* qmm_quantize_x_q8 followed by qmm_gemv_q8, in one launch and bit for bit the same y: x is f32
+ * [ncol][K], quantised to q8 per 32 inside the GEMV (no q8 buffer).  No reference counterpart (the
+ * reference quantises in the producing kernel, e.g. add_rmsnorm_quant, ops.hip:79-98).
+ * fmt Q4_K, ncol <= 4, K <= 6144, K % 256 == 0. */
+int qmm_gemv_q8_f32x(int fmt, const void* W, const float* x, float* y, int N, int K, int ncol, void* stream);
 /* f32-activation Q4_K GEMV: acc += (d*sc)*sum(x*q) - (dmin*m)*sum(x) per sub-block
  * (reference: gemv_q4_K_f32, gemv.h:57, gemv.hip:1177-1216,1486-1489); ncol 1..8. */
 int qmm_gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int ncol, int tpr, void* stream);

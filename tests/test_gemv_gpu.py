@@ -122,16 +122,38 @@ def test_gemv_multi_equals_separate_calls(gpu):
         assert torch.equal(y, y1)
 
 
-@pytest.mark.parametrize("N,K", [(17408, 5120), (999, 256), (4096, 2048)])
+@pytest.mark.parametrize("N,K", [(17408, 5120), (999, 256), (4096, 2048), (77, 768), (300, 17408)])
 def test_gemv_q4_K_f32_parity(gpu, N, K):
+    """f32 x (the 1e-5 semantics of gemv.hip:1177-1216) against the oracle; column 0 is bitwise the
+    same for every ncol (K = 17408 exercises the long-row kernel)"""
     W = synth.matrix(700 + N, synth.Q4_K, N, K)
     x = synth.normal_f32(701, (8, K))
     ref, mag = oracle.gemv_ref(synth.Q4_K, W, N, K, x)
     Wd = dev(W)
-    for ncol in (1, 2, 8):
+    col0 = None
+    for ncol in (1, 2, 3, 4, 8):
         y = torch.zeros((ncol, N), dtype=torch.float32, device="cuda")
         qmm.gemv_q4_K_f32(Wd, dev(x[:ncol]), y, N, K, ncol)
         yh = host(y)
         print(f"f32x N={N} K={K} ncol={ncol} relL2={rel_l2(yh, ref[:ncol]):.2e}", flush=True)
         assert rel_l2(yh, ref[:ncol]) <= TOL
         assert max_rel_mag(yh, ref[:ncol], mag[:ncol]) < TOL
+        if col0 is None:
+            col0 = yh[0].copy()
+        assert np.array_equal(yh[0].view(np.uint32), col0.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,K,ncol", [(17408, 5120, 1), (17408, 5120, 4), (1000, 256, 2), (77, 2048, 3), (333, 6144, 1),
+                                      (5, 768, 4)])
+def test_gemv_q8_f32x_equals_quantize_then_gemv(gpu, N, K, ncol):
+    """the fused f32-x entry (quantisation inside the GEMV) is bit for bit quantize_x_q8 + gemv_q8"""
+    W = synth.matrix(1300 + N, synth.Q4_K, N, K)
+    x = synth.normal_f32(1301 + K, (ncol, K))
+    x[0, :32] = 0.0                                 # amax = 0 block
+    x[-1, 64:96] *= 1e-30                           # tiny magnitudes
+    ref = run_q8(synth.Q4_K, W, N, K, x, ncol)
+    y = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+    qmm.gemv_q8_f32x(synth.Q4_K, dev(W), dev(x), y, N, K, ncol)
+    got = host(y)
+    print(f"gemv_q8_f32x N={N} K={K} ncol={ncol}: {int((got.view(np.uint32) != ref.view(np.uint32)).sum())} differing", flush=True)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
