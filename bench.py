@@ -129,10 +129,12 @@ def graph_us(torch, fns, reps=5):
 
 
 def extra_cfg1(torch):
-    """one dense decode layer (gate+up Q4_K 2x17408x5120, down Q6_K 5120x17408,
+    """one dense decode layer (gate+up Q4_K 2x17408x5120, down Q6_K 5120x17408 (SoA),
     QKV Q4_K 8192x5120, O Q4_K 5120x6144) at M = 1, 4, 8, weights rotated over >= 1 GiB."""
     from hipster_amd import qmm, synth
-    sh = dict(gate=(synth.Q4_K, 17408, 5120), up=(synth.Q4_K, 17408, 5120), down=(synth.Q6_K, 5120, 17408),
+    # the down projection in the engine's GEMV layout: Q6_K rows repacked to SoA at load time
+    # (engine/kernels/gemv.h:15, gemv.hip:1341-1350)
+    sh = dict(gate=(synth.Q4_K, 17408, 5120), up=(synth.Q4_K, 17408, 5120), down=(synth.Q6_K_SOA, 5120, 17408),
               qkv=(synth.Q4_K, 8192, 5120), o=(synth.Q4_K, 5120, 6144))
     host = {k: synth.matrix(synth.SEEDS["cfg1"] + i, *v) for i, (k, v) in enumerate(sh.items())}
     layer_bytes = sum(a.nbytes for a in host.values())
@@ -150,7 +152,7 @@ def extra_cfg1(torch):
                 W = copies[c]
                 qmm.gemv_multi([(synth.Q4_K, W["gate"], ys["gate"], 17408, 5120), (synth.Q4_K, W["up"], ys["up"], 17408, 5120)],
                                xs[5120], M)
-                qmm.gemv_q8(synth.Q6_K, W["down"], xs[17408], ys["down"], 5120, 17408, M)
+                qmm.gemv_q8(synth.Q6_K_SOA, W["down"], xs[17408], ys["down"], 5120, 17408, M)
                 qmm.gemv_q8(synth.Q4_K, W["qkv"], xs[5120], ys["qkv"], 8192, 5120, M)
                 qmm.gemv_q8(synth.Q4_K, W["o"], xs[6144], ys["o"], 5120, 6144, M)
             return f

@@ -18,6 +18,8 @@
 #include "qmm_common.hpp"
 
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <string.h>
 
 namespace qmm {
@@ -310,6 +312,191 @@ __global__ void __launch_bounds__(kBlock) k_gemv_q6k_q8(const uint8_t* __restric
 }
 
 // ------------------------------------------------------------------------------------------
+// Q6_K x int8 GEMV, "unit" mapping: one row per wave, a lane owns quarter blocks.  Quarter
+// (n, lh) of a block (engine/src/quant.h:65-80: for half n, l < 32, the four weights 128n + l +
+// {0, 32, 64, 96} come from ql[64n + l] (low / high nibble), ql[64n + 32 + l] and qh[32n + l] bits
+// {0-1, 2-3, 4-5, 6-7}) takes l = 16lh .. 16lh+15: 16 bytes of ql run A, 16 of ql run B, 16 of qh,
+// scales sc[8n + lh + {0, 2, 4, 6}] and d -- 64 weights, every byte of the block read once.  Unit
+// u = 4b + 2n + lh; lane l takes units l, l + 64, ... (all of them loaded before any compute).
+// x (q8) is staged per workgroup in LDS transposed for this order: the 16 x of group g of unit u
+// (x[256b + 128n + 32g + 16lh ..]) at (g * K/64 + u) * 16, and the four q8 scales the unit needs
+// (d of q8 blocks 8b + 4n + g) as a float4 at K + 16u.  Per group: isum = sum (q - 32) * xq over 16
+// (v_dot4), acc += (d * xd) * (float)(sc * isum).
+struct Q6Unit { uint4 a, b, h; uint32_t sc0, sc1; float d; };
+
+template <int F>
+__device__ __forceinline__ void q6k_load_unit(const uint8_t* __restrict__ rp, int nb, int u, Q6Unit& o) {
+    const int b = u >> 2, n = (u >> 1) & 1, lh = u & 1;
+    if constexpr (F == QMM_Q6_K_SOA) {
+        const uint8_t* ql = rp + (size_t)b * 128 + 64 * n + 16 * lh;
+        o.a = ld16_a4(ql);
+        o.b = ld16_a4(ql + 32);
+        o.h = ld16_a4(rp + (size_t)nb * 128 + (size_t)b * 64 + 32 * n + 16 * lh);
+        const u32x2_a4 sc = *(const u32x2_a4*)(rp + (size_t)nb * 192 + (size_t)b * 16 + 8 * n);
+        o.sc0 = sc.x; o.sc1 = sc.y;
+        o.d = h2f(*(const uint16_t*)(rp + (size_t)nb * 208 + 2 * b));
+    } else {
+        // 210-byte blocks start 0 or 2 bytes into a dword: dword-aligned loads, realigned by sh
+        const uintptr_t addr = (uintptr_t)(rp + (size_t)b * 210);
+        const uint32_t sh = (uint32_t)(addr & 3u);
+        const uint8_t* base = (const uint8_t*)(addr & ~(uintptr_t)3);
+        auto piece = [&](int off) {
+            const uint4 v = ld16_a4(base + off);
+            const uint32_t e = *(const uint32_t*)(base + off + 16);
+            return make_uint4(alignbyte(v.y, v.x, sh), alignbyte(v.z, v.y, sh), alignbyte(v.w, v.z, sh), alignbyte(e, v.w, sh));
+        };
+        o.a = piece(64 * n + 16 * lh);
+        o.b = piece(64 * n + 32 + 16 * lh);
+        o.h = piece(128 + 32 * n + 16 * lh);
+        const uint4 sc = ld16_a4(base + 192 + 8 * n);             // bytes 192+8n .. +15 (+sh)
+        o.sc0 = alignbyte(sc.y, sc.x, sh);
+        o.sc1 = alignbyte(sc.z, sc.y, sh);
+        // d = bytes 208..209: the top half of the dword at 208 when sh = 2, else the bottom of 208
+        const uint32_t dw = *(const uint32_t*)(base + 208);
+        o.d = h2f(sh ? dw >> 16 : dw);
+    }
+}
+
+// stage q8 x of nc columns in the unit-transposed layout (column c at c * 5K/4)
+__device__ __forceinline__ void stage_xq8_q6units(uint8_t* lds, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                  int K, int nc) {
+    const int U = K >> 6, nx = U * 4, nsb = K >> 5;
+    for (int v = threadIdx.x; v < nc * nx; v += blockDim.x) {
+        const int c = v / nx, r = v - c * nx, g = r / U, u = r - g * U;
+        const int b = u >> 2, n = (u >> 1) & 1, lh = u & 1;
+        *(uint4*)(lds + (size_t)c * (K + (K >> 2)) + (size_t)(g * U + u) * 16) =
+            ld16(xq + (size_t)c * K + (size_t)b * 256 + 128 * n + 32 * g + 16 * lh);
+    }
+    for (int v = threadIdx.x; v < nc * U; v += blockDim.x) {
+        const int c = v / U, u = v - c * U;
+        const int b = u >> 2, n = (u >> 1) & 1;
+        *(float4*)(lds + (size_t)c * (K + (K >> 2)) + (size_t)K + (size_t)u * 16) =
+            *(const float4*)(xd + (size_t)c * nsb + 8 * b + 4 * n);
+    }
+    __syncthreads();
+}
+
+// x-first staging of the first pass (nc <= 2 columns): the x units are loaded into registers before
+// the weight loads are issued and written to LDS after, so waiting for x does not wait for the
+// weights (vmcnt retires in issue order).  Unit v < nc*4U: 16 x bytes of (column, group g, unit u);
+// above: the q8 scale float4 of (column, unit).
+template <int UX>
+struct XQ6Stage { uint4 v[UX]; };
+
+template <int UX>
+__device__ __forceinline__ void q6x_load(const int8_t* __restrict__ xq, const float* __restrict__ xd, int K, int nc,
+                                         XQ6Stage<UX>& S) {
+    const int U = K >> 6, nx = 4 * U, nq = nc * nx, nt = nq + nc * U, nsb = K >> 5;
+#pragma unroll
+    for (int k = 0; k < UX; ++k) {
+        const int v = min((int)threadIdx.x + kBlock * k, nt - 1);
+        if (v < nq) {
+            const int c = v / nx, r = v - c * nx, g = r / U, u = r - g * U;
+            S.v[k] = ld16(xq + (size_t)c * K + (size_t)(u >> 2) * 256 + 128 * ((u >> 1) & 1) + 32 * g + 16 * (u & 1));
+        } else {
+            const int w = v - nq, c = w / U, u = w - c * U;
+            const float4 f = *(const float4*)(xd + (size_t)c * nsb + 8 * (u >> 2) + 4 * ((u >> 1) & 1));
+            S.v[k] = make_uint4(__float_as_uint(f.x), __float_as_uint(f.y), __float_as_uint(f.z), __float_as_uint(f.w));
+        }
+    }
+}
+template <int UX>
+__device__ __forceinline__ void q6x_store(uint8_t* lds, int K, int nc, const XQ6Stage<UX>& S) {
+    const int U = K >> 6, nx = 4 * U, nq = nc * nx, nt = nq + nc * U;
+#pragma unroll
+    for (int k = 0; k < UX; ++k) {
+        const int v = (int)threadIdx.x + kBlock * k;
+        if (v >= nt) continue;
+        size_t off;
+        if (v < nq) {
+            const int c = v / nx, r = v - c * nx, g = r / U, u = r - g * U;
+            off = (size_t)c * (K + (K >> 2)) + (size_t)(g * U + u) * 16;
+        } else {
+            const int w = v - nq, c = w / U, u = w - c * U;
+            off = (size_t)c * (K + (K >> 2)) + (size_t)K + (size_t)u * 16;
+        }
+        *(uint4*)(lds + off) = S.v[k];
+    }
+}
+
+// Columns are staged and computed in passes of cpp (what the LDS budget holds); the weights are
+// loaded once, and every column gets the same arithmetic whatever NCOL and cpp are.
+template <int F, int NCOL, int NIT>
+__global__ void __launch_bounds__(kBlock) k_gemv_q6k_u(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                       const float* __restrict__ xd, float* __restrict__ y, int N, int K, int cpp) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nb = K >> 8, U = K >> 6, nsb = K >> 5;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * kWavesPerBlock + wave;
+    const uint8_t* rp = W + (size_t)min(row, N - 1) * ((size_t)nb * 210);
+    Q6Unit P[NIT];
+    if constexpr (NCOL <= 2) {
+        // K <= 4096 NIT: (4U + U) * NCOL / 256 <= 1.25 NIT NCOL units per thread
+        XQ6Stage<(5 * NIT * NCOL + 3) / 4> S;
+        q6x_load(xq, xd, K, min(cpp, NCOL), S);              // x first (older loads) ...
+#pragma unroll
+        for (int i = 0; i < NIT; ++i) q6k_load_unit<F>(rp, nb, min(lane + 64 * i, U - 1), P[i]);   // ... then the weights
+        q6x_store(smem, K, min(cpp, NCOL), S);               // waits for x only
+        lds_barrier();
+    } else {
+        stage_xq8_q6units(smem, xq, xd, K, min(cpp, NCOL));
+#pragma unroll
+        for (int i = 0; i < NIT; ++i) q6k_load_unit<F>(rp, nb, min(lane + 64 * i, U - 1), P[i]);
+    }
+    float acc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+    for (int c0 = 0; c0 < NCOL; c0 += cpp) {
+        if (c0 > 0) {
+            __syncthreads();                                   // the previous pass's x reads are done
+            stage_xq8_q6units(smem, xq + (size_t)c0 * K, xd + (size_t)c0 * nsb, K, min(cpp, NCOL - c0));
+        }
+#pragma unroll
+        for (int i = 0; i < NIT; ++i) {
+            const int u = lane + 64 * i, uc = min(u, U - 1), lh = uc & 1;
+            const Q6Unit& q = P[i];
+            const uint32_t A[4] = {q.a.x, q.a.y, q.a.z, q.a.w}, B[4] = {q.b.x, q.b.y, q.b.z, q.b.w}, H[4] = {q.h.x, q.h.y, q.h.z, q.h.w};
+            // scales sc[lh + 2g], g = 0..3, of the unit's 8-byte scale run {sc0, sc1}: bytes lh, lh+2,
+            // lh+4, lh+6 gathered with one byte permute
+            const uint32_t scr = __builtin_amdgcn_perm(q.sc1, q.sc0, lh ? 0x07050301u : 0x06040200u);
+            uint32_t qw[4][4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                qw[0][w] = q6_signed((A[w] & 0x0f0f0f0fu) | ((H[w] << 4) & 0x30303030u));
+                qw[1][w] = q6_signed((B[w] & 0x0f0f0f0fu) | ((H[w] << 2) & 0x30303030u));
+                qw[2][w] = q6_signed(((A[w] >> 4) & 0x0f0f0f0fu) | (H[w] & 0x30303030u));
+                qw[3][w] = q6_signed(((B[w] >> 4) & 0x0f0f0f0fu) | ((H[w] >> 2) & 0x30303030u));
+            }
+#pragma unroll
+            for (int c = 0; c < NCOL; ++c) {
+                if (c < c0 || c >= c0 + cpp) continue;
+                const uint8_t* xc = smem + (size_t)(c - c0) * (K + (K >> 2));
+                const float4 xs4 = *(const float4*)(xc + (size_t)K + (size_t)uc * 16);
+                const float xsg[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+                float v = 0.f;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const uint4 xv = *(const uint4*)(xc + (size_t)(g * U + uc) * 16);
+                    int is = sdot4(qw[g][0], xv.x, 0);
+                    is = sdot4(qw[g][1], xv.y, is);
+                    is = sdot4(qw[g][2], xv.z, is);
+                    is = sdot4(qw[g][3], xv.w, is);
+                    const int scg = (int)(int8_t)((scr >> (8 * g)) & 0xffu);
+                    v = __builtin_fmaf(q.d * xsg[g], (float)(scg * is), v);
+                }
+                acc[c] += u < U ? v : 0.f;
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = wave_sum(acc[c]);
+    if (lane == 0 && row < N) {
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // Q4_K x f32 GEMV (gemv.hip:1177-1216 semantics): acc += dA*sum(x*qA) + dB*sum(x*qB) - the min
 // terms once per sub-block, with f32 x and per-sub-block sums of x staged in LDS when they fit.
 // Same chunk-coalesced weight stream as k_gemv_q4k_q8.
@@ -453,6 +640,20 @@ int launch_q6k_q8_t(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_
 }
 template <int F, int NCOL>
 int launch_q6k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    const size_t per_col = (size_t)K + K / 4;
+    const int g = (int)std::min<size_t>(NCOL, kXLdsBudget / per_col);
+    if (g >= 1 && K <= 64 * 64 * 6) {                       // unit kernel: at most 6 units per lane
+        const int grid = (N + kWavesPerBlock - 1) / kWavesPerBlock;
+        const size_t lds_u = (size_t)g * per_col;
+#define QMM_Q6U(IV) case IV: hipLaunchKernelGGL((k_gemv_q6k_u<F, NCOL, IV>), dim3(grid), dim3(kBlock), lds_u, s, (const uint8_t*)W, x.q, x.d, y, N, K, g); break;
+        switch ((K / 64 + 63) / 64) {
+            QMM_Q6U(1) QMM_Q6U(2) QMM_Q6U(3) QMM_Q6U(4) QMM_Q6U(5) QMM_Q6U(6)
+            default: return QMM_ERR_SHAPE;
+        }
+#undef QMM_Q6U
+        QMM_LAUNCH_CHECK();
+        return QMM_OK;
+    }
     switch (q6k_tpr(K)) {
         case 1: return launch_q6k_q8_t<F, NCOL, 1>(W, x, y, N, K, s);
         case 2: return launch_q6k_q8_t<F, NCOL, 2>(W, x, y, N, K, s);
