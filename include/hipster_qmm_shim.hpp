@@ -105,6 +105,11 @@ public:
 inline void gemm_wq(WFmt f, const void* W, const uint16_t* A, float* D, int M, int N, int K, hipStream_t s) {
     detail::ck(qmm_gemm_wq((int)f, W, A, D, M, N, K, (void*)s), "gemm_wq");
 }
+// quantize_x_q8 + gemv_q8 in one launch for Q4_K (x f32 [ncol][K], ncol <= 4, K <= 6144); the same y
+// bit for bit, one launch fewer per decode matvec
+inline void gemv_q8_f32x(WFmt f, const void* W, const float* x, float* y, int N, int K, int ncol, hipStream_t s) {
+    detail::ck(qmm_gemv_q8_f32x((int)f, W, x, y, N, K, ncol, (void*)s), "gemv_q8_f32x");
+}
 // device sort of the routed slots (replaces the host block of qwen4exp.cpp:628-645; no host sync)
 inline void moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* kpos, int* rowtok, MoeTile* tiles,
                      int* counts, hipStream_t s) {

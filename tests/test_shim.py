@@ -26,7 +26,10 @@ int main() {
     try {
         hip::moe_sort((const int*)16, 4, 11, 4096, 64, (int*)16, (int*)16, (hip::MoeTile*)16, (int*)16, nullptr);
     } catch (const std::runtime_error&) { ++caught; }
-    if (caught != 2) return 4;
+    try {   // ncol above the fused kernel's limit
+        hip::gemv_q8_f32x(hip::WFmt::Q4_K, (void*)16, (const float*)16, (float*)16, 16, 256, 5, nullptr);
+    } catch (const std::runtime_error&) { ++caught; }
+    if (caught != 3) return 4;
     try {
         hip::gemv_q8(hip::WFmt::Q5_K, (void*)16, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, (float*)16, 16, 256, 1, 0, 1, nullptr);
     } catch (const std::runtime_error& e) {
