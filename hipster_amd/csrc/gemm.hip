@@ -20,6 +20,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace qmm {
@@ -366,7 +367,7 @@ struct WRawQ4KHalf {
 };
 
 __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
-                                                           float* __restrict__ D, int M, int N, int K) {
+                                                           float* __restrict__ D, int M, int N, int K, int ldd) {
     const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
     int tm, tn;
     tile_of(blockIdx.x, mt, nt, tm, tn);
@@ -447,16 +448,31 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __re
 #pragma unroll
             for (int jn = 0; jn < 2; ++jn) {
                 const int n = n0 + 64 * wn + 32 * jn + fr;
-                if (n < N) D[(size_t)m * N + n] = acc[i][jn][e];
+                if (n < N) D[(size_t)m * ldd + n] = acc[i][jn][e];
             }
         }
     }
 }
 
+// One workgroup of k_gemm_q4k_pp fills a CU (160 KiB of LDS), so its tiles run in rounds of one per
+// CU.  When the last round would keep at most a quarter of the CUs busy for a whole tile time, the
+// 256 x 256 kernel takes only whole rounds (whole columns of M tiles) and the remaining columns go
+// to the grouped-GEMM kernel as (32 rows x 256 columns) work units, enough of them to spread over
+// every CU.  Every output element is one bf16 MFMA dot product over K in the same order either way.
 int launch_gemm_q4k(const void* W, const uint16_t* A, float* D, int M, int N, int K, hipStream_t s) {
-    const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-    hipLaunchKernelGGL(k_gemm_q4k_pp, dim3(grid), dim3(kPPThreads), 0, s, A, (const uint8_t*)W, D, M, N, K);
-    QMM_LAUNCH_CHECK();
+    const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN, cus = device_cu_count();
+    int nbig = nt;                                   // column tiles for the 256 x 256 kernel
+    const int total = mt * nt, rem = total % cus;
+    if (total > cus && rem != 0 && 4 * rem <= cus && mt <= cus) nbig = (total - rem) / mt;
+    const int nb_cols = std::min(N, nbig * GBN);
+    if (nbig > 0) {
+        hipLaunchKernelGGL(k_gemm_q4k_pp, dim3(mt * nbig), dim3(kPPThreads), 0, s, A, (const uint8_t*)W, D, M, nb_cols, K, N);
+        QMM_LAUNCH_CHECK();
+    }
+    if (nb_cols < N) {
+        const size_t rowbytes = (size_t)(K / 256) * 144;
+        return launch_q4k_rows_gemm((const uint8_t*)W + (size_t)nb_cols * rowbytes, A, D + nb_cols, M, N - nb_cols, K, N, 32, s);
+    }
     return QMM_OK;
 }
 

@@ -37,7 +37,7 @@ constexpr size_t kXLdsBudget = QMM_XLDS_BUDGET;   // bytes of LDS a workgroup ma
 #endif
 
 int g_cu_count = 0;
-int cu_count() {
+int device_cu_count() {
     if (g_cu_count == 0) {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
@@ -575,7 +575,7 @@ inline size_t xq8_lds_bytes(int ncol, int K) { return (size_t)ncol * K + 2 * (si
 // workgroups for the persistent row-range kernels: enough to give every CU several waves, never
 // more than one row per wave
 inline int persistent_grid(int N) {
-    const int want = cu_count() * 4;
+    const int want = device_cu_count() * 4;
     const int maxg = (N + kWavesPerBlock - 1) / kWavesPerBlock;
     return want < maxg ? want : maxg;
 }

@@ -225,8 +225,10 @@ struct XArgs {
     const int* counts;
     const int* rowtab;
     const uint16_t* A;
-    void* D;               // f32 [k][N], or bf16 h [k][N] in gate/up mode
+    void* D;               // f32 [k][ldd], or bf16 h [k][ldd] in gate/up mode
     int N, K, nb;          // nb = weight-row blocks per tile
+    int ldd;               // row stride of D (elements)
+    int trows, nimp, M;    // tiles == nullptr: implicit tiles of trows rows of expert 0, nimp of them, M rows
 };
 
 // 8 values (one per byte of {u0, u1}, already masked to one nibble) -> bf16 fma(dl, q, -ml), k order
@@ -445,7 +447,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
                     const int r = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
                     if (r >= tl.ncols || n >= N) continue;
                     const float g = acc[i][e], u = xch[((wq * NRB + i) * 16 + e) * 64 + lane];
-                    H[(size_t)(tl.k0 + r) * N + n] = (uint16_t)f2bf_bits(g / (1.f + __expf(-g)) * u);
+                    H[(size_t)(tl.k0 + r) * a.ldd + n] = (uint16_t)f2bf_bits(g / (1.f + __expf(-g)) * u);
                 }
         }
     } else {
@@ -456,7 +458,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int r = 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (r < tl.ncols && n < N) D[(size_t)(tl.k0 + r) * N + n] = acc[i][e];
+                if (r < tl.ncols && n < N) D[(size_t)(tl.k0 + r) * a.ldd + n] = acc[i][e];
             }
     }
 }
@@ -469,8 +471,10 @@ __global__ void __launch_bounds__(XTHREADS) k_moe_gemm_x(XArgs a) {
     __shared__ int rows[XBM];
     const int id = blockIdx.x, sid = id >> 3;
     const int tix = 8 * (sid / a.nb) + (id & 7), nbi = sid % a.nb;
-    if (tix >= a.counts[0] + a.counts[1]) return;
-    qmm_moe_tile tl = a.tiles[tix];
+    if (tix >= (a.tiles ? a.counts[0] + a.counts[1] : a.nimp)) return;
+    qmm_moe_tile tl;
+    if (a.tiles) tl = a.tiles[tix];
+    else tl = qmm_moe_tile{0, tix * a.trows, min(a.trows, a.M - tix * a.trows)};
     tl.ncols = max(1, min(tl.ncols, XBM));
     if (threadIdx.x < XBM) {
         const int k = tl.k0 + min((int)threadIdx.x, tl.ncols - 1);
@@ -495,6 +499,17 @@ int launch_moe_gemm_x(bool gu, const XArgs& a, int max_tiles, hipStream_t s) {
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }
+
+}  // namespace
+
+int launch_q4k_rows_gemm(const void* W, const uint16_t* A, float* D, int M, int N, int K, int ldd, int trows, hipStream_t s) {
+    const int nimp = (M + trows - 1) / trows;
+    XArgs a{(const uint8_t*)W, (const uint8_t*)W, nullptr, nullptr, 0, nullptr, nullptr, nullptr, A, D, N, K,
+            (N + XBW - 1) / XBW, ldd, trows, nimp, M};
+    return launch_moe_gemm_x(false, a, nimp, s);
+}
+
+namespace {
 
 // ------------------------------------------------------------------------------------------
 // h = bf16(silu(g) * u), RNE; silu(x) = x / (1 + __expf(-x)) as the reference (fn.hip:8)
@@ -538,7 +553,7 @@ int qmm_moe_gemm_bf16(int fmt, int shared_fmt, const void* W, const void* Wsh, s
     if (N <= 0 || K <= 0 || K % 256 != 0 || max_tiles < 0) return QMM_ERR_SHAPE;
     if (max_tiles == 0) return QMM_OK;
     XArgs a{(const uint8_t*)W, (const uint8_t*)Wsh, nullptr, nullptr, ebytes, tiles, counts, rowtab, A, D, N, K,
-            (N + XBW - 1) / XBW};
+            (N + XBW - 1) / XBW, N, 0, 0, 0};
     return launch_moe_gemm_x(false, a, max_tiles, (hipStream_t)stream);
 }
 
@@ -550,7 +565,7 @@ int qmm_moe_gemm_gate_up_bf16(int fmt, int shared_fmt, const void* Wg, const voi
     if (N <= 0 || K <= 0 || K % 256 != 0 || max_tiles < 0) return QMM_ERR_SHAPE;
     if (max_tiles == 0) return QMM_OK;
     XArgs a{(const uint8_t*)Wg, (const uint8_t*)Wgsh, (const uint8_t*)Wu, (const uint8_t*)Wush, ebytes, tiles, counts,
-            rowtab, A, H, N, K, (N + XBW / 2 - 1) / (XBW / 2)};
+            rowtab, A, H, N, K, (N + XBW / 2 - 1) / (XBW / 2), N, 0, 0, 0};
     return launch_moe_gemm_x(true, a, max_tiles, (hipStream_t)stream);
 }
 

@@ -114,6 +114,21 @@ __device__ __forceinline__ uint32_t f2bf_bits(float f) {
 }
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 
+// ---- host side ----------------------------------------------------------------------------
+// CUs of the current device (cached after the first call)
+inline int device_cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, v = 0;
+        n = (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+    }
+    return n;
+}
+// D[m][n] (row stride ldd) = A[m][:] . dequant(W[n][:]) for m < M, n < N with the grouped-GEMM kernel of
+// moe_prefill.hip over implicit tiles of `trows` consecutive rows (one Q4_K matrix, no row gather):
+// the dense GEMM hands it the columns that would leave its last round of 256 x 256 tiles thin.
+int launch_q4k_rows_gemm(const void* W, const uint16_t* A, float* D, int M, int N, int K, int ldd, int trows, hipStream_t s);
+
 }  // namespace qmm
 
 // Host-side launch check shared by the C-ABI wrappers.

@@ -71,6 +71,13 @@ def test_gemm_wq_small_and_ragged(gpu, M, N, K):
     gemm_check(M, N, K, 1300 + M, npairs=64)
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 8548, 512), (300, 40000, 256)])
+def test_gemm_wq_split_last_round(gpu, M, N, K):
+    """shapes whose last round of 256 x 256 tiles would be thin: the trailing columns (ragged) go to
+    the grouped kernel's implicit row tiles (ragged M too); the whole D is checked"""
+    gemm_check(M, N, K, 1350 + M, npairs=64)
+
+
 def test_gemm_wq_config3_full_shape(gpu):
     gemm_check(2048, 17408, 5120, synth.SEEDS["cfg3"], npairs=256)
 

@@ -157,3 +157,31 @@ def test_gemv_q8_f32x_equals_quantize_then_gemv(gpu, N, K, ncol):
     got = host(y)
     print(f"gemv_q8_f32x N={N} K={K} ncol={ncol}: {int((got.view(np.uint32) != ref.view(np.uint32)).sum())} differing", flush=True)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,K", [(17408, 5120), (16411, 512), (16384, 256), (16500, 4352), (20000, 6144), (16385, 768),
+                                 (30000, 2048), (17000, 5120)])
+def test_q4k_large_n_columns_and_fused_entry(gpu, N, K):
+    """Large decode shapes over every pair-iteration class (K = 256 .. 6144) and ragged N: each column
+    of ncol = 1..4 is bitwise the column of ncol = 5, the fused f32-x entry gives the same bits as
+    quantize + gemv_q8, and column 0 matches the oracle."""
+    W = synth.matrix(1500 + N + K, synth.Q4_K, N, K)
+    x = synth.normal_f32(1501 + K, (5, K))
+    Wd = dev(W)
+    xb = q8_on_gpu(x)
+    y5 = torch.zeros((5, N), dtype=torch.float32, device="cuda")
+    qmm.gemv_q8(synth.Q4_K, Wd, xb, y5, N, K, 5)
+    ref5 = host(y5)
+    q, d, _ = oracle.quantize_x_q8(x[:1])
+    ref, mag = oracle.gemv_ref(synth.Q4_K, W, N, K, oracle.q8_to_f32(q, d))
+    assert rel_l2(ref5[:1], ref) <= TOL
+    assert max_rel_mag(ref5[:1], ref, mag) < TOL
+    for ncol in (1, 2, 3, 4):
+        y = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+        qmm.gemv_q8(synth.Q4_K, Wd, xb, y, N, K, ncol)
+        got = host(y)
+        print(f"large-N q8 N={N} K={K} ncol={ncol}: {int((got.view(np.uint32) != ref5[:ncol].view(np.uint32)).sum())} differing", flush=True)
+        assert np.array_equal(got.view(np.uint32), ref5[:ncol].view(np.uint32))
+        yf = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+        qmm.gemv_q8_f32x(synth.Q4_K, Wd, dev(x[:ncol]), yf, N, K, ncol)
+        assert np.array_equal(host(yf).view(np.uint32), ref5[:ncol].view(np.uint32))
