@@ -362,8 +362,6 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
             wait_rem(min(nk - 1, t + 3) - (t + 1), t + 1);
             lds_barrier();
         }
-        if (t + 4 < nk) issue(t + 4, st4);
-        if ((t & 3) == 0 && t + 4 < nk) issue_w((t >> 2) + 1);
         __builtin_amdgcn_sched_barrier(0);
         const uint4* la = As + st * kXA;
         Raw r;
@@ -374,6 +372,11 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
         for (int i = 0; i < NRB; ++i) af[i] = af0[i];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
+            if (s == 1) {       // DMA for step t+4 (its stage was last read in step t-1) after chunk 0's MFMAs
+                if (t + 4 < nk) issue(t + 4, st4);
+                if ((t & 3) == 0 && t + 4 < nk) issue_w((t >> 2) + 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             afrag(s < 3 ? la : As + st1 * kXA, s < 3 ? s + 1 : 0, afn);
             if (s == 0) c = decode(r.hd, (t + 1) & 3);
             nxt[s] = deq(r, c, s);
