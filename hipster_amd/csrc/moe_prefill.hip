@@ -15,6 +15,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 namespace qmm {
 namespace {
 
@@ -24,14 +26,16 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // ------------------------------------------------------------------------------------------
 // Expert sort.  Slots te = t*nslot + e are ordered by key = id + 1 (0 = shared expert, id -1, then
 // the experts ascending), stable in te: the reference's std::sort by (expert id, te)
-// (qwen4exp.cpp:631-632).  One workgroup of 16 waves; wave w owns a contiguous slot range.
-// Pass 1 counts keys per wave; pass 2 turns the counts into per-(key, wave) start offsets, key-major
-// then wave order; pass 3 scatters each wave's range in order, a lane's rank among equal keys of
-// its 64-slot chunk coming from ballot peer masks over the key bits -- deterministic and stable.
+// (qwen4exp.cpp:631-632).  A workgroup of 16 waves; wave w owns a contiguous slot range.  Pass 1
+// counts keys per wave; pass 2 turns the counts into per-(key, wave) start offsets, key-major then
+// wave order; pass 3 scatters each wave's range in order, a lane's rank among equal keys of its
+// 64-slot chunk coming from ballot peer masks over the key bits -- deterministic and stable.  Large
+// slot counts spread the same passes over several workgroups (k_moe_sort_count / _offsets /
+// _scatter); small ones run in one (k_moe_sort).
 // Tiles: per key, ceil(count / maxc) tiles of consecutive sorted positions (the reference cuts a
 // tile at each expert change and every maxc positions, qwen4exp.cpp:636-641); routed-expert tiles
 // first in expert order, then the shared-expert tiles.  counts = {routed tiles, shared tiles}.
-constexpr int kSortThreads = 1024, kSortWaves = kSortThreads / 64, kMaxKeys = 1025, kSortBatch = 16;
+constexpr int kSortThreads = 1024, kSortWaves = kSortThreads / 64, kMaxKeys = 1025, kSortBatch = 16, kSortMaxGroups = 64;
 
 // exclusive scan over the workgroup of one int per thread; *total gets the sum
 __device__ __forceinline__ int block_exscan(int v, int* wsum, int* total) {
@@ -59,21 +63,20 @@ __device__ __forceinline__ int block_exscan(int v, int* wsum, int* total) {
     return x - v + (wave > 0 ? wsum[wave - 1] : 0);
 }
 
-__global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict__ ids, int ns, int nslot, int nkeys, int maxc,
-                                                           int* __restrict__ kpos, qmm_moe_tile* __restrict__ tiles,
-                                                           int* __restrict__ counts) {
-    extern __shared__ int sm[];
-    int* cnt = sm;                                   // [kSortWaves][nkeys]: per-wave counts, then running offsets
-    int* tot = cnt + kSortWaves * nkeys;             // [nkeys]
-    __shared__ int wsum[kSortWaves];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    for (int i = tid; i < kSortWaves * nkeys; i += kSortThreads) cnt[i] = 0;
-    __syncthreads();
-    const int per = ((ns + kSortWaves - 1) / kSortWaves + 63) & ~63;
-    const int lo = min(ns, wave * per), hi = min(ns, lo + per);
-    // pass 1: per-wave key counts (ids outside [-1, nkeys-2] are clamped into range by the host
-    // check; the kernel trusts them).  The ids of a wave's range are loaded kSortBatch per lane at a
-    // time, so the loads overlap instead of each waiting behind the previous LDS atomic.
+// Slots [lo, hi) of one workgroup are split over its 16 waves in contiguous runs of `per` (a
+// multiple of 64); the same split is used by every kernel that counts or scatters them.
+__device__ __forceinline__ void wave_range(int lo, int hi, int wave, int& wlo, int& whi) {
+    const int per = ((hi - lo + kSortWaves - 1) / kSortWaves + 63) & ~63;
+    wlo = min(hi, lo + wave * per);
+    whi = min(hi, wlo + per);
+}
+
+// pass 1: key counts of the wave's slots into cnt[wave * nkeys + key] (LDS, zeroed by the caller).
+// ids outside [-1, nkeys-2] are rejected by the host check; the kernel trusts them.  The ids are
+// loaded kSortBatch per lane at a time, so the loads overlap instead of each waiting behind the
+// previous LDS atomic.
+__device__ __forceinline__ void sort_count(const int* __restrict__ ids, int lo, int hi, int nkeys, int* cnt) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int c0 = lo; c0 < hi; c0 += 64 * kSortBatch) {
         int kk[kSortBatch];
 #pragma unroll
@@ -86,29 +89,14 @@ __global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict
         for (int u = 0; u < kSortBatch; ++u)
             if (kk[u] >= 0) atomicAdd(&cnt[wave * nkeys + kk[u]], 1);
     }
-    __syncthreads();
-    // each thread owns a contiguous key range [k0, k1)
-    const int kper = (nkeys + kSortThreads - 1) / kSortThreads;
-    const int k0 = min(nkeys, tid * kper), k1 = min(nkeys, k0 + kper);
-    int run = 0;
-    for (int k = k0; k < k1; ++k) {
-        int s = 0;
-        for (int w = 0; w < kSortWaves; ++w) s += cnt[w * nkeys + k];
-        tot[k] = s;
-        run += s;
-    }
-    int total = 0;
-    int base = block_exscan(run, wsum, &total);
-    // pass 2: per-(key, wave) start offsets
-    for (int k = k0; k < k1; ++k) {
-        for (int w = 0; w < kSortWaves; ++w) {
-            const int c = cnt[w * nkeys + k];
-            cnt[w * nkeys + k] = base;
-            base += c;
-        }
-    }
-    __syncthreads();
-    // pass 3: stable scatter, each wave over its own range in order
+}
+
+// pass 3: stable scatter of the wave's slots in order; cnt[wave * nkeys + key] holds the wave's
+// running offset of each key.  A lane's rank among the equal keys of its 64-slot chunk comes from
+// ballot peer masks over the 11 key bits.
+__device__ __forceinline__ void sort_scatter(const int* __restrict__ ids, int lo, int hi, int nkeys, int* cnt,
+                                             int* __restrict__ kpos) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const unsigned long long lt = (1ull << lane) - 1ull;
     for (int b0 = lo; b0 < hi; b0 += 64 * kSortBatch) {
         int kk[kSortBatch];
@@ -142,32 +130,146 @@ __global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict
             __builtin_amdgcn_wave_barrier();
         }
     }
-    __syncthreads();
-    // tiles.  After pass 3 the running offset of the last wave for key k is the end of key k's run
-    // in sorted order, so start(k) = cnt[last][k] - tot[k].
+}
+
+// tiles of the keys [k0, k1) owned by this thread, given each key's start and count (routed
+// experts, keys >= 1, first in key order; then thread 0 writes the shared expert's, key 0)
+__device__ __forceinline__ void sort_tiles(const int* start, const int* tot, int k0, int k1, int maxc, int* wsum,
+                                           qmm_moe_tile* __restrict__ tiles, int* __restrict__ counts) {
     int nt = 0;
     for (int k = max(k0, 1); k < k1; ++k) nt += (tot[k] + maxc - 1) / maxc;
     int nrouted = 0;
     int tb = block_exscan(nt, wsum, &nrouted);
     for (int k = max(k0, 1); k < k1; ++k) {
-        const int start = cnt[(kSortWaves - 1) * nkeys + k] - tot[k];
         for (int r = 0; r < tot[k]; r += maxc) {
             qmm_moe_tile tl;
-            tl.expert = k - 1; tl.k0 = start + r; tl.ncols = min(maxc, tot[k] - r);
+            tl.expert = k - 1; tl.k0 = start[k] + r; tl.ncols = min(maxc, tot[k] - r);
             tiles[tb++] = tl;
         }
     }
-    if (tid == 0) {
-        const int start = cnt[(kSortWaves - 1) * nkeys + 0] - tot[0];
+    if (threadIdx.x == 0) {
         int n = 0;
         for (int r = 0; r < tot[0]; r += maxc) {
             qmm_moe_tile tl;
-            tl.expert = -1; tl.k0 = start + r; tl.ncols = min(maxc, tot[0] - r);
+            tl.expert = -1; tl.k0 = start[0] + r; tl.ncols = min(maxc, tot[0] - r);
             tiles[nrouted + n++] = tl;
         }
         counts[0] = nrouted;
         counts[1] = n;
     }
+}
+
+// Whole sort in one workgroup (small slot counts)
+__global__ void __launch_bounds__(kSortThreads) k_moe_sort(const int* __restrict__ ids, int ns, int nslot, int nkeys, int maxc,
+                                                           int* __restrict__ kpos, qmm_moe_tile* __restrict__ tiles,
+                                                           int* __restrict__ counts) {
+    extern __shared__ int sm[];
+    int* cnt = sm;                                   // [kSortWaves][nkeys]: per-wave counts, then running offsets
+    int* tot = cnt + kSortWaves * nkeys;             // [nkeys]
+    int* start = tot + nkeys;                        // [nkeys]
+    __shared__ int wsum[kSortWaves];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    for (int i = tid; i < kSortWaves * nkeys; i += kSortThreads) cnt[i] = 0;
+    __syncthreads();
+    int lo, hi;
+    wave_range(0, ns, wave, lo, hi);
+    sort_count(ids, lo, hi, nkeys, cnt);
+    __syncthreads();
+    // each thread owns a contiguous key range [k0, k1)
+    const int kper = (nkeys + kSortThreads - 1) / kSortThreads;
+    const int k0 = min(nkeys, tid * kper), k1 = min(nkeys, k0 + kper);
+    int run = 0;
+    for (int k = k0; k < k1; ++k) {
+        int s = 0;
+        for (int w = 0; w < kSortWaves; ++w) s += cnt[w * nkeys + k];
+        tot[k] = s;
+        run += s;
+    }
+    int total = 0;
+    int base = block_exscan(run, wsum, &total);
+    // pass 2: per-(key, wave) start offsets
+    for (int k = k0; k < k1; ++k) {
+        start[k] = base;
+        for (int w = 0; w < kSortWaves; ++w) {
+            const int c = cnt[w * nkeys + k];
+            cnt[w * nkeys + k] = base;
+            base += c;
+        }
+    }
+    __syncthreads();
+    sort_scatter(ids, lo, hi, nkeys, cnt, kpos);
+    sort_tiles(start, tot, k0, k1, maxc, wsum, tiles, counts);
+}
+
+// The same sort over G workgroups (large slot counts), in two launches: each workgroup counts the
+// keys of its contiguous slot range into hist[g][key] (global scratch); then each workgroup counts
+// its range again per wave, derives its start per (key, wave) from the whole table (keys before,
+// then the same key in earlier workgroups and waves) and scatters; workgroup 0 also writes the
+// tiles.  The order is the one-workgroup order: key, then workgroup, then wave, then slot -- i.e.
+// key, then slot.
+__global__ void __launch_bounds__(kSortThreads) k_moe_sort_count(const int* __restrict__ ids, int ns, int nkeys, int per,
+                                                                 int* __restrict__ hist) {
+    extern __shared__ int sm[];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    for (int i = tid; i < kSortWaves * nkeys; i += kSortThreads) sm[i] = 0;
+    __syncthreads();
+    const int glo = min(ns, (int)blockIdx.x * per), ghi = min(ns, glo + per);
+    int lo, hi;
+    wave_range(glo, ghi, wave, lo, hi);
+    sort_count(ids, lo, hi, nkeys, sm);
+    __syncthreads();
+    for (int k = tid; k < nkeys; k += kSortThreads) {
+        int s = 0;
+        for (int w = 0; w < kSortWaves; ++w) s += sm[w * nkeys + k];
+        hist[(size_t)blockIdx.x * nkeys + k] = s;
+    }
+}
+
+__global__ void __launch_bounds__(kSortThreads) k_moe_sort_scatter(const int* __restrict__ ids, int ns, int nkeys, int per, int G,
+                                                                   int maxc, const int* __restrict__ hist, int* __restrict__ kpos,
+                                                                   qmm_moe_tile* __restrict__ tiles, int* __restrict__ counts) {
+    extern __shared__ int sm[];
+    int* cnt = sm;                                   // [kSortWaves][nkeys]
+    int* tot = cnt + kSortWaves * nkeys;             // [nkeys]
+    int* start = tot + nkeys;                        // [nkeys]
+    __shared__ int wsum[kSortWaves];
+    const int tid = threadIdx.x, wave = tid >> 6, g = blockIdx.x;
+    for (int i = tid; i < kSortWaves * nkeys; i += kSortThreads) cnt[i] = 0;
+    __syncthreads();
+    const int glo = min(ns, g * per), ghi = min(ns, glo + per);
+    int lo, hi;
+    wave_range(glo, ghi, wave, lo, hi);
+    sort_count(ids, lo, hi, nkeys, cnt);
+    // this workgroup's start per key: the keys before it, then the same key in earlier workgroups
+    const int kper = (nkeys + kSortThreads - 1) / kSortThreads;
+    const int k0 = min(nkeys, tid * kper), k1 = min(nkeys, k0 + kper);
+    int run = 0;
+    for (int k = k0; k < k1; ++k) {
+        int s = 0, before = 0;
+        for (int gg = 0; gg < G; ++gg) {
+            const int c = hist[(size_t)gg * nkeys + k];
+            before += gg < g ? c : 0;
+            s += c;
+        }
+        tot[k] = s;
+        start[k] = before;                           // offset within the key for now
+        run += s;
+    }
+    int total = 0;
+    int base = block_exscan(run, wsum, &total);      // also orders the count pass before the reads below
+    for (int k = k0; k < k1; ++k) {
+        int r = base + start[k];
+        start[k] = base;
+        base += tot[k];
+        for (int w = 0; w < kSortWaves; ++w) {
+            const int c = cnt[w * nkeys + k];
+            cnt[w * nkeys + k] = r;
+            r += c;
+        }
+    }
+    __syncthreads();
+    sort_scatter(ids, lo, hi, nkeys, cnt, kpos);
+    if (g == 0) sort_tiles(start, tot, k0, k1, maxc, wsum, tiles, counts);
 }
 
 // rowtok[kpos[i]] = token of slot i: the inverse permutation, written by the whole grid (scattered
@@ -535,14 +637,26 @@ int qmm_moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* 
                  int* counts, void* stream) {
     if (!ids || !kpos || !rowtok || !tiles || !counts) return QMM_ERR_NULL;
     if (T < 0 || nslot < 1 || nexperts < 1 || nexperts + 1 > kMaxKeys || maxc < 1) return QMM_ERR_SHAPE;
-    const int nkeys = nexperts + 1;
-    const size_t lds = (size_t)(kSortWaves + 1) * nkeys * 4;
-    hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(kSortThreads), lds, (hipStream_t)stream, ids, T * nslot, nslot, nkeys, maxc, kpos,
-                       tiles, counts);
-    QMM_LAUNCH_CHECK();
-    const int ns = T * nslot;
+    const int nkeys = nexperts + 1, ns = T * nslot;
+    hipStream_t st = (hipStream_t)stream;
+    // G workgroups of at least 1024 slots each, their counts (G x nkeys) held in rowtok until the
+    // rowtok kernel overwrites it; one workgroup when that does not give at least 4
+    const int G = std::min(std::min(ns / 1024, ns / nkeys), kSortMaxGroups);
+    if (G >= 4) {
+        const int per = (ns + G - 1) / G;
+        const size_t lds_w = (size_t)kSortWaves * nkeys * 4;
+        hipLaunchKernelGGL(k_moe_sort_count, dim3(G), dim3(kSortThreads), lds_w, st, ids, ns, nkeys, per, rowtok);
+        QMM_LAUNCH_CHECK();
+        hipLaunchKernelGGL(k_moe_sort_scatter, dim3(G), dim3(kSortThreads), lds_w + (size_t)2 * nkeys * 4, st, ids, ns, nkeys, per, G,
+                           maxc, rowtok, kpos, tiles, counts);
+        QMM_LAUNCH_CHECK();
+    } else {
+        const size_t lds = (size_t)(kSortWaves + 2) * nkeys * 4;
+        hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(kSortThreads), lds, st, ids, ns, nslot, nkeys, maxc, kpos, tiles, counts);
+        QMM_LAUNCH_CHECK();
+    }
     if (ns > 0) {
-        hipLaunchKernelGGL(k_moe_rowtok, dim3((ns + 255) / 256), dim3(256), 0, (hipStream_t)stream, kpos, rowtok, ns, nslot);
+        hipLaunchKernelGGL(k_moe_rowtok, dim3((ns + 255) / 256), dim3(256), 0, st, kpos, rowtok, ns, nslot);
         QMM_LAUNCH_CHECK();
     }
     return QMM_OK;

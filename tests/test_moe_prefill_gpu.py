@@ -29,8 +29,11 @@ def sort_on_gpu(ids_h, n_exp, maxc=qmm.MOE_TILE_ROWS):
 
 
 @pytest.mark.parametrize("T,n_exp,zipf,maxc", [(1, 512, None, 64), (7, 64, None, 16), (2048, 512, 1.1, 64),
-                                               (2048, 512, None, 64), (300, 1000, 1.1, 32)])
+                                               (2048, 512, None, 64), (300, 1000, 1.1, 32), (4096, 512, 1.1, 128),
+                                               (8192, 1000, 1.1, 128), (777, 128, 1.1, 16)])
 def test_moe_sort_matches_oracle(gpu, T, n_exp, zipf, maxc):
+    """one workgroup for small slot counts, several (count / offsets / scatter) for large ones:
+    kpos, rowtok and the tiles bit-exact against the oracle either way"""
     ids_h, _ = oracle.moe_route(synth.router_logits(1400 + T, T, n_exp, zipf), n_exp, 10)
     kpos, rowtok, tiles, counts, _ = sort_on_gpu(ids_h, n_exp, maxc)
     kp, rt, tl, st = oracle.moe_sort(ids_h, maxc)
