@@ -154,21 +154,23 @@ __global__ void __launch_bounds__(kBlock) k_gemv_q4k_q8(const uint8_t* __restric
 // f32 x in, q8 arithmetic: the q8 quantisation of x fused into the staging of k_gemv_q4k_q8 (x
 // loaded ahead of the weights and quantised while they stream in), so quantize_x_q8 + gemv_q8 is
 // one launch with bit-identical results.  Rows of NITER pair iterations (K <= 1024 * NITER).
-template <int NCOL, int NITER>
-__global__ void __launch_bounds__(kBlock) k_gemv_q4k_fx(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                        float* __restrict__ y, int N, int K) {
+// BS threads (BS/64 waves of 4 rows): the per-lane work is the same for any BS; a larger workgroup
+// stages (and quantises) x once for more rows.
+template <int NCOL, int NITER, int BS>
+__global__ void __launch_bounds__(BS) k_gemv_q4k_fx(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                    float* __restrict__ y, int N, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int nb = K >> 8, ntask = 4 * nb;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = lane & 15, j = t & 3;
-    const int row = (blockIdx.x * kWavesPerBlock + wave) * 4 + (lane >> 4);
+    const int row = (blockIdx.x * (BS / 64) + wave) * 4 + (lane >> 4);
     const uint8_t* rp = W + (size_t)min(row, N - 1) * ((size_t)nb * 144);
     Q4kPairs<NITER> A;
     {
-        XStageF<NCOL, (NCOL * NITER + 1) / 2> S;          // NCOL * K/8 <= 256 * NCOL * NITER / 2
-        stagef_load<NCOL>(x, K, S);                       // x first (older loads) ...
+        XStageF<NCOL, (128 * NCOL * NITER + BS - 1) / BS> S;   // NCOL * K/8 <= 128 * NCOL * NITER slots
+        stagef_load<NCOL, (128 * NCOL * NITER + BS - 1) / BS, BS>(x, K, S);   // x first (older loads) ...
         q4k_load_pairs<NITER>(rp, t, j, ntask, 0, A);     // ... then the weights
-        stagef_store<NCOL>(smem, K, S);                   // quantise while the weights stream in
+        stagef_store<NCOL, (128 * NCOL * NITER + BS - 1) / BS, BS>(smem, K, S);   // quantise while the weights stream in
         lds_barrier();
     }
     XPairSrc<true> xsrc[NCOL];
@@ -609,11 +611,13 @@ int launch_q4k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t 
     }
 }
 
+// 256 threads: measured against 320, 384 and 512 (12.6 vs 15.5-16.8 us at 17408 x 5120, M=1)
 template <int NCOL>
 int launch_q4k_fx(const void* W, const float* x, float* y, int N, int K, hipStream_t s) {
+    constexpr int BS = kBlock, ROWS = 4 * (BS / 64);
     const size_t lds = (size_t)NCOL * (K + K / 4);
-    const int grid = (N + 4 * kWavesPerBlock - 1) / (4 * kWavesPerBlock);
-#define QMM_FX(IV) case IV: hipLaunchKernelGGL((k_gemv_q4k_fx<NCOL, IV>), dim3(grid), dim3(kBlock), lds, s, (const uint8_t*)W, x, y, N, K); break;
+    const int grid = (N + ROWS - 1) / ROWS;
+#define QMM_FX(IV) case IV: hipLaunchKernelGGL((k_gemv_q4k_fx<NCOL, IV, BS>), dim3(grid), dim3(BS), lds, s, (const uint8_t*)W, x, y, N, K); break;
     switch ((K / 256 * 4 + 15) / 16) {
         QMM_FX(1) QMM_FX(2) QMM_FX(3) QMM_FX(4) QMM_FX(5) QMM_FX(6)
         default: return QMM_ERR_SHAPE;

@@ -164,17 +164,17 @@ __device__ __forceinline__ void stage_pairs_store(uint8_t* lds, int K, const XSt
 // the quad: values 8k..8k+7, two float4) and quantises them with the arithmetic of the q8 quantiser
 // (gemv.hip:36-51 semantics: d = amax/127, q = rne(x * 127/amax), s = d * sum(q)), so q, d and s
 // are bit-identical to staging its output; the quad reductions are DPP lane permutations.  Thread
-// slot e = threadIdx.x + 256*u covers floats 8e..8e+7 of the column-major [NCOL][K] array;
-// U * 256 >= NCOL * K/8.
+// slot e = threadIdx.x + BS*u (BS = threads of the workgroup) covers floats 8e..8e+7 of the
+// column-major [NCOL][K] array; U * BS >= NCOL * K/8.
 template <int NCOL, int U>
 struct XStageF { float4 v[U][2]; };
 
-template <int NCOL, int U>
+template <int NCOL, int U, int BS = kPairBlock>
 __device__ __forceinline__ void stagef_load(const float* __restrict__ x, int K, XStageF<NCOL, U>& S) {
     const int n8 = NCOL * (K >> 3);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const float4* p = (const float4*)x + 2 * min((int)threadIdx.x + kPairBlock * u, n8 - 1);
+        const float4* p = (const float4*)x + 2 * min((int)threadIdx.x + BS * u, n8 - 1);
         S.v[u][0] = p[0];
         S.v[u][1] = p[1];
     }
@@ -186,12 +186,12 @@ __device__ __forceinline__ int quad_xor(int v) {
     return __builtin_amdgcn_mov_dpp(v, M == 1 ? 0xB1 : 0x4E, 0xf, 0xf, false);
 }
 
-template <int NCOL, int U>
+template <int NCOL, int U, int BS = kPairBlock>
 __device__ __forceinline__ void stagef_store(uint8_t* lds, int K, const XStageF<NCOL, U>& S) {
     const int k8 = K >> 3, n8 = NCOL * k8, kq = K >> 6;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int e = (int)threadIdx.x + kPairBlock * u;      // n8 is a multiple of 4: quads share e < n8
+        const int e = (int)threadIdx.x + BS * u;              // n8 is a multiple of 4: quads share e < n8
         const float4 a = S.v[u][0], b = S.v[u][1];
         float amax = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
                            fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
