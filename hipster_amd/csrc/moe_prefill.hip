@@ -330,18 +330,52 @@ struct XArgs {
     void* D;               // f32 [k][ldd], or bf16 h [k][ldd] in gate/up mode
     int N, K, nb;          // nb = weight-row blocks per tile
     int ldd;               // row stride of D (elements)
-    int trows, nimp, M;    // tiles == nullptr: implicit tiles of trows rows of expert 0, nimp of them, M rows
+    int trows, nimp, M;    // tiles == nullptr: implicit tiles of trows rows of expert 0, nimp of them, M rows;
+                           // otherwise nimp = capacity of tiles (the device count is clamped to it)
+    int bpu;               // k_moe_gemm_as: 256-row weight blocks per work unit
 };
 
-// 8 values (one per byte of {u0, u1}, already masked to one nibble) -> bf16 fma(dl, q, -ml), k order
-// = byte order
-__device__ __forceinline__ bf16x8 q4_bf16x8(uint32_t u0, uint32_t u1, float dl, float ml) {
-    __bf16 v[8];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) v[b] = (__bf16)__builtin_fmaf(dl, (float)((u0 >> (8 * b)) & 0xffu), -ml);
-#pragma unroll
-    for (int b = 0; b < 4; ++b) v[4 + b] = (__bf16)__builtin_fmaf(dl, (float)((u1 >> (8 * b)) & 0xffu), -ml);
-    return *(const bf16x8*)v;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// fma(value of the f16 half, s, c) -- v_fma_mix_f32.  A half whose bits are a small integer q
+// (exponent field 0) is the subnormal q * 2^-24, exactly, so with s = x * 2^24 the product is
+// exactly q * x and the result is the single rounding of q * x + c: fmaf(x, q, c) bit for bit.
+__device__ __forceinline__ float mix_lo(uint32_t v, float s, float c) {
+    return __builtin_fmaf((float)__builtin_bit_cast(f16x2, v)[0], s, c);
+}
+__device__ __forceinline__ float mix_hi(uint32_t v, float s, float c) {
+    return __builtin_fmaf((float)__builtin_bit_cast(f16x2, v)[1], s, c);
+}
+// 8 weights bf16(fma(dl, q, -ml)) from the nibbles of bytes 0..7 of {u0, u1} (k order = byte
+// order).  m = 0x000f000f takes the low nibbles (s24 = dl * 2^24), m = 0x00f000f0 the high ones in
+// place, 16q (s24 = dl * 2^20).  Bit for bit the dequantisation bf16(fmaf(dl, (float)q, -ml)) (RNE),
+// in 17 VALU per 8 weights (byte-to-float conversions, fma and packing take 22).  Relies on f16
+// subnormals being kept, the kernels' default mode (float_denorm_mode_16_64 = 3).
+__device__ __forceinline__ bf16x8 q4_bf16x8_mix(uint32_t u0, uint32_t u1, uint32_t m, float s24, float c) {
+    const uint32_t e0 = u0 & m, o0 = (u0 >> 8) & m, e1 = u1 & m, o1 = (u1 >> 8) & m;
+    bf16x8 r;
+    r[0] = (__bf16)mix_lo(e0, s24, c);
+    r[1] = (__bf16)mix_lo(o0, s24, c);
+    r[2] = (__bf16)mix_hi(e0, s24, c);
+    r[3] = (__bf16)mix_hi(o0, s24, c);
+    r[4] = (__bf16)mix_lo(e1, s24, c);
+    r[5] = (__bf16)mix_lo(o1, s24, c);
+    r[6] = (__bf16)mix_hi(e1, s24, c);
+    r[7] = (__bf16)mix_hi(o1, s24, c);
+    return r;
+}
+
+// scales of K step j (qs pair j: sub-blocks 2j, 2j+1) of a Q4_K block header, pre-scaled for
+// q4_bf16x8_mix: {d*sc[2j] * 2^24, dmin*m[2j], d*sc[2j+1] * 2^20, dmin*m[2j+1]}
+struct StepScl { float sa, ma, sb, mb; };
+__device__ __forceinline__ StepScl q4k_step_scales(const uint4 hd, int j) {
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
+    StepScl c;
+    c.sa = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j) * 16777216.f;
+    c.ma = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
+    c.sb = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1) * 1048576.f;
+    c.mb = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
+    return c;
 }
 
 template <bool GU, int NRB>
@@ -412,24 +446,11 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
         r.q0 = *(const uint2*)(rp + 16 + 32 * j + 8 * h);
         r.q1 = *(const uint2*)(rp + 32 + 32 * j + 8 * h);
     };
-    struct Scl { float dA, mA, dB16, mB; };
-    auto decode = [&](const uint4 hd, int j) {
-        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-        const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
-        Scl c;
-        c.dA = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j);
-        c.mA = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j);
-        // high nibbles stay in place (16 q): the exact factor 1/16 moves into the scale
-        c.dB16 = d * (float)byte8(sb.sc_lo, sb.sc_hi, 2 * j + 1) * 0.0625f;
-        c.mB = dmin * (float)byte8(sb.m_lo, sb.m_hi, 2 * j + 1);
-        return c;
-    };
     // K slice s (16 wide) of the step: s 0, 1 = low nibbles of the two qs halves (sub-block 2j),
     // s 2, 3 = their high nibbles (sub-block 2j+1)
-    auto deq = [&](const Raw& r, const Scl& c, int s) {
+    auto deq = [&](const Raw& r, const StepScl& c, int s) {
         const uint2 q = (s & 1) ? r.q1 : r.q0;
-        const uint32_t m = s < 2 ? 0x0f0f0f0fu : 0xf0f0f0f0u;
-        return q4_bf16x8(opaque(q.x & m), opaque(q.y & m), s < 2 ? c.dA : c.dB16, s < 2 ? c.mA : c.mB);
+        return s < 2 ? q4_bf16x8_mix(q.x, q.y, 0x000f000fu, c.sa, -c.ma) : q4_bf16x8_mix(q.x, q.y, 0x00f000f0u, c.sb, -c.mb);
     };
     // before dequantising step p (waves 4-7 hold at most one block in flight: the next one is
     // issued at the first step of the current block, after this wait)
@@ -450,7 +471,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
     {
         Raw r;
         rawread(0, r);
-        const Scl c = decode(r.hd, 0);
+        const StepScl c = q4k_step_scales(r.hd, 0);
 #pragma unroll
         for (int s = 0; s < 4; ++s) wa[s] = deq(r, c, s);
         afrag(As, 0, af0);
@@ -468,7 +489,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
         const uint4* la = As + st * kXA;
         Raw r;
         rawread(t + 1, r);
-        Scl c;
+        StepScl c;
         bf16x8 af[NRB], afn[NRB];
 #pragma unroll
         for (int i = 0; i < NRB; ++i) af[i] = af0[i];
@@ -480,7 +501,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
                 __builtin_amdgcn_sched_barrier(0);
             }
             afrag(s < 3 ? la : As + st1 * kXA, s < 3 ? s + 1 : 0, afn);
-            if (s == 0) c = decode(r.hd, (t + 1) & 3);
+            if (s == 0) c = q4k_step_scales(r.hd, (t + 1) & 3);
             nxt[s] = deq(r, c, s);
             asm volatile("" : : "v"(nxt[s]));   // keeps the dequantisation inside this chunk
 #pragma unroll
@@ -576,7 +597,7 @@ __global__ void __launch_bounds__(XTHREADS) k_moe_gemm_x(XArgs a) {
     __shared__ int rows[XBM];
     const int id = blockIdx.x, sid = id >> 3;
     const int tix = 8 * (sid / a.nb) + (id & 7), nbi = sid % a.nb;
-    if (tix >= (a.tiles ? a.counts[0] + a.counts[1] : a.nimp)) return;
+    if (tix >= (a.tiles ? min(a.counts[0] + a.counts[1], a.nimp) : a.nimp)) return;
     qmm_moe_tile tl;
     if (a.tiles) tl = a.tiles[tix];
     else tl = qmm_moe_tile{0, tix * a.trows, min(a.trows, a.M - tix * a.trows)};
@@ -601,6 +622,203 @@ int launch_moe_gemm_x(bool gu, const XArgs& a, int max_tiles, hipStream_t s) {
     const int grid = 8 * ((max_tiles + 7) / 8) * a.nb;
     if (gu) hipLaunchKernelGGL(k_moe_gemm_x<true>, dim3(grid), dim3(XTHREADS), kXLds, s, a);
     else hipLaunchKernelGGL(k_moe_gemm_x<false>, dim3(grid), dim3(XTHREADS), kXLds, s, a);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+// ------------------------------------------------------------------------------------------
+// Grouped expert GEMM with the tile's activations resident in LDS, for K = 512 (the MoE down
+// projection).  Work unit = (tile, run of bpu consecutive 256-row weight blocks).  The tile's A rows
+// (at most 128 x 512 bf16 = 128 KiB) are copied global -> LDS once per unit; after that every wave
+// works alone: it streams its own 32 weight rows of each block straight into registers, dequantises
+// them and multiplies them against A fragments read from LDS, block after block, and stores each
+// block's f32 results.  The main loop has no workgroup barrier and no LDS writes, and A is read from
+// global memory once per unit instead of once per weight block.
+// The K order is k_moe_gemm_x's (same MFMA sequence, so the same results bit for bit): per 64-wide
+// K step lane l (weight row l%32, h = l/32) takes qs bytes 8h..8h+7 and 16+8h..16+8h+7 of the step's
+// pair, slices 0 and 1 their low nibbles, slices 2 and 3 their high nibbles, and the A fragment of
+// slice s is chunk 2s + h of the step.  A in LDS: row r at r * 1040 bytes
+// (64 chunks of 16 B and 16 B of padding), so the 16 rows a quarter-wave reads fall in 16 distinct
+// bank groups and every fragment address is one lane base plus a constant; one DMA instruction
+// copies one row.
+constexpr int kAsK = 512, kAsThreads = 512, kAsBlocksPerUnit = 4, kAsRowBytes = 1040;
+constexpr bool kAsDeferStores = false;
+
+// f32 store the compiler does not see (address = wave-uniform base in SGPRs + per-lane 32-bit byte
+// offset): its waits for the weight loads issued before it are then computed over loads only (loads
+// complete in order, so such a wait can only last longer), instead of the full vmcnt(0) it places
+// once loads and stores are both outstanding.
+__device__ __forceinline__ void st_f32_nc(const uint8_t* base, uint32_t voff, float v) {
+    asm volatile("global_store_dword %0, %1, %2" : : "v"(voff), "v"(v), "s"(base) : "memory");
+}
+
+// one Q4_K block (4 K steps) of the lane's weight row: header and the lane's two 8-byte qs pieces
+// per step j (bytes 8h.. and 16+8h.. of pair j)
+struct AsRaw { uint4 hd; uint2 a0, b0, a1, b1, a2, b2, a3, b3; };
+
+template <int NRB>
+__device__ __forceinline__ void moe_as_unit(const XArgs& a, const qmm_moe_tile tl, int b0, int b1, const int* rows,
+                                            uint8_t* As) {
+    const int lane = threadIdx.x & 63, fr = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr uint32_t rowbytes = 2 * 144u;          // two Q4_K blocks per weight row
+    const int N = a.N;
+    const uint8_t* w = tl.expert >= 0 ? a.w0 + (size_t)tl.expert * a.ebytes : a.w0sh;
+    {   // A rows 0 .. 32 NRB - 1 -> LDS, one DMA instruction (64 lanes x 16 B) per row
+        const uint32_t la = lds_addr(As);
+        for (int r = wave; r < NRB * 32; r += 8)
+            dma16((const uint8_t*)a.A + ((size_t)rows[r] * kAsK + (size_t)(8 * lane)) * 2, la + (uint32_t)(r * kAsRowBytes));
+    }
+    // group g = Q4_K block g % 2 of weight block b0 + g / 2; the lane's row in it (clamped: rows past
+    // N load row N-1 and are not stored)
+    const int nblk = b1 - b0, ng = 2 * nblk;
+    auto load = [&](int g, AsRaw& r) {
+        const int b = b0 + (g >> 1);
+        const uint8_t* p = w + (size_t)min(b * 256 + 32 * wave + fr, N - 1) * rowbytes + (size_t)(g & 1) * 144;
+        const uint8_t* pq = p + 16 + 8 * h;
+        r.hd = ld16(p);
+        r.a0 = *(const uint2*)(pq);
+        r.b0 = *(const uint2*)(pq + 16);
+        r.a1 = *(const uint2*)(pq + 32);
+        r.b1 = *(const uint2*)(pq + 48);
+        r.a2 = *(const uint2*)(pq + 64);
+        r.b2 = *(const uint2*)(pq + 80);
+        r.a3 = *(const uint2*)(pq + 96);
+        r.b3 = *(const uint2*)(pq + 112);
+    };
+    f32x16 acc0[NRB], acc1[NRB];
+#pragma unroll
+    for (int i = 0; i < NRB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc0[i][e] = acc1[i][e] = 0.f;
+    AsRaw ra, rb;
+    load(0, ra);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));      // the A copy has landed (and group 0)
+    __syncthreads();
+    // lane bases: row fr (row blocks 0, 1) and row 64 + fr (row blocks 2, 3), chunk h
+    typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+    const lds_u8* alo = (const lds_u8*)As + fr * kAsRowBytes + 16 * h;
+    const lds_u8* ahi = alo + 64 * kAsRowBytes;
+    asm volatile("" : "+v"(ahi));     // a base of its own: otherwise folded into alo + offsets past 64 KiB
+
+    // K step t (0..7) of the row; the four slices' NRB MFMAs each
+    auto step = [&](const uint2 qa, const uint2 qb, const StepScl& c, int t, f32x16 (&acc)[NRB]) {
+        bf16x8 wv[4];
+        wv[0] = q4_bf16x8_mix(qa.x, qa.y, 0x000f000fu, c.sa, -c.ma);
+        wv[1] = q4_bf16x8_mix(qb.x, qb.y, 0x000f000fu, c.sa, -c.ma);
+        wv[2] = q4_bf16x8_mix(qa.x, qa.y, 0x00f000f0u, c.sb, -c.mb);
+        wv[3] = q4_bf16x8_mix(qb.x, qb.y, 0x00f000f0u, c.sb, -c.mb);
+        // A fragments one slice ahead, each slice fenced: two slices' fragments live at most
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 af[NRB], an[NRB];
+        auto rd = [&](u32x4 (&v)[NRB], int s) {
+            const int off = (8 * t + 2 * s) * 16;
+#pragma unroll
+            for (int i = 0; i < NRB; ++i)
+                v[i] = *(const __attribute__((address_space(3))) u32x4*)((i < 2 ? alo : ahi) + (i & 1) * 32 * kAsRowBytes + off);
+        };
+        rd(af, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s < 3) rd(an, s + 1);
+#pragma unroll
+            for (int i = 0; i < NRB; ++i)
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[i]), wv[s], acc[i], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < NRB; ++i) af[i] = an[i];
+        }
+    };
+    // results of weight block b (tile row 32i + 8(e/4) + e%4 + 4h): the uniform row part walks a
+    // scalar pointer (kept opaque, so its 64 values are formed one at a time instead of hoisted out of
+    // the loop), the lane part (4h rows, column n) is a fixed byte offset; then the set restarts at 0
+    auto store = [&](f32x16 (&acc)[NRB], int b) {
+        const int n = b * 256 + 32 * wave + fr;
+        const uint32_t voff = (uint32_t)(4 * h * a.ldd + n) * 4u;
+        int rem = n < N ? tl.ncols - 4 * h : 0;     // the lane stores uniform row offsets below rem
+        asm volatile("" : "+v"(rem));               // (compared here, not as 64 hoisted masks)
+        const size_t rs = (size_t)a.ldd * 4;
+        const uint8_t* p = (const uint8_t*)a.D + (size_t)tl.k0 * rs;
+#pragma unroll
+        for (int i = 0; i < NRB; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                asm volatile("" : "+s"(p));
+                if (32 * i + 8 * (e >> 2) + (e & 3) < rem) st_f32_nc(p, voff, acc[i][e]);
+                acc[i][e] = 0.f;
+                p += (e & 3) == 3 ? 5 * rs : rs;     // next row: +1, or +5 after the 4th of a group of 8
+            }
+    };
+    // group g (Q4_K block kb = g % 2 of its weight block): the K steps of raw r into acc; the next
+    // group's loads go out after the first step.  Deferred stores: the previous block's set accp is
+    // stored after the first step of a block's first group (the wait for the next weights, three
+    // steps later, then finds those stores drained); otherwise a block's set is stored at its end.
+    // Fenced steps: hoisting a step's A fragments and dequantisation over the previous step's MFMAs
+    // runs out of registers.
+    auto group = [&](int g, int kb, const AsRaw& r, AsRaw& fill, f32x16 (&acc)[NRB], f32x16 (&accp)[NRB]) {
+        const int t0 = 4 * kb;
+        step(r.a0, r.b0, q4k_step_scales(r.hd, 0), t0, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load(min(g + 1, ng - 1), fill);
+        if (kAsDeferStores && kb == 0 && g > 0) store(accp, b0 + (g >> 1) - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        step(r.a1, r.b1, q4k_step_scales(r.hd, 1), t0 + 1, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        step(r.a2, r.b2, q4k_step_scales(r.hd, 2), t0 + 2, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        step(r.a3, r.b3, q4k_step_scales(r.hd, 3), t0 + 3, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (!kAsDeferStores && kb == 1) store(acc, b0 + (g >> 1));
+    };
+    if constexpr (kAsDeferStores) {
+        // blocks in pairs: acc0 for even blocks, acc1 for odd ones
+        for (int bi = 0; bi < nblk; bi += 2) {
+            group(2 * bi, 0, ra, rb, acc0, acc1);
+            group(2 * bi + 1, 1, rb, ra, acc0, acc1);
+            if (bi + 1 < nblk) {
+                group(2 * bi + 2, 0, ra, rb, acc1, acc0);
+                group(2 * bi + 3, 1, rb, ra, acc1, acc0);
+            }
+        }
+        if ((nblk - 1) & 1) store(acc1, b1 - 1);
+        else store(acc0, b1 - 1);
+    } else {
+        for (int bi = 0; bi < nblk; ++bi) {
+            group(2 * bi, 0, ra, rb, acc0, acc1);
+            group(2 * bi + 1, 1, rb, ra, acc0, acc1);
+        }
+    }
+}
+
+// One workgroup per (tile, run of bpu weight blocks); workgroup id i runs on XCD i % 8 and XCD x
+// takes tiles x, x+8, ... with all their runs (the runs of a tile share its A rows in one L2).
+__global__ void __launch_bounds__(kAsThreads) k_moe_gemm_as(XArgs a) {
+    extern __shared__ __align__(16) uint8_t smem_raw[];
+    __shared__ int rows[XBM];
+    const int nu = (a.nb + a.bpu - 1) / a.bpu;
+    const int id = blockIdx.x, sid = id >> 3;
+    const int tix = 8 * (sid / nu) + (id & 7), ui = sid % nu;
+    if (tix >= min(a.counts[0] + a.counts[1], a.nimp)) return;
+    qmm_moe_tile tl = a.tiles[tix];
+    tl.ncols = max(1, min(tl.ncols, XBM));
+    if (threadIdx.x < XBM) {
+        const int k = tl.k0 + min((int)threadIdx.x, tl.ncols - 1);
+        rows[threadIdx.x] = a.rowtab ? a.rowtab[k] : k;
+    }
+    __syncthreads();
+    const int b0 = ui * a.bpu, b1 = min(a.nb, b0 + a.bpu);
+    switch ((tl.ncols + 31) >> 5) {
+        case 1: moe_as_unit<1>(a, tl, b0, b1, rows, smem_raw); break;
+        case 2: moe_as_unit<2>(a, tl, b0, b1, rows, smem_raw); break;
+        case 3: moe_as_unit<3>(a, tl, b0, b1, rows, smem_raw); break;
+        default: moe_as_unit<4>(a, tl, b0, b1, rows, smem_raw); break;
+    }
+}
+
+int launch_moe_gemm_as(XArgs a, int max_tiles, hipStream_t s) {
+    const int nu = (a.nb + a.bpu - 1) / a.bpu;
+    const int grid = 8 * ((max_tiles + 7) / 8) * nu;
+    hipLaunchKernelGGL(k_moe_gemm_as, dim3(grid), dim3(kAsThreads), (size_t)XBM * kAsRowBytes, s, a);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }
@@ -670,7 +888,8 @@ int qmm_moe_gemm_bf16(int fmt, int shared_fmt, const void* W, const void* Wsh, s
     if (N <= 0 || K <= 0 || K % 256 != 0 || max_tiles < 0) return QMM_ERR_SHAPE;
     if (max_tiles == 0) return QMM_OK;
     XArgs a{(const uint8_t*)W, (const uint8_t*)Wsh, nullptr, nullptr, ebytes, tiles, counts, rowtab, A, D, N, K,
-            (N + XBW - 1) / XBW, N, 0, 0, 0};
+            (N + XBW - 1) / XBW, N, 0, max_tiles, 0, kAsBlocksPerUnit};
+    if (K == kAsK) return launch_moe_gemm_as(a, max_tiles, (hipStream_t)stream);
     return launch_moe_gemm_x(false, a, max_tiles, (hipStream_t)stream);
 }
 
@@ -682,7 +901,7 @@ int qmm_moe_gemm_gate_up_bf16(int fmt, int shared_fmt, const void* Wg, const voi
     if (N <= 0 || K <= 0 || K % 256 != 0 || max_tiles < 0) return QMM_ERR_SHAPE;
     if (max_tiles == 0) return QMM_OK;
     XArgs a{(const uint8_t*)Wg, (const uint8_t*)Wgsh, (const uint8_t*)Wu, (const uint8_t*)Wush, ebytes, tiles, counts,
-            rowtab, A, H, N, K, (N + XBW / 2 - 1) / (XBW / 2), N, 0, 0, 0};
+            rowtab, A, H, N, K, (N + XBW / 2 - 1) / (XBW / 2), N, 0, max_tiles, 0};
     return launch_moe_gemm_x(true, a, max_tiles, (hipStream_t)stream);
 }
 
