@@ -44,6 +44,9 @@ SIGNATURES = {
     "qmm_status_string": (ctypes.c_char_p, [c_int]),
     "qmm_wfmt_row_bytes": (ctypes.c_size_t, [c_int, c_int]),
     "qmm_repack_row_q6_K": (c_int, [c_vp, c_vp, c_int]),
+    "qmm_repack_row_q8_0": (c_int, [c_vp, c_vp, c_int]),
+    "qmm_repack_row_q5_1": (c_int, [c_vp, c_vp, c_int]),
+    "qmm_repack_row_q5_0": (c_int, [c_vp, c_vp, c_int]),
     "qmm_quantize_x_q8": (c_int, [c_vp, XQ8, c_int, c_int, c_vp]),
     "qmm_gemv_q8": (c_int, [c_int, c_vp, XQ8, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
     "qmm_gemv_multi": (c_int, [ctypes.POINTER(GemvSeg), c_int, XQ8, c_int, c_vp]),

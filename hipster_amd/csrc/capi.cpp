@@ -1,8 +1,46 @@
 // capi.cpp -- host-only entry points of the C ABI (no kernels): version, status strings and the
-// row-layout helpers of the reference (engine/kernels/gemv.hip:1337-1350).
+// row-layout helpers of the reference (engine/kernels/gemv.hip:1337-1354,1448-1465).
+#include <math.h>
+#include <stdint.h>
 #include <string.h>
 
 #include "../../include/hipster_qmm.h"
+
+namespace {
+// IEEE half <-> float for the host repacks (g++ here has no _Float16).  f2h rounds to nearest
+// even, overflow gives infinity; NaN keeps its sign and becomes a quiet NaN.
+float h2f_host(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) bits = sign;
+        else {
+            const float v = ldexpf((float)m, -24);
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) bits = sign | 0x7f800000u | (m << 13);
+    else bits = sign | ((e + 112) << 23) | (m << 13);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+uint16_t f2h_host(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    const float a = fabsf(f);
+    if (a != a) return (uint16_t)(sign | 0x7e00u);
+    if (!(a < 65520.f)) return (uint16_t)(sign | 0x7c00u);
+    if (a < 6.103515625e-05f) return (uint16_t)(sign | (uint16_t)nearbyintf(a * 16777216.f));
+    uint32_t v;
+    memcpy(&v, &a, 4);
+    const uint32_t mant = v & 0x7fffffu, exp = (v >> 23) - 112u, rest = mant & 0x1fffu;
+    uint32_t h = (exp << 10) | (mant >> 13);
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+}
+}  // namespace
 
 extern "C" {
 
@@ -21,12 +59,18 @@ const char* qmm_status_string(int status) {
     }
 }
 
-// gemv.hip:1337-1340, for the formats this build reads
+// gemv.hip:1337-1340
 size_t qmm_wfmt_row_bytes(int fmt, int K) {
-    if (K <= 0 || K % 256 != 0) return 0;
+    if (K <= 0) return 0;
+    const bool b32 = fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA;
+    if (K % (b32 ? 32 : 256) != 0) return 0;
     switch (fmt) {
         case QMM_Q4_K: return (size_t)K / 256 * 144;
+        case QMM_Q5_K: return (size_t)K / 256 * 176;
+        case QMM_IQ4_XS: return (size_t)K / 256 * 136;
         case QMM_Q6_K: case QMM_Q6_K_SOA: return (size_t)K / 256 * 210;
+        case QMM_Q8_0_SOA: return (size_t)K + (size_t)K / 16;
+        case QMM_Q5_1_SOA: return (size_t)K / 32 * 24;
         default: return 0;
     }
 }
@@ -42,6 +86,52 @@ int qmm_repack_row_q6_K(const uint8_t* src, uint8_t* dst, int K) {
         memcpy(dst + nb * 128 + b * 64, blk + 128, 64);
         memcpy(dst + nb * 192 + b * 16, blk + 192, 16);
         memcpy(dst + nb * 208 + b * 2, blk + 208, 2);
+    }
+    return QMM_OK;
+}
+
+// gemv.hip:1351-1354: GGUF Q8_0 row {f16 d, i8 qs[32]} x K/32 -> [qs K][d (K/32) x f16]
+int qmm_repack_row_q8_0(const uint8_t* src, uint8_t* dst, int K) {
+    if (!src || !dst) return QMM_ERR_NULL;
+    if (K <= 0 || K % 32 != 0) return QMM_ERR_SHAPE;
+    for (size_t b = 0; b < (size_t)K / 32; ++b) {
+        memcpy(dst + b * 32, src + b * 34 + 2, 32);
+        memcpy(dst + (size_t)K + b * 2, src + b * 34, 2);
+    }
+    return QMM_OK;
+}
+
+// gemv.hip:1458-1465: GGUF Q5_1 row {f16 d, f16 m, u8 qh[4], u8 qs[16]} x K/32 ->
+// [qs K/2][qh K/8][d (K/32) x f16][m (K/32) x f16]
+int qmm_repack_row_q5_1(const uint8_t* src, uint8_t* dst, int K) {
+    if (!src || !dst) return QMM_ERR_NULL;
+    if (K <= 0 || K % 32 != 0) return QMM_ERR_SHAPE;
+    const size_t qh = (size_t)K / 2, dd = qh + (size_t)K / 8, mm = dd + (size_t)K / 16;
+    for (size_t b = 0; b < (size_t)K / 32; ++b) {
+        const uint8_t* blk = src + b * 24;
+        memcpy(dst + b * 16, blk + 8, 16);
+        memcpy(dst + qh + b * 4, blk + 4, 4);
+        memcpy(dst + dd + b * 2, blk, 2);
+        memcpy(dst + mm + b * 2, blk + 2, 2);
+    }
+    return QMM_OK;
+}
+
+// gemv.hip:1448-1457: GGUF Q5_0 row {f16 d, u8 qh[4], u8 qs[16]} x K/32 -> the Q5_1 SoA layout with
+// m = f16(-16 d): w = q d - 16 d = (q - 16) d, exactly
+int qmm_repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K) {
+    if (!src || !dst) return QMM_ERR_NULL;
+    if (K <= 0 || K % 32 != 0) return QMM_ERR_SHAPE;
+    const size_t qh = (size_t)K / 2, dd = qh + (size_t)K / 8, mm = dd + (size_t)K / 16;
+    for (size_t b = 0; b < (size_t)K / 32; ++b) {
+        const uint8_t* blk = src + b * 22;
+        uint16_t d;
+        memcpy(&d, blk, 2);
+        const uint16_t m = f2h_host(-16.0f * h2f_host(d));
+        memcpy(dst + b * 16, blk + 6, 16);
+        memcpy(dst + qh + b * 4, blk + 2, 4);
+        memcpy(dst + dd + b * 2, &d, 2);
+        memcpy(dst + mm + b * 2, &m, 2);
     }
     return QMM_OK;
 }

@@ -796,7 +796,10 @@ int launch_q4k_f32(const void* W, const float* x, float* y, int N, int K, hipStr
     return QMM_OK;
 }
 
-bool fmt_supported_q8(int fmt) { return fmt == QMM_Q4_K || fmt == QMM_Q6_K || fmt == QMM_Q6_K_SOA; }
+bool fmt_supported_q8(int fmt) {
+    return fmt == QMM_Q4_K || fmt == QMM_Q6_K || fmt == QMM_Q6_K_SOA || fmt == QMM_Q5_K || fmt == QMM_IQ4_XS ||
+           fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA;
+}
 
 int check_gemv_shape(int fmt, int N, int K) {
     if (N <= 0 || K <= 0 || K % 256 != 0) return QMM_ERR_SHAPE;
@@ -807,6 +810,8 @@ int check_gemv_shape(int fmt, int N, int K) {
 }  // namespace
 
 int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    if (fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA)
+        return gemv_fmt_dispatch(fmt, W, x, y, N, K, ncol, s);
     switch (ncol) {
         case 1: return launch_gemv_q8_ncol<1>(fmt, W, x, y, N, K, s);
         case 2: return launch_gemv_q8_ncol<2>(fmt, W, x, y, N, K, s);

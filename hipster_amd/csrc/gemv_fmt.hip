@@ -1,0 +1,232 @@
+// gemv_fmt.hip -- q8-activation GEMV on gfx950 for the other weight formats of the call surface:
+// Q5_K and IQ4_XS (GGUF blocks) and Q8_0_SOA / Q5_1_SOA (the engine's load-time row-SoA repacks of
+// Q8_0 and Q5_1 / Q5_0 rows).  Reached through qmm_gemv_q8 / qmm_gemv_multi (gemv.hip), which is
+// the reference's gemv_q8 / gemv_multi (engine/kernels/gemv.h:25,28) for these formats; the
+// per-format arithmetic is the reference's (block decoders gemv.hip:90-163,214-268).
+//
+// One row per wave.  A unit is one scale's worth of weights -- 32 (one sub-block) for IQ4_XS,
+// Q8_0_SOA and Q5_1_SOA, 64 for Q5_K (the two sub-blocks sharing one 32-byte qs pair) -- and lane l
+// takes units l, l + 64, ... of the row, NIT at a time, with all of a pass's weight loads issued
+// before its compute.  The q8 x of a unit (32 bytes per sub-block, its d and s) is read from
+// global memory; the four rows of a workgroup read the same x, which L1 serves.  Per sub-block the
+// weights become int8 lanes of a dword, the integer dot with the q8 x uses v_dot4_i32_i8, and the
+// reference's fix-up follows:
+//   Q5_K    acc += (d sc) xd isum - (dmin m) xs          (q = nibble | fifth bit << 4, 0..31)
+//   IQ4_XS  acc += (d (ls - 32)) xd isum                 (q = level[nibble], signed)
+//   Q8_0    acc += d xd isum
+//   Q5_1    acc += d xd isum + m xs                      (q = nibble | fifth bit << 4)
+// A lane accumulates its units in a fixed order and the wave reduces with a fixed butterfly, so a
+// column's result does not depend on ncol (T-invariant).  K % 256 == 0 (checked by the caller).
+#include "qmm_common.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace qmm {
+namespace {
+
+constexpr int kFmtBlock = 256, kFmtWaves = kFmtBlock / 64;
+
+template <int F>
+__device__ __forceinline__ size_t fmt_row_bytes(int K) {
+    if constexpr (F == QMM_Q5_K) return (size_t)K / 256 * 176;
+    else if constexpr (F == QMM_IQ4_XS) return (size_t)K / 256 * 136;
+    else if constexpr (F == QMM_Q8_0_SOA) return (size_t)K + (size_t)K / 16;
+    else return (size_t)K / 32 * 24;                        // QMM_Q5_1_SOA
+}
+template <int F>
+__host__ __device__ __forceinline__ int fmt_units(int K) { return F == QMM_Q5_K ? K / 64 : K / 32; }
+
+// the 16 signed levels of IQ4 (quant.h:35) as bytes, four per little-endian word: levels 0-3, 4-7,
+// 8-11, 12-15
+constexpr uint32_t kIq4L0 = 0xBFAD9881u, kIq4L1 = 0xF6EADDCFu, kIq4H0 = 0x26190D01u, kIq4H1 = 0x71594535u;
+// four nibbles (one per byte, 0..15) -> four signed levels: one byte permute per half of the table,
+// then a per-byte select on bit 3
+__device__ __forceinline__ uint32_t iq4_levels4(uint32_t nib) {
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4L1, kIq4L0, sel), hi = __builtin_amdgcn_perm(kIq4H1, kIq4H0, sel);
+    const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xffu;
+    return (hi & m) | (lo & ~m);
+}
+// four bits h (0..15) -> bit 4 of each byte: h * 0x02040810 puts bit i of h at bit 8i + 4 (and the
+// other partial products at positions that are not 4 mod 8, none overlapping), the mask keeps those
+__device__ __forceinline__ uint32_t bits4_to_byte_bit4(uint32_t h) { return (h * 0x02040810u) & 0x10101010u; }
+
+// 32 int8 weights (8 dwords) against 32 q8 x bytes (two 16-byte loads)
+__device__ __forceinline__ int dot32(const uint32_t (&w)[8], const int8_t* __restrict__ x) {
+    const uint4 a = ld16(x), b = ld16(x + 16);
+    int s = sdot4(w[0], a.x, 0);
+    s = sdot4(w[1], a.y, s);
+    s = sdot4(w[2], a.z, s);
+    s = sdot4(w[3], a.w, s);
+    s = sdot4(w[4], b.x, s);
+    s = sdot4(w[5], b.y, s);
+    s = sdot4(w[6], b.z, s);
+    return sdot4(w[7], b.w, s);
+}
+
+// ---- per-format unit: its raw bytes, their load, and the unit's contribution to one column ----
+template <int F> struct FmtUnit;
+
+template <> struct FmtUnit<QMM_Q8_0_SOA> {            // row = [qs K][d (K/32) x f16]
+    struct Raw { uint4 a, b; uint32_t d; };
+    static __device__ __forceinline__ void load(const uint8_t* rp, int K, int u, Raw& r) {
+        r.a = ld16(rp + 32 * (size_t)u);
+        r.b = ld16(rp + 32 * (size_t)u + 16);
+        r.d = *(const uint16_t*)(rp + K + 2 * (size_t)u);
+    }
+    static __device__ __forceinline__ float col(const Raw& r, int u, const int8_t* xq, const float* xd, const float*) {
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        return h2f(r.d) * xd[u] * (float)dot32(w, xq + 32 * u);
+    }
+};
+
+template <> struct FmtUnit<QMM_Q5_1_SOA> {            // row = [qs K/2][qh K/8][d K/32 x f16][m K/32 x f16]
+    struct Raw { uint4 qs; uint32_t qh, d, m; };
+    static __device__ __forceinline__ void load(const uint8_t* rp, int K, int u, Raw& r) {
+        r.qs = ld16(rp + 16 * (size_t)u);
+        r.qh = *(const uint32_t*)(rp + K / 2 + 4 * (size_t)u);
+        r.d = *(const uint16_t*)(rp + K / 2 + K / 8 + 2 * (size_t)u);
+        r.m = *(const uint16_t*)(rp + K / 2 + K / 8 + K / 16 + 2 * (size_t)u);
+    }
+    static __device__ __forceinline__ float col(const Raw& r, int u, const int8_t* xq, const float* xd, const float* xs) {
+        // weight j (< 16): low nibble of qs byte j, fifth bit = qh bit j; weight j + 16: high nibble,
+        // qh bit j + 16 (quant.h:82-88)
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t w[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            w[k] = (q[k] & 0x0f0f0f0fu) | bits4_to_byte_bit4((r.qh >> (4 * k)) & 0xfu);
+            w[4 + k] = ((q[k] >> 4) & 0x0f0f0f0fu) | bits4_to_byte_bit4((r.qh >> (16 + 4 * k)) & 0xfu);
+        }
+        return h2f(r.d) * xd[u] * (float)dot32(w, xq + 32 * u) + h2f(r.m) * xs[u];
+    }
+};
+
+template <> struct FmtUnit<QMM_IQ4_XS> {              // block = {f16 d, u16 scales_h, u8 scales_l[4], qs[128]}
+    struct Raw { uint2 hd; uint4 qs; };
+    static __device__ __forceinline__ void load(const uint8_t* rp, int, int u, Raw& r) {
+        const uint8_t* blk = rp + (size_t)(u >> 3) * 136;
+        r.hd = *(const uint2*)blk;
+        r.qs = ld16_a4(blk + 8 + 16 * (u & 7));              // 136-byte blocks: 8-byte aligned
+    }
+    static __device__ __forceinline__ float col(const Raw& r, int u, const int8_t* xq, const float* xd, const float*) {
+        const int ib = u & 7;
+        const int ls = (int)((r.hd.y >> (4 * ib)) & 0xfu) | (int)(((r.hd.x >> (16 + 2 * ib)) & 3u) << 4);
+        const float dl = h2f(r.hd.x) * (float)(ls - 32);
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t w[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            w[k] = iq4_levels4(q[k] & 0x0f0f0f0fu);            // weights 4k..4k+3
+            w[4 + k] = iq4_levels4((q[k] >> 4) & 0x0f0f0f0fu); // weights 16+4k..
+        }
+        return dl * xd[u] * (float)dot32(w, xq + 32 * u);
+    }
+};
+
+template <> struct FmtUnit<QMM_Q5_K> {                // block = {f16 d, dmin, scales[12], qh[32], qs[128]}
+    struct Raw { uint4 hd, h0, h1, q0, q1; };
+    static __device__ __forceinline__ void load(const uint8_t* rp, int, int u, Raw& r) {
+        const uint8_t* blk = rp + (size_t)(u >> 2) * 176;     // 176-byte blocks: 16-byte aligned
+        r.hd = ld16(blk);
+        r.h0 = ld16(blk + 16);
+        r.h1 = ld16(blk + 32);
+        r.q0 = ld16(blk + 48 + 32 * (u & 3));
+        r.q1 = ld16(blk + 64 + 32 * (u & 3));
+    }
+    static __device__ __forceinline__ float col(const Raw& r, int u, const int8_t* xq, const float* xd, const float* xs) {
+        // pair j of block b: weights 64j + l (sub-block 2j) = low nibble of qs[32j + l] with bit 2j of
+        // qh[l] as the fifth bit, 64j + 32 + l (sub-block 2j + 1) = high nibble with bit 2j + 1
+        const int j = u & 3, sb = 2 * u;                     // global sub-block index of 2j
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t h[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+        uint32_t wl[8], wh[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            wl[k] = (q[k] & 0x0f0f0f0fu) | (((h[k] >> (2 * j)) & 0x01010101u) << 4);
+            wh[k] = ((q[k] >> 4) & 0x0f0f0f0fu) | (((h[k] >> (2 * j + 1)) & 0x01010101u) << 4);
+        }
+        const int i0 = dot32(wl, xq + 32 * sb), i1 = dot32(wh, xq + 32 * sb + 32);
+        const float d = h2f(r.hd.x), dmin = h2f(r.hd.x >> 16);
+        const Q4kScaleBytes s = q4k_scale_bytes(r.hd.y, r.hd.z, r.hd.w);
+        const float d0 = d * (float)byte8(s.sc_lo, s.sc_hi, 2 * j), m0 = dmin * (float)byte8(s.m_lo, s.m_hi, 2 * j);
+        const float d1 = d * (float)byte8(s.sc_lo, s.sc_hi, 2 * j + 1), m1 = dmin * (float)byte8(s.m_lo, s.m_hi, 2 * j + 1);
+        return d0 * xd[sb] * (float)i0 - m0 * xs[sb] + (d1 * xd[sb + 1] * (float)i1 - m1 * xs[sb + 1]);
+    }
+};
+
+template <int F, int NCOL, int NIT>
+__global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                        const float* __restrict__ xd, const float* __restrict__ xs,
+                                                        float* __restrict__ y, int N, int K) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * kFmtWaves + wave;
+    const uint8_t* rp = W + (size_t)min(row, N - 1) * fmt_row_bytes<F>(K);
+    const int U = fmt_units<F>(K), nsb = K / 32;
+    float acc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+    for (int base = 0; base < U; base += 64 * NIT) {
+        typename FmtUnit<F>::Raw R[NIT];
+#pragma unroll
+        for (int i = 0; i < NIT; ++i) FmtUnit<F>::load(rp, K, min(base + lane + 64 * i, U - 1), R[i]);
+#pragma unroll
+        for (int i = 0; i < NIT; ++i) {
+            const int u = base + lane + 64 * i, uc = min(u, U - 1);
+#pragma unroll
+            for (int c = 0; c < NCOL; ++c) {
+                const float v = FmtUnit<F>::col(R[i], uc, xq + (size_t)c * K, xd + (size_t)c * nsb, xs + (size_t)c * nsb);
+                acc[c] += u < U ? v : 0.f;
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = wave_sum(acc[c]);
+    if (lane == 0 && row < N) {
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+    }
+}
+
+template <int F, int NCOL>
+int launch_fmt(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    const int grid = (N + kFmtWaves - 1) / kFmtWaves;
+    const int per_lane = (fmt_units<F>(K) + 63) / 64;
+#define QMM_FMTL(IV) hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV>), dim3(grid), dim3(kFmtBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K)
+    if (per_lane <= 1) QMM_FMTL(1);
+    else if (per_lane == 2) QMM_FMTL(2);
+    else if (per_lane == 3) QMM_FMTL(3);
+    else QMM_FMTL(4);                                      // longer rows: passes of 4 units per lane
+#undef QMM_FMTL
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+template <int NCOL>
+int launch_fmt_ncol(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    switch (fmt) {
+        case QMM_Q5_K: return launch_fmt<QMM_Q5_K, NCOL>(W, x, y, N, K, s);
+        case QMM_IQ4_XS: return launch_fmt<QMM_IQ4_XS, NCOL>(W, x, y, N, K, s);
+        case QMM_Q8_0_SOA: return launch_fmt<QMM_Q8_0_SOA, NCOL>(W, x, y, N, K, s);
+        case QMM_Q5_1_SOA: return launch_fmt<QMM_Q5_1_SOA, NCOL>(W, x, y, N, K, s);
+        default: return QMM_ERR_FORMAT;
+    }
+}
+
+}  // namespace
+
+int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    switch (ncol) {
+        case 1: return launch_fmt_ncol<1>(fmt, W, x, y, N, K, s);
+        case 2: return launch_fmt_ncol<2>(fmt, W, x, y, N, K, s);
+        case 3: return launch_fmt_ncol<3>(fmt, W, x, y, N, K, s);
+        case 4: return launch_fmt_ncol<4>(fmt, W, x, y, N, K, s);
+        case 5: return launch_fmt_ncol<5>(fmt, W, x, y, N, K, s);
+        case 6: return launch_fmt_ncol<6>(fmt, W, x, y, N, K, s);
+        case 7: return launch_fmt_ncol<7>(fmt, W, x, y, N, K, s);
+        case 8: return launch_fmt_ncol<8>(fmt, W, x, y, N, K, s);
+        default: return QMM_ERR_SHAPE;
+    }
+}
+
+}  // namespace qmm

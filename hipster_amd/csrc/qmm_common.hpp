@@ -128,6 +128,8 @@ inline int device_cu_count() {
 // moe_prefill.hip over implicit tiles of `trows` consecutive rows (one Q4_K matrix, no row gather):
 // the dense GEMM hands it the columns that would leave its last round of 256 x 256 tiles thin.
 int launch_q4k_rows_gemm(const void* W, const uint16_t* A, float* D, int M, int N, int K, int ldd, int trows, hipStream_t s);
+// q8 GEMV of gemv_fmt.hip for QMM_Q5_K, QMM_IQ4_XS, QMM_Q8_0_SOA, QMM_Q5_1_SOA (ncol 1..8, K % 256 == 0)
+int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s);
 
 }  // namespace qmm
 

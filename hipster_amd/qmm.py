@@ -64,6 +64,29 @@ def repack_row_q6_K(src, K):
     return dst
 
 
+def _repack(name, src, K, dst_bytes):
+    import numpy as np
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.empty(dst_bytes, dtype=np.uint8)
+    check(getattr(_lib.lib(), "qmm_" + name)(src.ctypes.data, dst.ctypes.data, K), name)
+    return dst
+
+
+def repack_row_q8_0(src, K):
+    """Host repack of one GGUF Q8_0 row to the Q8_0_SOA layout (gemv.h:16, gemv.hip:1351-1354)."""
+    return _repack("repack_row_q8_0", src, K, K + K // 16)
+
+
+def repack_row_q5_1(src, K):
+    """Host repack of one GGUF Q5_1 row to the Q5_1_SOA layout (gemv.h:17, gemv.hip:1458-1465)."""
+    return _repack("repack_row_q5_1", src, K, K // 32 * 24)
+
+
+def repack_row_q5_0(src, K):
+    """Host repack of one GGUF Q5_0 row to the Q5_1_SOA layout, m = -16 d (gemv.h:18, gemv.hip:1448-1457)."""
+    return _repack("repack_row_q5_0", src, K, K // 32 * 24)
+
+
 def quantize_x_q8(x, out, ncol, K, stream=None):
     """gemv.h:10: x f32 [ncol][K] -> out (XQ8Buf)."""
     _dev(x, torch.float32, "x")

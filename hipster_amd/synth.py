@@ -7,6 +7,10 @@ on every host running the same numpy.  Distributions:
   appear), the 12 scale bytes and the 128 quant bytes uniform random bytes, which makes the 6-bit
   scales/mins and the 4-bit quants exactly uniform.
 * Q6_K block (quant.h:24): ql, qh and the int8 scales uniform random bytes, d = fp16(|N(0, 0.01)|).
+* The other formats of the call surface (quant.h:23,26-30), same recipe: every scale fp16(|N(0, 0.01)|)
+  (the Q5_1 offset m fp16(N(0, 0.01)), signed), every other byte uniform random -- Q5_K (176 B / 256),
+  IQ4_XS (136 B / 256), Q8_0 (34 B / 32), Q5_1 (24 B / 32), Q5_0 (22 B / 32), and the row-SoA
+  repacks the engine makes of Q8_0 and Q5_1 / Q5_0 rows at load time.
 * activations N(0, 1) f32 (or bf16 for the prefill configs).
 * router logits N(0, 1); for the prefill MoE config plus a Zipf(s=1.1) bias
   b_e = -1.1 * ln(rank_e) with ranks a seeded permutation of 1..n_exp.
@@ -17,8 +21,12 @@ Q4K_BYTES = 144
 Q6K_BYTES = 210
 QK = 256
 
-# format ids (include/hipster_qmm.h)
-Q4_K, Q6_K_SOA, Q6_K = 0, 3, 6
+# format ids (include/hipster_qmm.h); 8, 9, 10 are the GGUF-native 32-weight block rows that the
+# engine repacks into Q8_0_SOA / Q5_1_SOA (they are not weight formats of the C ABI)
+Q4_K, Q5_K, IQ4_XS, Q6_K_SOA, Q8_0_SOA, Q5_1_SOA, Q6_K = 0, 1, 2, 3, 4, 5, 6
+Q8_0, Q5_1, Q5_0 = 8, 9, 10
+BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), IQ4_XS: (256, 136), Q6_K: (256, 210), Q6_K_SOA: (256, 210),
+         Q8_0: (32, 34), Q5_1: (32, 24), Q5_0: (32, 22), Q8_0_SOA: (32, 34), Q5_1_SOA: (32, 24)}
 
 
 def rng(seed):
@@ -46,24 +54,49 @@ def q6k_blocks(g, nblocks):
     return out
 
 
+def blocks(g, fmt, nblocks):
+    """nblocks GGUF blocks of fmt (Q4_K, Q5_K, IQ4_XS, Q6_K, Q8_0, Q5_1, Q5_0) as uint8 [nblocks, bytes]."""
+    if fmt == Q4_K:
+        return q4k_blocks(g, nblocks)
+    if fmt == Q6_K:
+        return q6k_blocks(g, nblocks)
+    nbytes = BLOCK[fmt][1]
+    out = g.integers(0, 256, (nblocks, nbytes), dtype=np.uint8)
+    if fmt in (Q5_K, Q8_0, Q5_0, IQ4_XS):        # d (and Q5_K's dmin) at bytes 0..1 (2..3)
+        out[:, 0:2] = _f16_abs_normal(g, nblocks).view(np.uint8).reshape(nblocks, 2)
+        if fmt == Q5_K:
+            out[:, 2:4] = _f16_abs_normal(g, nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif fmt == Q5_1:                              # d, then the signed offset m
+        out[:, 0:2] = _f16_abs_normal(g, nblocks).view(np.uint8).reshape(nblocks, 2)
+        out[:, 2:4] = g.normal(0.0, 0.01, nblocks).astype(np.float16).view(np.uint8).reshape(nblocks, 2)
+    else:
+        raise ValueError(f"format {fmt}")
+    return out
+
+
 def row_bytes(fmt, K):
-    assert K % QK == 0
-    return K // QK * (Q4K_BYTES if fmt == Q4_K else Q6K_BYTES)
+    per, nbytes = BLOCK[fmt]
+    assert K % per == 0
+    if fmt == Q8_0_SOA:
+        return K + K // 16
+    return K // per * nbytes
 
 
 def matrix(seed, fmt, N, K):
-    """A [N][K] weight in format fmt as uint8 [N, row_bytes].  Q6_K_SOA is the SoA repack of the
-    GGUF Q6_K matrix drawn with the same seed."""
+    """A [N][K] weight in format fmt as uint8 [N, row_bytes].  The SoA formats are the repacks of
+    the GGUF matrix drawn with the same seed (Q6_K -> Q6_K_SOA, Q8_0 -> Q8_0_SOA, Q5_1 -> Q5_1_SOA)."""
     g = rng(seed)
-    nb = K // QK
-    if fmt == Q4_K:
-        return q4k_blocks(g, N * nb).reshape(N, nb * Q4K_BYTES)
-    blocks = q6k_blocks(g, N * nb).reshape(N, nb, Q6K_BYTES)
-    if fmt == Q6_K:
-        return blocks.reshape(N, nb * Q6K_BYTES)
+    src = {Q6_K_SOA: Q6_K, Q8_0_SOA: Q8_0, Q5_1_SOA: Q5_1}.get(fmt, fmt)
+    per, nbytes = BLOCK[src]
+    nb = K // per
+    W = blocks(g, src, N * nb).reshape(N, nb * nbytes)
     if fmt == Q6_K_SOA:
-        return repack_q6k_soa(blocks.reshape(N, nb * Q6K_BYTES), K)
-    raise ValueError(f"format {fmt}")
+        return repack_q6k_soa(W, K)
+    if fmt == Q8_0_SOA:
+        return repack_q8_0_soa(W, K)
+    if fmt == Q5_1_SOA:
+        return repack_q5_1_soa(W, K)
+    return W
 
 
 def repack_q6k_soa(W, K):
@@ -73,6 +106,21 @@ def repack_q6k_soa(W, K):
     b = W.reshape(N, nb, Q6K_BYTES)
     return np.concatenate([b[:, :, :128].reshape(N, -1), b[:, :, 128:192].reshape(N, -1),
                            b[:, :, 192:208].reshape(N, -1), b[:, :, 208:210].reshape(N, -1)], axis=1)
+
+
+def repack_q8_0_soa(W, K):
+    """GGUF Q8_0 rows -> [qs K][d (K/32) x f16] per row (engine/kernels/gemv.hip:1351-1354)."""
+    N = W.shape[0]
+    b = W.reshape(N, K // 32, 34)
+    return np.concatenate([b[:, :, 2:].reshape(N, -1), b[:, :, :2].reshape(N, -1)], axis=1)
+
+
+def repack_q5_1_soa(W, K):
+    """GGUF Q5_1 rows -> [qs K/2][qh K/8][d (K/32) x f16][m (K/32) x f16] (gemv.hip:1458-1465)."""
+    N = W.shape[0]
+    b = W.reshape(N, K // 32, 24)
+    return np.concatenate([b[:, :, 8:24].reshape(N, -1), b[:, :, 4:8].reshape(N, -1), b[:, :, 0:2].reshape(N, -1),
+                           b[:, :, 2:4].reshape(N, -1)], axis=1)
 
 
 def experts(seed, fmt, n_exp, N, K):

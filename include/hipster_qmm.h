@@ -41,11 +41,11 @@ enum {
  * plus QMM_Q6_K, the GGUF-native 210-byte Q6_K block read without a repack (this build). ---- */
 enum {
     QMM_Q4_K = 0,      /* GGUF block_q4_K, 144 B / 256 weights (engine/src/quant.h:22) */
-    QMM_Q5_K = 1,      /* not supported yet */
-    QMM_IQ4_XS = 2,    /* not supported yet */
+    QMM_Q5_K = 1,      /* GGUF block_q5_K, 176 B / 256 weights (quant.h:23); GEMV only */
+    QMM_IQ4_XS = 2,    /* GGUF block_iq4_xs, 136 B / 256 weights (quant.h:30); GEMV only */
     QMM_Q6_K_SOA = 3,  /* Q6_K rows repacked [ql K/2][qh K/4][sc K/16][d K/128] (gemv.h:15) */
-    QMM_Q8_0_SOA = 4,  /* not supported yet */
-    QMM_Q5_1_SOA = 5,  /* not supported yet */
+    QMM_Q8_0_SOA = 4,  /* Q8_0 rows repacked [qs K][d K/32 x f16] (gemv.h:16); GEMV only */
+    QMM_Q5_1_SOA = 5,  /* Q5_1 / Q5_0 rows repacked [qs K/2][qh K/8][d K/32][m K/32] (gemv.h:17-18); GEMV only */
     QMM_Q6_K = 6       /* GGUF block_q6_K, 210 B / 256 weights (quant.h:24) */
 };
 
@@ -63,10 +63,20 @@ typedef struct { int32_t expert, k0, ncols; } qmm_moe_tile;
 /* ---- library / host helpers ---- */
 const char* qmm_version(void);
 const char* qmm_status_string(int status);
-/* bytes of one row of K weights (reference: wfmt_row_bytes, gemv.hip:1337-1340); 0 if unknown */
+/* bytes of one row of K weights (reference: wfmt_row_bytes, gemv.hip:1337-1340); 0 if the format
+ * is unknown or K is not a multiple of its block (256, or 32 for QMM_Q8_0_SOA / QMM_Q5_1_SOA) */
 size_t qmm_wfmt_row_bytes(int fmt, int K);
 /* one GGUF Q6_K row -> the SoA layout of QMM_Q6_K_SOA (reference: repack_row_q6_K, gemv.hip:1341-1350) */
 int qmm_repack_row_q6_K(const uint8_t* src, uint8_t* dst, int K);
+/* one GGUF Q8_0 row (34 B / 32) -> QMM_Q8_0_SOA, same size (reference: repack_row_q8_0, gemv.h:16,
+ * gemv.hip:1351-1354); K % 32 == 0 */
+int qmm_repack_row_q8_0(const uint8_t* src, uint8_t* dst, int K);
+/* one GGUF Q5_1 row (24 B / 32) -> QMM_Q5_1_SOA, same size (reference: repack_row_q5_1, gemv.h:17,
+ * gemv.hip:1458-1465); K % 32 == 0 */
+int qmm_repack_row_q5_1(const uint8_t* src, uint8_t* dst, int K);
+/* one GGUF Q5_0 row (22 B / 32) -> QMM_Q5_1_SOA (K*24/32 bytes) with m = f16(-16 d), exact
+ * (reference: repack_row_q5_0, gemv.h:18, gemv.hip:1448-1457); K % 32 == 0 */
+int qmm_repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K);
 
 /* ---- activation quantiser (reference: quantize_x_q8, gemv.h:10, gemv.hip:36-51,1333-1336) ----
  * per 32 values: d = amax/127, q = round-half-even(x*127/amax), s = d*sum(q); x f32 [ncol][K]. */

@@ -45,6 +45,15 @@ inline size_t wfmt_row_bytes(WFmt f, int K) { return qmm_wfmt_row_bytes((int)f, 
 inline void repack_row_q6_K(const uint8_t* src, uint8_t* dst, int K) {
     detail::ck(qmm_repack_row_q6_K(src, dst, K), "repack_row_q6_K");
 }
+inline void repack_row_q8_0(const uint8_t* src, uint8_t* dst, int K) {                       // gemv.h:16
+    detail::ck(qmm_repack_row_q8_0(src, dst, K), "repack_row_q8_0");
+}
+inline void repack_row_q5_1(const uint8_t* src, uint8_t* dst, int K) {                       // gemv.h:17
+    detail::ck(qmm_repack_row_q5_1(src, dst, K), "repack_row_q5_1");
+}
+inline void repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K) {                       // gemv.h:18
+    detail::ck(qmm_repack_row_q5_0(src, dst, K), "repack_row_q5_0");
+}
 inline void gemv_q8(WFmt f, const void* W, XQ8 x, float* y, int N, int K, int ncol, int tpr, int rpt, hipStream_t s) {
     detail::ck(qmm_gemv_q8((int)f, W, to_c(x), y, N, K, ncol, tpr, rpt, (void*)s), "gemv_q8");
 }

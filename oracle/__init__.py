@@ -1,5 +1,6 @@
-"""ctypes binding of the CPU oracle (oracle/liboracle.so) and of the reference's own quant.h
-(oracle/_ref/libqmm_ref.so, when it was built).
+"""ctypes binding of the CPU oracle (oracle/liboracle.so), of the reference's own quant.h
+(oracle/_ref/libqmm_ref.so) and of the reference's gemv.hip layout helpers
+(oracle/_ref/libqmm_ref_gemv.so), the latter two when they were built.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
 leg, as the checker.  The product package (hipster_amd/) never imports it.
@@ -12,10 +13,13 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(_HERE, "liboracle.so")
 REF_LIB = os.path.join(_HERE, "_ref", "libqmm_ref.so")
+REF_GEMV_LIB = os.path.join(_HERE, "_ref", "libqmm_ref_gemv.so")
 
-Q4_K, Q6_K_SOA, Q6_K = 0, 3, 6
+Q4_K, Q5_K, IQ4_XS, Q6_K_SOA, Q8_0_SOA, Q5_1_SOA, Q6_K = 0, 1, 2, 3, 4, 5, 6
+Q8_0, Q5_1, Q5_0 = 8, 9, 10
 _o = None
 _r = None
+_rg = None
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -35,12 +39,19 @@ def lib():
         L.qo_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.qo_f32_to_bf16.restype = ctypes.c_uint16
         L.qo_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.qo_f32_to_f16.restype = ctypes.c_uint16
+        L.qo_f32_to_f16.argtypes = [ctypes.c_float]
+        L.qo_k_granule.restype = I
+        L.qo_k_granule.argtypes = [I]
         L.qo_row_bytes.restype = ctypes.c_size_t
         L.qo_row_bytes.argtypes = [I, I]
         for name, args in {
             "qo_scale_min_k4": [I, P, P, P],
             "qo_dequant_q4_K_block": [P, P], "qo_dequant_q6_K_block": [P, P],
             "qo_repack_row_q6_K": [P, P, I],
+            "qo_dequant_q5_K_block": [P, P], "qo_dequant_iq4_xs_block": [P, P], "qo_dequant_q8_0_block": [P, P],
+            "qo_dequant_q5_1_block": [P, P], "qo_dequant_q5_0_block": [P, P],
+            "qo_repack_row_q8_0": [P, P, I], "qo_repack_row_q5_1": [P, P, I], "qo_repack_row_q5_0": [P, P, I],
             "qo_dequant_row": [I, P, P, I],
             "qo_dequant_matrix": [I, P, I, I, P, I], "qo_dequant_matrix_bf16": [I, P, I, I, P, I],
             "qo_quantize_x_q8": [P, I, P, P, P], "qo_q8_to_f32": [P, P, I, P],
@@ -57,9 +68,8 @@ def lib():
         }.items():
             f = getattr(L, name)
             f.argtypes = args
-            f.restype = None if name in ("qo_scale_min_k4", "qo_dequant_q4_K_block", "qo_dequant_q6_K_block",
-                                         "qo_repack_row_q6_K", "qo_quantize_x_q8", "qo_q8_to_f32", "qo_silu_mul",
-                                         "qo_moe_route") else I
+            f.restype = None if (name.startswith("qo_dequant_q") and name.endswith("_block")) or name.startswith("qo_repack_row") \
+                or name in ("qo_scale_min_k4", "qo_quantize_x_q8", "qo_q8_to_f32", "qo_silu_mul", "qo_moe_route") else I
         _o = L
     return _o
 
@@ -241,3 +251,18 @@ def gemm_wq_ref(fmt, W, A_bf16, M, N, K, ms, ns):
     if lib().qo_gemm_wq_ref(fmt, _ptr(W), _ptr(A), M, N, K, _ptr(ms), _ptr(ns), len(ms), _ptr(out)) != 0:
         raise ValueError("gemm_wq_ref")
     return out
+
+
+def ref_gemv_lib():
+    """The reference's engine/kernels/gemv.hip host layout helpers (row bytes, load-time repacks)
+    compiled by oracle/Makefile, or None when they were not built.  Host functions only."""
+    global _rg
+    if _rg is None and os.path.exists(REF_GEMV_LIB):
+        L = ctypes.CDLL(REF_GEMV_LIB)
+        L.refg_wfmt_row_bytes.restype = ctypes.c_size_t
+        L.refg_wfmt_row_bytes.argtypes = [I, I]
+        for n in ("refg_repack_row_q6_K", "refg_repack_row_q8_0", "refg_repack_row_q5_1", "refg_repack_row_q5_0"):
+            getattr(L, n).argtypes = [P, P, I]
+            getattr(L, n).restype = None
+        _rg = L
+    return _rg

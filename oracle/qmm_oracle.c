@@ -51,6 +51,24 @@ float qo_f16_to_f32(uint16_t h) {
     else bits = sign | ((exp + 112) << 23) | (man << 13);
     float f; memcpy(&f, &bits, 4); return f;
 }
+/* float -> IEEE half, round to nearest even (the conversion `(_Float16)x` of gemv.hip:1453);
+ * overflow gives infinity, tiny values become subnormal halves.  NaN is not needed here. */
+uint16_t qo_f32_to_f16(float f) {
+    uint32_t u; memcpy(&u, &f, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const float a = fabsf(f);
+    if (!(a < 65520.f)) return (uint16_t)(sign | 0x7c00u);               /* rounds to infinity */
+    if (a < 6.103515625e-05f) {                                          /* subnormal half: steps of 2^-24 */
+        const float q = nearbyintf(a * 16777216.f);                     /* exact scaling, RNE */
+        return (uint16_t)(sign | (uint32_t)q);
+    }
+    uint32_t v; memcpy(&v, &a, 4);
+    const uint32_t mant = v & 0x7fffffu, exp = (v >> 23) - 112u;         /* rebias 127 -> 15 */
+    uint32_t h = (exp << 10) | (mant >> 13);
+    const uint32_t rest = mant & 0x1fffu;                                /* 13 dropped bits */
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h;            /* RNE; a carry bumps the exponent */
+    return (uint16_t)(sign | h);
+}
 /* gemm.hip:12: bf16 = round-to-nearest-even of the top 16 bits (no NaN special case) */
 uint16_t qo_f32_to_bf16(float f) {
     uint32_t u; memcpy(&u, &f, 4);
@@ -126,19 +144,166 @@ void qo_repack_row_q6_K(const uint8_t* src, uint8_t* dst, int K) {
     }
 }
 
-size_t qo_row_bytes(int wfmt, int K) {
-    switch (wfmt) {
-        case QO_Q4_K: return (size_t)K / 256 * 144;
-        case QO_Q6_K_SOA: case QO_Q6_K: return (size_t)K / 256 * 210;
-        default: return 0;
+/* quant.h:23,54-64.  Block = {f16 d, f16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]}.  Like Q4_K,
+ * with a fifth bit per weight: weight 64j+l (l < 32) adds 16 when bit 2j of qh[l] is set, weight
+ * 64j+32+l when bit 2j+1 is.  w = (d*sc)*q - (dmin*m). */
+void qo_dequant_q5_K_block(const uint8_t* blk, float* y) {
+    uint16_t hd, hm; memcpy(&hd, blk, 2); memcpy(&hm, blk + 2, 2);
+    const float d = qo_f16_to_f32(hd), dmin = qo_f16_to_f32(hm);
+    const uint8_t* scales = blk + 4; const uint8_t* qh = blk + 16; const uint8_t* qs = blk + 48;
+    for (int j = 0; j < 4; ++j) {
+        uint8_t sc, m;
+        qo_scale_min_k4(2 * j, scales, &sc, &m);
+        const float dl = d * (float)sc, ml = dmin * (float)m;
+        qo_scale_min_k4(2 * j + 1, scales, &sc, &m);
+        const float dh = d * (float)sc, mh = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) {
+            const int lo = (qs[32 * j + l] & 0x0f) + (((qh[l] >> (2 * j)) & 1) ? 16 : 0);
+            const int hi = (qs[32 * j + l] >> 4) + (((qh[l] >> (2 * j + 1)) & 1) ? 16 : 0);
+            y[64 * j + l] = dl * (float)lo - ml;
+            y[64 * j + 32 + l] = dh * (float)hi - mh;
+        }
     }
 }
 
+/* The 16 non-linear 4-bit levels of IQ4_NL / IQ4_XS (quant.h:35; GGUF's kvalues_iq4nl). */
+const int8_t qo_iq4nl_levels[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* quant.h:30,93-100.  Block = {f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128]}.  Sub-block ib (32
+ * weights) has the 6-bit scale ls = nibble ib of scales_l | bits 2ib..2ib+1 of scales_h << 4 and
+ * dl = d*(ls - 32); its weights j and j+16 are the low and high nibbles of qs[16ib + j], mapped
+ * through the level table.  w = dl * level. */
+void qo_dequant_iq4_xs_block(const uint8_t* blk, float* y) {
+    uint16_t hd, sh; memcpy(&hd, blk, 2); memcpy(&sh, blk + 2, 2);
+    const float d = qo_f16_to_f32(hd);
+    const uint8_t* sl = blk + 4; const uint8_t* qs = blk + 8;
+    for (int ib = 0; ib < 8; ++ib) {
+        const int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 0x0f) | (((sh >> (2 * ib)) & 3) << 4);
+        const float dl = d * (float)(ls - 32);
+        for (int j = 0; j < 16; ++j) {
+            y[32 * ib + j] = dl * (float)qo_iq4nl_levels[qs[16 * ib + j] & 0x0f];
+            y[32 * ib + j + 16] = dl * (float)qo_iq4nl_levels[qs[16 * ib + j] >> 4];
+        }
+    }
+}
+
+/* quant.h:26,81.  Block = {f16 d, i8 qs[32]}: w = q*d. */
+void qo_dequant_q8_0_block(const uint8_t* blk, float* y) {
+    uint16_t hd; memcpy(&hd, blk, 2);
+    const float d = qo_f16_to_f32(hd);
+    for (int j = 0; j < 32; ++j) y[j] = (float)(int8_t)blk[2 + j] * d;
+}
+
+/* quant.h:27,82-88.  Block = {f16 d, f16 m, u8 qh[4], u8 qs[16]}: weight j (j < 16) is the low nibble
+ * of qs[j] plus 16 when bit j of the little-endian qh word is set, weight j+16 the high nibble plus
+ * 16 when bit j+16 is.  w = q*d + m. */
+void qo_dequant_q5_1_block(const uint8_t* blk, float* y) {
+    uint16_t hd, hm; uint32_t qh; memcpy(&hd, blk, 2); memcpy(&hm, blk + 2, 2); memcpy(&qh, blk + 4, 4);
+    const float d = qo_f16_to_f32(hd), m = qo_f16_to_f32(hm);
+    const uint8_t* qs = blk + 8;
+    for (int j = 0; j < 16; ++j) {
+        const int lo = (qs[j] & 0x0f) | (int)(((qh >> j) & 1u) << 4);
+        const int hi = (qs[j] >> 4) | (int)(((qh >> (j + 16)) & 1u) << 4);
+        y[j] = (float)lo * d + m;
+        y[j + 16] = (float)hi * d + m;
+    }
+}
+
+/* GGUF Q5_0 block = {f16 d, u8 qh[4], u8 qs[16]} (22 B): w = (q - 16)*d, q as in Q5_1.  The engine
+ * never dequantises it directly: it repacks Q5_0 rows into the Q5_1 row-SoA layout with m = -16d
+ * (gemv.hip:1448-1457).  This restatement is the format's definition, used to check that repack. */
+void qo_dequant_q5_0_block(const uint8_t* blk, float* y) {
+    uint16_t hd; uint32_t qh; memcpy(&hd, blk, 2); memcpy(&qh, blk + 2, 4);
+    const float d = qo_f16_to_f32(hd);
+    const uint8_t* qs = blk + 6;
+    for (int j = 0; j < 16; ++j) {
+        const int lo = (qs[j] & 0x0f) | (int)(((qh >> j) & 1u) << 4);
+        const int hi = (qs[j] >> 4) | (int)(((qh >> (j + 16)) & 1u) << 4);
+        y[j] = (float)(lo - 16) * d;
+        y[j + 16] = (float)(hi - 16) * d;
+    }
+}
+
+/* gemv.hip:1351-1354: Q8_0 row -> row-SoA [qs K][d (K/32) x f16] */
+void qo_repack_row_q8_0(const uint8_t* src, uint8_t* dst, int K) {
+    for (int b = 0; b < K / 32; ++b) {
+        memcpy(dst + (size_t)b * 32, src + (size_t)b * 34 + 2, 32);
+        memcpy(dst + (size_t)K + (size_t)b * 2, src + (size_t)b * 34, 2);
+    }
+}
+/* gemv.hip:1458-1465: Q5_1 row -> row-SoA [qs K/2][qh K/8][d (K/32) x f16][m (K/32) x f16] */
+void qo_repack_row_q5_1(const uint8_t* src, uint8_t* dst, int K) {
+    for (int b = 0; b < K / 32; ++b) {
+        const uint8_t* blk = src + (size_t)b * 24;
+        memcpy(dst + (size_t)b * 16, blk + 8, 16);
+        memcpy(dst + (size_t)K / 2 + (size_t)b * 4, blk + 4, 4);
+        memcpy(dst + (size_t)K / 2 + K / 8 + (size_t)b * 2, blk, 2);
+        memcpy(dst + (size_t)K / 2 + K / 8 + K / 16 + (size_t)b * 2, blk + 2, 2);
+    }
+}
+/* gemv.hip:1448-1457: Q5_0 row -> the Q5_1 row-SoA layout with m = f16(-16*d) (exact: a power-of-two
+ * multiple of an f16 value, rounded to f16 -- exact unless it overflows) */
+void qo_repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K) {
+    for (int b = 0; b < K / 32; ++b) {
+        const uint8_t* blk = src + (size_t)b * 22;
+        uint16_t hd; memcpy(&hd, blk, 2);
+        const uint16_t hm = qo_f32_to_f16(-16.f * qo_f16_to_f32(hd));
+        memcpy(dst + (size_t)b * 16, blk + 6, 16);
+        memcpy(dst + (size_t)K / 2 + (size_t)b * 4, blk + 2, 4);
+        memcpy(dst + (size_t)K / 2 + K / 8 + (size_t)b * 2, &hd, 2);
+        memcpy(dst + (size_t)K / 2 + K / 8 + K / 16 + (size_t)b * 2, &hm, 2);
+    }
+}
+
+size_t qo_row_bytes(int wfmt, int K) {
+    switch (wfmt) {
+        case QO_Q4_K: return (size_t)K / 256 * 144;
+        case QO_Q5_K: return (size_t)K / 256 * 176;
+        case QO_IQ4_XS: return (size_t)K / 256 * 136;
+        case QO_Q6_K_SOA: case QO_Q6_K: return (size_t)K / 256 * 210;
+        case QO_Q8_0_SOA: return (size_t)K + (size_t)K / 16;
+        case QO_Q5_1_SOA: return (size_t)K / 32 * 24;
+        case QO_Q8_0: return (size_t)K / 32 * 34;
+        case QO_Q5_1: return (size_t)K / 32 * 24;
+        case QO_Q5_0: return (size_t)K / 32 * 22;
+        default: return 0;
+    }
+}
+/* K granularity of a format: 256 for the super-block formats, 32 for the 32-weight block ones */
+int qo_k_granule(int wfmt) {
+    return (wfmt == QO_Q8_0_SOA || wfmt == QO_Q5_1_SOA || wfmt == QO_Q8_0 || wfmt == QO_Q5_1 || wfmt == QO_Q5_0) ? 32 : 256;
+}
+
 int qo_dequant_row(int wfmt, const uint8_t* row, float* y, int K) {
-    const int nb = K / 256;
-    if (K % 256 != 0) return -1;
+    const int nb = K / 256, n32 = K / 32;
+    if (!qo_row_bytes(wfmt, K) || K % qo_k_granule(wfmt) != 0) return -1;
     switch (wfmt) {
         case QO_Q4_K: for (int b = 0; b < nb; ++b) qo_dequant_q4_K_block(row + (size_t)b * 144, y + (size_t)b * 256); return 0;
+        case QO_Q5_K: for (int b = 0; b < nb; ++b) qo_dequant_q5_K_block(row + (size_t)b * 176, y + (size_t)b * 256); return 0;
+        case QO_IQ4_XS: for (int b = 0; b < nb; ++b) qo_dequant_iq4_xs_block(row + (size_t)b * 136, y + (size_t)b * 256); return 0;
+        case QO_Q8_0: for (int b = 0; b < n32; ++b) qo_dequant_q8_0_block(row + (size_t)b * 34, y + (size_t)b * 32); return 0;
+        case QO_Q5_1: for (int b = 0; b < n32; ++b) qo_dequant_q5_1_block(row + (size_t)b * 24, y + (size_t)b * 32); return 0;
+        case QO_Q5_0: for (int b = 0; b < n32; ++b) qo_dequant_q5_0_block(row + (size_t)b * 22, y + (size_t)b * 32); return 0;
+        case QO_Q8_0_SOA: {     /* gather block b back from the SoA streams, then decode as a GGUF block */
+            uint8_t blk[34];
+            for (int b = 0; b < n32; ++b) {
+                memcpy(blk, row + (size_t)K + (size_t)b * 2, 2);
+                memcpy(blk + 2, row + (size_t)b * 32, 32);
+                qo_dequant_q8_0_block(blk, y + (size_t)b * 32);
+            }
+            return 0;
+        }
+        case QO_Q5_1_SOA: {
+            uint8_t blk[24];
+            for (int b = 0; b < n32; ++b) {
+                memcpy(blk, row + (size_t)K / 2 + K / 8 + (size_t)b * 2, 2);
+                memcpy(blk + 2, row + (size_t)K / 2 + K / 8 + K / 16 + (size_t)b * 2, 2);
+                memcpy(blk + 4, row + (size_t)K / 2 + (size_t)b * 4, 4);
+                memcpy(blk + 8, row + (size_t)b * 16, 16);
+                qo_dequant_q5_1_block(blk, y + (size_t)b * 32);
+            }
+            return 0;
+        }
         case QO_Q6_K: for (int b = 0; b < nb; ++b) qo_dequant_q6_K_block(row + (size_t)b * 210, y + (size_t)b * 256); return 0;
         case QO_Q6_K_SOA: {
             /* gather block b back from the SoA streams, then decode as a GGUF block */
@@ -170,12 +335,12 @@ static void dq_body(void* p, int lo, int hi) {
     free(tmp);
 }
 int qo_dequant_matrix(int wfmt, const uint8_t* W, int N, int K, float* out, int nthreads) {
-    if (!qo_row_bytes(wfmt, K) || K % 256) return -1;
+    if (!qo_row_bytes(wfmt, K) || K % qo_k_granule(wfmt)) return -1;
     dq_ctx c = {wfmt, W, K, qo_row_bytes(wfmt, K), out, NULL};
     qo_parallel(N, nthreads, dq_body, &c); return 0;
 }
 int qo_dequant_matrix_bf16(int wfmt, const uint8_t* W, int N, int K, uint16_t* out, int nthreads) {
-    if (!qo_row_bytes(wfmt, K) || K % 256) return -1;
+    if (!qo_row_bytes(wfmt, K) || K % qo_k_granule(wfmt)) return -1;
     dq_ctx c = {wfmt, W, K, qo_row_bytes(wfmt, K), NULL, out};
     qo_parallel(N, nthreads, dq_body, &c); return 0;
 }
@@ -232,13 +397,13 @@ static void gv_ref_body(void* p, int lo, int hi) {
 }
 int qo_gemv_ref(int wfmt, const uint8_t* W, int N, int K, const float* x, int ncol,
                 double* y, double* mag, int nthreads) {
-    if (!qo_row_bytes(wfmt, K) || K % 256) return -1;
+    if (!qo_row_bytes(wfmt, K) || K % qo_k_granule(wfmt)) return -1;
     gv_ctx c = {wfmt, W, N, K, x, ncol, qo_row_bytes(wfmt, K), y, mag, NULL, NULL};
     qo_parallel(N, nthreads, gv_ref_body, &c); return 0;
 }
 int qo_gemv_ref_rows(int wfmt, const uint8_t* W, int N, int K, const float* x, int ncol,
                      const int* rows, int nrows, double* y, double* mag) {
-    if (!qo_row_bytes(wfmt, K) || K % 256) return -1;
+    if (!qo_row_bytes(wfmt, K) || K % qo_k_granule(wfmt)) return -1;
     for (int i = 0; i < nrows; ++i) if (rows[i] < 0 || rows[i] >= N) return -2;
     /* y/mag are [ncol][nrows]: reuse the body with N := nrows as the output stride */
     gv_ctx c = {wfmt, W, nrows, K, x, ncol, qo_row_bytes(wfmt, K), y, mag, NULL, rows};
@@ -261,7 +426,7 @@ static void gv_f32_body(void* p, int lo, int hi) {
     free(w);
 }
 int qo_gemv_f32(int wfmt, const uint8_t* W, int N, int K, const float* x, int ncol, float* y, int nthreads) {
-    if (!qo_row_bytes(wfmt, K) || K % 256) return -1;
+    if (!qo_row_bytes(wfmt, K) || K % qo_k_granule(wfmt)) return -1;
     gv_ctx c = {wfmt, W, N, K, x, ncol, qo_row_bytes(wfmt, K), NULL, NULL, y, NULL};
     qo_parallel(N, nthreads, gv_f32_body, &c); return 0;
 }

@@ -10,8 +10,12 @@
  * brute force) is listed in tests/test_oracle.py; a function with no such check says so here.
  *
  * Weight format ids follow the reference's WFmt enum (engine/kernels/gemv.h:13):
- *   QO_Q4_K = 0 (GGUF block, 144 B / 256 weights), QO_Q6_K_SOA = 3 (row-SoA repack of Q6_K),
- * plus one id of this build: QO_Q6_K = 6 (GGUF-native 210 B Q6_K block, no repack).
+ *   QO_Q4_K = 0 (GGUF block, 144 B / 256 weights), QO_Q5_K = 1 (176 B / 256), QO_IQ4_XS = 2
+ *   (136 B / 256), QO_Q6_K_SOA = 3 (row-SoA repack of Q6_K), QO_Q8_0_SOA = 4 (row-SoA repack of
+ *   Q8_0: [qs K][d K/32 x f16]), QO_Q5_1_SOA = 5 (row-SoA repack of Q5_1 or Q5_0:
+ *   [qs K/2][qh K/8][d K/32 x f16][m K/32 x f16]),
+ * plus ids of this build for the GGUF-native rows the repacks start from: QO_Q6_K = 6 (210 B
+ * Q6_K block), QO_Q8_0 = 8 (34 B / 32), QO_Q5_1 = 9 (24 B / 32), QO_Q5_0 = 10 (22 B / 32).
  */
 #ifndef QMM_ORACLE_H
 #define QMM_ORACLE_H
@@ -22,11 +26,13 @@
 extern "C" {
 #endif
 
-enum { QO_Q4_K = 0, QO_Q6_K_SOA = 3, QO_Q6_K = 6 };
+enum { QO_Q4_K = 0, QO_Q5_K = 1, QO_IQ4_XS = 2, QO_Q6_K_SOA = 3, QO_Q8_0_SOA = 4, QO_Q5_1_SOA = 5,
+       QO_Q6_K = 6, QO_Q8_0 = 8, QO_Q5_1 = 9, QO_Q5_0 = 10 };
 
 /* ---- scalar number formats ---- */
 float qo_f16_to_f32(uint16_t h);   /* engine/src/quant.h:11-17 (exact, subnormals included) */
 uint16_t qo_f32_to_bf16(float f);  /* engine/kernels/gemm.hip:12 (round-to-nearest-even, no NaN case) */
+uint16_t qo_f32_to_f16(float f);   /* round to nearest even, as (_Float16)x (gemv.hip:1453); no NaN case */
 float qo_bf16_to_f32(uint16_t b);  /* engine/kernels/fn.hip:23 */
 
 /* ---- weight blocks ---- */
@@ -34,7 +40,17 @@ void qo_scale_min_k4(int j, const uint8_t* q, uint8_t* sc, uint8_t* m); /* quant
 void qo_dequant_q4_K_block(const uint8_t* blk, float* y);              /* quant.h:43-53 */
 void qo_dequant_q6_K_block(const uint8_t* blk, float* y);              /* quant.h:65-80 */
 void qo_repack_row_q6_K(const uint8_t* src, uint8_t* dst, int K);      /* gemv.hip:1341-1350 */
+void qo_dequant_q5_K_block(const uint8_t* blk, float* y);              /* quant.h:54-64 */
+extern const int8_t qo_iq4nl_levels[16];                               /* quant.h:35 */
+void qo_dequant_iq4_xs_block(const uint8_t* blk, float* y);            /* quant.h:93-100 */
+void qo_dequant_q8_0_block(const uint8_t* blk, float* y);              /* quant.h:81 */
+void qo_dequant_q5_1_block(const uint8_t* blk, float* y);              /* quant.h:82-88 */
+void qo_dequant_q5_0_block(const uint8_t* blk, float* y);              /* GGUF Q5_0 definition (see .c) */
+void qo_repack_row_q8_0(const uint8_t* src, uint8_t* dst, int K);      /* gemv.hip:1351-1354 */
+void qo_repack_row_q5_1(const uint8_t* src, uint8_t* dst, int K);      /* gemv.hip:1458-1465 */
+void qo_repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K);      /* gemv.hip:1448-1457 */
 size_t qo_row_bytes(int wfmt, int K);                                  /* gemv.hip:1337-1340 */
+int qo_k_granule(int wfmt);                                            /* 256, or 32 for the 32-weight block formats */
 /* one row of K weights in format wfmt -> f32; returns 0, or -1 for an unknown format */
 int qo_dequant_row(int wfmt, const uint8_t* row, float* y, int K);     /* quant.h:185-201 */
 /* whole matrix [N][K] -> f32 or bf16 (gemm.hip:16-76 semantics: f32 dequant, then RNE to bf16) */

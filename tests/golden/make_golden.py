@@ -4,9 +4,14 @@ The reference (dzannotti/hipster) ships no kernel-level golden vectors, so this 
 it calls engine/src/quant.h (f16_to_f32, get_scale_min_k4, dequant_row for GGUF types 12 = Q4_K and
 14 = Q6_K), compiled unchanged from the reference checkout by oracle/Makefile into
 oracle/_ref/libqmm_ref.so, on seeded random blocks plus hand-made special blocks, and stores the
-inputs and the reference's outputs.  Run from the repo root after `make -C oracle`:
+inputs and the reference's outputs (quant_golden.npz).  A second file, quant_golden_fmt.npz, holds
+the same for the other formats of the call surface -- dequant_row types 13 = Q5_K, 23 = IQ4_XS,
+8 = Q8_0, 7 = Q5_1 -- and the bytes the reference's load-time repacks (engine/kernels/gemv.hip:
+1351-1354,1448-1465, compiled into oracle/_ref/libqmm_ref_gemv.so) make of seeded Q8_0, Q5_1 and
+Q5_0 rows.  Run from the repo root after `make -C oracle`:
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py             # quant_golden.npz
+    python tests/golden/make_golden.py --formats   # quant_golden_fmt.npz
 """
 import ctypes
 import os
@@ -62,7 +67,73 @@ def ref_dequant(ref, gtype, blocks):
     return out
 
 
+def ref_dequant_n(ref, gtype, blocks, per):
+    out = np.empty((blocks.shape[0], per), np.float32)
+    for i in range(blocks.shape[0]):
+        blk = np.ascontiguousarray(blocks[i])
+        ref.ref_dequant_row(gtype, ctypes.c_void_p(blk.ctypes.data), ctypes.c_void_p(out[i].ctypes.data), per)
+    return out
+
+
+def fmt_special(fmt):
+    """Edge blocks: zero scale, negative scale, subnormal scale, all-ones quant bytes, all-zero ones."""
+    per, nbytes = synth.BLOCK[fmt]
+    g = synth.rng(300 + fmt)
+    bl = []
+    for k in range(5):
+        b = synth.blocks(g, fmt, 1)[0].copy()
+        if k == 0:
+            b[0:2] = 0
+        elif k == 1:
+            b[0:2] = np.array([f16(-0.03125)], np.uint16).view(np.uint8)
+        elif k == 2:
+            b[0:2] = [0x05, 0x00]
+        elif k == 3:
+            b[4 if fmt != Q5_0 else 2:] = 0xFF
+        else:
+            b[4 if fmt != Q5_0 else 2:] = 0x00
+        bl.append(b)
+    return np.stack(bl)
+
+
+Q5_K, IQ4_XS, Q8_0, Q5_1, Q5_0 = synth.Q5_K, synth.IQ4_XS, synth.Q8_0, synth.Q5_1, synth.Q5_0
+
+
+def main_formats():
+    ref, refg = oracle.ref_lib(), oracle.ref_gemv_lib()
+    if ref is None or refg is None:
+        sys.exit("oracle/_ref libraries not built (needs the reference checkout): make -C oracle")
+    out = {}
+    for name, fmt, gtype in (("q5k", Q5_K, 13), ("iq4xs", IQ4_XS, 23), ("q8_0", Q8_0, 8), ("q5_1", Q5_1, 7)):
+        per = synth.BLOCK[fmt][0]
+        bl = np.concatenate([fmt_special(fmt), synth.blocks(synth.rng(20260 + fmt), fmt, 200)])
+        out[f"{name}_blocks"] = bl
+        out[f"{name}_y"] = ref_dequant_n(ref, gtype, bl, per)
+    # load-time repacks of whole rows (K = 512 and K = 96: a K that is not a multiple of 256)
+    for name, fmt, fn in (("q8_0", Q8_0, refg.refg_repack_row_q8_0), ("q5_1", Q5_1, refg.refg_repack_row_q5_1),
+                          ("q5_0", Q5_0, refg.refg_repack_row_q5_0)):
+        for K in (512, 96):
+            per, nbytes = synth.BLOCK[fmt]
+            rows = synth.blocks(synth.rng(20270 + fmt + K), fmt, 4 * (K // per)).reshape(4, -1)
+            if fmt == Q5_0:
+                rows.reshape(4, K // per, 22)[0, 0, 0:2] = [0x00, 0x7c]     # d = inf: -16 d overflows
+                rows.reshape(4, K // per, 22)[0, 1, 0:2] = [0x01, 0x00]     # subnormal d
+            dst_bytes = K // 32 * 24 if fmt != Q8_0 else K + K // 16
+            dst = np.zeros((4, dst_bytes), np.uint8)
+            for r in range(4):
+                s = np.ascontiguousarray(rows[r])
+                fn(ctypes.c_void_p(s.ctypes.data), ctypes.c_void_p(dst[r].ctypes.data), K)
+            out[f"repack_{name}_K{K}_src"] = rows
+            out[f"repack_{name}_K{K}_dst"] = dst
+    out["row_bytes"] = np.array([[refg.refg_wfmt_row_bytes(f, K) for f in range(6)] for K in (256, 512, 5120, 17408)],
+                                dtype=np.int64)
+    np.savez_compressed(os.path.join(HERE, "quant_golden_fmt.npz"), **out)
+    print("wrote quant_golden_fmt.npz:", {k: v.shape for k, v in out.items()})
+
+
 def main():
+    if "--formats" in sys.argv:
+        return main_formats()
     ref = oracle.ref_lib()
     if ref is None:
         sys.exit("oracle/_ref/libqmm_ref.so not built (needs the reference checkout): make -C oracle")

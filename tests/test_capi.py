@@ -40,7 +40,14 @@ def test_row_bytes_and_repack_match_oracle():
     assert L.qmm_wfmt_row_bytes(_lib.QMM_Q6_K, 17408) == 68 * 210
     assert L.qmm_wfmt_row_bytes(_lib.QMM_Q6_K_SOA, 17408) == 68 * 210
     assert L.qmm_wfmt_row_bytes(_lib.QMM_Q4_K, 100) == 0
-    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q5_K, 256) == 0
+    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q5_K, 100) == 0
+    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q8_0_SOA, 96) == 102 and L.qmm_wfmt_row_bytes(_lib.QMM_Q5_1_SOA, 96) == 72
+    assert L.qmm_wfmt_row_bytes(_lib.QMM_Q8_0_SOA, 100) == 0 and L.qmm_wfmt_row_bytes(99, 256) == 0
+    # every format against the reference's own wfmt_row_bytes (golden table)
+    G = np.load(os.path.join(os.path.dirname(__file__), "golden", "quant_golden_fmt.npz"))
+    for i, K in enumerate((256, 512, 5120, 17408)):
+        for fmt in range(6):
+            assert L.qmm_wfmt_row_bytes(fmt, K) == G["row_bytes"][i, fmt], (fmt, K)
     W = synth.matrix(5, synth.Q6_K, 4, 2048)
     soa = synth.repack_q6k_soa(W, 2048)
     for r in range(4):
@@ -50,6 +57,22 @@ def test_row_bytes_and_repack_match_oracle():
     assert L.qmm_repack_row_q6_K(None, None, 256) == -3
 
 
+@pytest.mark.parametrize("name,fn", [("q8_0", "qmm_repack_row_q8_0"), ("q5_1", "qmm_repack_row_q5_1"),
+                                     ("q5_0", "qmm_repack_row_q5_0")])
+@pytest.mark.parametrize("K", [512, 96])
+def test_repacks_match_reference_bytes(name, fn, K):
+    """The three load-time repacks against the bytes the reference's own gemv.hip wrote (golden)."""
+    G = np.load(os.path.join(os.path.dirname(__file__), "golden", "quant_golden_fmt.npz"))
+    src, want = G[f"repack_{name}_K{K}_src"], G[f"repack_{name}_K{K}_dst"]
+    L = _lib.lib()
+    for r in range(src.shape[0]):
+        s = np.ascontiguousarray(src[r]); d = np.zeros(want.shape[1], np.uint8)
+        assert getattr(L, fn)(s.ctypes.data, d.ctypes.data, K) == 0
+        assert np.array_equal(d, want[r])
+    assert getattr(L, fn)(None, None, 32) == -3
+    assert getattr(L, fn)(src.ctypes.data, src.ctypes.data, 100) == -2
+
+
 def _xq(p=1):
     return _lib.XQ8(p, p, p, 0)
 
@@ -57,9 +80,11 @@ def _xq(p=1):
 def test_argument_validation_without_device_work():
     L = _lib.lib()
     dummy = ctypes.c_void_p(16)
-    # unsupported formats are refused (the reference aborts here)
-    for fmt in (_lib.QMM_Q5_K, _lib.QMM_IQ4_XS, _lib.QMM_Q8_0_SOA, _lib.QMM_Q5_1_SOA, 99):
-        assert L.qmm_gemv_q8(fmt, dummy, _xq(16), dummy, 16, 256, 1, 0, 1, None) == -1
+    # unknown formats are refused (the reference aborts here); the other formats check their shape
+    assert L.qmm_gemv_q8(99, dummy, _xq(16), dummy, 16, 256, 1, 0, 1, None) == -1
+    for fmt in (_lib.QMM_Q5_K, _lib.QMM_IQ4_XS, _lib.QMM_Q8_0_SOA, _lib.QMM_Q5_1_SOA):
+        assert L.qmm_gemv_q8(fmt, dummy, _xq(16), dummy, 16, 96, 1, 0, 1, None) == -2
+        assert L.qmm_gemv_q8(fmt, dummy, _xq(16), dummy, 16, 256, 9, 0, 1, None) == -2
     # bad shapes
     assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 300, 1, 0, 1, None) == -2
     assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 0, 256, 1, 0, 1, None) == -2

@@ -30,8 +30,20 @@ int main() {
         hip::gemv_q8_f32x(hip::WFmt::Q4_K, (void*)16, (const float*)16, (float*)16, 16, 256, 5, nullptr);
     } catch (const std::runtime_error&) { ++caught; }
     if (caught != 3) return 4;
-    try {
-        hip::gemv_q8(hip::WFmt::Q5_K, (void*)16, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, (float*)16, 16, 256, 1, 0, 1, nullptr);
+    {   // the load-time repacks of the other formats (gemv.h:16-18), host only
+        uint8_t src[34 * 2] = {0}, dst[34 * 2];
+        src[0] = 0x00; src[1] = 0x3c;                      // Q8_0 block 0: d = 1
+        hip::repack_row_q8_0(src, dst, 64);
+        if (dst[64] != 0x00 || dst[65] != 0x3c) return 5;
+        uint8_t s5[22] = {0x00, 0x3c}, d5[24];            // Q5_0: d = 1 -> m = -16 (0xcc00)
+        hip::repack_row_q5_0(s5, d5, 32);
+        if (d5[22] != 0x00 || d5[23] != 0xcc) return 6;
+        uint8_t s51[24] = {0}, d51[24];
+        hip::repack_row_q5_1(s51, d51, 32);
+        if (hip::wfmt_row_bytes(hip::WFmt::Q8_0_SOA, 96) != 102) return 7;
+    }
+    try {   // a format id the library does not know
+        hip::gemv_q8((hip::WFmt)99, (void*)16, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, (float*)16, 16, 256, 1, 0, 1, nullptr);
     } catch (const std::runtime_error& e) {
         std::printf("%s\n", e.what());
         return 0;
