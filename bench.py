@@ -22,7 +22,8 @@ Prints ONE JSON line:
 The other BASELINE configurations are measured too and reported under "extra" (parity-test
 shapes, not the headline): the dense decode layer at M = 1, 4, 8 (config 1), the MoE decode step at
 T = 1, 4, 8 (config 2), the dense prefill GEMM and the M = 3..6 verify GEMVs (config 3) and the MoE
-prefill pipeline at 2048 tokens (config 4).  --no-extra skips them.
+prefill pipeline at 2048 tokens (config 4), and the q8 GEMV of every weight format of the call surface
+at config 0's shape.  --no-extra skips them.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--cpu-seconds 10] [--no-extra]
 """
@@ -127,6 +128,32 @@ def graph_us(torch, fns, reps=5):
     g = capture(torch, [f for _ in range(reps) for f in fns])
     timed_replay(torch, g)
     return timed_replay(torch, g) / reps * 1e3
+
+
+def extra_formats(torch):
+    """The other weight formats of the call surface at config 0's shape (17408 x 5120), q8 GEMV at M = 1
+    and 4, weights rotated over >= 1 GiB: time per call and weight bytes / time."""
+    from hipster_amd import qmm, synth
+    N, K = synth.CFG0["N"], synth.CFG0["K"]
+    out = {}
+    for name, fmt in (("Q4_K", synth.Q4_K), ("Q5_K", synth.Q5_K), ("IQ4_XS", synth.IQ4_XS), ("Q6_K_SOA", synth.Q6_K_SOA),
+                      ("Q8_0_SOA", synth.Q8_0_SOA), ("Q5_1_SOA", synth.Q5_1_SOA)):
+        W = synth.matrix(synth.SEEDS["cfg0"] + 50 + fmt, fmt, N, K)
+        ncopy = max(2, -(-ROTATE_BYTES // W.nbytes))
+        Wt = torch.from_numpy(W)
+        Wd = [Wt.to("cuda") for _ in range(ncopy)]
+        r = {"row_bytes": int(W.shape[1])}
+        for M in (1, 4):
+            xb = qmm.XQ8Buf(M, K)
+            qmm.quantize_x_q8(torch.randn((M, K), device="cuda"), xb, M, K)
+            y = torch.zeros((M, N), device="cuda")
+            us = graph_us(torch, [(lambda i: (lambda: qmm.gemv_q8(fmt, Wd[i], xb, y, N, K, M)))(i) for i in range(ncopy)],
+                          reps=2) / ncopy
+            r[f"M{M}"] = {"us": round(us, 2), "GB_s": round(W.nbytes / us / 1e3, 1)}
+        out[name] = r
+        del Wd, Wt
+        torch.cuda.empty_cache()
+    return out
 
 
 def extra_cfg1(torch):
@@ -342,6 +369,8 @@ def main():
         del tb
         torch.cuda.empty_cache()
         extra["cfg3_dense_prefill"] = extra_cfg3(torch)
+        torch.cuda.empty_cache()
+        extra["formats_gemv_17408x5120"] = extra_formats(torch)
         out["extra"] = extra
     print(json.dumps(out), flush=True)
 

@@ -4,11 +4,11 @@
 // the reference's gemv_q8 / gemv_multi (engine/kernels/gemv.h:25,28) for these formats; the
 // per-format arithmetic is the reference's (block decoders gemv.hip:90-163,214-268).
 //
-// One row per wave.  A unit is one scale's worth of weights -- 32 (one sub-block) for IQ4_XS,
+// RPW rows per wave (4; 2 for Q5_K).  A unit is one scale's worth of weights -- 32 (one sub-block) for IQ4_XS,
 // Q8_0_SOA and Q5_1_SOA, 64 for Q5_K (the two sub-blocks sharing one 32-byte qs pair) -- and lane l
 // takes units l, l + 64, ... of the row, NIT at a time, with all of a pass's weight loads issued
 // before its compute.  The q8 x of a unit (32 bytes per sub-block, its d and s) is read from
-// global memory; the four rows of a workgroup read the same x, which L1 serves.  Per sub-block the
+// global memory (L1) once per wave and used for all of the wave's rows.  Per sub-block the
 // weights become int8 lanes of a dword, the integer dot with the q8 x uses v_dot4_i32_i8, and the
 // reference's fix-up follows:
 //   Q5_K    acc += (d sc) xd isum - (dmin m) xs          (q = nibble | fifth bit << 4, 0..31)
@@ -51,9 +51,8 @@ __device__ __forceinline__ uint32_t iq4_levels4(uint32_t nib) {
 // other partial products at positions that are not 4 mod 8, none overlapping), the mask keeps those
 __device__ __forceinline__ uint32_t bits4_to_byte_bit4(uint32_t h) { return (h * 0x02040810u) & 0x10101010u; }
 
-// 32 int8 weights (8 dwords) against 32 q8 x bytes (two 16-byte loads)
-__device__ __forceinline__ int dot32(const uint32_t (&w)[8], const int8_t* __restrict__ x) {
-    const uint4 a = ld16(x), b = ld16(x + 16);
+// 32 int8 weights (8 dwords) against 32 q8 x bytes
+__device__ __forceinline__ int dot32(const uint32_t (&w)[8], const uint4 a, const uint4 b) {
     int s = sdot4(w[0], a.x, 0);
     s = sdot4(w[1], a.y, s);
     s = sdot4(w[2], a.z, s);
@@ -64,31 +63,51 @@ __device__ __forceinline__ int dot32(const uint32_t (&w)[8], const int8_t* __res
     return sdot4(w[7], b.w, s);
 }
 
-// ---- per-format unit: its raw bytes, their load, and the unit's contribution to one column ----
+// q8 x of one 32-weight sub-block of one column: its 32 bytes, d and s
+struct X32 { uint4 a, b; float d, s; };
+__device__ __forceinline__ void x32_load(const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                         const float* __restrict__ xs, int sb, X32& x) {
+    x.a = ld16(xq + 32 * (size_t)sb);
+    x.b = ld16(xq + 32 * (size_t)sb + 16);
+    x.d = xd[sb];
+    x.s = xs[sb];
+}
+
+// ---- per-format unit: its raw weight bytes and load, its x, and its contribution to a column ----
+// The loads (weights once, x per column) are issued before any arithmetic, so a unit never waits
+// for one memory access after another.
 template <int F> struct FmtUnit;
 
 template <> struct FmtUnit<QMM_Q8_0_SOA> {            // row = [qs K][d (K/32) x f16]
     struct Raw { uint4 a, b; uint32_t d; };
+    typedef X32 X;
     static __device__ __forceinline__ void load(const uint8_t* rp, int K, int u, Raw& r) {
         r.a = ld16(rp + 32 * (size_t)u);
         r.b = ld16(rp + 32 * (size_t)u + 16);
         r.d = *(const uint16_t*)(rp + K + 2 * (size_t)u);
     }
-    static __device__ __forceinline__ float col(const Raw& r, int u, const int8_t* xq, const float* xd, const float*) {
+    static __device__ __forceinline__ void xload(const int8_t* xq, const float* xd, const float* xs, int u, X& x) {
+        x32_load(xq, xd, xs, u, x);
+    }
+    static __device__ __forceinline__ float col(const Raw& r, const X& x, int) {
         const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-        return h2f(r.d) * xd[u] * (float)dot32(w, xq + 32 * u);
+        return h2f(r.d) * x.d * (float)dot32(w, x.a, x.b);
     }
 };
 
 template <> struct FmtUnit<QMM_Q5_1_SOA> {            // row = [qs K/2][qh K/8][d K/32 x f16][m K/32 x f16]
     struct Raw { uint4 qs; uint32_t qh, d, m; };
+    typedef X32 X;
     static __device__ __forceinline__ void load(const uint8_t* rp, int K, int u, Raw& r) {
         r.qs = ld16(rp + 16 * (size_t)u);
         r.qh = *(const uint32_t*)(rp + K / 2 + 4 * (size_t)u);
         r.d = *(const uint16_t*)(rp + K / 2 + K / 8 + 2 * (size_t)u);
         r.m = *(const uint16_t*)(rp + K / 2 + K / 8 + K / 16 + 2 * (size_t)u);
     }
-    static __device__ __forceinline__ float col(const Raw& r, int u, const int8_t* xq, const float* xd, const float* xs) {
+    static __device__ __forceinline__ void xload(const int8_t* xq, const float* xd, const float* xs, int u, X& x) {
+        x32_load(xq, xd, xs, u, x);
+    }
+    static __device__ __forceinline__ float col(const Raw& r, const X& x, int) {
         // weight j (< 16): low nibble of qs byte j, fifth bit = qh bit j; weight j + 16: high nibble,
         // qh bit j + 16 (quant.h:82-88)
         const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
@@ -98,18 +117,22 @@ template <> struct FmtUnit<QMM_Q5_1_SOA> {            // row = [qs K/2][qh K/8][
             w[k] = (q[k] & 0x0f0f0f0fu) | bits4_to_byte_bit4((r.qh >> (4 * k)) & 0xfu);
             w[4 + k] = ((q[k] >> 4) & 0x0f0f0f0fu) | bits4_to_byte_bit4((r.qh >> (16 + 4 * k)) & 0xfu);
         }
-        return h2f(r.d) * xd[u] * (float)dot32(w, xq + 32 * u) + h2f(r.m) * xs[u];
+        return h2f(r.d) * x.d * (float)dot32(w, x.a, x.b) + h2f(r.m) * x.s;
     }
 };
 
 template <> struct FmtUnit<QMM_IQ4_XS> {              // block = {f16 d, u16 scales_h, u8 scales_l[4], qs[128]}
     struct Raw { uint2 hd; uint4 qs; };
+    typedef X32 X;
     static __device__ __forceinline__ void load(const uint8_t* rp, int, int u, Raw& r) {
         const uint8_t* blk = rp + (size_t)(u >> 3) * 136;
         r.hd = *(const uint2*)blk;
         r.qs = ld16_a4(blk + 8 + 16 * (u & 7));              // 136-byte blocks: 8-byte aligned
     }
-    static __device__ __forceinline__ float col(const Raw& r, int u, const int8_t* xq, const float* xd, const float*) {
+    static __device__ __forceinline__ void xload(const int8_t* xq, const float* xd, const float* xs, int u, X& x) {
+        x32_load(xq, xd, xs, u, x);
+    }
+    static __device__ __forceinline__ float col(const Raw& r, const X& x, int u) {
         const int ib = u & 7;
         const int ls = (int)((r.hd.y >> (4 * ib)) & 0xfu) | (int)(((r.hd.x >> (16 + 2 * ib)) & 3u) << 4);
         const float dl = h2f(r.hd.x) * (float)(ls - 32);
@@ -120,12 +143,13 @@ template <> struct FmtUnit<QMM_IQ4_XS> {              // block = {f16 d, u16 sca
             w[k] = iq4_levels4(q[k] & 0x0f0f0f0fu);            // weights 4k..4k+3
             w[4 + k] = iq4_levels4((q[k] >> 4) & 0x0f0f0f0fu); // weights 16+4k..
         }
-        return dl * xd[u] * (float)dot32(w, xq + 32 * u);
+        return dl * x.d * (float)dot32(w, x.a, x.b);
     }
 };
 
 template <> struct FmtUnit<QMM_Q5_K> {                // block = {f16 d, dmin, scales[12], qh[32], qs[128]}
     struct Raw { uint4 hd, h0, h1, q0, q1; };
+    struct X { X32 lo, hi; };                          // sub-blocks 2j and 2j + 1
     static __device__ __forceinline__ void load(const uint8_t* rp, int, int u, Raw& r) {
         const uint8_t* blk = rp + (size_t)(u >> 2) * 176;     // 176-byte blocks: 16-byte aligned
         r.hd = ld16(blk);
@@ -134,10 +158,14 @@ template <> struct FmtUnit<QMM_Q5_K> {                // block = {f16 d, dmin, s
         r.q0 = ld16(blk + 48 + 32 * (u & 3));
         r.q1 = ld16(blk + 64 + 32 * (u & 3));
     }
-    static __device__ __forceinline__ float col(const Raw& r, int u, const int8_t* xq, const float* xd, const float* xs) {
+    static __device__ __forceinline__ void xload(const int8_t* xq, const float* xd, const float* xs, int u, X& x) {
+        x32_load(xq, xd, xs, 2 * u, x.lo);                    // unit u = 4b + j: sub-blocks 8b + 2j = 2u, 2u + 1
+        x32_load(xq, xd, xs, 2 * u + 1, x.hi);
+    }
+    static __device__ __forceinline__ float col(const Raw& r, const X& x, int u) {
         // pair j of block b: weights 64j + l (sub-block 2j) = low nibble of qs[32j + l] with bit 2j of
         // qh[l] as the fifth bit, 64j + 32 + l (sub-block 2j + 1) = high nibble with bit 2j + 1
-        const int j = u & 3, sb = 2 * u;                     // global sub-block index of 2j
+        const int j = u & 3;
         const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
         const uint32_t h[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
         uint32_t wl[8], wh[8];
@@ -146,57 +174,84 @@ template <> struct FmtUnit<QMM_Q5_K> {                // block = {f16 d, dmin, s
             wl[k] = (q[k] & 0x0f0f0f0fu) | (((h[k] >> (2 * j)) & 0x01010101u) << 4);
             wh[k] = ((q[k] >> 4) & 0x0f0f0f0fu) | (((h[k] >> (2 * j + 1)) & 0x01010101u) << 4);
         }
-        const int i0 = dot32(wl, xq + 32 * sb), i1 = dot32(wh, xq + 32 * sb + 32);
+        const int i0 = dot32(wl, x.lo.a, x.lo.b), i1 = dot32(wh, x.hi.a, x.hi.b);
         const float d = h2f(r.hd.x), dmin = h2f(r.hd.x >> 16);
         const Q4kScaleBytes s = q4k_scale_bytes(r.hd.y, r.hd.z, r.hd.w);
         const float d0 = d * (float)byte8(s.sc_lo, s.sc_hi, 2 * j), m0 = dmin * (float)byte8(s.m_lo, s.m_hi, 2 * j);
         const float d1 = d * (float)byte8(s.sc_lo, s.sc_hi, 2 * j + 1), m1 = dmin * (float)byte8(s.m_lo, s.m_hi, 2 * j + 1);
-        return d0 * xd[sb] * (float)i0 - m0 * xs[sb] + (d1 * xd[sb + 1] * (float)i1 - m1 * xs[sb + 1]);
+        return d0 * x.lo.d * (float)i0 - m0 * x.lo.s + (d1 * x.hi.d * (float)i1 - m1 * x.hi.s);
     }
 };
 
-template <int F, int NCOL, int NIT>
+// RPW rows per wave: the q8 x of a unit is loaded once into registers and used by all RPW rows
+// (x traffic per row / RPW; with one row per wave the x reads outweigh the weight bytes).
+template <int F, int NCOL, int NIT, int RPW>
 __global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                         const float* __restrict__ xd, const float* __restrict__ xs,
                                                         float* __restrict__ y, int N, int K) {
+    typedef FmtUnit<F> FU;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = blockIdx.x * kFmtWaves + wave;
-    const uint8_t* rp = W + (size_t)min(row, N - 1) * fmt_row_bytes<F>(K);
+    const int row0 = (blockIdx.x * kFmtWaves + wave) * RPW;
+    const size_t rb = fmt_row_bytes<F>(K);
     const int U = fmt_units<F>(K), nsb = K / 32;
-    float acc[NCOL];
+    float acc[RPW][NCOL];
 #pragma unroll
-    for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) acc[r][c] = 0.f;
     for (int base = 0; base < U; base += 64 * NIT) {
-        typename FmtUnit<F>::Raw R[NIT];
+        typename FU::Raw R[RPW][NIT];
+        typename FU::X X[NIT];
 #pragma unroll
-        for (int i = 0; i < NIT; ++i) FmtUnit<F>::load(rp, K, min(base + lane + 64 * i, U - 1), R[i]);
+        for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int i = 0; i < NIT; ++i) {
-            const int u = base + lane + 64 * i, uc = min(u, U - 1);
+            for (int i = 0; i < NIT; ++i) FU::load(W + (size_t)min(row0 + r, N - 1) * rb, K, min(base + lane + 64 * i, U - 1), R[r][i]);
 #pragma unroll
-            for (int c = 0; c < NCOL; ++c) {
-                const float v = FmtUnit<F>::col(R[i], uc, xq + (size_t)c * K, xd + (size_t)c * nsb, xs + (size_t)c * nsb);
-                acc[c] += u < U ? v : 0.f;
+        for (int c = 0; c < NCOL; ++c) {
+#pragma unroll
+            for (int i = 0; i < NIT; ++i)
+                FU::xload(xq + (size_t)c * K, xd + (size_t)c * nsb, xs + (size_t)c * nsb, min(base + lane + 64 * i, U - 1), X[i]);
+            // all loads issued before any arithmetic (the scheduler would otherwise sink each load
+            // to its use to save registers, one memory latency after another)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < NIT; ++i) {
+                const int u = base + lane + 64 * i;
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const float v = FU::col(R[r][i], X[i], min(u, U - 1));
+                    acc[r][c] += u < U ? v : 0.f;
+                }
             }
         }
     }
 #pragma unroll
-    for (int c = 0; c < NCOL; ++c) acc[c] = wave_sum(acc[c]);
-    if (lane == 0 && row < N) {
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+        for (int c = 0; c < NCOL; ++c) acc[r][c] = wave_sum(acc[r][c]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+            if (row0 + r < N) {
+#pragma unroll
+                for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row0 + r] = acc[r][c];
+            }
     }
 }
 
 template <int F, int NCOL>
 int launch_fmt(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
-    const int grid = (N + kFmtWaves - 1) / kFmtWaves;
+    // rows per wave: 2 at one column (more waves in flight), 4 above (the shared x pays more), 2 for
+    // Q5_K (its units hold 20 registers of raw weights)
+    constexpr int RPW = (F == QMM_Q5_K || NCOL == 1) ? 2 : 4;
+    const int grid = (N + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const int per_lane = (fmt_units<F>(K) + 63) / 64;
-#define QMM_FMTL(IV) hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV>), dim3(grid), dim3(kFmtBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K)
+#define QMM_FMTL(IV) hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV, RPW>), dim3(grid), dim3(kFmtBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K)
+    // units per lane and pass: all of them when they are few, else passes of two (registers: RPW
+    // rows x NIT units of raw weights are live at once)
     if (per_lane <= 1) QMM_FMTL(1);
-    else if (per_lane == 2) QMM_FMTL(2);
-    else if (per_lane == 3) QMM_FMTL(3);
-    else QMM_FMTL(4);                                      // longer rows: passes of 4 units per lane
+    else if (per_lane == 3 && F != QMM_Q5_K) QMM_FMTL(3);
+    else QMM_FMTL(2);
 #undef QMM_FMTL
     QMM_LAUNCH_CHECK();
     return QMM_OK;
