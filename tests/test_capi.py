@@ -149,7 +149,8 @@ def test_prefill_argument_validation_without_device_work():
     assert L.qmm_gemm_wq(q4, d, None, d, 16, 16, 256, None) == -3
     assert L.qmm_gemm_bf16(d, d, d, 16, 16, 100, None) == -2
     assert L.qmm_dequant_bf16(q4, d, d, 16, 100, None) == -2
-    assert L.qmm_dequant_bf16(_lib.QMM_Q5_K, d, d, 16, 256, None) == -1
+    assert L.qmm_dequant_bf16(99, d, d, 16, 256, None) == -1
+    assert L.qmm_dequant_bf16(_lib.QMM_Q5_K, d, d, 16, 100, None) == -2
     assert L.qmm_gemv_q8_f32x(q6, d, d, d, 16, 256, 1, None) == -1
     assert L.qmm_gemv_q8_f32x(q4, d, None, d, 16, 256, 1, None) == -3
     assert L.qmm_gemv_q8_f32x(q4, d, d, d, 16, 256, 5, None) == -2      # ncol above 4

@@ -23,13 +23,24 @@ def bf16_dev(a_bits):
 
 
 @pytest.mark.parametrize("fmt,N,K", [(synth.Q4_K, 333, 5120), (synth.Q6_K, 129, 2048), (synth.Q6_K_SOA, 64, 4096),
-                                     (synth.Q4_K, 17408, 5120)])
+                                     (synth.Q4_K, 17408, 5120), (synth.Q5_K, 300, 5120), (synth.IQ4_XS, 129, 2048),
+                                     (synth.Q8_0_SOA, 77, 4096), (synth.Q5_1_SOA, 256, 2560), (synth.Q5_K, 4096, 17408)])
 def test_dequant_bf16_bit_exact(gpu, fmt, N, K):
     W = synth.matrix(900 + N, fmt, N, K)
     out = torch.zeros((N, K), dtype=torch.int16, device="cuda")
     qmm.dequant_bf16(fmt, dev(W), out, N, K)
     ref = oracle.dequant_rows_bf16(fmt, W, K)
     assert np.array_equal(host(out).view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("fmt,key", [(synth.Q5_K, "q5k"), (synth.IQ4_XS, "iq4xs")])
+def test_dequant_bf16_golden_blocks_other_formats(gpu, fmt, key):
+    """GGUF blocks (edge blocks included) whose f32 values the reference's own quant.h wrote"""
+    G = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "quant_golden_fmt.npz"))
+    blocks = G[key + "_blocks"]
+    out = torch.zeros((blocks.shape[0], 256), dtype=torch.int16, device="cuda")
+    qmm.dequant_bf16(fmt, dev(blocks), out, blocks.shape[0], 256)
+    assert np.array_equal(host(out).view(np.uint16), synth.to_bf16_bits(G[key + "_y"]))
 
 
 @pytest.mark.parametrize("fmt,key", [(synth.Q4_K, "q4k"), (synth.Q6_K, "q6k")])
