@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
+    p.add_argument("--only-extra", choices=["activation_producers", "formats"], default=None,
+                   help="only run one of the extra measurements and print its JSON (for profiling it alone)")
     p.add_argument("--calib-copy", action="store_true",
                    help="only run 10 plain device copies of 256 MiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
@@ -152,6 +154,43 @@ def extra_formats(torch):
             r[f"M{M}"] = {"us": round(us, 2), "GB_s": round(W.nbytes / us / 1e3, 1)}
         out[name] = r
         del Wd, Wt
+        torch.cuda.empty_cache()
+    return out
+
+
+def extra_act(torch):
+    """The producers of the matmul inputs at the dense model's shapes (hidden 5120, ffn 17408), decode
+    (T = 1) and prefill (T = 2048): time per call and algorithmic bytes / time (x, y, x written back,
+    w, the outputs; rows rotated so that a prefill call does not re-read what the last one left in L2)."""
+    from hipster_amd import qmm
+    n, F = 5120, 17408
+    out = {}
+    for T in (1, 2048):
+        nrot = 1 if T > 1 else 64
+        xs = [torch.randn((T, n), device="cuda") for _ in range(nrot)]
+        ys = [torch.randn((T, n), device="cuda") * 1e-3 for _ in range(nrot)]
+        w = torch.randn(n, device="cuda")
+        xn = torch.empty((T, n), device="cuda")
+        xq = qmm.XQ8Buf(T, n)
+        xb = torch.empty((T, n), dtype=torch.int16, device="cuda")
+        us = graph_us(torch, [(lambda i: (lambda: qmm.add_rmsnorm_quant(xs[i], ys[i], w, xn, xq, T, n, 1e-6)))(i)
+                              for i in range(nrot)], reps=4) / nrot
+        nbytes = T * n * (4 + 4 + 4 + 4 + 1) + T * (n // 32) * 8 + n * 4
+        out[f"add_rmsnorm_quant_T{T}"] = {"us": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1)}
+        us = graph_us(torch, [(lambda i: (lambda: qmm.add_rmsnorm_bf16(xs[i], ys[i], w, xb, T, n, 1e-6)))(i)
+                              for i in range(nrot)], reps=4) / nrot
+        nbytes = T * n * (4 + 4 + 4 + 2) + n * 4
+        out[f"add_rmsnorm_bf16_T{T}"] = {"us": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1)}
+        del xs, ys, xn, xq, xb
+        m = T * F
+        g = torch.randn(m, device="cuda"); u = torch.randn(m, device="cuda")
+        hq = qmm.XQ8Buf(1, m)
+        hb = torch.empty(m, dtype=torch.int16, device="cuda")
+        us = graph_us(torch, [lambda: qmm.silu_mul_quant(g, u, hq, m)], reps=20)
+        out[f"silu_mul_quant_T{T}"] = {"us": round(us, 2), "GB_s": round((m * 9 + m // 32 * 8) / us / 1e3, 1)}
+        us = graph_us(torch, [lambda: qmm.silu_mul_bf16(g, u, hb, m)], reps=20)
+        out[f"silu_mul_bf16_T{T}"] = {"us": round(us, 2), "GB_s": round(m * 10 / us / 1e3, 1)}
+        del g, u, hq, hb
         torch.cuda.empty_cache()
     return out
 
@@ -320,6 +359,10 @@ def main():
     if args.calib_copy:
         calib_copy()
         return
+    if args.only_extra:
+        fn = {"activation_producers": extra_act, "formats": extra_formats}[args.only_extra]
+        print(json.dumps({args.only_extra: fn(torch)}), flush=True)
+        return
     from hipster_amd import _lib
     _lib.lib()   # fails loudly if the HIP library is missing
 
@@ -371,6 +414,7 @@ def main():
         extra["cfg3_dense_prefill"] = extra_cfg3(torch)
         torch.cuda.empty_cache()
         extra["formats_gemv_17408x5120"] = extra_formats(torch)
+        extra["activation_producers"] = extra_act(torch)
         out["extra"] = extra
     print(json.dumps(out), flush=True)
 

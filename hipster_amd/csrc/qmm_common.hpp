@@ -106,6 +106,70 @@ __device__ __forceinline__ float group_sum(float v, int width) {
     return v;
 }
 
+// ---- half-wave (32-lane) butterflies ----
+// ds_swizzle in bit mode (offset[15] = 0: and_mask 0x1f, or_mask 0, xor_mask O) reads lane l^O
+// within each group of 32 lanes without touching LDS memory.  After the five steps O = 16..1
+// every lane of the half-wave holds the same value: the pairwise tree that pairs lane l with
+// l^16 first, then l^8, ..., l^1 (addition commutes, so both partners compute the same sum).
+template <int O>
+__device__ __forceinline__ float swz_xor(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (O << 10) | 0x1f));
+}
+__device__ __forceinline__ float hw32_sum(float v) {
+    v += swz_xor<16>(v); v += swz_xor<8>(v); v += swz_xor<4>(v); v += swz_xor<2>(v); v += swz_xor<1>(v);
+    return v;
+}
+// Reductions whose result does not depend on the order (max, integer sum) over 8 or 32 lanes, on the
+// VALU instead of the LDS pipe: DPP quad_perm [1,0,3,2] and [2,3,0,1] (lanes l^1, l^2), row_half_mirror
+// (lane 7-l of each 8-lane half-row: the other quad), row_mirror (lane 15-l of each 16-lane row: the
+// other half-row), then v_permlane16_swap, which exchanges the odd rows of one operand with the even
+// rows of the other: swapping a value with itself yields the row pair (r0, r1) in one result and
+// (r1, r0) in the other, so combining the two gives every lane of a half-wave its 32-lane total.
+// Every source lane lies inside the group being reduced.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+__device__ __forceinline__ float g8_max(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v)); v = fmaxf(v, dpp_f<kDppXor2>(v));
+    return fmaxf(v, dpp_f<kDppHalfMirror>(v));
+}
+__device__ __forceinline__ int g8_isum(int v) {
+    v += dpp_i<kDppXor1>(v); v += dpp_i<kDppXor2>(v);
+    return v + dpp_i<kDppHalfMirror>(v);
+}
+__device__ __forceinline__ float g32_max(float v) {
+    v = g8_max(v);
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ int g32_isum(int v) {
+    v = g8_isum(v);
+    v += dpp_i<kDppMirror>(v);
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)r[0] + (int)r[1];
+}
+
+// q8 per 32 (engine/kernels/ops.hip:48-59, == gemv.hip:36-51): lane l of a half-wave holds value l
+// of sub-block sb.  d = amax/127, id = 127/amax (0 when amax == 0), q = round-half-even(v*id),
+// s = d * sum(q); ds (optional) receives the packed (d, s) pair.
+__device__ __forceinline__ void hw32_quant(float v, int8_t* __restrict__ q, float* __restrict__ d, float* __restrict__ s,
+                                           float2* __restrict__ ds, size_t sb, int l) {
+    const float amax = g32_max(fabsf(v));
+    const float dd = amax / 127.f, id = amax > 0.f ? 127.f / amax : 0.f;
+    const int qi = __float2int_rn(v * id);
+    const int sum = g32_isum(qi);
+    q[sb * 32 + l] = (int8_t)qi;
+    if (l == 0) {
+        const float ss = dd * (float)sum;
+        d[sb] = dd; s[sb] = ss;
+        if (ds) ds[sb] = make_float2(dd, ss);
+    }
+}
+
 // bf16 round-to-nearest-even of the top half (no NaN special case, as engine/kernels/gemm.hip:12)
 __device__ __forceinline__ uint32_t f2bf_bits(float f) {
     uint32_t u = __float_as_uint(f);

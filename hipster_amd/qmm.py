@@ -167,6 +167,37 @@ def moe_silu_quant(gate, up, xq, rows, n, stream=None):
     check(_lib.lib().qmm_moe_silu_quant(_p(gate), _p(up), xq.c(), rows, n, _stream(stream)), "moe_silu_quant")
 
 
+# ---- activation producers (engine/kernels/ops.h) ----
+def add_rmsnorm_quant(x, y, w, xn, xq, T, n, eps, stream=None):
+    """ops.h:14: per row, x += y (y may be None), xn = rmsnorm(x) * w, xq = q8(xn) (XQ8Buf of T x n)."""
+    _dev(x, torch.float32, "x"); _dev(w, torch.float32, "w"); _dev(xn, torch.float32, "xn")
+    if y is not None:
+        _dev(y, torch.float32, "y")
+    check(_lib.lib().qmm_add_rmsnorm_quant(_p(x), 0 if y is None else _p(y), _p(w), _p(xn), xq.c(), T, n, eps,
+                                           _stream(stream)), "add_rmsnorm_quant")
+
+
+def add_rmsnorm_bf16(x, y, w, xb, T, n, eps, stream=None):
+    """ops.h:18: per row, x += y (y may be None), xb = bf16(rmsnorm(x) * w) (xb int16/uint16/bfloat16 storage)."""
+    _dev(x, torch.float32, "x"); _dev(w, torch.float32, "w")
+    if y is not None:
+        _dev(y, torch.float32, "y")
+    check(_lib.lib().qmm_add_rmsnorm_bf16(_p(x), 0 if y is None else _p(y), _p(w), _p(xb), T, n, eps,
+                                          _stream(stream)), "add_rmsnorm_bf16")
+
+
+def silu_mul_quant(gate, up, xq, n, stream=None):
+    """ops.h:24: xq = q8(silu(gate) * up) per 32 over n values."""
+    _dev(gate, torch.float32, "gate"); _dev(up, torch.float32, "up")
+    check(_lib.lib().qmm_silu_mul_quant(_p(gate), _p(up), xq.c(), n, _stream(stream)), "silu_mul_quant")
+
+
+def silu_mul_bf16(gate, up, out, n, stream=None):
+    """ops.h:20: out = bf16(silu(gate) * up) over n values."""
+    _dev(gate, torch.float32, "gate"); _dev(up, torch.float32, "up")
+    check(_lib.lib().qmm_silu_mul_bf16(_p(gate), _p(up), _p(out), n, _stream(stream)), "silu_mul_bf16")
+
+
 # ---- prefill GEMM (engine/kernels/gemm.h) ----
 def dequant_bf16(fmt, W, out, N, K, stream=None):
     """gemm.h:12: W -> bf16 [N][K] (out: int16/uint16-sized tensor of N*K elements), bit-exact."""

@@ -172,6 +172,23 @@ int qmm_moe_gemm_gate_up_bf16(int fmt, int shared_fmt, const void* Wg, const voi
 /* h = bf16(silu(gate) * up), n elements (the bf16-path counterpart of fn::moe_silu_quant, fn.hip:206-211) */
 int qmm_moe_silu_bf16(const float* gate, const float* up, uint16_t* h, size_t n, void* stream);
 
+/* ---- activation producers (the kernels whose outputs the matmuls read) ---- */
+/* per row t < T: if y != NULL, x += y (written back); xn = x * rs * w with rs = 1/sqrt(mean(x^2) + eps);
+ * xq = q8(xn) per 32 (ds filled when given).  n % 32 == 0, n <= 16384 (reference: add_rmsnorm_quant,
+ * ops.h:14, ops.hip:62-98,760-762; the reference processes only the first 6144 values of a row).
+ * The sum of squares is the reference's (same per-thread fma order, same pairwise tree); rs is
+ * correctly rounded where the reference uses the hardware rsqrt (within about 1 ulp). */
+int qmm_add_rmsnorm_quant(float* x, const float* y, const float* w, float* xn, qmm_xq8 xq, int T, int n, float eps,
+                          void* stream);
+/* as qmm_add_rmsnorm_quant with xb = bf16(x * rs * w) (RNE) as the only output besides x; any n <= 16384
+ * (reference: add_rmsnorm_bf16, ops.h:18, ops.hip:111-120,763) */
+int qmm_add_rmsnorm_bf16(float* x, const float* y, const float* w, uint16_t* xb, int T, int n, float eps, void* stream);
+/* xq = q8(silu(gate) * up) per 32, silu(v) = v / (1 + exp(-v)); n % 32 == 0 (reference: silu_mul_quant,
+ * ops.h:24, ops.hip:146-151,770-772) */
+int qmm_silu_mul_quant(const float* gate, const float* up, qmm_xq8 xq, int n, void* stream);
+/* out = bf16(silu(gate) * up), n elements (reference: silu_mul_bf16, ops.h:20, ops.hip:131,765) */
+int qmm_silu_mul_bf16(const float* gate, const float* up, uint16_t* out, size_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

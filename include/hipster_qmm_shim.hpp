@@ -148,6 +148,22 @@ inline void moe_silu_bf16(const float* gate, const float* up, uint16_t* h, size_
     detail::ck(qmm_moe_silu_bf16(gate, up, h, n, (void*)s), "moe_silu_bf16");
 }
 
+// ---- ops.h (the q8 / bf16 producers of the matmul inputs) -----------------------------------
+inline void add_rmsnorm_quant(float* x, const float* y, const float* w, float* xn, XQ8 xq, int T, int n, float eps,
+                              hipStream_t s) {                                                      // ops.h:14
+    detail::ck(qmm_add_rmsnorm_quant(x, y, w, xn, to_c(xq), T, n, eps, (void*)s), "add_rmsnorm_quant");
+}
+inline void add_rmsnorm_bf16(float* x, const float* y, const float* w, uint16_t* xb, int T, int n, float eps,
+                             hipStream_t s) {                                                       // ops.h:18
+    detail::ck(qmm_add_rmsnorm_bf16(x, y, w, xb, T, n, eps, (void*)s), "add_rmsnorm_bf16");
+}
+inline void silu_mul_quant(const float* gate, const float* up, XQ8 xq, int n, hipStream_t s) {      // ops.h:24
+    detail::ck(qmm_silu_mul_quant(gate, up, to_c(xq), n, (void*)s), "silu_mul_quant");
+}
+inline void silu_mul_bf16(const float* gate, const float* up, uint16_t* out, size_t n, hipStream_t s) {  // ops.h:20
+    detail::ck(qmm_silu_mul_bf16(gate, up, out, n, (void*)s), "silu_mul_bf16");
+}
+
 namespace fn {
 // ---- fn.h (MoE part) ----------------------------------------------------------------------
 inline void moe_route(const float* logits, int* ids, float* w, int T, hipStream_t s) {

@@ -42,6 +42,8 @@ def lib():
         L.qo_f32_to_f16.restype = ctypes.c_uint16
         L.qo_f32_to_f16.argtypes = [ctypes.c_float]
         L.qo_k_granule.restype = I
+        L.qo_block_sum1024.restype = ctypes.c_float
+        L.qo_block_sum1024.argtypes = [P]
         L.qo_k_granule.argtypes = [I]
         L.qo_row_bytes.restype = ctypes.c_size_t
         L.qo_row_bytes.argtypes = [I, I]
@@ -56,6 +58,8 @@ def lib():
             "qo_dequant_matrix": [I, P, I, I, P, I], "qo_dequant_matrix_bf16": [I, P, I, I, P, I],
             "qo_quantize_x_q8": [P, I, P, P, P], "qo_q8_to_f32": [P, P, I, P],
             "qo_silu_mul": [P, P, ctypes.c_size_t, P],
+            "qo_add_rmsnorm_quant": [P, P, P, P, P, P, P, I, I, ctypes.c_float],
+            "qo_add_rmsnorm_bf16": [P, P, P, P, I, I, ctypes.c_float],
             "qo_gemv_ref": [I, P, I, I, P, I, P, P, I],
             "qo_gemv_ref_rows": [I, P, I, I, P, I, P, I, P, P],
             "qo_gemv_f32": [I, P, I, I, P, I, P, I],
@@ -123,6 +127,40 @@ def quantize_x_q8(x):
     for c in range(ncol):
         lib().qo_quantize_x_q8(_ptr(x[c]), K, _ptr(q[c]), _ptr(d[c]), _ptr(s[c]))
     return q, d, s
+
+
+def add_rmsnorm_quant(x, y, w, eps):
+    """ops.hip:79-98 over rows of x [T][n]: returns (x + y, xn, q, d, s); x is not modified."""
+    x = np.array(np.atleast_2d(x), dtype=np.float32, order="C", copy=True)
+    T, n = x.shape
+    yy = None if y is None else np.ascontiguousarray(np.atleast_2d(y), dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    xn = np.empty_like(x)
+    q = np.empty((T, n), dtype=np.int8)
+    d = np.empty((T, n // 32), dtype=np.float32)
+    s = np.empty((T, n // 32), dtype=np.float32)
+    if lib().qo_add_rmsnorm_quant(_ptr(x), None if yy is None else _ptr(yy), _ptr(w), _ptr(xn), _ptr(q), _ptr(d), _ptr(s),
+                                  T, n, eps) != 0:
+        raise ValueError("add_rmsnorm_quant: n")
+    return x, xn, q, d, s
+
+
+def add_rmsnorm_bf16(x, y, w, eps):
+    """ops.hip:111-120 over rows of x [T][n]: returns (x + y, xb uint16 bits)."""
+    x = np.array(np.atleast_2d(x), dtype=np.float32, order="C", copy=True)
+    T, n = x.shape
+    yy = None if y is None else np.ascontiguousarray(np.atleast_2d(y), dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    xb = np.empty((T, n), dtype=np.uint16)
+    if lib().qo_add_rmsnorm_bf16(_ptr(x), None if yy is None else _ptr(yy), _ptr(w), _ptr(xb), T, n, eps) != 0:
+        raise ValueError("add_rmsnorm_bf16: n")
+    return x, xb
+
+
+def block_sum1024(part):
+    part = np.ascontiguousarray(part, dtype=np.float32)
+    assert part.shape == (1024,)
+    return lib().qo_block_sum1024(_ptr(part))
 
 
 def q8_to_f32(q, d):

@@ -371,6 +371,72 @@ void qo_silu_mul(const float* g, const float* u, size_t n, float* h) {
     for (size_t i = 0; i < n; ++i) h[i] = g[i] / (1.f + expf(-g[i])) * u[i];
 }
 
+/* ops.hip:64-78 (block_sum1024): 1024 per-thread partials folded by the xor butterfly of
+ * __shfl_xor(v, o, 32), o = 16..1, inside each group of 32 threads, then the same butterfly over the
+ * 32 group sums.  Lane l adds lane l^o; both partners form the same sum, so it is a pairwise tree. */
+float qo_block_sum1024(const float* part) {
+    float g[32];
+    for (int w = 0; w < 32; ++w) {
+        float a[32], b[32];
+        for (int l = 0; l < 32; ++l) a[l] = part[w * 32 + l];
+        for (int o = 16; o > 0; o >>= 1) {
+            for (int l = 0; l < 32; ++l) b[l] = a[l] + a[l ^ o];
+            for (int l = 0; l < 32; ++l) a[l] = b[l];
+        }
+        g[w] = a[0];
+    }
+    for (int o = 16; o > 0; o >>= 1) {
+        float b[32];
+        for (int l = 0; l < 32; ++l) b[l] = g[l] + g[l ^ o];
+        for (int l = 0; l < 32; ++l) g[l] = b[l];
+    }
+    return g[0];
+}
+
+/* one row of ops.hip:79-98 / 111-120: x += y (when y), the scale 1/sqrt(ss/n + eps) with ss the sum
+ * of squares of 1024 threads (thread t: fma over elements t, t+1024, ... in that order, then
+ * block_sum1024).  The reference's rsqrtf is replaced by the correctly rounded value (1/sqrt in
+ * double, rounded once), which the library computes the same way. */
+static float rms_row(float* x, const float* y, int n, float eps) {
+    float part[1024];
+    for (int t = 0; t < 1024; ++t) {
+        float ss = 0.f;
+        for (int i = t; i < n; i += 1024) {
+            float a = x[i];
+            if (y) { a += y[i]; x[i] = a; }
+            ss = fmaf(a, a, ss);
+        }
+        part[t] = ss;
+    }
+    const float tot = qo_block_sum1024(part);
+    return (float)(1.0 / sqrt((double)(tot / (float)n + eps)));
+}
+
+/* ops.hip:79-98: per row, x += y, xn = x * sc * w ((x*sc)*w, two roundings), q8 of xn per 32 */
+int qo_add_rmsnorm_quant(float* x, const float* y, const float* w, float* xn, int8_t* q, float* d, float* s, int T, int n,
+                         float eps) {
+    if (n <= 0 || n % 32 != 0 || n > 32768) return -1;
+    for (int t = 0; t < T; ++t) {
+        float* xr = x + (size_t)t * n;
+        float* on = xn + (size_t)t * n;
+        const float sc = rms_row(xr, y ? y + (size_t)t * n : NULL, n, eps);
+        for (int i = 0; i < n; ++i) on[i] = xr[i] * sc * w[i];
+        qo_quantize_x_q8(on, n, q + (size_t)t * n, d + (size_t)t * (n / 32), s + (size_t)t * (n / 32));
+    }
+    return 0;
+}
+
+/* ops.hip:111-120: per row, x += y, xb = bf16(x * sc * w) */
+int qo_add_rmsnorm_bf16(float* x, const float* y, const float* w, uint16_t* xb, int T, int n, float eps) {
+    if (n <= 0 || n > 32768) return -1;
+    for (int t = 0; t < T; ++t) {
+        float* xr = x + (size_t)t * n;
+        const float sc = rms_row(xr, y ? y + (size_t)t * n : NULL, n, eps);
+        for (int i = 0; i < n; ++i) xb[(size_t)t * n + i] = qo_f32_to_bf16(xr[i] * sc * w[i]);
+    }
+    return 0;
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* GEMV references                                                                             */
 

@@ -65,6 +65,15 @@ void qo_q8_to_f32(const int8_t* q, const float* d, int K, float* xr);
 /* silu(g)*u per element, then the q8 quantiser over rows of n (fn.hip:206-211) */
 void qo_silu_mul(const float* g, const float* u, size_t n, float* h);
 
+/* ops.hip:64-78: the pairwise tree of block_sum1024 over 1024 per-thread partials */
+float qo_block_sum1024(const float* part);
+/* ops.hip:79-98: per row t < T: x += y (y may be NULL), xn = (x*sc)*w with sc = 1/sqrt(ss/n + eps)
+ * (correctly rounded; the reference's rsqrtf is within about 1 ulp), q8 of xn; n % 32 == 0 */
+int qo_add_rmsnorm_quant(float* x, const float* y, const float* w, float* xn, int8_t* q, float* d, float* s, int T, int n,
+                         float eps);
+/* ops.hip:111-120: as above, xb = bf16((x*sc)*w) */
+int qo_add_rmsnorm_bf16(float* x, const float* y, const float* w, uint16_t* xb, int T, int n, float eps);
+
 /* ---- GEMV references ---- */
 /* y[c][n] = sum_k w[n][k] * x[c][k] in double, mag[c][n] = sum_k |w*x| (bench_gemv.cpp:95-104) */
 int qo_gemv_ref(int wfmt, const uint8_t* W, int N, int K, const float* x, int ncol,

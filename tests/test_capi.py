@@ -128,6 +128,25 @@ def test_moe_argument_validation_without_device_work():
     assert L.qmm_moe_combine_sorted(d, d, None, d, 4, 11, 2048, None) == -3
 
 
+def test_activation_producer_validation_without_device_work():
+    L = _lib.lib()
+    d = ctypes.c_void_p(16)
+    assert L.qmm_add_rmsnorm_quant(d, None, d, d, _xq(16), 1, 5000, 1e-6, None) == -2      # n % 32 != 0
+    assert L.qmm_add_rmsnorm_quant(d, None, d, d, _xq(16), 1, 16416, 1e-6, None) == -2     # n above 16384
+    assert L.qmm_add_rmsnorm_quant(d, None, d, None, _xq(16), 1, 5120, 1e-6, None) == -3   # xn missing
+    assert L.qmm_add_rmsnorm_quant(d, None, d, d, _lib.XQ8(16, 0, 16, 0), 1, 5120, 1e-6, None) == -3
+    assert L.qmm_add_rmsnorm_quant(d, None, d, d, _xq(16), 0, 5120, 1e-6, None) == 0       # empty batch
+    assert L.qmm_add_rmsnorm_quant(d, None, d, d, _xq(16), -1, 5120, 1e-6, None) == -2
+    assert L.qmm_add_rmsnorm_bf16(d, None, d, None, 1, 5120, 1e-6, None) == -3
+    assert L.qmm_add_rmsnorm_bf16(d, None, d, d, 1, 20000, 1e-6, None) == -2
+    assert L.qmm_add_rmsnorm_bf16(d, None, d, d, 0, 77, 1e-6, None) == 0
+    assert L.qmm_silu_mul_quant(d, d, _xq(16), 100, None) == -2
+    assert L.qmm_silu_mul_quant(None, d, _xq(16), 128, None) == -3
+    assert L.qmm_silu_mul_quant(d, d, _xq(16), 0, None) == 0
+    assert L.qmm_silu_mul_bf16(d, None, d, 128, None) == -3
+    assert L.qmm_silu_mul_bf16(d, d, d, 0, None) == 0
+
+
 def test_prefill_argument_validation_without_device_work():
     L = _lib.lib()
     d = ctypes.c_void_p(16)
