@@ -29,33 +29,44 @@ namespace {
 constexpr int kMaxCols = 8;        // columns per pass of the gather GEMV
 
 // ------------------------------------------------------------------------------------------
-// Routing (fn.hip:157-205 semantics).  One wave per token (4 tokens per workgroup), VPL logits per
-// lane (expert lane + 64 j).  Top-k is taken on the logits (softmax is monotone, so this is the
-// top-k of the probabilities without their rounding), ties to the lower expert id, by k rounds of
-// wave argmax over the lanes' best untaken values.  Weights are p_i / sum_{selected} p with
-// p = exp(l - max) / sum_all exp(l - max), the selected sum in selection order; slot k is the
-// shared expert: id -1, weight sigmoid(logit[nexp]).
-__device__ __forceinline__ bool route_better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+// Routing (fn.hip:157-205).  One wave per token (4 tokens per workgroup), VPL logits per lane (expert
+// lane + 64 j).  The arithmetic is the reference's: mx = max of the logits; e = __expf(l - mx); the
+// denominator is the xor-butterfly sum of e over each 32 consecutive experts (experts 32g..32g+31 are
+// the 32 lanes of half g & 1 of value j = g >> 1), then those group sums added in order; p = e / sum;
+// the top-k by p with ties to the lower id; weights p / (the selected p summed in selection order);
+// slot k is the shared expert: id -1, weight sigmoid(logit[nexp]).  Each round takes the wave max of
+// the lanes' best untaken p (DPP on the bits as integers), finds the lane holding it with one ballot
+// and, only when several lanes hold that value, the lowest id among them.
 
-// one DPP step of the (value, id) argmax: combine with the lane the DPP control names (lanes
-// without a source see (-inf, INT_MAX))
+// one DPP step of a wave max / min (lanes without a source see the neutral value)
 template <int CTRL, int ROWS>
-__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
-    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), CTRL, ROWS, 0xf, false));
-    const int oi = __builtin_amdgcn_update_dpp(0x7fffffff, i, CTRL, ROWS, 0xf, false);
-    if (route_better(ov, oi, v, i)) { v = ov; i = oi; }
+__device__ __forceinline__ float max_dpp(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), CTRL, ROWS, 0xf, false)));
 }
-// argmax over the wave (larger value, then lower id), result in every lane: DPP row_shr 1/2/4/8
-// leaves each row's best in its lane 15, row_bcast15 / row_bcast31 carry them into lane 63
-__device__ __forceinline__ void wave_argmax64(float& v, int& i) {
-    argmax_dpp<0x111, 0xf>(v, i);
-    argmax_dpp<0x112, 0xf>(v, i);
-    argmax_dpp<0x114, 0xf>(v, i);
-    argmax_dpp<0x118, 0xf>(v, i);
-    argmax_dpp<0x142, 0xa>(v, i);
-    argmax_dpp<0x143, 0xc>(v, i);
-    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-    i = __builtin_amdgcn_readlane(i, 63);
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int min_dpp(int v) {
+    return min(v, __builtin_amdgcn_update_dpp(0x7fffffff, v, CTRL, ROWS, 0xf, false));
+}
+// DPP row_shr 1/2/4/8 leave each row's result in its lane 15; row_bcast15 / row_bcast31 carry them
+// into lane 63, which is read back as a wave-uniform value.
+__device__ __forceinline__ float wave_max64(float v) {
+    v = max_dpp<0x111, 0xf>(v); v = max_dpp<0x112, 0xf>(v); v = max_dpp<0x114, 0xf>(v); v = max_dpp<0x118, 0xf>(v);
+    v = max_dpp<0x142, 0xa>(v); v = max_dpp<0x143, 0xc>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int imax_dpp(int v) {
+    return max(v, __builtin_amdgcn_update_dpp((int)0x80000000, v, CTRL, ROWS, 0xf, false));
+}
+__device__ __forceinline__ int wave_imax64(int v) {
+    v = imax_dpp<0x111, 0xf>(v); v = imax_dpp<0x112, 0xf>(v); v = imax_dpp<0x114, 0xf>(v); v = imax_dpp<0x118, 0xf>(v);
+    v = imax_dpp<0x142, 0xa>(v); v = imax_dpp<0x143, 0xc>(v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ int wave_min64(int v) {
+    v = min_dpp<0x111, 0xf>(v); v = min_dpp<0x112, 0xf>(v); v = min_dpp<0x114, 0xf>(v); v = min_dpp<0x118, 0xf>(v);
+    v = min_dpp<0x142, 0xa>(v); v = min_dpp<0x143, 0xc>(v);
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 constexpr int kRouteMaxK = 16, kRouteMaxExp = 1024;
@@ -72,41 +83,63 @@ __global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ log
         const float x = l[min(lane + 64 * j, nexp - 1)];
         v[j] = lane + 64 * j < nexp ? x : -INFINITY;
     }
+    const float gate = l[nexp];
     float mx = v[0];
 #pragma unroll
     for (int j = 1; j < VPL; ++j) mx = fmaxf(mx, v[j]);
+    mx = wave_max64(mx);
+    float e[VPL], gs[VPL];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    float e = 0.f;
+    for (int j = 0; j < VPL; ++j) e[j] = lane + 64 * j < nexp ? __expf(v[j] - mx) : 0.f;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j)
-        if (lane + 64 * j < nexp) e += __expf(v[j] - mx);
-    const float sum = wave_sum(e);
-    uint32_t taken = 0;
+    for (int j = 0; j < VPL; ++j) gs[j] = hw32_sum(e[j]);
+    float sum = 0.f;                                     // groups past nexp add +0 (exact)
 #pragma unroll
-    for (int j = 0; j < VPL; ++j)
-        if (lane + 64 * j >= nexp) taken |= 1u << j;
+    for (int j = 0; j < VPL; ++j) {
+        sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs[j]), 0));
+        sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs[j]), 32));
+    }
+    // p of a taken expert becomes -1 (below every p >= 0), a missing one is -inf
+    float p[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) p[j] = lane + 64 * j < nexp ? e[j] / sum : -INFINITY;
+    float bv = p[0];
+    int bj = 0;
+#pragma unroll
+    for (int j = 1; j < VPL; ++j)
+        if (p[j] > bv) { bv = p[j]; bj = j; }            // strict: ties keep the lower id
     float psel = 0.f, wsum = 0.f;
+    int isel = 0;
+    // the round's max on the bits of p as signed ints: every p >= 0 orders as its float (and beats
+    // the negative marks of taken or missing experts, whose order among themselves never matters:
+    // an untaken expert with p >= 0 is always left)
+    for (int r = 0; r < topk; ++r) {
+        const int mb = wave_imax64(__float_as_int(bv));
+        const float m = __int_as_float(mb);
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(__float_as_int(bv) == mb);
+        int wl;
+        if (__builtin_popcountll(hit) == 1) {
+            wl = __builtin_ctzll(hit);
+        } else {                                         // a tie across lanes: the lowest id wins
+            wl = wave_min64(__float_as_int(bv) == mb ? lane + 64 * bj : 0x7fffffff) & 63;
+        }
+        const int wj = __builtin_amdgcn_readlane(bj, wl);
+        if (lane == r) { psel = m; isel = wl + 64 * wj; }
+        wsum += m;                                       // selection order
+        if (lane == wl) {
+#pragma unroll
+            for (int j = 0; j < VPL; ++j)
+                if (j == wj) p[j] = -1.f;
+            bv = p[0]; bj = 0;
+#pragma unroll
+            for (int j = 1; j < VPL; ++j)
+                if (p[j] > bv) { bv = p[j]; bj = j; }
+        }
+    }
     int* idt = ids + (size_t)t * (topk + 1);
     float* wt = w + (size_t)t * (topk + 1);
-    for (int r = 0; r < topk; ++r) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < VPL; ++j)
-            if (!((taken >> j) & 1u) && route_better(v[j], lane + 64 * j, bv, bi)) { bv = v[j]; bi = lane + 64 * j; }
-        wave_argmax64(bv, bi);
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        const float p = __expf(bv - mx) / sum;          // wave-uniform
-        wsum += p;                                       // selection order
-        if (lane == r) psel = p;
-        if (lane == 0) idt[r] = bi;
-    }
-    if (lane < topk) wt[lane] = psel / wsum;
-    if (lane == 0) {
-        idt[topk] = -1;
-        wt[topk] = 1.f / (1.f + __expf(-l[nexp]));
-    }
+    if (lane < topk) { idt[lane] = isel; wt[lane] = psel / wsum; }
+    if (lane == topk) { idt[topk] = -1; wt[topk] = 1.f / (1.f + __expf(-gate)); }
 }
 
 // ------------------------------------------------------------------------------------------

@@ -102,9 +102,10 @@ int qmm_gemv_q8_f32x(int fmt, const void* W, const float* x, float* y, int N, in
 int qmm_gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int ncol, int tpr, void* stream);
 
 /* ---- MoE decode ---- */
-/* routing (reference: fn::moe_route, fn.h:43, fn.hip:160-205,301): logits [T][513] f32 -> softmax over
- * 512 experts -> top-10 (ties to the lower id) -> weights renormalised over the 10; slot 10 is the
- * shared expert (id -1, weight sigmoid(logits[t][512])).  ids [T][11] int32, w [T][11] f32. */
+/* routing (reference: fn::moe_route, fn.h:43, fn.hip:157-205,301): logits [T][513] f32 -> softmax over
+ * 512 experts (p = exp(l - max) / sum, the sum in the reference's order) -> top-10 by p (ties to the
+ * lower id) -> weights renormalised over the 10 in selection order; slot 10 is the shared expert
+ * (id -1, weight sigmoid(logits[t][512])).  ids [T][11] int32, w [T][11] f32. */
 int qmm_moe_route(const float* logits, int* ids, float* w, int T, void* stream);
 /* the same for nexp <= 1024 experts, row stride >= nexp+1 (logit nexp = shared gate), topk <= 16:
  * ids/w [T][topk+1].  No reference counterpart (the reference fixes 512/513/10 at compile time). */

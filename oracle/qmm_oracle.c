@@ -500,33 +500,47 @@ int qo_gemv_f32(int wfmt, const uint8_t* W, int N, int K, const float* x, int nc
 /* ------------------------------------------------------------------------------------------ */
 /* MoE routing, sort, decode and prefill references                                            */
 
-/* fn.hip:157-205.  The reference selects by repeated argmax over the softmax probabilities with
- * ties going to the smaller index.  exp is monotone, so this is the top-k of the logits; the
- * oracle selects on the logits themselves (exact, no rounding) with the same tie rule.  The
- * weights are p_i / sum of the selected p (p = exp(l - max) / sum over all), accumulated in
- * selection order; the shared slot gets sigmoid(logit[nexp]). */
+/* fn.hip:157-205 (k_moe_route), for nexp experts (the reference: 512) and top-k (the reference: 10):
+ *   mx = max of the logits; e_i = exp(l_i - mx);
+ *   sum = S_0 + S_1 + ... in that order, S_g the xor-butterfly sum (lane l with l^16, then l^8, ..., l^1;
+ *         a pairwise tree) of e over experts 32g .. 32g+31 (experts past nexp add nothing);
+ *   p_i = e_i / sum; the top-k by p, ties to the lower id (k rounds of argmax); w_r = p_r / wsum with
+ *   wsum the sum of the selected p in selection order; slot k: id -1, w = sigmoid(l[nexp]).
+ * The device exp (__expf) and the host libm's expf may differ in the last ulp. */
+static float tree32(const float* e) {
+    float a[32], b[32];
+    for (int l = 0; l < 32; ++l) a[l] = e[l];
+    for (int o = 16; o > 0; o >>= 1) {
+        for (int l = 0; l < 32; ++l) b[l] = a[l] + a[l ^ o];
+        for (int l = 0; l < 32; ++l) a[l] = b[l];
+    }
+    return a[0];
+}
 void qo_moe_route(const float* logits, int T, int nexp, int stride, int topk, int* ids, float* w) {
+    const int ng = (nexp + 31) / 32;
+    float* e = (float*)calloc((size_t)ng * 32, sizeof(float));
     float* p = (float*)malloc(sizeof(float) * (size_t)nexp);
     char* used = (char*)malloc((size_t)nexp);
     for (int t = 0; t < T; ++t) {
         const float* l = logits + (size_t)t * stride;
         float mx = l[0];
         for (int i = 1; i < nexp; ++i) mx = fmaxf(mx, l[i]);
+        for (int i = 0; i < nexp; ++i) e[i] = expf(l[i] - mx);
         float sum = 0.f;
-        for (int i = 0; i < nexp; ++i) { p[i] = expf(l[i] - mx); sum += p[i]; }
-        for (int i = 0; i < nexp; ++i) p[i] = p[i] / sum;
+        for (int g = 0; g < ng; ++g) sum += tree32(e + 32 * g);
+        for (int i = 0; i < nexp; ++i) p[i] = e[i] / sum;
         memset(used, 0, (size_t)nexp);
         float wsum = 0.f;
         int* id = ids + (size_t)t * (topk + 1); float* ww = w + (size_t)t * (topk + 1);
         for (int r = 0; r < topk; ++r) {
             int bi = -1;
-            for (int i = 0; i < nexp; ++i) if (!used[i] && (bi < 0 || l[i] > l[bi])) bi = i;
+            for (int i = 0; i < nexp; ++i) if (!used[i] && (bi < 0 || p[i] > p[bi])) bi = i;
             used[bi] = 1; id[r] = bi; ww[r] = p[bi]; wsum += p[bi];
         }
         for (int r = 0; r < topk; ++r) ww[r] /= wsum;
         id[topk] = -1; ww[topk] = 1.f / (1.f + expf(-l[nexp]));
     }
-    free(p); free(used);
+    free(e); free(p); free(used);
 }
 
 /* qwen4exp.cpp:628-641.  Sorting by (eid, te) is a stable counting sort over the slots taken in

@@ -85,9 +85,10 @@ int qo_gemv_ref_rows(int wfmt, const uint8_t* W, int N, int K, const float* x, i
 int qo_gemv_f32(int wfmt, const uint8_t* W, int N, int K, const float* x, int ncol, float* y, int nthreads);
 
 /* ---- MoE routing / sort / combine ---- */
-/* softmax over nexp logits (row stride `stride`), top-k by value with ties -> lower id, weights
- * renormalised over the k; slot k is the shared expert: id -1, w = sigmoid(logits[nexp])
- * (engine/kernels/fn.hip:157-205).  ids/w are [T][k+1]. */
+/* softmax over nexp logits (row stride `stride`; the denominator summed per 32 experts with the
+ * xor-butterfly tree, then across groups in order), top-k by the rounded probability with ties ->
+ * lower id, weights renormalised over the k in selection order; slot k is the shared expert: id -1,
+ * w = sigmoid(logits[nexp]) (engine/kernels/fn.hip:157-205).  ids/w are [T][k+1]. */
 void qo_moe_route(const float* logits, int T, int nexp, int stride, int topk, int* ids, float* w);
 /* slots te = t*NE+e sorted by (expert id, te) with the shared slots (id < 0) kept in their own
  * list; tiles of <= maxc consecutive sorted positions per expert (engine/src/qwen4exp.cpp:628-641).

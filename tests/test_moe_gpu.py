@@ -23,6 +23,22 @@ def experts(seed, n_exp, N, K):
     return synth.experts(seed, synth.Q4_K, n_exp, N, K)
 
 
+def assert_route_matches(ids, w, ids_ref, w_ref, logits, nexp):
+    """ids bit-exact, except where two candidates' probabilities are within 1e-6 of each other: the
+    selection runs on the rounded p (as the reference), and the device exp (__expf) and the host libm's
+    expf may differ by an ulp, which can swap such a near-tie.  Weights within 1e-5."""
+    bad = np.nonzero((ids != ids_ref).any(axis=1))[0]
+    for t in bad:
+        l = logits[t, :nexp].astype(np.float64)
+        p = np.exp(l - l.max()); p /= p.sum()
+        for a, b in zip(ids[t], ids_ref[t]):
+            if a != b:
+                assert a >= 0 and b >= 0 and abs(p[a] - p[b]) <= 1e-6 * max(p[a], p[b]), (t, a, b, p[a], p[b])
+    assert len(bad) <= 2, bad
+    ok = np.setdiff1d(np.arange(ids.shape[0]), bad)
+    np.testing.assert_allclose(w[ok], w_ref[ok], rtol=1e-5, atol=1e-7)
+
+
 @pytest.mark.parametrize("T,zipf", [(1, None), (4, None), (8, None), (2048, 1.1)])
 def test_route_matches_oracle(gpu, T, zipf):
     logits = synth.router_logits(1200 + T, T, 512, zipf)
@@ -30,8 +46,24 @@ def test_route_matches_oracle(gpu, T, zipf):
     ids = torch.zeros((T, 11), dtype=torch.int32, device="cuda")
     w = torch.zeros((T, 11), dtype=torch.float32, device="cuda")
     qmm.moe_route(dev(logits), ids, w, T)
-    assert np.array_equal(host(ids), ids_ref)
-    np.testing.assert_allclose(host(w), w_ref, rtol=1e-5, atol=1e-7)
+    ids_h = host(ids)
+    print(f"route T={T}: {int((ids_h != ids_ref).any(axis=1).sum())} tokens differ from the oracle", flush=True)
+    assert_route_matches(ids_h, host(w), ids_ref, w_ref, logits, 512)
+
+
+def test_route_selects_on_rounded_probabilities(gpu):
+    """Experts 3 (logit -2^-30) and 8 (logit 0) both get exp(.) = 1.0 and so the same p: the lower id
+    is taken first, as the reference's argmax on p does (fn.hip:176-180)."""
+    logits = np.full((2, 513), -4.0, np.float32)
+    logits[:, 8] = 0.0
+    logits[:, 3] = -2.0 ** -30
+    ids = torch.zeros((2, 11), dtype=torch.int32, device="cuda")
+    w = torch.zeros((2, 11), dtype=torch.float32, device="cuda")
+    qmm.moe_route(dev(logits), ids, w, 2)
+    ids_h, w_h = host(ids), host(w)
+    assert list(ids_h[0, :2]) == [3, 8] and w_h[0, 0] == w_h[0, 1]
+    ids_ref, _ = oracle.moe_route(logits, 512, 10)
+    assert np.array_equal(ids_h, ids_ref)
 
 
 def test_route_ties_and_small_expert_counts(gpu):
@@ -45,8 +77,7 @@ def test_route_ties_and_small_expert_counts(gpu):
         ids = torch.zeros((6, topk + 1), dtype=torch.int32, device="cuda")
         w = torch.zeros((6, topk + 1), dtype=torch.float32, device="cuda")
         qmm.moe_route_n(dev(lg), ids, w, 6, nexp, lg.shape[1], topk)
-        assert np.array_equal(host(ids), ids_ref), (nexp, topk)
-        np.testing.assert_allclose(host(w), w_ref, rtol=1e-5, atol=1e-7)
+        assert_route_matches(host(ids), host(w), ids_ref, w_ref, lg, nexp)
 
 
 def test_moe_silu_quant(gpu):

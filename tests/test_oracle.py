@@ -222,6 +222,19 @@ def test_route_ties_go_to_lower_id_and_zipf():
     assert np.array_equal(ids, bi)
 
 
+def test_route_selects_on_rounded_probabilities():
+    """fn.hip:176-180: the argmax runs on p = exp(l - max) / sum as floats, ties to the lower id.  Logits
+    0 and -2^-30 both give exp(.) = 1.0f (the exact value 1 - 9.3e-10 is far closer to 1 than to the
+    next float below, 1 - 6e-8), so experts 3 (logit -2^-30) and 8 (logit 0, the larger) tie on p and
+    the lower id, 3, is taken first; a rule on the logits would take 8 first."""
+    logits = np.full((1, 65), -4.0, np.float32)
+    logits[0, 8] = 0.0
+    logits[0, 3] = -2.0 ** -30
+    ids, w = oracle.moe_route(logits, 64, 4)
+    assert list(ids[0, :2]) == [3, 8]
+    assert w[0, 0] == w[0, 1]
+
+
 def test_sort_tiles_invariants():
     logits = synth.router_logits(41, 300, zipf_s=1.1)
     ids, _ = oracle.moe_route(logits)
