@@ -48,7 +48,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
-    p.add_argument("--only-extra", choices=["activation_producers", "formats"], default=None,
+    p.add_argument("--only-extra", choices=["activation_producers", "formats", "router"], default=None,
                    help="only run one of the extra measurements and print its JSON (for profiling it alone)")
     p.add_argument("--calib-copy", action="store_true",
                    help="only run 10 plain device copies of 256 MiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -192,6 +192,25 @@ def extra_act(torch):
         out[f"silu_mul_bf16_T{T}"] = {"us": round(us, 2), "GB_s": round(m * 10 / us / 1e3, 1)}
         del g, u, hq, hb
         torch.cuda.empty_cache()
+    return out
+
+
+def extra_router(torch):
+    """The MoE router matmul (f32, 513 x hidden 2048 as config 2) and the router + routing call at
+    decode batch sizes, router copies rotated beyond one XCD's L2: time per call and W bytes / time."""
+    from hipster_amd import qmm
+    K, N, R = 2048, 513, 8
+    Ws = [torch.randn((N, K), device="cuda") * 0.05 for _ in range(R)]
+    out = {}
+    for T in (1, 4, 8):
+        x = torch.randn((T, K), device="cuda")
+        lg = torch.zeros((T, N), device="cuda")
+        ids = torch.zeros((T, 11), dtype=torch.int32, device="cuda")
+        w = torch.zeros((T, 11), device="cuda")
+        us = graph_us(torch, [(lambda i: (lambda: qmm.f32_gemv(Ws[i], x, lg, N, K, T)))(i) for i in range(R)], reps=4) / R
+        us2 = graph_us(torch, [(lambda i: (lambda: qmm.moe_router(Ws[i], x, lg, ids, w, T, 512, K, 10)))(i) for i in range(R)],
+                       reps=4) / R
+        out[f"T{T}"] = {"f32_gemv_us": round(us, 2), "GB_s": round(N * K * 4 / us / 1e3, 1), "router_and_route_us": round(us2, 2)}
     return out
 
 
@@ -360,7 +379,7 @@ def main():
         calib_copy()
         return
     if args.only_extra:
-        fn = {"activation_producers": extra_act, "formats": extra_formats}[args.only_extra]
+        fn = {"activation_producers": extra_act, "formats": extra_formats, "router": extra_router}[args.only_extra]
         print(json.dumps({args.only_extra: fn(torch)}), flush=True)
         return
     from hipster_amd import _lib
@@ -415,6 +434,7 @@ def main():
         torch.cuda.empty_cache()
         extra["formats_gemv_17408x5120"] = extra_formats(torch)
         extra["activation_producers"] = extra_act(torch)
+        extra["moe_router"] = extra_router(torch)
         out["extra"] = extra
     print(json.dumps(out), flush=True)
 

@@ -167,6 +167,20 @@ def moe_silu_quant(gate, up, xq, rows, n, stream=None):
     check(_lib.lib().qmm_moe_silu_quant(_p(gate), _p(up), xq.c(), rows, n, _stream(stream)), "moe_silu_quant")
 
 
+def f32_gemv(W, x, y, N, K, T, stream=None):
+    """fn.h:37: y[t][n] = W[n] . x[t] in f32 (the reference's arithmetic and order)."""
+    _dev(W, torch.float32, "W"); _dev(x, torch.float32, "x"); _dev(y, torch.float32, "y")
+    check(_lib.lib().qmm_f32_gemv(_p(W), _p(x), _p(y), N, K, T, _stream(stream)), "f32_gemv")
+
+
+def moe_router(Wr, x, logits, ids, w, T, nexp=512, K=None, topk=10, stream=None):
+    """qwen4exp.cpp:346-347 in one call: logits = Wr . x (f32_gemv), then moe_route_n on them."""
+    _dev(Wr, torch.float32, "Wr"); _dev(x, torch.float32, "x"); _dev(logits, torch.float32, "logits")
+    K = x.shape[-1] if K is None else K
+    check(_lib.lib().qmm_moe_router(_p(Wr), _p(x), _p(logits), _p(ids), _p(w), T, nexp, K, topk, _stream(stream)),
+          "moe_router")
+
+
 # ---- activation producers (engine/kernels/ops.h) ----
 def add_rmsnorm_quant(x, y, w, xn, xq, T, n, eps, stream=None):
     """ops.h:14: per row, x += y (y may be None), xn = rmsnorm(x) * w, xq = q8(xn) (XQ8Buf of T x n)."""

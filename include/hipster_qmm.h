@@ -110,6 +110,16 @@ int qmm_moe_route(const float* logits, int* ids, float* w, int T, void* stream);
 /* the same for nexp <= 1024 experts, row stride >= nexp+1 (logit nexp = shared gate), topk <= 16:
  * ids/w [T][topk+1].  No reference counterpart (the reference fixes 512/513/10 at compile time). */
 int qmm_moe_route_n(const float* logits, int* ids, float* w, int T, int nexp, int stride, int topk, void* stream);
+/* router matmul (reference: fn::f32_gemv, fn.h:37, fn.hip:251-277): y[t][n] = W[n] . x[t], W [N][K] f32,
+ * x [T][K] f32, y [T][N] f32, K % 4 == 0, W and x 16-byte aligned.  The reference's arithmetic and
+ * order (32 lanes per row over float4 steps 4l + 128k, its fma contraction, the xor-butterfly sum):
+ * the same bits. */
+int qmm_f32_gemv(const float* W, const float* x, float* y, int N, int K, int T, void* stream);
+/* qmm_f32_gemv of the router (nexp+1 rows: the experts and the shared gate) into logits [T][nexp+1],
+ * then qmm_moe_route_n on them: the two calls of qwen4exp.cpp:346-347 in one (two launches, no host
+ * work between).  No reference counterpart as one function. */
+int qmm_moe_router(const float* Wr, const float* x, float* logits, int* ids, float* w, int T, int nexp, int K, int topk,
+                   void* stream);
 /* expert GEMV (reference: gemv_moe, gemv.h:44, gemv.hip:1075-1129,1385-1394).  Slot te = t*nexp+e
  * uses expert ids[te] (ids < 0: the shared matrices a->shared[g]); x row = te if xrow_te else t.
  * Without a->slotw: y[g][te][N] = W[g][ids[te]] . x[row] for g < nseg (gate|up share the launch);

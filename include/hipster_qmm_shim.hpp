@@ -174,6 +174,9 @@ inline void moe_gemv(WFmt fmt, WFmt shared_fmt, const MoeSegs& a, int nseg, cons
     // the reference's forwarder: the down projection (slot weights set) reads per-(t, e) rows
     hip::gemv_moe(fmt, shared_fmt, a, nseg, ids, nexp, xq, N, K, T, a.slotw != nullptr, s);
 }
+inline void f32_gemv(const float* W, const float* x, float* y, int N, int K, int T, hipStream_t s) {   // fn.h:37
+    detail::ck(qmm_f32_gemv(W, x, y, N, K, T, (void*)s), "f32_gemv");
+}
 inline void moe_silu_quant(const float* gate, const float* up, XQ8 xq, int rows, int n, hipStream_t s) {
     detail::ck(qmm_moe_silu_quant(gate, up, to_c(xq), rows, n, (void*)s), "moe_silu_quant");
 }

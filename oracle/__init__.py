@@ -64,6 +64,7 @@ def lib():
             "qo_gemv_ref_rows": [I, P, I, I, P, I, P, I, P, P],
             "qo_gemv_f32": [I, P, I, I, P, I, P, I],
             "qo_moe_route": [P, I, I, I, I, P, P],
+            "qo_f32_gemv": [P, P, P, I, I, I],
             "qo_moe_sort": [P, I, I, I, P, P, P, P],
             "qo_moe_decode": [I, P, P, P, ctypes.c_size_t, ctypes.c_size_t, P, P, P, P, P, P, I, I, I, I, P, P, P, P],
             "qo_moe_down_q8": [I, P, ctypes.c_size_t, P, P, P, P, P, I, I, I, I, P, P],
@@ -214,6 +215,18 @@ def moe_route(logits, nexp=512, topk=10):
     w = np.empty((T, topk + 1), dtype=np.float32)
     lib().qo_moe_route(_ptr(logits), T, nexp, stride, topk, _ptr(ids), _ptr(w))
     return ids, w
+
+
+def f32_gemv(W, x):
+    """fn.hip:251-277: W [N][K] f32, x [T][K] f32 -> y [T][N] (the reference's arithmetic and order)."""
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    N, K = W.shape
+    T = x.shape[0]
+    y = np.empty((T, N), dtype=np.float32)
+    if lib().qo_f32_gemv(_ptr(W), _ptr(x), _ptr(y), N, K, T) != 0:
+        raise ValueError("f32_gemv: K % 4 != 0")
+    return y
 
 
 def moe_sort(ids, maxc):

@@ -543,6 +543,31 @@ void qo_moe_route(const float* logits, int T, int nexp, int stride, int topk, in
     free(e); free(p); free(used);
 }
 
+/* fn.hip:251-277 (k_f32_gemv), y[t][n] = W[n] . x[t]: 32 lanes per row, lane l summing the float4 steps
+ * i = 4l + 128k in order, each step t = fma(a.w,b.w, fma(a.z,b.z, fma(a.x,b.x, a.y*b.y))) and
+ * acc = acc + t -- the contraction the reference's own hipcc build (-O3) makes of
+ * `acc += a.x*b.x + a.y*b.y + a.z*b.z + a.w*b.w` (v_mul, then three v_fmac, then v_add) -- and the
+ * 32 partial sums folded by the xor butterfly.  K % 4 == 0. */
+int qo_f32_gemv(const float* W, const float* x, float* y, int N, int K, int T) {
+    if (K <= 0 || K % 4 != 0) return -1;
+    for (int t = 0; t < T; ++t)
+        for (int n = 0; n < N; ++n) {
+            const float* a = W + (size_t)n * K;
+            const float* b = x + (size_t)t * K;
+            float acc[32];
+            for (int l = 0; l < 32; ++l) {
+                float s = 0.f;
+                for (int i = 4 * l; i < K; i += 128) {
+                    const float u = fmaf(a[i + 3], b[i + 3], fmaf(a[i + 2], b[i + 2], fmaf(a[i], b[i], a[i + 1] * b[i + 1])));
+                    s = s + u;
+                }
+                acc[l] = s;
+            }
+            y[(size_t)t * N + n] = tree32(acc);
+        }
+    return 0;
+}
+
 /* qwen4exp.cpp:628-641.  Sorting by (eid, te) is a stable counting sort over the slots taken in
  * te order; -1 (shared) sorts first. */
 int qo_moe_sort(const int* eid, int T, int NE, int maxc, int* kpos, int* rowtok, int* tiles, int* nstiles) {

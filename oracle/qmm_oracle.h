@@ -90,6 +90,10 @@ int qo_gemv_f32(int wfmt, const uint8_t* W, int N, int K, const float* x, int nc
  * lower id, weights renormalised over the k in selection order; slot k is the shared expert: id -1,
  * w = sigmoid(logits[nexp]) (engine/kernels/fn.hip:157-205).  ids/w are [T][k+1]. */
 void qo_moe_route(const float* logits, int T, int nexp, int stride, int topk, int* ids, float* w);
+/* y[t][n] = W[n] . x[t] with the reference's f32_gemv arithmetic (fn.hip:251-277): 32 lanes per row
+ * over float4 steps 4l + 128k, t = fma(a.w,b.w, fma(a.z,b.z, fma(a.x,b.x, a.y*b.y))), acc += t,
+ * xor-butterfly sum.  K % 4 == 0. */
+int qo_f32_gemv(const float* W, const float* x, float* y, int N, int K, int T);
 /* slots te = t*NE+e sorted by (expert id, te) with the shared slots (id < 0) kept in their own
  * list; tiles of <= maxc consecutive sorted positions per expert (engine/src/qwen4exp.cpp:628-641).
  * kpos[te] = sorted position, rowtok[k] = token of sorted position k, tiles as {expert,k0,ncols}.

@@ -147,6 +147,18 @@ def test_activation_producer_validation_without_device_work():
     assert L.qmm_silu_mul_bf16(d, d, d, 0, None) == 0
 
 
+def test_router_validation_without_device_work():
+    L = _lib.lib()
+    d = ctypes.c_void_p(256)
+    assert L.qmm_f32_gemv(d, d, d, 513, 2050, 1, None) == -2           # K % 4 != 0
+    assert L.qmm_f32_gemv(d, ctypes.c_void_p(260), d, 513, 2048, 1, None) == -6   # x not 16-byte aligned
+    assert L.qmm_f32_gemv(None, d, d, 513, 2048, 1, None) == -3
+    assert L.qmm_f32_gemv(d, d, d, 0, 2048, 1, None) == 0
+    assert L.qmm_moe_router(d, d, d, d, d, 1, 2048, 2048, 10, None) == -2  # too many experts for the routing
+    assert L.qmm_moe_router(d, d, d, d, d, 1, 512, 2048, 17, None) == -2   # top-k above 16
+    assert L.qmm_moe_router(d, d, d, None, d, 1, 512, 2048, 10, None) == -3
+
+
 def test_prefill_argument_validation_without_device_work():
     L = _lib.lib()
     d = ctypes.c_void_p(16)

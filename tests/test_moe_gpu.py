@@ -12,7 +12,7 @@ import torch
 
 import oracle
 from hipster_amd import qmm, synth
-from tests.gpu_util import dev, host, rel_l2
+from tests.gpu_util import assert_route_matches, dev, host, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -21,22 +21,6 @@ H, F = 2048, 512          # hidden 2048, expert FF 512
 
 def experts(seed, n_exp, N, K):
     return synth.experts(seed, synth.Q4_K, n_exp, N, K)
-
-
-def assert_route_matches(ids, w, ids_ref, w_ref, logits, nexp):
-    """ids bit-exact, except where two candidates' probabilities are within 1e-6 of each other: the
-    selection runs on the rounded p (as the reference), and the device exp (__expf) and the host libm's
-    expf may differ by an ulp, which can swap such a near-tie.  Weights within 1e-5."""
-    bad = np.nonzero((ids != ids_ref).any(axis=1))[0]
-    for t in bad:
-        l = logits[t, :nexp].astype(np.float64)
-        p = np.exp(l - l.max()); p /= p.sum()
-        for a, b in zip(ids[t], ids_ref[t]):
-            if a != b:
-                assert a >= 0 and b >= 0 and abs(p[a] - p[b]) <= 1e-6 * max(p[a], p[b]), (t, a, b, p[a], p[b])
-    assert len(bad) <= 2, bad
-    ok = np.setdiff1d(np.arange(ids.shape[0]), bad)
-    np.testing.assert_allclose(w[ok], w_ref[ok], rtol=1e-5, atol=1e-7)
 
 
 @pytest.mark.parametrize("T,zipf", [(1, None), (4, None), (8, None), (2048, 1.1)])

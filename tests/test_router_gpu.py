@@ -1,0 +1,58 @@
+"""GPU parity of the router matmul (engine/kernels/fn.hip:251-277, fn::f32_gemv) and of the router
+matmul + routing call (qwen4exp.cpp:346-347) against the CPU oracle, through the C ABI.
+
+Bars: the logits bit-exact (the library computes them with the reference's lane partition, fma
+contraction and summation tree, which the oracle restates); ids bit-exact apart from near-ties in p
+that the device exp may decide (see assert_route_matches); weights within 1e-5.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hipster_amd import qmm, synth
+from tests.gpu_util import assert_route_matches, dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("N,K,T", [(513, 2560, 1), (513, 2048, 8), (513, 2560, 13), (100, 2052, 3), (7, 4, 2),
+                                   (513, 132, 9), (64, 1024, 64)])
+def test_f32_gemv_bit_exact(gpu, N, K, T):
+    print(f"f32_gemv N={N} K={K} T={T}", flush=True)
+    W = synth.normal_f32(800 + K, (N, K)) * 0.05
+    x = synth.normal_f32(801 + T, (T, K))
+    y = torch.full((T, N), float("nan"), device="cuda")
+    qmm.f32_gemv(dev(W), dev(x), y, N, K, T)
+    ref = oracle.f32_gemv(W, x)
+    got = host(y)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), int((got != ref).sum())
+
+
+def test_f32_gemv_t_invariant(gpu):
+    """A token's logits are the same bits alone and inside a batch of any size."""
+    N, K = 513, 2048
+    W = dev(synth.normal_f32(810, (N, K)) * 0.05)
+    x = synth.normal_f32(811, (11, K))
+    yb = torch.zeros((11, N), device="cuda")
+    qmm.f32_gemv(W, dev(x), yb, N, K, 11)
+    for t in (0, 7, 10):
+        y1 = torch.zeros((1, N), device="cuda")
+        qmm.f32_gemv(W, dev(x[t:t + 1]), y1, N, K, 1)
+        assert torch.equal(y1[0], yb[t])
+
+
+@pytest.mark.parametrize("T,K", [(1, 2048), (4, 2560), (8, 2048), (300, 2048)])
+def test_moe_router(gpu, T, K):
+    print(f"moe_router T={T} K={K}", flush=True)
+    nexp = 512
+    Wr = synth.normal_f32(820 + K, (nexp + 1, K)) * 0.05
+    x = synth.normal_f32(821 + T, (T, K))
+    logits = torch.zeros((T, nexp + 1), device="cuda")
+    ids = torch.zeros((T, 11), dtype=torch.int32, device="cuda")
+    w = torch.zeros((T, 11), device="cuda")
+    qmm.moe_router(dev(Wr), dev(x), logits, ids, w, T, nexp, K, 10)
+    lg_ref = oracle.f32_gemv(Wr, x)
+    assert np.array_equal(host(logits).view(np.uint32), lg_ref.view(np.uint32))
+    ids_ref, w_ref = oracle.moe_route(lg_ref, nexp, 10)
+    assert_route_matches(host(ids), host(w), ids_ref, w_ref, lg_ref, nexp)
