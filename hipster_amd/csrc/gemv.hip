@@ -801,8 +801,13 @@ bool fmt_supported_q8(int fmt) {
            fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA;
 }
 
+// K granule per format: 256 for the block formats; the row-SoA repacks of 32-weight blocks take
+// K % 32 (Q5_1_SOA: 24-byte units, rows 8-byte aligned) or K % 64 (Q8_0_SOA: 34 bytes per 32 weights,
+// so K % 64 keeps every row dword aligned for the 16-byte loads)
+int gemv_k_granule(int fmt) { return fmt == QMM_Q5_1_SOA ? 32 : fmt == QMM_Q8_0_SOA ? 64 : 256; }
+
 int check_gemv_shape(int fmt, int N, int K) {
-    if (N <= 0 || K <= 0 || K % 256 != 0) return QMM_ERR_SHAPE;
+    if (N <= 0 || K <= 0 || K % gemv_k_granule(fmt) != 0) return QMM_ERR_SHAPE;
     if (fmt == QMM_Q6_K_SOA && ((K / 256) & 1)) return QMM_ERR_SHAPE;   // streams must stay dword aligned
     return QMM_OK;
 }

@@ -16,7 +16,8 @@
 //   Q8_0    acc += d xd isum
 //   Q5_1    acc += d xd isum + m xs                      (q = nibble | fifth bit << 4)
 // A lane accumulates its units in a fixed order and the wave reduces with a fixed butterfly, so a
-// column's result does not depend on ncol (T-invariant).  K % 256 == 0 (checked by the caller).
+// column's result does not depend on ncol (T-invariant).  K % 256 == 0 for the block formats, K % 64
+// (Q8_0_SOA) or K % 32 (Q5_1_SOA) for the row-SoA ones (checked by the caller).
 #include "qmm_common.hpp"
 
 #include <hip/hip_runtime.h>
@@ -28,13 +29,14 @@ constexpr int kFmtBlock = 256, kFmtWaves = kFmtBlock / 64;
 
 template <int F>
 __device__ __forceinline__ size_t fmt_row_bytes(int K) {
-    if constexpr (F == QMM_Q5_K) return (size_t)K / 256 * 176;
+    if constexpr (F == QMM_Q4_K) return (size_t)K / 256 * 144;
+    else if constexpr (F == QMM_Q5_K) return (size_t)K / 256 * 176;
     else if constexpr (F == QMM_IQ4_XS) return (size_t)K / 256 * 136;
     else if constexpr (F == QMM_Q8_0_SOA) return (size_t)K + (size_t)K / 16;
     else return (size_t)K / 32 * 24;                        // QMM_Q5_1_SOA
 }
 template <int F>
-__host__ __device__ __forceinline__ int fmt_units(int K) { return F == QMM_Q5_K ? K / 64 : K / 32; }
+__host__ __device__ __forceinline__ int fmt_units(int K) { return (F == QMM_Q5_K || F == QMM_Q4_K) ? K / 64 : K / 32; }
 
 // the 16 signed levels of IQ4 (quant.h:35) as bytes, four per little-endian word: levels 0-3, 4-7,
 // 8-11, 12-15
@@ -81,9 +83,9 @@ template <int F> struct FmtUnit;
 template <> struct FmtUnit<QMM_Q8_0_SOA> {            // row = [qs K][d (K/32) x f16]
     struct Raw { uint4 a, b; uint32_t d; };
     typedef X32 X;
-    static __device__ __forceinline__ void load(const uint8_t* rp, int K, int u, Raw& r) {
-        r.a = ld16(rp + 32 * (size_t)u);
-        r.b = ld16(rp + 32 * (size_t)u + 16);
+    static __device__ __forceinline__ void load(const uint8_t* rp, int K, int u, Raw& r) {   // rows dword aligned
+        r.a = ld16_a4(rp + 32 * (size_t)u);
+        r.b = ld16_a4(rp + 32 * (size_t)u + 16);
         r.d = *(const uint16_t*)(rp + K + 2 * (size_t)u);
     }
     static __device__ __forceinline__ void xload(const int8_t* xq, const float* xd, const float* xs, int u, X& x) {
@@ -98,8 +100,8 @@ template <> struct FmtUnit<QMM_Q8_0_SOA> {            // row = [qs K][d (K/32) x
 template <> struct FmtUnit<QMM_Q5_1_SOA> {            // row = [qs K/2][qh K/8][d K/32 x f16][m K/32 x f16]
     struct Raw { uint4 qs; uint32_t qh, d, m; };
     typedef X32 X;
-    static __device__ __forceinline__ void load(const uint8_t* rp, int K, int u, Raw& r) {
-        r.qs = ld16(rp + 16 * (size_t)u);
+    static __device__ __forceinline__ void load(const uint8_t* rp, int K, int u, Raw& r) {   // rows 8-byte aligned
+        r.qs = ld16_a4(rp + 16 * (size_t)u);
         r.qh = *(const uint32_t*)(rp + K / 2 + 4 * (size_t)u);
         r.d = *(const uint16_t*)(rp + K / 2 + K / 8 + 2 * (size_t)u);
         r.m = *(const uint16_t*)(rp + K / 2 + K / 8 + K / 16 + 2 * (size_t)u);
@@ -183,18 +185,50 @@ template <> struct FmtUnit<QMM_Q5_K> {                // block = {f16 d, dmin, s
     }
 };
 
+template <> struct FmtUnit<QMM_Q4_K> {                // block = {f16 d, dmin, scales[12], qs[128]}
+    struct Raw { uint4 hd, q0, q1; };
+    struct X { X32 lo, hi; };                          // sub-blocks 2j and 2j + 1
+    static __device__ __forceinline__ void load(const uint8_t* rp, int, int u, Raw& r) {
+        const uint8_t* blk = rp + (size_t)(u >> 2) * 144;     // 144-byte blocks: 16-byte aligned
+        r.hd = ld16(blk);
+        r.q0 = ld16(blk + 16 + 32 * (u & 3));
+        r.q1 = ld16(blk + 32 + 32 * (u & 3));
+    }
+    static __device__ __forceinline__ void xload(const int8_t* xq, const float* xd, const float* xs, int u, X& x) {
+        x32_load(xq, xd, xs, 2 * u, x.lo);
+        x32_load(xq, xd, xs, 2 * u + 1, x.hi);
+    }
+    static __device__ __forceinline__ float col(const Raw& r, const X& x, int u) {
+        // pair j of block b (quant.h:44-53): weights 64j + l = low nibble of qs[32j + l] (sub-block
+        // 2j), 64j + 32 + l = its high nibble (sub-block 2j + 1)
+        const int j = u & 3;
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        uint32_t wl[8], wh[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            wl[k] = q[k] & 0x0f0f0f0fu;
+            wh[k] = (q[k] >> 4) & 0x0f0f0f0fu;
+        }
+        const int i0 = dot32(wl, x.lo.a, x.lo.b), i1 = dot32(wh, x.hi.a, x.hi.b);
+        const float d = h2f(r.hd.x), dmin = h2f(r.hd.x >> 16);
+        const Q4kScaleBytes s = q4k_scale_bytes(r.hd.y, r.hd.z, r.hd.w);
+        const float d0 = d * (float)byte8(s.sc_lo, s.sc_hi, 2 * j), m0 = dmin * (float)byte8(s.m_lo, s.m_hi, 2 * j);
+        const float d1 = d * (float)byte8(s.sc_lo, s.sc_hi, 2 * j + 1), m1 = dmin * (float)byte8(s.m_lo, s.m_hi, 2 * j + 1);
+        return d0 * x.lo.d * (float)i0 - m0 * x.lo.s + (d1 * x.hi.d * (float)i1 - m1 * x.hi.s);
+    }
+};
+
 // RPW rows per wave: the q8 x of a unit is loaded once into registers and used by all RPW rows
-// (x traffic per row / RPW; with one row per wave the x reads outweigh the weight bytes).
+// (x traffic per row / RPW; with one row per wave the x reads outweigh the weight bytes).  Column c
+// reads its q8 x at xq[c], xd[c], xs[c]; acc[r][c] is lane-partial (the caller reduces over the wave).
 template <int F, int NCOL, int NIT, int RPW>
-__global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
-                                                        const float* __restrict__ xd, const float* __restrict__ xs,
-                                                        float* __restrict__ y, int N, int K) {
+__device__ __forceinline__ void fmt_rows(const uint8_t* __restrict__ W, int row0, int N, int K,
+                                         const int8_t* const (&xq)[NCOL], const float* const (&xd)[NCOL],
+                                         const float* const (&xs)[NCOL], float (&acc)[RPW][NCOL]) {
     typedef FmtUnit<F> FU;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * kFmtWaves + wave) * RPW;
+    const int lane = threadIdx.x & 63;
     const size_t rb = fmt_row_bytes<F>(K);
-    const int U = fmt_units<F>(K), nsb = K / 32;
-    float acc[RPW][NCOL];
+    const int U = fmt_units<F>(K);
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
@@ -209,8 +243,7 @@ __global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restric
 #pragma unroll
         for (int c = 0; c < NCOL; ++c) {
 #pragma unroll
-            for (int i = 0; i < NIT; ++i)
-                FU::xload(xq + (size_t)c * K, xd + (size_t)c * nsb, xs + (size_t)c * nsb, min(base + lane + 64 * i, U - 1), X[i]);
+            for (int i = 0; i < NIT; ++i) FU::xload(xq[c], xd[c], xs[c], min(base + lane + 64 * i, U - 1), X[i]);
             // all loads issued before any arithmetic (the scheduler would otherwise sink each load
             // to its use to save registers, one memory latency after another)
             __builtin_amdgcn_sched_barrier(0);
@@ -225,6 +258,25 @@ __global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restric
             }
         }
     }
+}
+
+template <int F, int NCOL, int NIT, int RPW>
+__global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                        const float* __restrict__ xd, const float* __restrict__ xs,
+                                                        float* __restrict__ y, int N, int K) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kFmtWaves + wave) * RPW;
+    const int nsb = K / 32;
+    const int8_t* xqc[NCOL];
+    const float *xdc[NCOL], *xsc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+        xqc[c] = xq + (size_t)c * K;
+        xdc[c] = xd + (size_t)c * nsb;
+        xsc[c] = xs + (size_t)c * nsb;
+    }
+    float acc[RPW][NCOL];
+    fmt_rows<F, NCOL, NIT, RPW>(W, row0, N, K, xqc, xdc, xsc, acc);
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
@@ -237,6 +289,125 @@ __global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restric
                 for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row0 + r] = acc[r][c];
             }
     }
+}
+
+// ---- MoE decode for the formats above (reference: gemv_moe, gemv.h:44, gemv.hip:1385-1394) ----
+// Routed experts in format F, the shared expert in FS (F, or Q8_0_SOA as the reference allows).  A
+// slot's rows are computed by fmt_rows like the plain GEMV of its expert (same per-row order, so
+// the same bits as qmm_gemv_q8 on that expert), two rows per wave.
+constexpr int kMoeRpw = 2, kMoeCols = 8;
+
+template <int F, int FS, int NIT, int NC>
+__device__ __forceinline__ void moe_fmt_pass(const uint8_t* wbase, bool shared, int row0, int N, int K, const int8_t* xq,
+                                             const float* xd, const float* xs, const int* cols, int nc, int nexp,
+                                             int xrow_te, float* __restrict__ y) {
+    const int nsb = K / 32, lane = threadIdx.x & 63;
+    const int8_t* xqc[NC];
+    const float *xdc[NC], *xsc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int sl = cols[min(c, nc - 1)];
+        const size_t xr = (size_t)(xrow_te ? sl : sl / nexp);
+        xqc[c] = xq + xr * K;
+        xdc[c] = xd + xr * nsb;
+        xsc[c] = xs + xr * nsb;
+    }
+    float acc[kMoeRpw][NC];
+    if (shared) fmt_rows<FS, NC, NIT, kMoeRpw>(wbase, row0, N, K, xqc, xdc, xsc, acc);
+    else fmt_rows<F, NC, NIT, kMoeRpw>(wbase, row0, N, K, xqc, xdc, xsc, acc);
+#pragma unroll
+    for (int r = 0; r < kMoeRpw; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = wave_sum(acc[r][c]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < kMoeRpw; ++r)
+            if (row0 + r < N) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    if (c < nc) y[(size_t)cols[c] * N + row0 + r] = acc[r][c];
+            }
+    }
+}
+
+// gather (gate|up): grid = (row blocks of 4 waves x 2 rows, slots, segments).
+template <int F, int FS, int NIT>
+__global__ void __launch_bounds__(kFmtBlock) k_gemv_moe_fmt(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
+                                                            const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                            const float* __restrict__ xs, int N, int K, int nslot,
+                                                            int xrow_te) {
+    __shared__ int s_cols[64 + kMoeCols];
+    __shared__ int s_n, s_dup;
+    const int te = blockIdx.y, seg = blockIdx.z;
+    const int id = ids[te];
+    if (threadIdx.x < 64) moe_slot_columns(ids, nslot, te, id, s_cols, &s_n, &s_dup);
+    __syncthreads();
+    if (s_dup) return;
+    const int ncols = s_n, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kFmtWaves + wave) * kMoeRpw;
+    const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[seg] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[seg];
+    float* y = a.y[seg];
+    for (int c0 = 0; c0 < ncols; c0 += kMoeCols) {
+        const int nc = min(kMoeCols, ncols - c0);
+        const int* cols = s_cols + c0;
+        if (nc == 1) moe_fmt_pass<F, FS, NIT, 1>(wbase, id < 0, row0, N, K, xq, xd, xs, cols, nc, nexp, xrow_te, y);
+        else if (nc == 2) moe_fmt_pass<F, FS, NIT, 2>(wbase, id < 0, row0, N, K, xq, xd, xs, cols, nc, nexp, xrow_te, y);
+        else if (nc <= 4) moe_fmt_pass<F, FS, NIT, 4>(wbase, id < 0, row0, N, K, xq, xd, xs, cols, nc, nexp, xrow_te, y);
+        else moe_fmt_pass<F, FS, NIT, 8>(wbase, id < 0, row0, N, K, xq, xd, xs, cols, nc, nexp, xrow_te, y);
+    }
+}
+
+// down projection + weighted combine: grid = (row blocks of 2 rows, tokens); wave w takes the slots
+// e = w, w + 4, ... of the token; lane r < 2 then sums row r over the slots in order (the combine of
+// the Q4_K kernel, the same expression).
+template <int F, int FS, int NIT>
+__global__ void __launch_bounds__(kFmtBlock) k_gemv_moe_down_fmt(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
+                                                                 const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                                 const float* __restrict__ xs, int N, int K) {
+    __shared__ float vres[kMoeMaxSlots][kMoeRpw];
+    const int tok = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int row0 = blockIdx.x * kMoeRpw, nsb = K / 32;
+    for (int e = wave; e < nexp; e += kFmtWaves) {
+        const int id = ids[tok * nexp + e];
+        const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[0] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[0];
+        const size_t xr = (size_t)tok * nexp + e;
+        const int8_t* xqc[1] = {xq + xr * K};
+        const float* xdc[1] = {xd + xr * nsb};
+        const float* xsc[1] = {xs + xr * nsb};
+        float acc[kMoeRpw][1];
+        if (id < 0) fmt_rows<FS, 1, NIT, kMoeRpw>(wbase, row0, N, K, xqc, xdc, xsc, acc);
+        else fmt_rows<F, 1, NIT, kMoeRpw>(wbase, row0, N, K, xqc, xdc, xsc, acc);
+#pragma unroll
+        for (int r = 0; r < kMoeRpw; ++r) {
+            const float v = wave_sum(acc[r][0]);
+            if (lane == 0) vres[e][r] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < kMoeRpw && row0 + tid < N) {
+        float acc = 0.f;
+        for (int e = 0; e < nexp; ++e) acc += a.slotw[tok * nexp + e] * vres[e][tid];
+        a.y[0][(size_t)tok * N + row0 + tid] = acc;
+    }
+}
+
+template <int F, int FS>
+int launch_moe_fmt(const qmm_moe_segs& a, int nseg, const int* ids, int nexp, qmm_xq8 x, int N, int K, int T, int xrow_te,
+                   hipStream_t s) {
+    const int per_lane = (max(fmt_units<F>(K), fmt_units<FS>(K)) + 63) / 64;
+    if (a.slotw) {
+        const dim3 grid((unsigned)((N + kMoeRpw - 1) / kMoeRpw), (unsigned)T);
+        if (per_lane <= 1) hipLaunchKernelGGL((k_gemv_moe_down_fmt<F, FS, 1>), grid, dim3(kFmtBlock), 0, s, a, ids, nexp, x.q, x.d, x.s, N, K);
+        else hipLaunchKernelGGL((k_gemv_moe_down_fmt<F, FS, 2>), grid, dim3(kFmtBlock), 0, s, a, ids, nexp, x.q, x.d, x.s, N, K);
+    } else {
+        const dim3 grid((unsigned)((N + kFmtWaves * kMoeRpw - 1) / (kFmtWaves * kMoeRpw)), (unsigned)(T * nexp), (unsigned)nseg);
+        if (per_lane <= 1)
+            hipLaunchKernelGGL((k_gemv_moe_fmt<F, FS, 1>), grid, dim3(kFmtBlock), 0, s, a, ids, nexp, x.q, x.d, x.s, N, K, T * nexp, xrow_te);
+        else
+            hipLaunchKernelGGL((k_gemv_moe_fmt<F, FS, 2>), grid, dim3(kFmtBlock), 0, s, a, ids, nexp, x.q, x.d, x.s, N, K, T * nexp, xrow_te);
+    }
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
 }
 
 template <int F, int NCOL>
@@ -282,6 +453,30 @@ int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K,
         case 8: return launch_fmt_ncol<8>(fmt, W, x, y, N, K, s);
         default: return QMM_ERR_SHAPE;
     }
+}
+
+// routed format fmt, shared format sfmt (fmt, or Q8_0_SOA); fmt may be Q4_K only with a Q8_0_SOA
+// shared expert (the all-Q4_K case has its own kernels).
+int moe_fmt_dispatch(int fmt, int sfmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x, int N, int K,
+                     int T, int xrow_te, hipStream_t s) {
+#define QMM_MF(F)                                                                                                    \
+    case F:                                                                                                          \
+        return sfmt == QMM_Q8_0_SOA ? launch_moe_fmt<F, QMM_Q8_0_SOA>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s) \
+                                    : launch_moe_fmt<F, F>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s);
+    if (sfmt != fmt && sfmt != QMM_Q8_0_SOA) return QMM_ERR_FORMAT;
+    switch (fmt) {
+        case QMM_Q4_K:
+            if (sfmt != QMM_Q8_0_SOA) return QMM_ERR_FORMAT;
+            return launch_moe_fmt<QMM_Q4_K, QMM_Q8_0_SOA>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s);
+        QMM_MF(QMM_Q5_K)
+        QMM_MF(QMM_IQ4_XS)
+        QMM_MF(QMM_Q5_1_SOA)
+        case QMM_Q8_0_SOA:
+            return launch_moe_fmt<QMM_Q8_0_SOA, QMM_Q8_0_SOA>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s);
+        default:
+            return QMM_ERR_FORMAT;
+    }
+#undef QMM_MF
 }
 
 }  // namespace qmm

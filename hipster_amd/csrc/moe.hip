@@ -218,30 +218,7 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
     __shared__ int s_n, s_dup;
     const int te = blockIdx.y, seg = blockIdx.z, tid = threadIdx.x;
     const int id = ids[te];
-    if (tid < 64) {
-        // dedup over the slots: leader = the first slot routed to this expert (shared: id < 0)
-        int n = 0, dup = 0;
-        for (int base = 0; base < nslot; base += 64) {
-            const int sl = base + tid;
-            const int sid0 = ids[min(sl, nslot - 1)];
-            const int sid = sl < nslot ? sid0 : 0x7fffffff;
-            const bool m = sl < nslot && (sid == id || (sid < 0 && id < 0));
-            const unsigned long long bal = __ballot(m);
-            // slots before te that match -> duplicate
-            const unsigned long long before = base + 64 <= te ? ~0ull : (te > base ? ((1ull << (te - base)) - 1ull) : 0ull);
-            if (bal & before) dup = 1;
-            // slots >= te that match, in order
-            const unsigned long long from = te <= base ? ~0ull : (te - base >= 64 ? 0ull : ~((1ull << (te - base)) - 1ull));
-            unsigned long long mm = bal & from;
-            while (mm && n < 64) {
-                const int b = __builtin_ctzll(mm);
-                if (tid == 0) s_cols[n] = base + b;
-                ++n;
-                mm &= mm - 1;
-            }
-        }
-        if (tid == 0) { s_n = n; s_dup = dup; }
-    }
+    if (tid < 64) moe_slot_columns(ids, nslot, te, id, s_cols, &s_n, &s_dup);
     __syncthreads();
     if (s_dup) return;
     const int ncols = s_n;
@@ -430,16 +407,23 @@ int qmm_moe_silu_quant(const float* gate, const float* up, qmm_xq8 xq, int rows,
 
 int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x, int N, int K,
                  int T, int xrow_te, void* stream) {
-    if (fmt != QMM_Q4_K || shared_fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+    // the reference's combinations (gemv.hip:1386-1392): the shared expert in the routed format or in
+    // Q8_0_SOA; routed Q4_K, Q5_K, IQ4_XS, Q8_0_SOA, Q5_1_SOA
+    const bool fmt_ok = fmt == QMM_Q4_K || fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA;
+    if (!fmt_ok || (shared_fmt != fmt && shared_fmt != QMM_Q8_0_SOA)) return QMM_ERR_FORMAT;
     if (!a || !ids || !x.q || !x.d || !x.s) return QMM_ERR_NULL;
-    if (nseg < 1 || nseg > 2 || N <= 0 || K <= 0 || K % 256 != 0 || T < 0 || nexp < 1 || nexp > kMaxSlots) return QMM_ERR_SHAPE;
+    auto kgran = [](int f) { return f == QMM_Q5_1_SOA ? 32 : f == QMM_Q8_0_SOA ? 64 : 256; };   // as qmm_gemv_q8
+    if (nseg < 1 || nseg > 2 || N <= 0 || K <= 0 || K % kgran(fmt) != 0 || K % kgran(shared_fmt) != 0 || T < 0 || nexp < 1 ||
+        nexp > kMaxSlots)
+        return QMM_ERR_SHAPE;
     if (T > 64) return QMM_ERR_SHAPE;   // at most 64 columns (tokens) per expert in the dedup list
     for (int g = 0; g < nseg; ++g)
         if (!a->w[g] || !a->shared[g] || !a->y[g]) return QMM_ERR_NULL;
     if (T == 0) return QMM_OK;
     hipStream_t s = (hipStream_t)stream;
+    if (a->slotw && nseg != 1) return QMM_ERR_ARG;
+    if (fmt != QMM_Q4_K || shared_fmt != QMM_Q4_K) return moe_fmt_dispatch(fmt, shared_fmt, a, nseg, ids, nexp, x, N, K, T, xrow_te, s);
     if (a->slotw) {
-        if (nseg != 1) return QMM_ERR_ARG;
         return moe_lpr(K) == 8 ? launch_down<8>(*a, ids, nexp, x, N, K, T, s) : launch_down<16>(*a, ids, nexp, x, N, K, T, s);
     }
     return moe_lpr(K) == 8 ? launch_gather<8>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s)

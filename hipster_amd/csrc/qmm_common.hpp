@@ -170,6 +170,37 @@ __device__ __forceinline__ void hw32_quant(float v, int8_t* __restrict__ q, floa
     }
 }
 
+// MoE decode dedup over the slots of a step, run by the 64 lanes of the first wave: slot te leads its
+// expert when no earlier slot routes to it (the shared expert: every id < 0); the leader lists, in
+// order, every slot >= te routed to the same expert (at most 64) in s_cols[0..*s_n).  *s_dup = 1
+// when te does not lead.
+__device__ __forceinline__ void moe_slot_columns(const int* __restrict__ ids, int nslot, int te, int id, int* s_cols,
+                                                 int* s_n, int* s_dup) {
+    const int tid = threadIdx.x;
+    int n = 0, dup = 0;
+    for (int base = 0; base < nslot; base += 64) {
+        const int sl = base + tid;
+        const int sid0 = ids[min(sl, nslot - 1)];
+        const int sid = sl < nslot ? sid0 : 0x7fffffff;
+        const bool m = sl < nslot && (sid == id || (sid < 0 && id < 0));
+        const unsigned long long bal = __ballot(m);
+        // slots before te that match -> duplicate
+        const unsigned long long before = base + 64 <= te ? ~0ull : (te > base ? ((1ull << (te - base)) - 1ull) : 0ull);
+        if (bal & before) dup = 1;
+        // slots >= te that match, in order
+        const unsigned long long from = te <= base ? ~0ull : (te - base >= 64 ? 0ull : ~((1ull << (te - base)) - 1ull));
+        unsigned long long mm = bal & from;
+        while (mm && n < 64) {
+            const int b = __builtin_ctzll(mm);
+            if (tid == 0) s_cols[n] = base + b;
+            ++n;
+            mm &= mm - 1;
+        }
+    }
+    if (tid == 0) { *s_n = n; *s_dup = dup; }
+}
+constexpr int kMoeMaxSlots = 16;    // slots per token (10 routed + shared in the reference)
+
 // bf16 round-to-nearest-even of the top half (no NaN special case, as engine/kernels/gemm.hip:12)
 __device__ __forceinline__ uint32_t f2bf_bits(float f) {
     uint32_t u = __float_as_uint(f);
@@ -194,6 +225,9 @@ inline int device_cu_count() {
 int launch_q4k_rows_gemm(const void* W, const uint16_t* A, float* D, int M, int N, int K, int ldd, int trows, hipStream_t s);
 // q8 GEMV of gemv_fmt.hip for QMM_Q5_K, QMM_IQ4_XS, QMM_Q8_0_SOA, QMM_Q5_1_SOA (ncol 1..8, K % 256 == 0)
 int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s);
+// MoE decode gather / down (qmm_gemv_moe) for the routed formats other than all-Q4_K (gemv_fmt.hip)
+int moe_fmt_dispatch(int fmt, int sfmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x, int N, int K,
+                     int T, int xrow_te, hipStream_t s);
 
 }  // namespace qmm
 

@@ -83,8 +83,9 @@ int qmm_repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K);
 int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream);
 
 /* ---- decode GEMV, int8 activations (reference: gemv_q8, gemv.h:25, gemv.hip:1466-1485) ----
- * y[c][n] = sum_k W[n][k] * x[c][k] for c < ncol (1..8), K % 256 == 0.  fmt: Q4_K, Q6_K,
- * Q6_K_SOA.  tpr/rpt are the reference's tuning knobs; this build picks its own launch shape from
+ * y[c][n] = sum_k W[n][k] * x[c][k] for c < ncol (1..8).  fmt: every format of the call surface
+ * (Q4_K, Q5_K, IQ4_XS, Q6_K, Q6_K_SOA, Q8_0_SOA, Q5_1_SOA); K % 256 == 0, or K % 64 for Q8_0_SOA and
+ * K % 32 for Q5_1_SOA (32-weight blocks).  tpr/rpt are the reference's tuning knobs; this build picks its own launch shape from
  * the tensor shape only (never from ncol, which keeps the result T-invariant) and accepts any
  * tpr in {0,1,2,4,8,16,32} and rpt in {0,1,2,3} for compatibility. */
 int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, int tpr, int rpt, void* stream);
@@ -125,7 +126,11 @@ int qmm_moe_router(const float* Wr, const float* x, float* logits, int* ids, flo
  * Without a->slotw: y[g][te][N] = W[g][ids[te]] . x[row] for g < nseg (gate|up share the launch);
  * each distinct expert is read once for all the slots routed to it.  With a->slotw (nseg = 1):
  * y[t][N] = sum_e slotw[te] * (W[ids[te]] . x[te]) summed in slot order (down + combine).
- * fmt = shared_fmt = QMM_Q4_K; K % 256 == 0, K <= 6144; nexp <= 16; T <= 64. */
+ * Formats as the reference's (gemv.hip:1386-1392): routed fmt Q4_K, Q5_K, IQ4_XS, Q8_0_SOA or Q5_1_SOA,
+ * shared_fmt = fmt or Q8_0_SOA; K as for qmm_gemv_q8 (so the engine's K = 640 down projection runs
+ * in the 32-weight formats); all-Q4_K also needs K <= 6144.  nexp <= 16; T <= 64.  Every slot's rows
+ * are bitwise the plain GEMV of its expert, except Q4_K routed experts beside a Q8_0_SOA shared expert
+ * (a different, equally exact, Q4_K decode). */
 int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x,
                  int N, int K, int T, int xrow_te, void* stream);
 /* h = silu(gate) * up quantised per 32 into xq, rows x n (reference: fn::moe_silu_quant, fn.h:48,

@@ -82,8 +82,9 @@ def test_argument_validation_without_device_work():
     dummy = ctypes.c_void_p(16)
     # unknown formats are refused (the reference aborts here); the other formats check their shape
     assert L.qmm_gemv_q8(99, dummy, _xq(16), dummy, 16, 256, 1, 0, 1, None) == -1
-    for fmt in (_lib.QMM_Q5_K, _lib.QMM_IQ4_XS, _lib.QMM_Q8_0_SOA, _lib.QMM_Q5_1_SOA):
-        assert L.qmm_gemv_q8(fmt, dummy, _xq(16), dummy, 16, 96, 1, 0, 1, None) == -2
+    # K granules: 256 (block formats), 64 (Q8_0_SOA: rows dword aligned), 32 (Q5_1_SOA)
+    for fmt, badk in ((_lib.QMM_Q5_K, 96), (_lib.QMM_IQ4_XS, 640), (_lib.QMM_Q8_0_SOA, 96), (_lib.QMM_Q5_1_SOA, 100)):
+        assert L.qmm_gemv_q8(fmt, dummy, _xq(16), dummy, 16, badk, 1, 0, 1, None) == -2
         assert L.qmm_gemv_q8(fmt, dummy, _xq(16), dummy, 16, 256, 9, 0, 1, None) == -2
     # bad shapes
     assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 300, 1, 0, 1, None) == -2
@@ -124,6 +125,11 @@ def test_moe_argument_validation_without_device_work():
     assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, None, 2, d, 11, _xq(16), 512, 2048, 1, 0, None) == -3
     segs.slotw = 16
     assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, ctypes.byref(segs), 2, d, 11, _xq(16), 512, 2048, 1, 1, None) == -6
+    # formats: the shared expert in the routed format or Q8_0_SOA; no Q6_K experts; K granules
+    assert L.qmm_gemv_moe(_lib.QMM_Q5_1_SOA, _lib.QMM_Q5_K, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 640, 1, 0, None) == -1
+    assert L.qmm_gemv_moe(_lib.QMM_Q6_K_SOA, _lib.QMM_Q6_K_SOA, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 512, 1, 0, None) == -1
+    assert L.qmm_gemv_moe(_lib.QMM_Q5_1_SOA, _lib.QMM_Q8_0_SOA, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 608, 1, 0, None) == -2
+    assert L.qmm_gemv_moe(_lib.QMM_Q5_K, _lib.QMM_Q5_K, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 640, 1, 0, None) == -2
     assert L.qmm_moe_silu_quant(d, d, _xq(16), 4, 100, None) == -2
     assert L.qmm_moe_combine_sorted(d, d, None, d, 4, 11, 2048, None) == -3
 

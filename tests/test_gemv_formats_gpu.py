@@ -43,7 +43,9 @@ def q8_reference(fmt, W, N, K, x):
 SHAPES = [(synth.Q5_K, 17408, 5120), (synth.Q5_K, 777, 256), (synth.Q5_K, 130, 17408),
           (synth.IQ4_XS, 5120, 17408), (synth.IQ4_XS, 1001, 2048), (synth.IQ4_XS, 4096, 5120),
           (synth.Q8_0_SOA, 4096, 5120), (synth.Q8_0_SOA, 130, 17408), (synth.Q8_0_SOA, 63, 256),
-          (synth.Q5_1_SOA, 2048, 5120), (synth.Q5_1_SOA, 65, 768), (synth.Q5_1_SOA, 515, 17408)]
+          (synth.Q5_1_SOA, 2048, 5120), (synth.Q5_1_SOA, 65, 768), (synth.Q5_1_SOA, 515, 17408),
+          # the engine's expert down projection, K = 640 (qwen4exp.h:22), and small K of 32-weight blocks
+          (synth.Q5_1_SOA, 2048, 640), (synth.Q8_0_SOA, 2048, 640), (synth.Q5_1_SOA, 100, 96), (synth.Q8_0_SOA, 33, 192)]
 
 
 @pytest.mark.parametrize("fmt,N,K", SHAPES)
