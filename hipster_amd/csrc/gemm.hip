@@ -16,6 +16,7 @@
 // (qmm_gemm_bf16): 256 x 256 tiles, 4 waves, v_mfma_f32_16x16x32_bf16, register-staged two-stage
 // LDS ring.  Both map workgroups XCD-aware: consecutive workgroup ids go to different XCDs, so tile
 // ids are assigned so that the M tiles of one weight tile run on the same XCD and share its L2.
+#include "fmt_dequant.hpp"
 #include "qmm_common.hpp"
 
 #include <hip/hip_runtime.h>
@@ -478,10 +479,8 @@ int launch_gemm_q4k(const void* W, const uint16_t* A, float* D, int M, int N, in
 
 
 // ---- bf16 dequantisation of the other formats (gemm.hip:16-50,83-92 of the reference): one thread
-// per 32-weight sub-block, 64 bytes of bf16 out.  Every product here is exact in f32 (at most 24
-// significant bits: an f16 scale times a 6-bit scale or an 8-bit level times a <= 8-bit quant), so
-// the contracted d*q - m rounds exactly like the reference's separately rounded operations; then
-// round-to-nearest-even to bf16 (gemm.hip:12).
+// per 32-weight sub-block (dq_sub32: exact f32), 64 bytes of bf16 out, round-to-nearest-even
+// (gemm.hip:12).
 template <int F>
 __global__ void __launch_bounds__(256) k_dequant_fmt_bf16(const uint8_t* __restrict__ W, uint16_t* __restrict__ out,
                                                          size_t nsub, int K) {
@@ -491,57 +490,7 @@ __global__ void __launch_bounds__(256) k_dequant_fmt_bf16(const uint8_t* __restr
     const size_t row = g / n32;
     const int sb = (int)(g - row * n32);
     float w[32];
-    if constexpr (F == QMM_Q5_K) {
-        const uint8_t* blk = W + row * ((size_t)(K >> 8) * 176) + (size_t)(sb >> 3) * 176;
-        const int s = sb & 7, j = s >> 1;
-        const uint4 hd = ld16(blk), h0 = ld16(blk + 16), h1 = ld16(blk + 32);
-        const uint4 q0 = ld16(blk + 48 + 32 * j), q1 = ld16(blk + 64 + 32 * j);
-        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-        const Q4kScaleBytes sc = q4k_scale_bytes(hd.y, hd.z, hd.w);
-        const float dl = d * (float)byte8(sc.sc_lo, sc.sc_hi, s), ml = dmin * (float)byte8(sc.m_lo, sc.m_hi, s);
-        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        const uint32_t hb[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-#pragma unroll
-        for (int l = 0; l < 32; ++l) {
-            const uint32_t qb = (q[l >> 2] >> (8 * (l & 3))) & 0xffu, hbit = (hb[l >> 2] >> (8 * (l & 3) + s)) & 1u;
-            w[l] = dl * (float)(((s & 1) ? qb >> 4 : qb & 15u) + 16u * hbit) - ml;
-        }
-    } else if constexpr (F == QMM_IQ4_XS) {
-        const uint8_t* blk = W + row * ((size_t)(K >> 8) * 136) + (size_t)(sb >> 3) * 136;
-        const int ib = sb & 7;
-        const uint2 hd = *(const uint2*)blk;
-        const uint4 qs = ld16_a4(blk + 8 + 16 * ib);
-        const int ls = (int)((hd.y >> (4 * ib)) & 0xfu) | (int)(((hd.x >> (16 + 2 * ib)) & 3u) << 4);
-        const float dl = h2f(hd.x) * (float)(ls - 32);
-        const int8_t lv[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
-        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
-#pragma unroll
-        for (int l = 0; l < 16; ++l) {
-            const uint32_t qb = (q[l >> 2] >> (8 * (l & 3))) & 0xffu;
-            w[l] = dl * (float)lv[qb & 15u];
-            w[l + 16] = dl * (float)lv[qb >> 4];
-        }
-    } else if constexpr (F == QMM_Q8_0_SOA) {
-        const uint8_t* rp = W + row * ((size_t)K + (size_t)(K >> 4));
-        const uint4 a = ld16(rp + 32 * (size_t)sb), b = ld16(rp + 32 * (size_t)sb + 16);
-        const float d = h2f(*(const uint16_t*)(rp + K + 2 * sb));
-        const uint32_t q[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int l = 0; l < 32; ++l) w[l] = (float)(int8_t)((q[l >> 2] >> (8 * (l & 3))) & 0xffu) * d;
-    } else {                                                   // QMM_Q5_1_SOA
-        const uint8_t* rp = W + row * ((size_t)(K >> 5) * 24);
-        const uint4 qs = ld16(rp + 16 * (size_t)sb);
-        const uint32_t qh = *(const uint32_t*)(rp + (K >> 1) + 4 * sb);
-        const float d = h2f(*(const uint16_t*)(rp + (K >> 1) + (K >> 3) + 2 * sb));
-        const float m = h2f(*(const uint16_t*)(rp + (K >> 1) + (K >> 3) + (K >> 4) + 2 * sb));
-        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
-#pragma unroll
-        for (int l = 0; l < 16; ++l) {
-            const uint32_t qb = (q[l >> 2] >> (8 * (l & 3))) & 0xffu;
-            w[l] = (float)((qb & 15u) | (((qh >> l) & 1u) << 4)) * d + m;
-            w[l + 16] = (float)((qb >> 4) | (((qh >> (l + 16)) & 1u) << 4)) * d + m;
-        }
-    }
+    dq_sub32<F>(W + row * fmt_row_bytes_rt(F, K), K, sb, w);
     uint4* dst = (uint4*)(out + row * (size_t)K + 32 * (size_t)sb);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -561,9 +510,12 @@ extern "C" {
 
 int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* stream) {
     if (!W || !out) return QMM_ERR_NULL;
-    if (N <= 0 || K <= 0 || K % 256 != 0) return QMM_ERR_SHAPE;
+    // K % 256, or K % 64 (Q8_0_SOA) / K % 32 (Q5_1_SOA) for the row-SoA repacks of 32-weight blocks
+    const int kg = fmt == QMM_Q5_1_SOA ? 32 : fmt == QMM_Q8_0_SOA ? 64 : 256;
+    if (N <= 0 || K <= 0 || K % kg != 0) return QMM_ERR_SHAPE;
     hipStream_t s = (hipStream_t)stream;
     const size_t nb = (size_t)N * (K / 256);
+    const size_t nsub = (size_t)N * (K / 32);      // 32-weight sub-blocks
     switch (fmt) {
         case QMM_Q4_K:
             hipLaunchKernelGGL(k_dequant_q4k_bf16, dim3((unsigned)((nb * 8 + 255) / 256)), dim3(256), 0, s, (const uint8_t*)W, out,
@@ -577,8 +529,8 @@ int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* 
             hipLaunchKernelGGL(k_dequant_q6k_bf16<QMM_Q6_K_SOA>, dim3((unsigned)((nb * 16 + 255) / 256)), dim3(256), 0, s,
                                (const uint8_t*)W, out, nb * 16, K);
             break;
-#define QMM_DQF(F) case F: hipLaunchKernelGGL(k_dequant_fmt_bf16<F>, dim3((unsigned)((nb * 8 + 255) / 256)), dim3(256), 0, s, \
-                                              (const uint8_t*)W, out, nb * 8, K); break;
+#define QMM_DQF(F) case F: hipLaunchKernelGGL(k_dequant_fmt_bf16<F>, dim3((unsigned)((nsub + 255) / 256)), dim3(256), 0, s, \
+                                              (const uint8_t*)W, out, nsub, K); break;
         QMM_DQF(QMM_Q5_K) QMM_DQF(QMM_IQ4_XS) QMM_DQF(QMM_Q8_0_SOA) QMM_DQF(QMM_Q5_1_SOA)
 #undef QMM_DQF
         default: return QMM_ERR_FORMAT;

@@ -883,10 +883,17 @@ int qmm_moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* 
 int qmm_moe_gemm_bf16(int fmt, int shared_fmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles,
                       const int* counts, int max_tiles, const int* rowtab, const uint16_t* A, float* D, int N, int K,
                       void* stream) {
-    if (fmt != QMM_Q4_K || shared_fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+    // the reference's moe_gemm formats (gemv.hip:962-968), routed and shared independent, and IQ4_XS;
+    // K granule per format as qmm_gemv_q8 (256; 64 for Q8_0_SOA, 32 for Q5_1_SOA)
+    auto fmt_ok = [](int f) { return f == QMM_Q4_K || f == QMM_Q5_K || f == QMM_IQ4_XS || f == QMM_Q8_0_SOA || f == QMM_Q5_1_SOA; };
+    auto kgran = [](int f) { return f == QMM_Q5_1_SOA ? 32 : f == QMM_Q8_0_SOA ? 64 : 256; };
+    if (!fmt_ok(fmt) || !fmt_ok(shared_fmt)) return QMM_ERR_FORMAT;
     if (!W || !Wsh || !tiles || !counts || !A || !D) return QMM_ERR_NULL;
-    if (N <= 0 || K <= 0 || K % 256 != 0 || max_tiles < 0) return QMM_ERR_SHAPE;
+    if (N <= 0 || K <= 0 || K % kgran(fmt) != 0 || K % kgran(shared_fmt) != 0 || max_tiles < 0) return QMM_ERR_SHAPE;
     if (max_tiles == 0) return QMM_OK;
+    if (fmt != QMM_Q4_K || shared_fmt != QMM_Q4_K)
+        return launch_moe_gemm_fmt(fmt, shared_fmt, W, Wsh, ebytes, tiles, counts, max_tiles, rowtab, A, D, N, K,
+                                   (hipStream_t)stream);
     XArgs a{(const uint8_t*)W, (const uint8_t*)Wsh, nullptr, nullptr, ebytes, tiles, counts, rowtab, A, D, N, K,
             (N + XBW - 1) / XBW, N, 0, max_tiles, 0, kAsBlocksPerUnit};
     if (K == kAsK) return launch_moe_gemm_as(a, max_tiles, (hipStream_t)stream);

@@ -144,8 +144,8 @@ int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, f
 
 /* ---- prefill GEMM ---- */
 /* whole weight -> bf16 [N][K], bit-exact: quant.h arithmetic ((d*sc)*q - dmin*m, no contraction) then
- * round-to-nearest-even (reference: dequant_bf16, gemm.h:12, gemm.hip:16-76,96-107).  fmt: Q4_K, Q6_K,
- * Q6_K_SOA; K % 256 == 0. */
+ * round-to-nearest-even (reference: dequant_bf16, gemm.h:12, gemm.hip:16-76,96-107).  fmt: every
+ * format of the call surface; K % 256 == 0 (K % 64 for Q8_0_SOA, K % 32 for Q5_1_SOA). */
 int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* stream);
 /* D[M][N] f32 = A[M][K] bf16 . W[N][K]^T with W in Q4_K, dequantised to bf16 inside the kernel
  * (bf16 MFMA, f32 accumulate).  Replaces the reference's dequant_bf16 + BlasLt::gemm pair
@@ -172,9 +172,11 @@ int qmm_moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* 
                  int* counts, void* stream);
 /* Grouped expert GEMM over sorted rows (reference: moe_gemm, gemv.h:49-50, gemv.hip:909-969,1377-1381,
  * with bf16 activations and the bf16 MFMA path): for tile i < counts[0] + counts[1] (read on the device)
- * and r < ncols: D[k0 + r][n] = A[rowtab ? rowtab[k0 + r] : k0 + r] . W_e[n] (f32), W_e the Q4_K
- * expert matrix at W + expert * ebytes, or Wsh for expert -1.  Tiles of at most 128 rows (qmm_moe_sort
- * with maxc <= 128); max_tiles bounds the grid (the capacity of tiles). */
+ * and r < ncols: D[k0 + r][n] = A[rowtab ? rowtab[k0 + r] : k0 + r] . W_e[n] (f32), W_e the expert
+ * matrix at W + expert * ebytes, or Wsh for expert -1, dequantised exactly to bf16.  fmt / shared_fmt:
+ * Q4_K, Q5_K, IQ4_XS, Q8_0_SOA, Q5_1_SOA, independently (the reference's moe_gemm formats,
+ * gemv.hip:962-968, and IQ4_XS); K as for qmm_gemv_q8.  Tiles of at most 128 rows (qmm_moe_sort with
+ * maxc <= 128); max_tiles bounds the grid (the capacity of tiles). */
 int qmm_moe_gemm_bf16(int fmt, int shared_fmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles,
                       const int* counts, int max_tiles, const int* rowtab, const uint16_t* A, float* D, int N, int K,
                       void* stream);
