@@ -19,13 +19,48 @@ __host__ __device__ __forceinline__ size_t fmt_row_bytes_rt(int fmt, int K) {
     }
 }
 
+// The raw bytes of one sub-block (at most 80: a Q5_K block header, its qh and a qs pair), loaded
+// apart from their decode so that a pipeline can issue the loads a step ahead.
+struct SubRaw { uint4 v[5]; };
+
 template <int F>
-__device__ __forceinline__ void dq_sub32(const uint8_t* __restrict__ rp, int K, int sb, float (&w)[32]) {
-    if constexpr (F == QMM_Q4_K) {                      // y = (d sc) q - (dmin m), quant.h:44-53
+__device__ __forceinline__ void sub_load(const uint8_t* __restrict__ rp, int K, int sb, SubRaw& r) {
+    if constexpr (F == QMM_Q4_K) {
         const uint8_t* blk = rp + (size_t)(sb >> 3) * 144;
-        const int s = sb & 7, j = s >> 1;
-        const uint4 hd = ld16(blk);
-        const uint4 q0 = ld16(blk + 16 + 32 * j), q1 = ld16(blk + 32 + 32 * j);
+        const int j = (sb & 7) >> 1;
+        r.v[0] = ld16(blk);
+        r.v[1] = ld16(blk + 16 + 32 * j);
+        r.v[2] = ld16(blk + 32 + 32 * j);
+    } else if constexpr (F == QMM_Q5_K) {
+        const uint8_t* blk = rp + (size_t)(sb >> 3) * 176;
+        const int j = (sb & 7) >> 1;
+        r.v[0] = ld16(blk);
+        r.v[1] = ld16(blk + 16);
+        r.v[2] = ld16(blk + 32);
+        r.v[3] = ld16(blk + 48 + 32 * j);
+        r.v[4] = ld16(blk + 64 + 32 * j);
+    } else if constexpr (F == QMM_IQ4_XS) {
+        const uint8_t* blk = rp + (size_t)(sb >> 3) * 136;
+        const uint2 hd = *(const uint2*)blk;
+        r.v[0] = make_uint4(hd.x, hd.y, 0u, 0u);
+        r.v[1] = ld16_a4(blk + 8 + 16 * (sb & 7));
+    } else if constexpr (F == QMM_Q8_0_SOA) {          // rows dword aligned (K % 64)
+        r.v[0] = ld16_a4(rp + 32 * (size_t)sb);
+        r.v[1] = ld16_a4(rp + 32 * (size_t)sb + 16);
+        r.v[2].x = *(const uint16_t*)(rp + K + 2 * sb);
+    } else {                                            // QMM_Q5_1_SOA, rows 8-byte aligned
+        r.v[0] = ld16_a4(rp + 16 * (size_t)sb);
+        r.v[1].x = *(const uint32_t*)(rp + (K >> 1) + 4 * sb);
+        r.v[1].y = *(const uint16_t*)(rp + (K >> 1) + (K >> 3) + 2 * sb);
+        r.v[1].z = *(const uint16_t*)(rp + (K >> 1) + (K >> 3) + (K >> 4) + 2 * sb);
+    }
+}
+
+template <int F>
+__device__ __forceinline__ void sub_decode(const SubRaw& r, int sb, float (&w)[32]) {
+    if constexpr (F == QMM_Q4_K) {                      // y = (d sc) q - (dmin m), quant.h:44-53
+        const int s = sb & 7;
+        const uint4 hd = r.v[0], q0 = r.v[1], q1 = r.v[2];
         const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
         const Q4kScaleBytes sc = q4k_scale_bytes(hd.y, hd.z, hd.w);
         const float dl = d * (float)byte8(sc.sc_lo, sc.sc_hi, s), ml = dmin * (float)byte8(sc.m_lo, sc.m_hi, s);
@@ -35,11 +70,9 @@ __device__ __forceinline__ void dq_sub32(const uint8_t* __restrict__ rp, int K, 
             const uint32_t qb = (q[l >> 2] >> (8 * (l & 3))) & 0xffu;
             w[l] = dl * (float)((s & 1) ? qb >> 4 : qb & 15u) - ml;
         }
-    } else if constexpr (F == QMM_Q5_K) {
-        const uint8_t* blk = rp + (size_t)(sb >> 3) * 176;
-        const int s = sb & 7, j = s >> 1;
-        const uint4 hd = ld16(blk), h0 = ld16(blk + 16), h1 = ld16(blk + 32);
-        const uint4 q0 = ld16(blk + 48 + 32 * j), q1 = ld16(blk + 64 + 32 * j);
+    } else if constexpr (F == QMM_Q5_K) {               // quant.h:54-64
+        const int s = sb & 7;
+        const uint4 hd = r.v[0], h0 = r.v[1], h1 = r.v[2], q0 = r.v[3], q1 = r.v[4];
         const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
         const Q4kScaleBytes sc = q4k_scale_bytes(hd.y, hd.z, hd.w);
         const float dl = d * (float)byte8(sc.sc_lo, sc.sc_hi, s), ml = dmin * (float)byte8(sc.m_lo, sc.m_hi, s);
@@ -50,33 +83,30 @@ __device__ __forceinline__ void dq_sub32(const uint8_t* __restrict__ rp, int K, 
             const uint32_t qb = (q[l >> 2] >> (8 * (l & 3))) & 0xffu, hbit = (hb[l >> 2] >> (8 * (l & 3) + s)) & 1u;
             w[l] = dl * (float)(((s & 1) ? qb >> 4 : qb & 15u) + 16u * hbit) - ml;
         }
-    } else if constexpr (F == QMM_IQ4_XS) {
-        const uint8_t* blk = rp + (size_t)(sb >> 3) * 136;
+    } else if constexpr (F == QMM_IQ4_XS) {             // quant.h:92-100
         const int ib = sb & 7;
-        const uint2 hd = *(const uint2*)blk;
-        const uint4 qs = ld16_a4(blk + 8 + 16 * ib);
-        const int ls = (int)((hd.y >> (4 * ib)) & 0xfu) | (int)(((hd.x >> (16 + 2 * ib)) & 3u) << 4);
-        const float dl = h2f(hd.x) * (float)(ls - 32);
-        const int8_t lv[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
-        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+        const uint32_t hx = r.v[0].x, hy = r.v[0].y;
+        const int ls = (int)((hy >> (4 * ib)) & 0xfu) | (int)(((hx >> (16 + 2 * ib)) & 3u) << 4);
+        const float dl = h2f(hx) * (float)(ls - 32);
+        const uint32_t q[4] = {r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w};
 #pragma unroll
-        for (int l = 0; l < 16; ++l) {
-            const uint32_t qb = (q[l >> 2] >> (8 * (l & 3))) & 0xffu;
-            w[l] = dl * (float)lv[qb & 15u];
-            w[l + 16] = dl * (float)lv[qb >> 4];
+        for (int k = 0; k < 4; ++k) {           // weights 4k..4k+3 (low nibbles) and 16+4k.. (high)
+            const uint32_t lo = iq4_levels4(q[k] & 0x0f0f0f0fu), hi = iq4_levels4((q[k] >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                w[4 * k + b] = dl * (float)(int8_t)(lo >> (8 * b));
+                w[16 + 4 * k + b] = dl * (float)(int8_t)(hi >> (8 * b));
+            }
         }
-    } else if constexpr (F == QMM_Q8_0_SOA) {          // rows dword aligned (K % 64)
-        const uint4 a = ld16_a4(rp + 32 * (size_t)sb), b = ld16_a4(rp + 32 * (size_t)sb + 16);
-        const float d = h2f(*(const uint16_t*)(rp + K + 2 * sb));
-        const uint32_t q[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    } else if constexpr (F == QMM_Q8_0_SOA) {          // quant.h:76-80 (SoA: gemv.hip:1351-1354)
+        const float d = h2f(r.v[2].x);
+        const uint32_t q[8] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w, r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w};
 #pragma unroll
         for (int l = 0; l < 32; ++l) w[l] = (float)(int8_t)((q[l >> 2] >> (8 * (l & 3))) & 0xffu) * d;
-    } else {                                            // QMM_Q5_1_SOA, rows 8-byte aligned
-        const uint4 qs = ld16_a4(rp + 16 * (size_t)sb);
-        const uint32_t qh = *(const uint32_t*)(rp + (K >> 1) + 4 * sb);
-        const float d = h2f(*(const uint16_t*)(rp + (K >> 1) + (K >> 3) + 2 * sb));
-        const float m = h2f(*(const uint16_t*)(rp + (K >> 1) + (K >> 3) + (K >> 4) + 2 * sb));
-        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+    } else {                                            // QMM_Q5_1_SOA, quant.h:82-88 (SoA: gemv.hip:1458-1465)
+        const uint32_t qh = r.v[1].x;
+        const float d = h2f(r.v[1].y), m = h2f(r.v[1].z);
+        const uint32_t q[4] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w};
 #pragma unroll
         for (int l = 0; l < 16; ++l) {
             const uint32_t qb = (q[l >> 2] >> (8 * (l & 3))) & 0xffu;
@@ -84,6 +114,13 @@ __device__ __forceinline__ void dq_sub32(const uint8_t* __restrict__ rp, int K, 
             w[l + 16] = (float)((qb >> 4) | (((qh >> (l + 16)) & 1u) << 4)) * d + m;
         }
     }
+}
+
+template <int F>
+__device__ __forceinline__ void dq_sub32(const uint8_t* __restrict__ rp, int K, int sb, float (&w)[32]) {
+    SubRaw r;
+    sub_load<F>(rp, K, sb, r);
+    sub_decode<F>(r, sb, w);
 }
 
 // the same with the format chosen at run time (a uniform branch)

@@ -367,15 +367,58 @@ struct WRawQ4KHalf {
     }
 };
 
-__global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
-                                                           float* __restrict__ D, int M, int N, int K, int ldd) {
+// W from bf16 rows [N][K] (the BlasLt::gemm twin): thread t copies the 32 weights of row t/2, half t&1
+// of the step, a step ahead
+struct WRawBf16Half {
+    uint4 v[4];
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
+        const int n = min(n0 + (int)(threadIdx.x >> 1), N - 1);
+        const uint16_t* p = (const uint16_t*)W + (size_t)n * K + k0 + 32 * (threadIdx.x & 1);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = *(const uint4*)(p + 8 * c);
+    }
+    __device__ __forceinline__ void store(uint4* Lb, int) const {
+        const int t = threadIdx.x, h = t & 1, row = t >> 1;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) Lb[swz(row, 4 * h + c)] = v[c];
+    }
+};
+
+// W in one of the other quantised formats: thread t loads the raw bytes of row t/2's sub-block
+// (k0/32 + (t&1)) a step ahead and dequantises them exactly (as qmm_dequant_bf16), RNE to bf16
+template <int F>
+struct WRawFmtHalf {
+    SubRaw r;
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
+        const int n = min(n0 + (int)(threadIdx.x >> 1), N - 1);
+        sub_load<F>(W + (size_t)n * fmt_row_bytes_rt(F, K), K, (k0 >> 5) + (int)(threadIdx.x & 1), r);
+    }
+    __device__ __forceinline__ void store(uint4* Lb, int k0) const {
+        const int t = threadIdx.x, h = t & 1, row = t >> 1;
+        float w[32];
+        sub_decode<F>(r, (k0 >> 5) + h, w);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = f2bf_bits(w[8 * c + 2 * k]) | (f2bf_bits(w[8 * c + 2 * k + 1]) << 16);
+            Lb[swz(row, 4 * h + c)] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
+};
+
+// D = A . W^T with W from the source WR (Q4_K blocks, bf16 rows or another format), f32 or bf16 (RNE)
+// out.  K % 128 == 0 (an even step count for the 3 x 2 stage unroll).
+template <class WR, bool OUT_BF16>
+__global__ void __launch_bounds__(kPPThreads) k_gemm_pp(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
+                                                       void* __restrict__ Dv, int M, int N, int K, int ldd) {
     const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
     int tm, tn;
     tile_of(blockIdx.x, mt, nt, tm, tn);
     const int m0 = tm * GBM, n0 = tn * GBN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave & 1, wn = wave >> 1;
     const int nk = K / GBK, lastk = (nk - 1) * GBK;
-    WRawQ4KHalf wr;
+    WR wr;
     wr.load(W, N, K, n0, 0);
     dma_a_pp(A, M, K, m0, 0, ga<0>());
     dma_a_pp(A, M, K, m0, min(GBK, lastk), ga<1>());
@@ -431,7 +474,7 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __re
         body(IC<1>(), IC<0>(), s + 4);
         body(IC<2>(), IC<1>(), s + 5);
     }
-    if (s < nk) {                              // nk % 4 == 0, so 2 or 4 steps remain
+    if (s < nk) {                              // nk is even, so 2 or 4 steps remain
         body(IC<0>(), IC<0>(), s);
         body(IC<1>(), IC<1>(), s + 1);
         if (s + 2 < nk) {
@@ -449,13 +492,16 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_q4k_pp(const uint16_t* __re
 #pragma unroll
             for (int jn = 0; jn < 2; ++jn) {
                 const int n = n0 + 64 * wn + 32 * jn + fr;
-                if (n < N) D[(size_t)m * ldd + n] = acc[i][jn][e];
+                if (n < N) {
+                    if constexpr (OUT_BF16) ((uint16_t*)Dv)[(size_t)m * ldd + n] = (uint16_t)f2bf_bits(acc[i][jn][e]);
+                    else ((float*)Dv)[(size_t)m * ldd + n] = acc[i][jn][e];
+                }
             }
         }
     }
 }
 
-// One workgroup of k_gemm_q4k_pp fills a CU (160 KiB of LDS), so its tiles run in rounds of one per
+// One workgroup of k_gemm_pp fills a CU (160 KiB of LDS), so its tiles run in rounds of one per
 // CU.  When the last round would keep at most a quarter of the CUs busy for a whole tile time, the
 // 256 x 256 kernel takes only whole rounds (whole columns of M tiles) and the remaining columns go
 // to the grouped-GEMM kernel as (32 rows x 256 columns) work units, enough of them to spread over
@@ -467,7 +513,8 @@ int launch_gemm_q4k(const void* W, const uint16_t* A, float* D, int M, int N, in
     if (total > cus && rem != 0 && 4 * rem <= cus && mt <= cus) nbig = (total - rem) / mt;
     const int nb_cols = std::min(N, nbig * GBN);
     if (nbig > 0) {
-        hipLaunchKernelGGL(k_gemm_q4k_pp, dim3(mt * nbig), dim3(kPPThreads), 0, s, A, (const uint8_t*)W, D, M, nb_cols, K, N);
+        hipLaunchKernelGGL((k_gemm_pp<WRawQ4KHalf, false>), dim3(mt * nbig), dim3(kPPThreads), 0, s, A, (const uint8_t*)W, D, M,
+                           nb_cols, K, N);
         QMM_LAUNCH_CHECK();
     }
     if (nb_cols < N) {
@@ -540,18 +587,35 @@ int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* 
 }
 
 int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int N, int K, void* stream) {
-    if (fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+    if (!(fmt == QMM_Q4_K || fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA))
+        return QMM_ERR_FORMAT;
     if (!W || !A || !D) return QMM_ERR_NULL;
-    if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0) return QMM_ERR_SHAPE;
-    return launch_gemm_q4k(W, A, D, M, N, K, (hipStream_t)stream);
+    // K % 256 for the block formats; the SoA formats need K % 128 (the kernel's even step count)
+    const int kg = (fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA) ? 2 * GBK : 256;
+    if (M <= 0 || N <= 0 || K <= 0 || K % kg != 0) return QMM_ERR_SHAPE;
+    hipStream_t s = (hipStream_t)stream;
+    if (fmt == QMM_Q4_K) return launch_gemm_q4k(W, A, D, M, N, K, s);
+    const dim3 grid((unsigned)(((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN)));
+#define QMM_GWQ(F) case F: hipLaunchKernelGGL((k_gemm_pp<WRawFmtHalf<F>, false>), grid, dim3(kPPThreads), 0, s, A, (const uint8_t*)W, \
+                                              (void*)D, M, N, K, N); break;
+    switch (fmt) {
+        QMM_GWQ(QMM_Q5_K) QMM_GWQ(QMM_IQ4_XS) QMM_GWQ(QMM_Q8_0_SOA) QMM_GWQ(QMM_Q5_1_SOA)
+    }
+#undef QMM_GWQ
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
 }
 
 int qmm_gemm_bf16(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, void* stream) {
     if (!A || !W || !D) return QMM_ERR_NULL;
     if (M <= 0 || N <= 0 || K <= 0 || K % GBK != 0) return QMM_ERR_SHAPE;
     const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-    hipLaunchKernelGGL((k_gemm<BLoadBf16, uint16_t, true>), dim3(grid), dim3(256), kGemmLds, (hipStream_t)stream, A, W,
-                       (void*)D, M, N, K);
+    if (K % (2 * GBK) == 0)     // the two-waves-per-SIMD kernel of the fused GEMM, bf16 rows as its W source
+        hipLaunchKernelGGL((k_gemm_pp<WRawBf16Half, true>), dim3(grid), dim3(kPPThreads), 0, (hipStream_t)stream, A,
+                           (const uint8_t*)W, (void*)D, M, N, K, N);
+    else
+        hipLaunchKernelGGL((k_gemm<BLoadBf16, uint16_t, true>), dim3(grid), dim3(256), kGemmLds, (hipStream_t)stream, A, W,
+                           (void*)D, M, N, K);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }

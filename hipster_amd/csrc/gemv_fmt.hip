@@ -38,17 +38,6 @@ __device__ __forceinline__ size_t fmt_row_bytes(int K) {
 template <int F>
 __host__ __device__ __forceinline__ int fmt_units(int K) { return (F == QMM_Q5_K || F == QMM_Q4_K) ? K / 64 : K / 32; }
 
-// the 16 signed levels of IQ4 (quant.h:35) as bytes, four per little-endian word: levels 0-3, 4-7,
-// 8-11, 12-15
-constexpr uint32_t kIq4L0 = 0xBFAD9881u, kIq4L1 = 0xF6EADDCFu, kIq4H0 = 0x26190D01u, kIq4H1 = 0x71594535u;
-// four nibbles (one per byte, 0..15) -> four signed levels: one byte permute per half of the table,
-// then a per-byte select on bit 3
-__device__ __forceinline__ uint32_t iq4_levels4(uint32_t nib) {
-    const uint32_t sel = nib & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(kIq4L1, kIq4L0, sel), hi = __builtin_amdgcn_perm(kIq4H1, kIq4H0, sel);
-    const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xffu;
-    return (hi & m) | (lo & ~m);
-}
 // four bits h (0..15) -> bit 4 of each byte: h * 0x02040810 puts bit i of h at bit 8i + 4 (and the
 // other partial products at positions that are not 4 mod 8, none overlapping), the mask keeps those
 __device__ __forceinline__ uint32_t bits4_to_byte_bit4(uint32_t h) { return (h * 0x02040810u) & 0x10101010u; }

@@ -51,6 +51,17 @@ __device__ __forceinline__ uint32_t byte8(uint32_t lo, uint32_t hi, int i) {
     return (v >> (8 * (i & 3))) & 0xffu;
 }
 
+// the 16 signed levels of IQ4 (quant.h:35) as bytes, four per little-endian word: levels 0-3, 4-7,
+// 8-11, 12-15
+constexpr uint32_t kIq4L0 = 0xBFAD9881u, kIq4L1 = 0xF6EADDCFu, kIq4H0 = 0x26190D01u, kIq4H1 = 0x71594535u;
+// four nibbles (one per byte, 0..15) -> four signed levels: one byte permute per half of the table,
+// then a per-byte select on bit 3
+__device__ __forceinline__ uint32_t iq4_levels4(uint32_t nib) {
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4L1, kIq4L0, sel), hi = __builtin_amdgcn_perm(kIq4H1, kIq4H0, sel);
+    const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xffu;
+    return (hi & m) | (lo & ~m);
+}
 // Q6_K: 6-bit values (0..63, one per byte) -> signed q-32 per byte without carries between bytes.
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 

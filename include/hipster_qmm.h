@@ -147,12 +147,15 @@ int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, f
  * round-to-nearest-even (reference: dequant_bf16, gemm.h:12, gemm.hip:16-76,96-107).  fmt: every
  * format of the call surface; K % 256 == 0 (K % 64 for Q8_0_SOA, K % 32 for Q5_1_SOA). */
 int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* stream);
-/* D[M][N] f32 = A[M][K] bf16 . W[N][K]^T with W in Q4_K, dequantised to bf16 inside the kernel
- * (bf16 MFMA, f32 accumulate).  Replaces the reference's dequant_bf16 + BlasLt::gemm pair
- * (engine/src/qwen35.cpp:204-239, engine/src/qwen4exp.cpp:513-527) with one launch and no scratch. */
+/* D[M][N] f32 = A[M][K] bf16 . W[N][K]^T with W dequantised to bf16 inside the kernel exactly as
+ * qmm_dequant_bf16 (bf16 MFMA, f32 accumulate).  Replaces the reference's dequant_bf16 + BlasLt::gemm
+ * pair (engine/src/qwen35.cpp:204-239, engine/src/qwen4exp.cpp:513-527) with one launch and no
+ * scratch.  fmt: Q4_K, Q5_K, IQ4_XS (K % 256), Q8_0_SOA, Q5_1_SOA (K % 128); Q6_K weights take
+ * qmm_dequant_bf16 + qmm_gemm_bf16. */
 int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int N, int K, void* stream);
 /* D[M][N] bf16 = A[M][K] bf16 . W[N][K]^T bf16, f32 accumulate, RNE to bf16 (reference: BlasLt::gemm,
- * gemm.h:27, gemm.hip:125-160; here an own MFMA kernel, no hipBLASLt).  K % 64 == 0. */
+ * gemm.h:27, gemm.hip:125-160; here an own MFMA kernel, no hipBLASLt: the fused GEMM's kernel with bf16
+ * rows as its weight source when K % 128 == 0).  K % 64 == 0. */
 int qmm_gemm_bf16(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, void* stream);
 /* bf16 helpers (reference: gemm.h:14-20, gemm.hip:77-95) */
 int qmm_f32_to_bf16(const float* x, uint16_t* out, size_t n, void* stream);

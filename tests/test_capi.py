@@ -168,6 +168,9 @@ def test_router_validation_without_device_work():
 def test_prefill_argument_validation_without_device_work():
     L = _lib.lib()
     d = ctypes.c_void_p(16)
+    assert L.qmm_gemm_wq(_lib.QMM_Q6_K, d, d, d, 64, 64, 256, None) == -1        # Q6_K: dequant_bf16 + gemm_bf16
+    assert L.qmm_gemm_wq(_lib.QMM_Q5_1_SOA, d, d, d, 64, 64, 96, None) == -2     # SoA formats: K % 128
+    assert L.qmm_gemm_wq(_lib.QMM_Q5_K, d, d, d, 64, 64, 384, None) == -2
     q4, q6 = _lib.QMM_Q4_K, _lib.QMM_Q6_K
     assert L.qmm_moe_sort(None, 4, 11, 512, 128, d, d, d, d, None) == -3
     assert L.qmm_moe_sort(d, 4, 11, 4096, 128, d, d, d, d, None) == -2       # more experts than the sort holds

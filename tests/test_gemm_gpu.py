@@ -93,8 +93,10 @@ def test_gemm_wq_config3_full_shape(gpu):
     gemm_check(2048, 17408, 5120, synth.SEEDS["cfg3"], npairs=256)
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 515, 640), (2048, 2048, 2048)])
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (300, 515, 640), (2048, 2048, 2048), (129, 384, 192)])
 def test_gemm_bf16(gpu, M, N, K):
+    """K % 128 == 0 runs the two-waves-per-SIMD kernel with bf16 rows as its W source, other K the
+    4-wave kernel"""
     A = synth.to_bf16_bits(synth.normal_f32(70 + M, (M, K)))
     W = synth.to_bf16_bits(synth.normal_f32(71 + N, (N, K)))
     D = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
@@ -102,6 +104,25 @@ def test_gemm_bf16(gpu, M, N, K):
     qmm.gemm_bf16(Ad, Wd, D, M, N, K)
     ref = torch.matmul(Ad.float(), Wd.float().t().contiguous())
     assert rel_l2(host(D.float()), host(ref)) <= 4e-3      # bf16 output rounding (2^-9) dominates
+
+
+@pytest.mark.parametrize("fmt,M,N,K", [(synth.Q5_K, 300, 515, 512), (synth.IQ4_XS, 128, 256, 256),
+                                         (synth.Q8_0_SOA, 257, 300, 640), (synth.Q5_1_SOA, 100, 1000, 128),
+                                         (synth.Q5_K, 2048, 2048, 2048), (synth.Q5_1_SOA, 513, 2560, 640)])
+def test_gemm_wq_other_formats(gpu, fmt, M, N, K):
+    """the fused GEMM for the other formats (dequantisation exactly as qmm_dequant_bf16, in the kernel)
+    against torch float32 of the same bf16 operands; the bar of the bf16 MFMA path, 2e-3 (measured
+    errors ~1e-7: f32 accumulation of exact bf16 products)"""
+    W = dev(synth.matrix(1450 + fmt + K, fmt, N, K))
+    A = bf16_dev(synth.to_bf16_bits(synth.normal_f32(1451 + M, (M, K))))
+    D = torch.full((M, N), float("nan"), device="cuda")
+    qmm.gemm_wq(fmt, W, A, D, M, N, K)
+    Wb = torch.zeros((N, K), dtype=torch.int16, device="cuda")
+    qmm.dequant_bf16(fmt, W, Wb, N, K)
+    ref = torch.matmul(A.float(), Wb.view(torch.bfloat16).float().t().contiguous())
+    err = rel_l2(host(D), host(ref))
+    print(f"gemm_wq fmt={fmt} M={M} N={N} K={K} rel-L2 {err:.2e}", flush=True)
+    assert err <= 2e-3
 
 
 def test_gemm_deterministic(gpu):
