@@ -1,6 +1,6 @@
 // fmt_dequant.hpp -- exact f32 dequantisation of one 32-weight sub-block of a weight row, for every
-// format of the call surface except Q6_K (engine/src/quant.h:37-100 and the SoA repacks of
-// engine/kernels/gemv.hip:1341-1354,1448-1465).  Every product here is exact in f32 (at most 24
+// format of the call surface (engine/src/quant.h:37-100 and the SoA repacks of
+// engine/kernels/gemv.hip:1341-1354,1448-1465; Q6_K in its row-SoA repack, the engine's only form).  Every product here is exact in f32 (at most 24
 // significant bits: an f16 scale times a 6-bit scale, an 8-bit level or a <= 8-bit quant), so a
 // contracted d*q - m rounds exactly like the reference's separately rounded operations.
 #pragma once
@@ -15,6 +15,7 @@ __host__ __device__ __forceinline__ size_t fmt_row_bytes_rt(int fmt, int K) {
         case QMM_Q5_K: return (size_t)(K >> 8) * 176;
         case QMM_IQ4_XS: return (size_t)(K >> 8) * 136;
         case QMM_Q8_0_SOA: return (size_t)K + (size_t)(K >> 4);
+        case QMM_Q6_K_SOA: return (size_t)(K >> 8) * 210;
         default: return (size_t)(K >> 5) * 24;          // QMM_Q5_1_SOA
     }
 }
@@ -44,6 +45,16 @@ __device__ __forceinline__ void sub_load(const uint8_t* __restrict__ rp, int K, 
         const uint2 hd = *(const uint2*)blk;
         r.v[0] = make_uint4(hd.x, hd.y, 0u, 0u);
         r.v[1] = ld16_a4(blk + 8 + 16 * (sb & 7));
+    } else if constexpr (F == QMM_Q6_K_SOA) {          // streams [ql][qh][scales][d], rows dword aligned (K % 512)
+        const int nb = K >> 8, b = sb >> 3, s = sb & 7, n = s >> 2, g = s & 3;
+        const uint8_t* ql = rp + (size_t)b * 128 + 64 * n + 32 * (g & 1);
+        const uint8_t* qh = rp + (size_t)nb * 128 + (size_t)b * 64 + 32 * n;
+        r.v[0] = ld16_a4(ql);
+        r.v[1] = ld16_a4(ql + 16);
+        r.v[2] = ld16_a4(qh);
+        r.v[3] = ld16_a4(qh + 16);
+        r.v[4].x = *(const uint16_t*)(rp + (size_t)nb * 192 + (size_t)b * 16 + 8 * n + 2 * g);   // the two scales
+        r.v[4].y = *(const uint16_t*)(rp + (size_t)nb * 208 + 2 * (size_t)b);                  // d
     } else if constexpr (F == QMM_Q8_0_SOA) {          // rows dword aligned (K % 64)
         r.v[0] = ld16_a4(rp + 32 * (size_t)sb);
         r.v[1] = ld16_a4(rp + 32 * (size_t)sb + 16);
@@ -97,6 +108,19 @@ __device__ __forceinline__ void sub_decode(const SubRaw& r, int sb, float (&w)[3
                 w[4 * k + b] = dl * (float)(int8_t)(lo >> (8 * b));
                 w[16 + 4 * k + b] = dl * (float)(int8_t)(hi >> (8 * b));
             }
+        }
+    } else if constexpr (F == QMM_Q6_K_SOA) {          // quant.h:65-75: weight 32g + l of half n
+        // (sub-block 4n + g) = d sc[8n + 2g + l/16] ((ql nibble) | (qh bits 2g, 2g+1) << 4) - 32)
+        const int g = sb & 3;
+        const float d = h2f(r.v[4].y);
+        const float ds0 = d * (float)(int8_t)(r.v[4].x & 0xffu), ds1 = d * (float)(int8_t)((r.v[4].x >> 8) & 0xffu);
+        const uint32_t ql[8] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w, r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w};
+        const uint32_t qh[8] = {r.v[2].x, r.v[2].y, r.v[2].z, r.v[2].w, r.v[3].x, r.v[3].y, r.v[3].z, r.v[3].w};
+#pragma unroll
+        for (int l = 0; l < 32; ++l) {
+            const uint32_t lo = (ql[l >> 2] >> (8 * (l & 3))) & 0xffu, hi = (qh[l >> 2] >> (8 * (l & 3))) & 0xffu;
+            const int q = (int)((g < 2 ? (lo & 15u) : (lo >> 4)) | (((hi >> (2 * g)) & 3u) << 4)) - 32;
+            w[l] = (l < 16 ? ds0 : ds1) * (float)q;
         }
     } else if constexpr (F == QMM_Q8_0_SOA) {          // quant.h:76-80 (SoA: gemv.hip:1351-1354)
         const float d = h2f(r.v[2].x);

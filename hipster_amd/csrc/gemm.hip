@@ -587,11 +587,13 @@ int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* 
 }
 
 int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int N, int K, void* stream) {
-    if (!(fmt == QMM_Q4_K || fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA))
+    if (!(fmt == QMM_Q4_K || fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q6_K_SOA || fmt == QMM_Q8_0_SOA ||
+          fmt == QMM_Q5_1_SOA))
         return QMM_ERR_FORMAT;
     if (!W || !A || !D) return QMM_ERR_NULL;
-    // K % 256 for the block formats; the SoA formats need K % 128 (the kernel's even step count)
-    const int kg = (fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA) ? 2 * GBK : 256;
+    // K % 256 for the block formats (K % 512 for Q6_K_SOA: an even block count keeps its streams dword
+    // aligned); the 32-weight SoA formats need K % 128 (the kernel's even step count)
+    const int kg = (fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA) ? 2 * GBK : fmt == QMM_Q6_K_SOA ? 512 : 256;
     if (M <= 0 || N <= 0 || K <= 0 || K % kg != 0) return QMM_ERR_SHAPE;
     hipStream_t s = (hipStream_t)stream;
     if (fmt == QMM_Q4_K) return launch_gemm_q4k(W, A, D, M, N, K, s);
@@ -599,7 +601,7 @@ int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int 
 #define QMM_GWQ(F) case F: hipLaunchKernelGGL((k_gemm_pp<WRawFmtHalf<F>, false>), grid, dim3(kPPThreads), 0, s, A, (const uint8_t*)W, \
                                               (void*)D, M, N, K, N); break;
     switch (fmt) {
-        QMM_GWQ(QMM_Q5_K) QMM_GWQ(QMM_IQ4_XS) QMM_GWQ(QMM_Q8_0_SOA) QMM_GWQ(QMM_Q5_1_SOA)
+        QMM_GWQ(QMM_Q5_K) QMM_GWQ(QMM_IQ4_XS) QMM_GWQ(QMM_Q6_K_SOA) QMM_GWQ(QMM_Q8_0_SOA) QMM_GWQ(QMM_Q5_1_SOA)
     }
 #undef QMM_GWQ
     QMM_LAUNCH_CHECK();

@@ -150,8 +150,9 @@ int qmm_dequant_bf16(int fmt, const void* W, uint16_t* out, int N, int K, void* 
 /* D[M][N] f32 = A[M][K] bf16 . W[N][K]^T with W dequantised to bf16 inside the kernel exactly as
  * qmm_dequant_bf16 (bf16 MFMA, f32 accumulate).  Replaces the reference's dequant_bf16 + BlasLt::gemm
  * pair (engine/src/qwen35.cpp:204-239, engine/src/qwen4exp.cpp:513-527) with one launch and no
- * scratch.  fmt: Q4_K, Q5_K, IQ4_XS (K % 256), Q8_0_SOA, Q5_1_SOA (K % 128); Q6_K weights take
- * qmm_dequant_bf16 + qmm_gemm_bf16. */
+ * scratch.  fmt: Q4_K, Q5_K, IQ4_XS (K % 256), Q6_K_SOA (K % 512), Q8_0_SOA, Q5_1_SOA (K % 128);
+ * GGUF-native Q6_K rows take qmm_dequant_bf16 + qmm_gemm_bf16 (the engine repacks Q6_K to the SoA
+ * layout at load). */
 int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int N, int K, void* stream);
 /* D[M][N] bf16 = A[M][K] bf16 . W[N][K]^T bf16, f32 accumulate, RNE to bf16 (reference: BlasLt::gemm,
  * gemm.h:27, gemm.hip:125-160; here an own MFMA kernel, no hipBLASLt: the fused GEMM's kernel with bf16

@@ -168,7 +168,8 @@ def test_router_validation_without_device_work():
 def test_prefill_argument_validation_without_device_work():
     L = _lib.lib()
     d = ctypes.c_void_p(16)
-    assert L.qmm_gemm_wq(_lib.QMM_Q6_K, d, d, d, 64, 64, 256, None) == -1        # Q6_K: dequant_bf16 + gemm_bf16
+    assert L.qmm_gemm_wq(_lib.QMM_Q6_K, d, d, d, 64, 64, 256, None) == -1        # GGUF Q6_K: dequant_bf16 + gemm_bf16
+    assert L.qmm_gemm_wq(_lib.QMM_Q6_K_SOA, d, d, d, 64, 64, 768, None) == -2    # Q6_K_SOA: K % 512
     assert L.qmm_gemm_wq(_lib.QMM_Q5_1_SOA, d, d, d, 64, 64, 96, None) == -2     # SoA formats: K % 128
     assert L.qmm_gemm_wq(_lib.QMM_Q5_K, d, d, d, 64, 64, 384, None) == -2
     q4, q6 = _lib.QMM_Q4_K, _lib.QMM_Q6_K

@@ -108,7 +108,8 @@ def test_gemm_bf16(gpu, M, N, K):
 
 @pytest.mark.parametrize("fmt,M,N,K", [(synth.Q5_K, 300, 515, 512), (synth.IQ4_XS, 128, 256, 256),
                                          (synth.Q8_0_SOA, 257, 300, 640), (synth.Q5_1_SOA, 100, 1000, 128),
-                                         (synth.Q5_K, 2048, 2048, 2048), (synth.Q5_1_SOA, 513, 2560, 640)])
+                                         (synth.Q5_K, 2048, 2048, 2048), (synth.Q5_1_SOA, 513, 2560, 640),
+                                         (synth.Q6_K_SOA, 300, 515, 512), (synth.Q6_K_SOA, 2048, 5120, 17408)])
 def test_gemm_wq_other_formats(gpu, fmt, M, N, K):
     """the fused GEMM for the other formats (dequantisation exactly as qmm_dequant_bf16, in the kernel)
     against torch float32 of the same bf16 operands; the bar of the bf16 MFMA path, 2e-3 (measured
