@@ -147,7 +147,27 @@ __device__ __forceinline__ void dq_sub32(const uint8_t* __restrict__ rp, int K, 
     sub_decode<F>(r, sb, w);
 }
 
-// the same with the format chosen at run time (a uniform branch)
+// load and decode with the format chosen at run time (a uniform branch)
+__device__ __forceinline__ void sub_load_rt(int fmt, const uint8_t* __restrict__ rp, int K, int sb, SubRaw& r) {
+    switch (fmt) {
+        case QMM_Q4_K: sub_load<QMM_Q4_K>(rp, K, sb, r); break;
+        case QMM_Q5_K: sub_load<QMM_Q5_K>(rp, K, sb, r); break;
+        case QMM_IQ4_XS: sub_load<QMM_IQ4_XS>(rp, K, sb, r); break;
+        case QMM_Q8_0_SOA: sub_load<QMM_Q8_0_SOA>(rp, K, sb, r); break;
+        default: sub_load<QMM_Q5_1_SOA>(rp, K, sb, r); break;
+    }
+}
+__device__ __forceinline__ void sub_decode_rt(int fmt, const SubRaw& r, int sb, float (&w)[32]) {
+    switch (fmt) {
+        case QMM_Q4_K: sub_decode<QMM_Q4_K>(r, sb, w); break;
+        case QMM_Q5_K: sub_decode<QMM_Q5_K>(r, sb, w); break;
+        case QMM_IQ4_XS: sub_decode<QMM_IQ4_XS>(r, sb, w); break;
+        case QMM_Q8_0_SOA: sub_decode<QMM_Q8_0_SOA>(r, sb, w); break;
+        default: sub_decode<QMM_Q5_1_SOA>(r, sb, w); break;
+    }
+}
+
+// the same in one call
 __device__ __forceinline__ void dq_sub32_rt(int fmt, const uint8_t* __restrict__ rp, int K, int sb, float (&w)[32]) {
     switch (fmt) {
         case QMM_Q4_K: dq_sub32<QMM_Q4_K>(rp, K, sb, w); break;

@@ -370,17 +370,17 @@ struct WRawQ4KHalf {
 // W from bf16 rows [N][K] (the BlasLt::gemm twin): thread t copies the 32 weights of row t/2, half t&1
 // of the step, a step ahead
 struct WRawBf16Half {
-    uint4 v[4];
+    SubRaw r;                               // r.v[0..3]: the 64 bytes
     __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
         const int n = min(n0 + (int)(threadIdx.x >> 1), N - 1);
         const uint16_t* p = (const uint16_t*)W + (size_t)n * K + k0 + 32 * (threadIdx.x & 1);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[c] = *(const uint4*)(p + 8 * c);
+        for (int c = 0; c < 4; ++c) r.v[c] = ld16(p + 8 * c);
     }
     __device__ __forceinline__ void store(uint4* Lb, int) const {
         const int t = threadIdx.x, h = t & 1, row = t >> 1;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) Lb[swz(row, 4 * h + c)] = v[c];
+        for (int c = 0; c < 4; ++c) Lb[swz(row, 4 * h + c)] = r.v[c];
     }
 };
 
