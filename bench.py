@@ -211,6 +211,14 @@ def extra_router(torch):
         us2 = graph_us(torch, [(lambda i: (lambda: qmm.moe_router(Ws[i], x, lg, ids, w, T, 512, K, 10)))(i) for i in range(R)],
                        reps=4) / R
         out[f"T{T}"] = {"f32_gemv_us": round(us, 2), "GB_s": round(N * K * 4 / us / 1e3, 1), "router_and_route_us": round(us2, 2)}
+    # the prefill router GEMM (BlasLt::gemm_f32): a 2048-token chunk, hidden 2048 (config 4) and 2560
+    for Kp in (2048, 2560):
+        Wp = [torch.randn((N, Kp), device="cuda") * 0.05 for _ in range(4)]
+        A = torch.randn((2048, Kp), device="cuda")
+        D = torch.zeros((2048, N), device="cuda")
+        us = graph_us(torch, [(lambda i: (lambda: qmm.gemm_f32(A, Wp[i], D, 2048, N, Kp)))(i) for i in range(4)], reps=4) / 4
+        out[f"gemm_f32_2048x513x{Kp}"] = {"us": round(us, 2), "TFLOPS": round(2 * 2048 * N * Kp / us / 1e6, 1)}
+        del Wp, A, D
     return out
 
 

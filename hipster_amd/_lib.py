@@ -64,6 +64,7 @@ SIGNATURES = {
                                           c_vp, c_int, c_int, c_vp]),
     "qmm_moe_silu_bf16": (c_int, [c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp]),
     "qmm_f32_gemv": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    "qmm_gemm_f32": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "qmm_moe_router": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
     "qmm_add_rmsnorm_quant": (c_int, [c_vp, c_vp, c_vp, c_vp, XQ8, c_int, c_int, ctypes.c_float, c_vp]),
     "qmm_add_rmsnorm_bf16": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, ctypes.c_float, c_vp]),

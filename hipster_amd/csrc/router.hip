@@ -3,6 +3,8 @@
 //   this library        reference
 //   qmm_f32_gemv        fn::f32_gemv            engine/kernels/fn.h:37, fn.hip:251-277
 //   qmm_moe_router      fn::f32_gemv + fn::moe_route (engine/src/qwen4exp.cpp:346-347)
+//   qmm_gemm_f32        hip::BlasLt::gemm_f32   engine/kernels/gemm.h:31, gemm.hip:162-186 (the prefill
+//                                               router, qwen4exp.cpp:626; hipBLASLt there)
 //
 // y[t][n] = W[n] . x[t] in f32, computed the reference's way so that the logits are its bits: a row is
 // one group of 32 lanes (here half a wave64), lane l accumulates the float4 steps i = 4l + 128k in
@@ -65,6 +67,101 @@ __global__ void __launch_bounds__(64) k_f32_gemv(const float* __restrict__ W, co
     }
 }
 
+// D[m][n] = A[m] . W[n] over K in f32 on the matrix cores (v_mfma_f32_32x32x2_f32): the prefill router
+// GEMM, 2048 x 513 x 2560 for a 2048-token chunk -- about one 32 x 32 output block per SIMD of the
+// chip, so the work is cut finer than the output: a workgroup owns one 32 x 32 block and its 4 waves
+// take a quarter of K each (steps of 16), added in a fixed order ((w0 + w1) + (w2 + w3)) through LDS
+// at the end.  There is no reuse inside a
+// workgroup to stage, so each lane loads its A and W pieces straight into registers, three steps
+// ahead of their MFMAs.  Tiles run W-block-fastest and each XCD takes a contiguous range of them
+// (workgroup i runs on XCD i % 8): an XCD holds a few A strips (2 MB for 8 strips of 2048-float rows)
+// and sweeps W with them, so the re-reads of A and W are L2 hits.  Lane (r, h) feeds row r at k = kb + 8h + i to MFMA i of a step (any pairing of
+// k across the MFMAs gives the same sum over k); one accumulator chain (back-to-back MFMAs of one
+// shape forward it), which keeps the kernel under 96 registers: 5 workgroups per CU, so the 1088
+// workgroups of a 2048-token chunk run in one round.  f32 accumulation in the matrix unit's order: the result agrees
+// with a double-precision dot to f32 rounding (the reference's hipBLASLt order is unspecified too).
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+constexpr int kFTile = 32, kFStep = 16, kFRing = 3;
+
+// p[k .. k + 3] if k < lim, else zeros (the address is clamped so that the load stays in the row)
+__device__ __forceinline__ float4 ld_f4z(const float* p, int k, int lim) {
+    const float4 v = *(const float4*)(p + min(k, lim - 4));
+    const bool in = k < lim;
+    return make_float4(in ? v.x : 0.f, in ? v.y : 0.f, in ? v.z : 0.f, in ? v.w : 0.f);
+}
+
+struct F32Piece { float4 a0, a1, w0, w1; };
+
+__global__ void __launch_bounds__(256) k_gemm_f32(const float* __restrict__ A, const float* __restrict__ W,
+                                                  float* __restrict__ D, int M, int N, int K, int nnt, int xcd_ord) {
+    __shared__ float red[4 * 16 * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int fr = lane & 31, h = lane >> 5;
+    const int id = blockIdx.x, total = gridDim.x;
+    const int t = xcd_ord ? (id & 7) * (total >> 3) + (id >> 3) : id;
+    const int m0 = (t / nnt) * kFTile, n0 = (t % nnt) * kFTile;
+    const float* ar = A + (size_t)min(m0 + fr, M - 1) * K;
+    const float* wr = W + (size_t)min(n0 + fr, N - 1) * K;
+    // steps of 16: the full ones [0, nfull) split over the 4 waves; a partial last step (K % 16 != 0)
+    // is done by wave 3 after its loop, with the lanes past K loading zeros
+    const int nfull = K / kFStep, nst = (K + kFStep - 1) / kFStep;
+    const int s0 = wave * nst / 4, s1 = min((wave + 1) * nst / 4, nfull);
+    F32Piece ring[kFRing];
+    // plain loads (every step of [s0, s1) is in the rows), consumed by the MFMAs as they are, so that
+    // the waits for one ring slot leave the next slots' loads in flight
+    auto load = [&](int s, F32Piece& p) {
+        const float* pa = ar + (size_t)s * kFStep + 8 * h;
+        const float* pw = wr + (size_t)s * kFStep + 8 * h;
+        p.a0 = *(const float4*)pa; p.a1 = *(const float4*)(pa + 4);
+        p.w0 = *(const float4*)pw; p.w1 = *(const float4*)(pw + 4);
+    };
+    f32x16_t acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    auto mma = [&](const F32Piece& p) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(p.a0.x, p.w0.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(p.a0.y, p.w0.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(p.a0.z, p.w0.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(p.a0.w, p.w0.w, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(p.a1.x, p.w1.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(p.a1.y, p.w1.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(p.a1.z, p.w1.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(p.a1.w, p.w1.w, acc, 0, 0, 0);
+    };
+    if (s0 < s1) {
+#pragma unroll
+        for (int i = 0; i < kFRing - 1; ++i) load(min(s0 + i, s1 - 1), ring[i]);
+        for (int s = s0; s < s1; s += kFRing) {         // ring slot i holds step s + i
+#pragma unroll
+            for (int i = 0; i < kFRing; ++i) {
+                // steps past the wave's share re-load its last step (in bounds) and are not used
+                load(min(s + i + kFRing - 1, s1 - 1), ring[(i + kFRing - 1) % kFRing]);
+                if (s + i < s1) mma(ring[i]);
+            }
+        }
+    }
+    if (wave == 3 && nfull < nst) {
+        F32Piece p;
+        const int k = nfull * kFStep + 8 * h;
+        p.a0 = ld_f4z(ar, k, K); p.a1 = ld_f4z(ar, k + 4, K);
+        p.w0 = ld_f4z(wr, k, K); p.w1 = ld_f4z(wr, k + 4, K);
+        mma(p);
+    }
+    // the four quarter sums, added in a fixed order; red[(w * 16 + e) * 64 + lane]
+#pragma unroll
+    for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
+    __syncthreads();
+    const int q = wave;                                  // this thread: elements 4q .. 4q + 3 of lane `lane`
+    const int n = n0 + fr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = 4 * q + i, o = e * 64 + lane;
+        const float v = (red[o] + red[16 * 64 + o]) + (red[2 * 16 * 64 + o] + red[3 * 16 * 64 + o]);
+        const int m = m0 + 8 * (e >> 2) + 4 * h + (e & 3);   // acc[e]: row 8 (e / 4) + 4 h + e % 4, column fr
+        if (m < M && n < N) D[(size_t)m * N + n] = v;
+    }
+}
+
 }  // namespace
 }  // namespace qmm
 
@@ -87,6 +184,19 @@ int qmm_f32_gemv(const float* W, const float* x, float* y, int N, int K, int T, 
     if (np == 1) hipLaunchKernelGGL((k_f32_gemv<1, 10>), dim3(gx, gy), dim3(64), 0, s, W, x, y, N, K, T);
     else if (np == 2) hipLaunchKernelGGL((k_f32_gemv<2, 8>), dim3(gx, gy), dim3(64), 0, s, W, x, y, N, K, T);
     else hipLaunchKernelGGL((k_f32_gemv<8, 3>), dim3(gx, gy), dim3(64), 0, s, W, x, y, N, K, T);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_gemm_f32(const float* A, const float* W, float* D, int M, int N, int K, void* stream) {
+    if (!A || !W || !D) return QMM_ERR_NULL;
+    if (M < 0 || N < 0 || K <= 0 || K % 4 != 0) return QMM_ERR_SHAPE;
+    if (((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(W)) & 15) != 0) return QMM_ERR_ARG;
+    if (M == 0 || N == 0) return QMM_OK;
+    const long long nmt = (M + kFTile - 1) / kFTile, nnt = (N + kFTile - 1) / kFTile, total = nmt * nnt;
+    if (total > 0x7fffffffLL) return QMM_ERR_SHAPE;
+    hipLaunchKernelGGL(k_gemm_f32, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, A, W, D, M, N, K, (int)nnt,
+                       (int)(total % 8 == 0));
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }

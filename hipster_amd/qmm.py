@@ -173,6 +173,12 @@ def f32_gemv(W, x, y, N, K, T, stream=None):
     check(_lib.lib().qmm_f32_gemv(_p(W), _p(x), _p(y), N, K, T, _stream(stream)), "f32_gemv")
 
 
+def gemm_f32(A, W, D, M, N, K, stream=None):
+    """gemm.h:31 (BlasLt::gemm_f32, the prefill router): D[m][n] = A[m] . W[n] in f32 on the matrix cores."""
+    _dev(A, torch.float32, "A"); _dev(W, torch.float32, "W"); _dev(D, torch.float32, "D")
+    check(_lib.lib().qmm_gemm_f32(_p(A), _p(W), _p(D), M, N, K, _stream(stream)), "gemm_f32")
+
+
 def moe_router(Wr, x, logits, ids, w, T, nexp=512, K=None, topk=10, stream=None):
     """qwen4exp.cpp:346-347 in one call: logits = Wr . x (f32_gemv), then moe_route_n on them."""
     _dev(Wr, torch.float32, "Wr"); _dev(x, torch.float32, "x"); _dev(logits, torch.float32, "logits")

@@ -116,6 +116,11 @@ int qmm_moe_route_n(const float* logits, int* ids, float* w, int T, int nexp, in
  * order (32 lanes per row over float4 steps 4l + 128k, its fma contraction, the xor-butterfly sum):
  * the same bits. */
 int qmm_f32_gemv(const float* W, const float* x, float* y, int N, int K, int T, void* stream);
+/* D[m][n] = A[m] . W[n] in f32 (reference: hip::BlasLt::gemm_f32, gemm.h:31, gemm.hip:162-186, which
+ * runs hipBLASLt; the prefill router, qwen4exp.cpp:626): A [M][K], W [N][K], D [M][N] f32, K % 4 == 0,
+ * A and W 16-byte aligned.  f32 matrix-core accumulation: within f32 rounding of the exact dot (the
+ * reference's summation order is hipBLASLt's, unspecified). */
+int qmm_gemm_f32(const float* A, const float* W, float* D, int M, int N, int K, void* stream);
 /* qmm_f32_gemv of the router (nexp+1 rows: the experts and the shared gate) into logits [T][nexp+1],
  * then qmm_moe_route_n on them: the two calls of qwen4exp.cpp:346-347 in one (two launches, no host
  * work between).  No reference counterpart as one function. */

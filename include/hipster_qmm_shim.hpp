@@ -106,6 +106,10 @@ public:
     void gemm(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, hipStream_t s) {
         detail::ck(qmm_gemm_bf16(A, W, D, M, N, K, (void*)s), "BlasLt::gemm");
     }
+    // D[M][N] f32 = A[M][K] f32 . W[N][K]^T f32: the prefill router (gemm.h:31)
+    void gemm_f32(const float* A, const float* W, float* D, int M, int N, int K, hipStream_t s) {
+        detail::ck(qmm_gemm_f32(A, W, D, M, N, K, (void*)s), "BlasLt::gemm_f32");
+    }
 };
 
 // ---- additions with no reference counterpart (the calls the engine's prefill moves to) ----------

@@ -160,6 +160,10 @@ def test_router_validation_without_device_work():
     assert L.qmm_f32_gemv(d, ctypes.c_void_p(260), d, 513, 2048, 1, None) == -6   # x not 16-byte aligned
     assert L.qmm_f32_gemv(None, d, d, 513, 2048, 1, None) == -3
     assert L.qmm_f32_gemv(d, d, d, 0, 2048, 1, None) == 0
+    assert L.qmm_gemm_f32(d, d, d, 2048, 513, 2562, None) == -2            # K % 4 != 0
+    assert L.qmm_gemm_f32(ctypes.c_void_p(264), d, d, 2048, 513, 2560, None) == -6   # A not 16-byte aligned
+    assert L.qmm_gemm_f32(d, d, None, 2048, 513, 2560, None) == -3
+    assert L.qmm_gemm_f32(d, d, d, 0, 513, 2560, None) == 0                # nothing to do: no launch
     assert L.qmm_moe_router(d, d, d, d, d, 1, 2048, 2048, 10, None) == -2  # too many experts for the routing
     assert L.qmm_moe_router(d, d, d, d, d, 1, 512, 2048, 17, None) == -2   # top-k above 16
     assert L.qmm_moe_router(d, d, d, None, d, 1, 512, 2048, 10, None) == -3
