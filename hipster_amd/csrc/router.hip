@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(64) k_f32_gemv(const float* __restrict__ W, co
 }
 
 // D[m][n] = A[m] . W[n] over K in f32 on the matrix cores (v_mfma_f32_32x32x2_f32): the prefill router
-// GEMM, 2048 x 513 x 2560 for a 2048-token chunk -- about one 32 x 32 output block per SIMD of the
+// GEMM for any K % 4 == 0 (K % 32 == 0 takes k_gemm_f32d below), 2048 x 513 x 2560 for a 2048-token chunk -- about one 32 x 32 output block per SIMD of the
 // chip, so the work is cut finer than the output: a workgroup owns one 32 x 32 block and its 4 waves
 // take a quarter of K each (steps of 16), added in a fixed order ((w0 + w1) + (w2 + w3)) through LDS
 // at the end.  There is no reuse inside a
@@ -162,6 +162,92 @@ __global__ void __launch_bounds__(256) k_gemm_f32(const float* __restrict__ A, c
     }
 }
 
+// The same product with the A and W pieces staged by DMA (global_load_lds_dwordx4) into a ring of NS
+// stages private to each wave (stage = 32 k: 4 KB of A rows, 4 KB of W rows), for K % 32 == 0.  One
+// DMA instruction moves 8 rows x 128 contiguous bytes (whole cache lines), where the register kernel's
+// loads touch 32 rows per instruction; the ring needs no registers.  With NS = 2 (64 KB per workgroup,
+// two workgroups per CU) a wave computes one stage while the next lands and the other workgroup's
+// wave on the same SIMD covers the rest of the latency: 59 us at 2048 x 513 x 2048 against 86 us for
+// the register kernel.  Slot (row, chunk q) of a stage
+// sits at row * 8 + (q ^ swz(row)): the DMA lanes of one instruction write 8 whole rows, and the
+// MFMA fragment reads (16 consecutive rows, one chunk) fall in distinct banks.
+__device__ __forceinline__ int f32_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+#define QMM_VMWAIT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+
+template <int NS>
+__global__ void __launch_bounds__(256) k_gemm_f32d(const float* __restrict__ A, const float* __restrict__ W,
+                                                   float* __restrict__ D, int M, int N, int K, int nnt, int xcd_ord) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int fr = lane & 31, h = lane >> 5;
+    const int id = blockIdx.x, total = gridDim.x;
+    const int t = xcd_ord ? (id & 7) * (total >> 3) + (id >> 3) : id;
+    const int m0 = (t / nnt) * kFTile, n0 = (t % nnt) * kFTile;
+    const int nstg = K / 32, s0 = wave * nstg / 4, n = (wave + 1) * nstg / 4 - s0;
+    uint8_t* wring = smem + (size_t)wave * NS * 8192;
+    const uint32_t lring = lds_addr(wring);
+    uint32_t aoff[4], woff[4];                      // byte offsets of this lane's DMA pieces at k = 0
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = 8 * j + (lane >> 3), q = (lane & 7) ^ f32_swz(row);
+        aoff[j] = ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + 4u * q) * 4u;
+        woff[j] = ((uint32_t)min(n0 + row, N - 1) * (uint32_t)K + 4u * q) * 4u;
+    }
+    auto issue = [&](int i) {                       // stage i of this wave into slot i % NS
+        const uint32_t st = lring + (uint32_t)(i % NS) * 8192u, kb = (uint32_t)(s0 + i) * 128u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16s(A, aoff[j] + kb, st + 1024u * j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16s(W, woff[j] + kb, st + 4096u + 1024u * j);
+    };
+    f32x16_t acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i)
+        if (i < n) issue(i);
+    for (int i = 0; i < n; ++i) {
+        if (i + NS - 1 < n) issue(i + NS - 1);     // into the slot of stage i - 1, read in the last iteration
+        const int after = min(NS - 1, n - 1 - i);  // stages issued after stage i (8 DMA instructions each)
+        if (after >= 3) QMM_VMWAIT(24);
+        else if (after == 2) QMM_VMWAIT(16);
+        else if (after == 1) QMM_VMWAIT(8);
+        else QMM_VMWAIT(0);
+        const uint8_t* st = wring + (size_t)(i % NS) * 8192;
+        const int sw = f32_swz(fr);
+        float4 av[4], wv[4];                        // the stage's fragments first, then its 16 MFMAs
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int slot = fr * 8 + ((4 * h + c) ^ sw);
+            av[c] = *(const float4*)(st + 16 * slot);
+            wv[c] = *(const float4*)(st + 4096 + 16 * slot);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c].x, wv[c].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c].y, wv[c].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c].z, wv[c].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[c].w, wv[c].w, acc, 0, 0, 0);
+        }
+    }
+    __syncthreads();                                // every wave done with its ring: reuse it for the sums
+    float* red = (float*)smem;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
+    __syncthreads();
+    const int nn = n0 + fr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = 4 * wave + i, o = e * 64 + lane;
+        const float v = (red[o] + red[16 * 64 + o]) + (red[2 * 16 * 64 + o] + red[3 * 16 * 64 + o]);
+        const int m = m0 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < M && nn < N) D[(size_t)m * N + nn] = v;
+    }
+}
+
+constexpr int kF32dStages = 2;   // 64 KB of LDS per workgroup: two workgroups per CU (measured against 3 and 4)
+
 }  // namespace
 }  // namespace qmm
 
@@ -195,8 +281,13 @@ int qmm_gemm_f32(const float* A, const float* W, float* D, int M, int N, int K, 
     if (M == 0 || N == 0) return QMM_OK;
     const long long nmt = (M + kFTile - 1) / kFTile, nnt = (N + kFTile - 1) / kFTile, total = nmt * nnt;
     if (total > 0x7fffffffLL) return QMM_ERR_SHAPE;
-    hipLaunchKernelGGL(k_gemm_f32, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, A, W, D, M, N, K, (int)nnt,
-                       (int)(total % 8 == 0));
+    const bool dma = K % 32 == 0 && (size_t)M * K * 4 <= 0xffffffffu && (size_t)N * K * 4 <= 0xffffffffu;
+    if (dma)
+        hipLaunchKernelGGL(k_gemm_f32d<kF32dStages>, dim3((unsigned)total), dim3(256), (size_t)kF32dStages * 4 * 8192,
+                           (hipStream_t)stream, A, W, D, M, N, K, (int)nnt, (int)(total % 8 == 0));
+    else
+        hipLaunchKernelGGL(k_gemm_f32, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, A, W, D, M, N, K, (int)nnt,
+                           (int)(total % 8 == 0));
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }
