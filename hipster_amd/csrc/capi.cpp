@@ -55,6 +55,7 @@ const char* qmm_status_string(int status) {
         case QMM_ERR_LAUNCH: return "kernel launch failed";
         case QMM_ERR_WORKSPACE: return "workspace missing or too small";
         case QMM_ERR_ARG: return "invalid argument";
+        case QMM_ERR_LAYOUT: return "weight layout not supported (the reference's experimental interleaved layouts)";
         default: return "unknown status";
     }
 }
@@ -132,6 +133,79 @@ int qmm_repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K) {
         memcpy(dst + qh + b * 4, blk + 2, 4);
         memcpy(dst + dd + b * 2, &d, 2);
         memcpy(dst + mm + b * 2, &m, 2);
+    }
+    return QMM_OK;
+}
+
+}  // extern "C"
+
+namespace {
+int block_bytes_il(int fmt) {
+    switch (fmt) {
+        case QMM_Q4_K: return 144;
+        case QMM_Q5_K: return 176;
+        case QMM_IQ4_XS: return 136;
+        case QMM_Q6_K_SOA: return 210;
+        case QMM_Q8_0_SOA: return 272;
+        default: return 0;
+    }
+}
+}  // namespace
+
+extern "C" {
+
+// gemv.hip:1442-1447: groups of 8 rows, block b of row r at block index (r/8)*8*nb + b*8 + r%8
+int qmm_repack_interleave8(int fmt, const uint8_t* src, uint8_t* dst, int N, int K) {
+    if (!src || !dst) return QMM_ERR_NULL;
+    if (fmt != QMM_Q4_K && fmt != QMM_Q5_K && fmt != QMM_IQ4_XS) return QMM_ERR_FORMAT;
+    if (N <= 0 || N % 8 != 0 || K <= 0 || K % 256 != 0) return QMM_ERR_SHAPE;
+    const size_t bb = (size_t)block_bytes_il(fmt), nb = (size_t)K / 256;
+    for (size_t r = 0; r < (size_t)N; ++r)
+        for (size_t b = 0; b < nb; ++b) memcpy(dst + ((r / 8) * 8 * nb + b * 8 + r % 8) * bb, src + (r * nb + b) * bb, bb);
+    return QMM_OK;
+}
+
+// gemv.hip:1280
+size_t qmm_wmma_il_bytes(int fmt, int N, int K) {
+    const int bb = block_bytes_il(fmt);
+    if (bb == 0 || N <= 0 || K <= 0 || K % 256 != 0) return 0;
+    return (size_t)((N + 15) / 16) * (size_t)(K / 256) * 16 * (size_t)bb;
+}
+
+// gemv.hip:1281-1303: rows in groups of 16 (N padded with zero rows); per group and 256-weight block the
+// 16 rows' bytes are stored piece-major, [piece][row][piece bytes]: 16-byte pieces for Q4_K and Q5_K,
+// 8-byte pieces for IQ4_XS, Q6_K_SOA as [ql 8 x 16 B][qh 4 x 16 B][scales 16 B][d 2 B] per row,
+// Q8_0_SOA as [q 16 x 16 B][d 16 B] per row
+int qmm_repack_wmma_il(int fmt, const uint8_t* src, uint8_t* dst, int N, int K) {
+    if (!src || !dst) return QMM_ERR_NULL;
+    const size_t total = qmm_wmma_il_bytes(fmt, N, K);
+    if (block_bytes_il(fmt) == 0) return QMM_ERR_FORMAT;
+    if (total == 0) return QMM_ERR_SHAPE;
+    const size_t nb = (size_t)K / 256, BB = (size_t)block_bytes_il(fmt), gb = 16 * BB;
+    memset(dst, 0, total);
+    for (size_t r = 0; r < (size_t)N; ++r) {
+        const size_t g = r / 16, r16 = r % 16;
+        uint8_t* gbase = dst + g * nb * gb;
+        for (size_t b = 0; b < nb; ++b) {
+            uint8_t* d = gbase + b * gb;
+            if (fmt == QMM_Q4_K || fmt == QMM_Q5_K) {
+                const uint8_t* blk = src + (r * nb + b) * BB;
+                for (size_t i = 0; i < BB / 16; ++i) memcpy(d + i * 256 + r16 * 16, blk + i * 16, 16);
+            } else if (fmt == QMM_IQ4_XS) {
+                const uint8_t* blk = src + (r * nb + b) * 136;
+                for (size_t i = 0; i < 17; ++i) memcpy(d + i * 128 + r16 * 8, blk + i * 8, 8);
+            } else if (fmt == QMM_Q6_K_SOA) {
+                const uint8_t* rp = src + r * ((size_t)K * 210 / 256);
+                for (size_t i = 0; i < 8; ++i) memcpy(d + i * 256 + r16 * 16, rp + b * 128 + i * 16, 16);
+                for (size_t i = 0; i < 4; ++i) memcpy(d + 2048 + i * 256 + r16 * 16, rp + nb * 128 + b * 64 + i * 16, 16);
+                memcpy(d + 3072 + r16 * 16, rp + nb * 192 + b * 16, 16);
+                memcpy(d + 3328 + r16 * 2, rp + nb * 208 + b * 2, 2);
+            } else {                                  // Q8_0_SOA
+                const uint8_t* rp = src + r * ((size_t)K + (size_t)K / 16);
+                for (size_t i = 0; i < 16; ++i) memcpy(d + i * 256 + r16 * 16, rp + b * 256 + i * 16, 16);
+                memcpy(d + 4096 + r16 * 16, rp + (size_t)K + b * 16, 16);
+            }
+        }
     }
     return QMM_OK;
 }

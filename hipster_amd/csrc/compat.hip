@@ -1,0 +1,367 @@
+// compat.hip -- the rest of the reference's quantized-matmul call surface on gfx950, so that the
+// engine and its validators compile and run against this library unchanged:
+//
+//   qmm_gemv_splitk        gemv_splitk     engine/kernels/gemv.h:55, gemv.hip:1397-1441
+//   qmm_hc_up_fused        hc_up_fused     gemv.h:52, gemv.hip:976-1005
+//   qmm_moe_gemm_q8        moe_gemm        gemv.h:49-50, gemv.hip:909-969,1377-1381 (q8 activations)
+//   qmm_quantize_x_q8k     quantize_x_q8k  gemv.h:34, gemv.hip:686-705,1254-1257
+//   qmm_gemv_q8k           gemv_wmma_q8k   gemv.h:35, gemv.hip:706-794,1259-1271
+//
+// All of them are built on the per-format units of fmt_unit.hpp: every (row, column) is the
+// reference's q8 arithmetic (integer dot per scale group, the per-sub-block fix-up in f32), a lane
+// accumulates its units in a fixed order and the wave reduces with a fixed butterfly, so a column's
+// result does not depend on how many columns a call carries.  They are VALU kernels: the engine's
+// hot calls go to the tuned kernels of gemv.hip / moe_prefill.hip; these keep the remaining call
+// sites working with the reference's exact (not bf16-rounded) numerics.
+#include "fmt_unit.hpp"
+#include "qmm_common.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+namespace qmm {
+namespace {
+
+constexpr int kCThreads = 256, kCWaves = kCThreads / 64, kCRpw = 2, kCCols = 8;
+
+// ---- split-K GEMV: part[(c * ksplit + ks) * N + n] = W[n][K range ks] . x[c][K range ks] ----------
+// The K range of split ks is the 256-weight blocks [ks*nb/ksplit, (ks+1)*nb/ksplit), nb = ceil(K/256)
+// (gemv.hip:1404), so every partial covers the same weights as the reference's.
+template <int F, int NC, int NIT>
+__global__ void __launch_bounds__(kCThreads) k_gemv_splitk(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                           const float* __restrict__ xd, const float* __restrict__ xs,
+                                                           float* __restrict__ part, int N, int K, int ksplit, int c0) {
+    const int ks = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kCWaves + wave) * kCRpw;
+    const int nb = (K + 255) >> 8, U = fmt_units<F>(K), upb = 256 / fmt_unit_weights<F>();
+    const int ub = min(ks * nb / ksplit * upb, U), ue = min((ks + 1) * nb / ksplit * upb, U);
+    const int nsb = K >> 5;
+    XSrcQ8 src[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) src[c] = XSrcQ8{xq + (size_t)(c0 + c) * K, xd + (size_t)(c0 + c) * nsb, xs + (size_t)(c0 + c) * nsb};
+    float acc[kCRpw][NC];
+    fmt_rows<F, NC, NIT, kCRpw>(W, row0, N, K, src, acc, ub, ue);
+#pragma unroll
+    for (int r = 0; r < kCRpw; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = wave_sum(acc[r][c]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < kCRpw; ++r)
+            if (row0 + r < N) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) part[((size_t)(c0 + c) * ksplit + ks) * N + row0 + r] = acc[r][c];
+            }
+    }
+}
+
+template <int F>
+int launch_splitk(const void* W, qmm_xq8 x, float* part, int N, int K, int ksplit, int ncol, hipStream_t s) {
+    const int nb = (K + 255) >> 8, upb = 256 / fmt_unit_weights<F>();
+    const int per_split = (nb + ksplit - 1) / ksplit * upb;       // units of the longest split
+    const dim3 grid((unsigned)((N + kCWaves * kCRpw - 1) / (kCWaves * kCRpw)), (unsigned)ksplit);
+    for (int c0 = 0; c0 < ncol; c0 += kCCols) {
+        const int nc = std::min(kCCols, ncol - c0);
+#define QMM_SK(NC, NIT) hipLaunchKernelGGL((k_gemv_splitk<F, NC, NIT>), grid, dim3(kCThreads), 0, s, (const uint8_t*)W, x.q, x.d, x.s, part, N, K, ksplit, c0)
+#define QMM_SKN(NIT) switch (nc) { case 1: QMM_SK(1, NIT); break; case 2: QMM_SK(2, NIT); break; case 3: QMM_SK(3, NIT); break; \
+                                   case 4: QMM_SK(4, NIT); break; case 5: QMM_SK(5, NIT); break; case 6: QMM_SK(6, NIT); break; \
+                                   case 7: QMM_SK(7, NIT); break; default: QMM_SK(8, NIT); break; }
+        if (per_split <= 64) { QMM_SKN(1) } else { QMM_SKN(2) }
+#undef QMM_SKN
+#undef QMM_SK
+        QMM_LAUNCH_CHECK();
+    }
+    return QMM_OK;
+}
+
+// ---- hyper-connection up-projection with its silu prologue (gemv.hip:976-1005) -------------------
+// x = silu(sum_k part[(t*ksplit + k)][320] / 4) (partials summed in k order, silu v / (1 + exp(-v))),
+// quantised per 32 into LDS, then y[t][n] = W[n] . x with W Q8_0_SOA [N][320].  Grid = (row
+// blocks of 32, T); 8 lanes per row, lane l of a row takes sub-blocks l and l + 8.
+constexpr int kHcK = 320, kHcSub = kHcK / 32, kHcRows = 32;
+
+__global__ void __launch_bounds__(kCThreads) k_hc_up_fused(const uint8_t* __restrict__ W, const float* __restrict__ part, int ksplit,
+                                                           float* __restrict__ y, int N) {
+    __shared__ __align__(16) int8_t sq[kHcK];
+    __shared__ float sxf[kHcK], sd[kHcSub], ss[kHcSub];
+    const int t = blockIdx.y, tid = threadIdx.x;
+    for (int i = tid; i < kHcK; i += kCThreads) {
+        float v = 0.f;
+        for (int k = 0; k < ksplit; ++k) v += part[((size_t)t * ksplit + k) * kHcK + i];
+        v *= 0.25f;
+        sxf[i] = v / (1.f + __expf(-v));
+    }
+    __syncthreads();
+    {   // q8 per 32, one half-wave per sub-block (the order-free max and integer sum of hw32_quant)
+        const int hw = tid >> 5, l = tid & 31;
+        for (int sb = hw; sb < kHcSub; sb += kCThreads / 32) {
+            const float v = sxf[sb * 32 + l];
+            const float amax = g32_max(fabsf(v));
+            const float dd = amax / 127.f, id = amax > 0.f ? 127.f / amax : 0.f;
+            const int qi = __float2int_rn(v * id);
+            const int sum = g32_isum(qi);
+            sq[sb * 32 + l] = (int8_t)qi;
+            if (l == 0) { sd[sb] = dd; ss[sb] = dd * (float)sum; }
+        }
+    }
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6, l8 = lane & 7;
+    const int row = blockIdx.x * kHcRows + wave * 8 + (lane >> 3);
+    const uint8_t* rp = W + (size_t)min(row, N - 1) * fmt_row_bytes<QMM_Q8_0_SOA>(kHcK);
+    const XSrcQ8 src{sq, sd, ss};
+    typedef FmtUnit<QMM_Q8_0_SOA> FU;
+    FU::Raw r0, r1;
+    FU::load(rp, kHcK, l8, r0);
+    FU::load(rp, kHcK, min(l8 + 8, kHcSub - 1), r1);
+    X32 x0, x1;
+    src.sub(l8, x0);
+    src.sub(min(l8 + 8, kHcSub - 1), x1);
+    float acc = FU::col(r0, x0, l8);
+    const float v1 = FU::col(r1, x1, l8 + 8);
+    acc += l8 + 8 < kHcSub ? v1 : 0.f;
+    acc = group_sum(acc, 8);
+    if (l8 == 0 && row < N) y[(size_t)t * N + row] = acc;
+}
+
+// ---- grouped expert GEMM over sorted slots with q8 activations (moe_gemm, gemv.hip:909-969) -------
+// Workgroup (row block, tile): tile = (expert, k0, ncols); column r < ncols is x row rowtab[k0+r]
+// (or k0+r), output row k0+r: y[(k0 + r) * N + n] = W_e[n] . x[row].  W_e = W + expert * ebytes in
+// format F, or Wsh when expert < 0 (read in F too: the reference's routed launch does the same).
+// Columns in passes of up to 8; rows of a wave as the plain GEMV of the format.
+template <int F, int NIT, int NC>
+__device__ __forceinline__ void moe_q8_pass(const uint8_t* wb, int row0, int N, int K, const int8_t* xq, const float* xd,
+                                            const float* xs, const int* rowtab, int k0, int nc, float* __restrict__ y) {
+    const int nsb = K >> 5, lane = threadIdx.x & 63;
+    XSrcQ8 src[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int k = k0 + min(c, nc - 1);
+        const size_t xr = (size_t)(rowtab ? rowtab[k] : k);
+        src[c] = XSrcQ8{xq + xr * K, xd + xr * nsb, xs + xr * nsb};
+    }
+    float acc[kCRpw][NC];
+    fmt_rows<F, NC, NIT, kCRpw>(wb, row0, N, K, src, acc, 0, fmt_units<F>(K));
+#pragma unroll
+    for (int r = 0; r < kCRpw; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = wave_sum(acc[r][c]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < kCRpw; ++r)
+            if (row0 + r < N) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    if (c < nc) y[(size_t)(k0 + c) * N + row0 + r] = acc[r][c];
+            }
+    }
+}
+
+template <int F, int NIT>
+__global__ void __launch_bounds__(kCThreads) k_moe_gemm_q8(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Wsh, size_t ebytes,
+                                                           const qmm_moe_tile* __restrict__ tiles, const int* __restrict__ rowtab,
+                                                           const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                           const float* __restrict__ xs, float* __restrict__ y, int N, int K) {
+    const qmm_moe_tile tl = tiles[blockIdx.y];
+    if (tl.ncols <= 0) return;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kCWaves + wave) * kCRpw;
+    const uint8_t* wb = tl.expert >= 0 ? W + (size_t)tl.expert * ebytes : Wsh;
+    for (int c0 = 0; c0 < tl.ncols; c0 += kCCols) {
+        const int nc = min(kCCols, tl.ncols - c0), k0 = tl.k0 + c0;
+        if (nc == 1) moe_q8_pass<F, NIT, 1>(wb, row0, N, K, xq, xd, xs, rowtab, k0, nc, y);
+        else if (nc == 2) moe_q8_pass<F, NIT, 2>(wb, row0, N, K, xq, xd, xs, rowtab, k0, nc, y);
+        else if (nc <= 4) moe_q8_pass<F, NIT, 4>(wb, row0, N, K, xq, xd, xs, rowtab, k0, nc, y);
+        else moe_q8_pass<F, NIT, 8>(wb, row0, N, K, xq, xd, xs, rowtab, k0, nc, y);
+    }
+}
+
+template <int F>
+int launch_moe_q8(const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles, int ntiles, const int* rowtab,
+                  qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    if (ntiles <= 0) return QMM_OK;
+    const dim3 grid((unsigned)((N + kCWaves * kCRpw - 1) / (kCWaves * kCRpw)), (unsigned)ntiles);
+    if ((fmt_units<F>(K) + 63) / 64 <= 1)
+        hipLaunchKernelGGL((k_moe_gemm_q8<F, 1>), grid, dim3(kCThreads), 0, s, (const uint8_t*)W, (const uint8_t*)Wsh, ebytes, tiles,
+                           rowtab, x.q, x.d, x.s, y, N, K);
+    else
+        hipLaunchKernelGGL((k_moe_gemm_q8<F, 2>), grid, dim3(kCThreads), 0, s, (const uint8_t*)W, (const uint8_t*)Wsh, ebytes, tiles,
+                           rowtab, x.q, x.d, x.s, y, N, K);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int moe_q8_dispatch(int fmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles, int ntiles,
+                    const int* rowtab, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    switch (fmt) {
+        case QMM_Q4_K: return launch_moe_q8<QMM_Q4_K>(W, Wsh, ebytes, tiles, ntiles, rowtab, x, y, N, K, s);
+        case QMM_Q5_K: return launch_moe_q8<QMM_Q5_K>(W, Wsh, ebytes, tiles, ntiles, rowtab, x, y, N, K, s);
+        case QMM_IQ4_XS: return launch_moe_q8<QMM_IQ4_XS>(W, Wsh, ebytes, tiles, ntiles, rowtab, x, y, N, K, s);
+        case QMM_Q8_0_SOA: return launch_moe_q8<QMM_Q8_0_SOA>(W, Wsh, ebytes, tiles, ntiles, rowtab, x, y, N, K, s);
+        case QMM_Q5_1_SOA: return launch_moe_q8<QMM_Q5_1_SOA>(W, Wsh, ebytes, tiles, ntiles, rowtab, x, y, N, K, s);
+        default: return QMM_ERR_FORMAT;
+    }
+}
+
+// ---- Q8_K activations (gemv.hip:686-705): one scale per 256 weights, int16 sums per 32 ------------
+// q [ncol][K] int8, d [K/256][16] f32, bs [K/256][16][8] int16; workgroup (block b, column c):
+// d = amax/127 over the 256 values, q = rne(x * 127/amax) (0 when amax == 0), bs = sum of the 32 q.
+__global__ void __launch_bounds__(256) k_quantize_x_q8k(const float* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ d,
+                                                        int16_t* __restrict__ bs, int K) {
+    __shared__ float red[8];
+    const int b = blockIdx.x, col = blockIdx.y, tid = threadIdx.x, hw = tid >> 5, l = tid & 31;
+    const size_t k = (size_t)col * K + (size_t)b * 256 + tid;
+    const float v = x[k];
+    const float m32 = g32_max(fabsf(v));
+    if (l == 0) red[hw] = m32;
+    __syncthreads();
+    float amax = red[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) amax = fmaxf(amax, red[i]);
+    const float dd = amax / 127.f, id = amax > 0.f ? 127.f / amax : 0.f;
+    const int qi = __float2int_rn(v * id);
+    const int sum = g32_isum(qi);
+    q[k] = (int8_t)qi;
+    if (l == 0) bs[((size_t)b * 16 + col) * 8 + hw] = (int16_t)sum;
+    if (tid == 0) d[(size_t)b * 16 + col] = dd;
+}
+
+// q8 GEMV on Q8_K activations: the fmt_rows arithmetic with each sub-block's (d, s) = (block scale,
+// block scale * bs); y[c][n] for c in [c0, c0 + NC).
+template <int F, int NC, int NIT>
+__global__ void __launch_bounds__(kCThreads) k_gemv_q8k(const uint8_t* __restrict__ W, const int8_t* __restrict__ q,
+                                                        const float* __restrict__ d, const int16_t* __restrict__ bs,
+                                                        float* __restrict__ y, int N, int K, int c0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kCWaves + wave) * kCRpw;
+    XSrcQ8K src[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) src[c] = XSrcQ8K{q + (size_t)(c0 + c) * K, d, bs, c0 + c};
+    float acc[kCRpw][NC];
+    fmt_rows<F, NC, NIT, kCRpw>(W, row0, N, K, src, acc, 0, fmt_units<F>(K));
+#pragma unroll
+    for (int r = 0; r < kCRpw; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = wave_sum(acc[r][c]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < kCRpw; ++r)
+            if (row0 + r < N) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) y[(size_t)(c0 + c) * N + row0 + r] = acc[r][c];
+            }
+    }
+}
+
+template <int F>
+int launch_q8k(const void* W, const qmm_xq8k& x, float* y, int N, int K, int ncol, hipStream_t s) {
+    const dim3 grid((unsigned)((N + kCWaves * kCRpw - 1) / (kCWaves * kCRpw)));
+    const int per_lane = (fmt_units<F>(K) + 63) / 64;
+    for (int c0 = 0; c0 < ncol; c0 += kCCols) {
+        const int nc = std::min(kCCols, ncol - c0);
+#define QMM_QK(NC, NIT) hipLaunchKernelGGL((k_gemv_q8k<F, NC, NIT>), grid, dim3(kCThreads), 0, s, (const uint8_t*)W, x.q, x.d, x.bs, y, N, K, c0)
+#define QMM_QKN(NIT) switch (nc) { case 1: QMM_QK(1, NIT); break; case 2: QMM_QK(2, NIT); break; case 3: QMM_QK(3, NIT); break; \
+                                   case 4: QMM_QK(4, NIT); break; case 5: QMM_QK(5, NIT); break; case 6: QMM_QK(6, NIT); break; \
+                                   case 7: QMM_QK(7, NIT); break; default: QMM_QK(8, NIT); break; }
+        if (per_lane <= 1) { QMM_QKN(1) } else { QMM_QKN(2) }
+#undef QMM_QKN
+#undef QMM_QK
+        QMM_LAUNCH_CHECK();
+    }
+    return QMM_OK;
+}
+
+// K granule of a format for these kernels (the block formats whole 256-weight blocks; Q6_K_SOA
+// 512 so that its rows stay dword aligned; the 32-weight SoA formats as qmm_gemv_q8)
+int kgran(int f) {
+    switch (f) {
+        case QMM_Q8_0_SOA: return 64;
+        case QMM_Q5_1_SOA: return 32;
+        case QMM_Q6_K_SOA: return 512;
+        default: return 256;
+    }
+}
+
+}  // namespace
+}  // namespace qmm
+
+using namespace qmm;
+
+extern "C" {
+
+int qmm_gemv_splitk(int fmt, const void* W, qmm_xq8 x, float* part, int N, int K, int ksplit, int ncol, void* stream) {
+    if (!W || !x.q || !x.d || !x.s || !part) return QMM_ERR_NULL;
+    if (N <= 0 || K <= 0 || K % kgran(fmt) != 0 || ncol < 1 || ksplit < 1 || ksplit > (K + 255) / 256) return QMM_ERR_SHAPE;
+    hipStream_t s = (hipStream_t)stream;
+    switch (fmt) {
+        case QMM_Q4_K: return launch_splitk<QMM_Q4_K>(W, x, part, N, K, ksplit, ncol, s);
+        case QMM_Q5_K: return launch_splitk<QMM_Q5_K>(W, x, part, N, K, ksplit, ncol, s);
+        case QMM_IQ4_XS: return launch_splitk<QMM_IQ4_XS>(W, x, part, N, K, ksplit, ncol, s);
+        case QMM_Q6_K_SOA: return launch_splitk<QMM_Q6_K_SOA>(W, x, part, N, K, ksplit, ncol, s);
+        case QMM_Q8_0_SOA: return launch_splitk<QMM_Q8_0_SOA>(W, x, part, N, K, ksplit, ncol, s);
+        case QMM_Q5_1_SOA: return launch_splitk<QMM_Q5_1_SOA>(W, x, part, N, K, ksplit, ncol, s);
+        default: return QMM_ERR_FORMAT;
+    }
+}
+
+int qmm_hc_up_fused(const void* W, const float* part, int ksplit, float* y, int N, int T, void* stream) {
+    if (!W || !part || !y) return QMM_ERR_NULL;
+    if (N <= 0 || T < 0 || ksplit < 1) return QMM_ERR_SHAPE;
+    if (T == 0) return QMM_OK;
+    hipLaunchKernelGGL(k_hc_up_fused, dim3((unsigned)((N + kHcRows - 1) / kHcRows), (unsigned)T), dim3(kCThreads), 0,
+                       (hipStream_t)stream, (const uint8_t*)W, part, ksplit, y, N);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_moe_gemm_q8(int fmt, int shared_fmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles, int ntiles,
+                    const qmm_moe_tile* stiles, int nstiles, int ct, const int* rowtab, qmm_xq8 x, float* y, int N, int K,
+                    void* stream) {
+    auto fmt_ok = [](int f) { return f == QMM_Q4_K || f == QMM_Q5_K || f == QMM_IQ4_XS || f == QMM_Q8_0_SOA || f == QMM_Q5_1_SOA; };
+    if (!fmt_ok(fmt) || (nstiles > 0 && !fmt_ok(shared_fmt))) return QMM_ERR_FORMAT;
+    if (!x.q || !x.d || !x.s || !y || (ntiles > 0 && (!W || !tiles)) || (nstiles > 0 && (!Wsh || !stiles))) return QMM_ERR_NULL;
+    if (N <= 0 || K <= 0 || K % kgran(fmt) != 0 || (nstiles > 0 && K % kgran(shared_fmt) != 0) || ntiles < 0 || nstiles < 0 ||
+        ct < 1 || ntiles > 65535 || nstiles > 65535)
+        return QMM_ERR_SHAPE;
+    hipStream_t s = (hipStream_t)stream;
+    int rc = moe_q8_dispatch(fmt, W, Wsh, ebytes, tiles, ntiles, rowtab, x, y, N, K, s);
+    if (rc != QMM_OK) return rc;
+    return moe_q8_dispatch(shared_fmt, Wsh, Wsh, 0, stiles, nstiles, rowtab, x, y, N, K, s);
+}
+
+int qmm_quantize_x_q8k(const float* x, qmm_xq8k out, int ncol, int K, void* stream) {
+    if (!x || !out.q || !out.d || !out.bs) return QMM_ERR_NULL;
+    if (K <= 0 || K % 256 != 0 || ncol < 1 || ncol > 16) return QMM_ERR_SHAPE;
+    hipLaunchKernelGGL(k_quantize_x_q8k, dim3((unsigned)(K / 256), (unsigned)ncol), dim3(256), 0, (hipStream_t)stream, x, out.q,
+                       out.d, out.bs, K);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+int qmm_gemv_q8k(const qmm_gemv_seg* segs, int nseg, qmm_xq8k x, int ncol, void* stream) {
+    if (!segs || !x.q || !x.d || !x.bs) return QMM_ERR_NULL;
+    if (nseg < 1 || ncol < 1 || ncol > 16) return QMM_ERR_SHAPE;
+    for (int i = 0; i < nseg; ++i) {
+        const qmm_gemv_seg& g = segs[i];
+        if (!g.w || !g.y) return QMM_ERR_NULL;
+        if (g.N <= 0 || g.K <= 0 || g.K % 256 != 0 || g.K % kgran(g.fmt) != 0 || g.K != segs[0].K) return QMM_ERR_SHAPE;
+        if (!(g.fmt == QMM_Q4_K || g.fmt == QMM_Q5_K || g.fmt == QMM_IQ4_XS || g.fmt == QMM_Q6_K_SOA || g.fmt == QMM_Q8_0_SOA))
+            return QMM_ERR_FORMAT;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    for (int i = 0; i < nseg; ++i) {
+        const qmm_gemv_seg& g = segs[i];
+        int rc = QMM_ERR_FORMAT;
+        switch (g.fmt) {
+            case QMM_Q4_K: rc = launch_q8k<QMM_Q4_K>(g.w, x, g.y, g.N, g.K, ncol, s); break;
+            case QMM_Q5_K: rc = launch_q8k<QMM_Q5_K>(g.w, x, g.y, g.N, g.K, ncol, s); break;
+            case QMM_IQ4_XS: rc = launch_q8k<QMM_IQ4_XS>(g.w, x, g.y, g.N, g.K, ncol, s); break;
+            case QMM_Q6_K_SOA: rc = launch_q8k<QMM_Q6_K_SOA>(g.w, x, g.y, g.N, g.K, ncol, s); break;
+            case QMM_Q8_0_SOA: rc = launch_q8k<QMM_Q8_0_SOA>(g.w, x, g.y, g.N, g.K, ncol, s); break;
+        }
+        if (rc != QMM_OK) return rc;
+    }
+    return QMM_OK;
+}
+
+}  // extern "C"

@@ -146,12 +146,12 @@ constexpr size_t kGemmLds = 2 * (size_t)kStageElems * 2;     // bytes (147,456)
 // A tile loader: bf16 [M][K] row-major; thread t owns 16-byte column t%8 of rows t/8 + 32p
 struct ALoad {
     uint4 r[8];
-    __device__ __forceinline__ void load(const uint16_t* __restrict__ A, int M, int K, int m0, int k0) {
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ A, int M, int lda, int m0, int k0) {
         const int t = threadIdx.x;
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
             const int m = min(m0 + 32 * p + (t >> 3), M - 1);
-            r[p] = ld16(A + (size_t)m * K + k0 + 8 * (t & 7));
+            r[p] = ld16(A + (size_t)m * lda + k0 + 8 * (t & 7));
         }
     }
     __device__ __forceinline__ void store(__bf16* La) const {
@@ -164,9 +164,9 @@ struct ALoad {
 // W tile loader, bf16 [N][K]: thread t copies the 64 elements of row n0+t
 struct BLoadBf16 {
     uint4 r[8];
-    __device__ __forceinline__ void load(const uint16_t* __restrict__ W, int N, int K, int n0, int k0) {
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ W, int N, int ldw, int n0, int k0) {
         const int n = min(n0 + (int)threadIdx.x, N - 1);
-        const uint16_t* p = W + (size_t)n * K + k0;
+        const uint16_t* p = W + (size_t)n * ldw + k0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) r[i] = ld16(p + 8 * i);
     }
@@ -208,7 +208,7 @@ __device__ __forceinline__ void mfma_step(const __bf16* La, const __bf16* Lb, in
 // then step s+1's registers are written (A copied, W dequantised) into the other stage.
 template <class BL, class WT, bool OUT_BF16>
 __global__ void __launch_bounds__(256) k_gemm(const uint16_t* __restrict__ A, const WT* __restrict__ W, void* __restrict__ D,
-                                              int M, int N, int K) {
+                                              int M, int N, int K, int lda, int ldw) {
     extern __shared__ __align__(16) uint8_t smem_raw[];
     __bf16* const lds = (__bf16*)smem_raw;
     const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
@@ -219,8 +219,8 @@ __global__ void __launch_bounds__(256) k_gemm(const uint16_t* __restrict__ A, co
     const int nk = K / GBK;
     ALoad al;
     BL bl;
-    al.load(A, M, K, m0, 0);
-    bl.load(W, N, K, n0, 0);
+    al.load(A, M, lda, m0, 0);
+    bl.load(W, N, ldw, n0, 0);
     al.store(lds);
     bl.store(lds + GBM * GLD, 0);
     lds_barrier();
@@ -234,8 +234,8 @@ __global__ void __launch_bounds__(256) k_gemm(const uint16_t* __restrict__ A, co
         const __bf16* La = lds + (size_t)(s & 1) * kStageElems;
         const bool more = s + 1 < nk;
         if (more) {
-            al.load(A, M, K, m0, (s + 1) * GBK);
-            bl.load(W, N, K, n0, (s + 1) * GBK);
+            al.load(A, M, lda, m0, (s + 1) * GBK);
+            bl.load(W, N, ldw, n0, (s + 1) * GBK);
         }
         mfma_step(La, La + GBM * GLD, wm, wn, fr, fk, acc);
         if (more) {
@@ -324,20 +324,20 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // dequantised by two threads, one sub-block (32 weights) each.
 constexpr int kPPThreads = 512;
 
-__device__ __forceinline__ void dma_a_pp(const uint16_t* __restrict__ A, int M, int K, int m0, int k0, uint4* La) {
+__device__ __forceinline__ void dma_a_pp(const uint16_t* __restrict__ A, int M, int lda, int m0, int k0, uint4* La) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         // chunk slot p = (4w + i) * 64 + lane: row r = 32w + 8i + lane/8, slot column lane%8
         const int r = 32 * wave + 8 * i + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-        const uint32_t off = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K + (uint32_t)(k0 + 8 * c);
+        const uint32_t off = (uint32_t)min(m0 + r, M - 1) * (uint32_t)lda + (uint32_t)(k0 + 8 * c);
         __builtin_amdgcn_global_load_lds(A + off, La + (4 * wave + i) * 64, 16, 0, 0);
     }
 }
 
 struct WRawQ4KHalf {
     uint4 hd, q0, q1;
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int, int n0, int k0) {
         const int n = min(n0 + (int)(threadIdx.x >> 1), N - 1);
         const uint8_t* bp = W + (size_t)n * ((size_t)(K >> 8) * 144) + (size_t)(k0 >> 8) * 144;
         const int j = (k0 >> 6) & 3;
@@ -371,9 +371,9 @@ struct WRawQ4KHalf {
 // of the step, a step ahead
 struct WRawBf16Half {
     SubRaw r;                               // r.v[0..3]: the 64 bytes
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int, int ldw, int n0, int k0) {
         const int n = min(n0 + (int)(threadIdx.x >> 1), N - 1);
-        const uint16_t* p = (const uint16_t*)W + (size_t)n * K + k0 + 32 * (threadIdx.x & 1);
+        const uint16_t* p = (const uint16_t*)W + (size_t)n * ldw + k0 + 32 * (threadIdx.x & 1);
 #pragma unroll
         for (int c = 0; c < 4; ++c) r.v[c] = ld16(p + 8 * c);
     }
@@ -389,7 +389,7 @@ struct WRawBf16Half {
 template <int F>
 struct WRawFmtHalf {
     SubRaw r;
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int n0, int k0) {
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ W, int N, int K, int, int n0, int k0) {
         const int n = min(n0 + (int)(threadIdx.x >> 1), N - 1);
         sub_load<F>(W + (size_t)n * fmt_row_bytes_rt(F, K), K, (k0 >> 5) + (int)(threadIdx.x & 1), r);
     }
@@ -411,7 +411,8 @@ struct WRawFmtHalf {
 // out.  K % 128 == 0 (an even step count for the 3 x 2 stage unroll).
 template <class WR, bool OUT_BF16>
 __global__ void __launch_bounds__(kPPThreads) k_gemm_pp(const uint16_t* __restrict__ A, const uint8_t* __restrict__ W,
-                                                       void* __restrict__ Dv, int M, int N, int K, int ldd) {
+                                                       void* __restrict__ Dv, int M, int N, int K, int ldd, int lda,
+                                                       int ldw) {
     const int mt = (M + GBM - 1) / GBM, nt = (N + GBN - 1) / GBN;
     int tm, tn;
     tile_of(blockIdx.x, mt, nt, tm, tn);
@@ -419,11 +420,11 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_pp(const uint16_t* __restri
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave & 1, wn = wave >> 1;
     const int nk = K / GBK, lastk = (nk - 1) * GBK;
     WR wr;
-    wr.load(W, N, K, n0, 0);
-    dma_a_pp(A, M, K, m0, 0, ga<0>());
-    dma_a_pp(A, M, K, m0, min(GBK, lastk), ga<1>());
+    wr.load(W, N, K, ldw, n0, 0);
+    dma_a_pp(A, M, lda, m0, 0, ga<0>());
+    dma_a_pp(A, M, lda, m0, min(GBK, lastk), ga<1>());
     wr.store(gb<0>(), 0);
-    wr.load(W, N, K, n0, min(GBK, lastk));
+    wr.load(W, N, K, ldw, n0, min(GBK, lastk));
     __builtin_amdgcn_s_waitcnt(0);
     lds_barrier();
     f32x16 acc[4][2];
@@ -445,7 +446,7 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_pp(const uint16_t* __restri
         constexpr int SA = decltype(sa_c)::value, SB = decltype(sb_c)::value;
         const uint4* La = ga<SA>();
         const uint4* Lb = gb<SB>();
-        dma_a_pp(A, M, K, m0, min((s + 2) * GBK, lastk), ga<(SA + 2) % 3>());
+        dma_a_pp(A, M, lda, m0, min((s + 2) * GBK, lastk), ga<(SA + 2) % 3>());
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             bf16x8 af[4], bf[2];
@@ -459,7 +460,7 @@ __global__ void __launch_bounds__(kPPThreads) k_gemm_pp(const uint16_t* __restri
                 for (int jn = 0; jn < 2; ++jn) acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
         }
         wr.store(gb<1 - SB>(), min((s + 1) * GBK, lastk));
-        wr.load(W, N, K, n0, min((s + 2) * GBK, lastk));
+        wr.load(W, N, K, ldw, n0, min((s + 2) * GBK, lastk));
         // A tile s+1 (DMA'd a step ago, before W tile s+1's loads) has landed once at most this
         // step's 4 DMAs and 3 W loads are outstanding
         __builtin_amdgcn_s_waitcnt(0x0F77);   // vmcnt <= 7
@@ -514,7 +515,7 @@ int launch_gemm_q4k(const void* W, const uint16_t* A, float* D, int M, int N, in
     const int nb_cols = std::min(N, nbig * GBN);
     if (nbig > 0) {
         hipLaunchKernelGGL((k_gemm_pp<WRawQ4KHalf, false>), dim3(mt * nbig), dim3(kPPThreads), 0, s, A, (const uint8_t*)W, D, M,
-                           nb_cols, K, N);
+                           nb_cols, K, N, K, K);
         QMM_LAUNCH_CHECK();
     }
     if (nb_cols < N) {
@@ -599,7 +600,7 @@ int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int 
     if (fmt == QMM_Q4_K) return launch_gemm_q4k(W, A, D, M, N, K, s);
     const dim3 grid((unsigned)(((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN)));
 #define QMM_GWQ(F) case F: hipLaunchKernelGGL((k_gemm_pp<WRawFmtHalf<F>, false>), grid, dim3(kPPThreads), 0, s, A, (const uint8_t*)W, \
-                                              (void*)D, M, N, K, N); break;
+                                              (void*)D, M, N, K, N, K, K); break;
     switch (fmt) {
         QMM_GWQ(QMM_Q5_K) QMM_GWQ(QMM_IQ4_XS) QMM_GWQ(QMM_Q6_K_SOA) QMM_GWQ(QMM_Q8_0_SOA) QMM_GWQ(QMM_Q5_1_SOA)
     }
@@ -608,18 +609,26 @@ int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int 
     return QMM_OK;
 }
 
-int qmm_gemm_bf16(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, void* stream) {
+int qmm_gemm_bf16_ld(const uint16_t* A, int lda, const uint16_t* W, int ldw, uint16_t* D, int M, int N, int K, void* stream) {
     if (!A || !W || !D) return QMM_ERR_NULL;
-    if (M <= 0 || N <= 0 || K <= 0 || K % GBK != 0) return QMM_ERR_SHAPE;
+    if (M <= 0 || N <= 0 || K <= 0 || K % GBK != 0 || lda < K || ldw < K) return QMM_ERR_SHAPE;
+    // 16-byte row pieces: both operands' rows start 16-byte aligned
+    if (((uintptr_t)A | (uintptr_t)W) % 16 != 0 || lda % 8 != 0 || ldw % 8 != 0) return QMM_ERR_ARG;
+    // the DMA of A addresses rows with 32-bit element offsets
+    if ((uint64_t)(M - 1) * (uint64_t)lda + (uint64_t)K > 0xffffffffull) return QMM_ERR_SHAPE;
     const int grid = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
     if (K % (2 * GBK) == 0)     // the two-waves-per-SIMD kernel of the fused GEMM, bf16 rows as its W source
         hipLaunchKernelGGL((k_gemm_pp<WRawBf16Half, true>), dim3(grid), dim3(kPPThreads), 0, (hipStream_t)stream, A,
-                           (const uint8_t*)W, (void*)D, M, N, K, N);
+                           (const uint8_t*)W, (void*)D, M, N, K, N, lda, ldw);
     else
         hipLaunchKernelGGL((k_gemm<BLoadBf16, uint16_t, true>), dim3(grid), dim3(256), kGemmLds, (hipStream_t)stream, A, W,
-                           (void*)D, M, N, K);
+                           (void*)D, M, N, K, lda, ldw);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
+}
+
+int qmm_gemm_bf16(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, void* stream) {
+    return qmm_gemm_bf16_ld(A, K, W, K, D, M, N, K, stream);
 }
 
 int qmm_f32_to_bf16(const float* x, uint16_t* out, size_t n, void* stream) {

@@ -863,6 +863,16 @@ int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int n
     if (!fmt_supported_q8(fmt)) return QMM_ERR_FORMAT;
     if (!W || !x.q || !x.d || !x.s || !y) return QMM_ERR_NULL;
     if (int e = check_gemv_shape(fmt, N, K)) return e;
+    // rpt 4 is the reference's route to its T-invariant WMMA GEMV (gemv.hip:1472-1475, up to 16
+    // columns), which every GEMV here already is; rpt 5 and rpt 4 with tpr 3 read its experimental
+    // interleaved weight layouts (repack_interleave8 / repack_wmma_il), which this library does not
+    // read: QMM_ERR_LAYOUT
+    if (rpt == 5 || (rpt == 4 && tpr == 3)) return QMM_ERR_LAYOUT;
+    if (rpt == 4) {
+        if (ncol < 1 || ncol > 16) return QMM_ERR_SHAPE;
+        const qmm_gemv_seg seg = {fmt, W, y, N, K};
+        return qmm_gemv_multi(&seg, 1, x, ncol, stream);
+    }
     if (ncol < 1 || ncol > 8) return QMM_ERR_SHAPE;
     if (!(tpr == 0 || tpr == 1 || tpr == 2 || tpr == 4 || tpr == 8 || tpr == 16 || tpr == 32)) return QMM_ERR_ARG;
     if (rpt < 0 || rpt > 3) return QMM_ERR_ARG;

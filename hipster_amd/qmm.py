@@ -11,7 +11,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import GemvSeg, MoeSegs, MoeTile, QmmError, XQ8, check  # noqa: F401
+from ._lib import GemvSeg, MoeSegs, MoeTile, QmmError, XQ8, XQ8K, check  # noqa: F401
 
 WFmt = type("WFmt", (), {"Q4_K": _lib.QMM_Q4_K, "Q5_K": _lib.QMM_Q5_K, "IQ4_XS": _lib.QMM_IQ4_XS,
                          "Q6_K_SOA": _lib.QMM_Q6_K_SOA, "Q8_0_SOA": _lib.QMM_Q8_0_SOA,
@@ -51,6 +51,19 @@ class XQ8Buf:
         return XQ8(self.q.data_ptr(), self.d.data_ptr(), self.s.data_ptr(), 0 if self.ds is None else self.ds.data_ptr())
 
 
+class XQ8KBuf:
+    """Device buffers of XQ8K (gemv.h:33): q [ncol][K] int8, d [K/256][16] f32, bs [K/256][16][8] int16."""
+
+    def __init__(self, ncol, K, device="cuda"):
+        self.ncol, self.K = ncol, K
+        self.q = torch.zeros((ncol, K), dtype=torch.int8, device=device)
+        self.d = torch.zeros((K // 256, 16), dtype=torch.float32, device=device)
+        self.bs = torch.zeros((K // 256, 16, 8), dtype=torch.int16, device=device)
+
+    def c(self):
+        return XQ8K(self.q.data_ptr(), self.d.data_ptr(), self.bs.data_ptr())
+
+
 def wfmt_row_bytes(fmt, K):
     return _lib.lib().qmm_wfmt_row_bytes(fmt, K)
 
@@ -85,6 +98,28 @@ def repack_row_q5_1(src, K):
 def repack_row_q5_0(src, K):
     """Host repack of one GGUF Q5_0 row to the Q5_1_SOA layout, m = -16 d (gemv.h:18, gemv.hip:1448-1457)."""
     return _repack("repack_row_q5_0", src, K, K // 32 * 24)
+
+
+def repack_interleave8(fmt, src, N, K):
+    """Host 8-row block interleave of a whole matrix (gemv.h:21, gemv.hip:1442-1447)."""
+    import numpy as np
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.empty_like(src)
+    check(_lib.lib().qmm_repack_interleave8(fmt, src.ctypes.data, dst.ctypes.data, N, K), "repack_interleave8")
+    return dst
+
+
+def wmma_il_bytes(fmt, N, K):
+    return _lib.lib().qmm_wmma_il_bytes(fmt, N, K)
+
+
+def repack_wmma_il(fmt, src, N, K):
+    """Host 16-row piece-major layout of a whole matrix (gemv.h:37-38, gemv.hip:1280-1303)."""
+    import numpy as np
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.empty(wmma_il_bytes(fmt, N, K), dtype=np.uint8)
+    check(_lib.lib().qmm_repack_wmma_il(fmt, src.ctypes.data, dst.ctypes.data, N, K), "repack_wmma_il")
+    return dst
 
 
 def quantize_x_q8(x, out, ncol, K, stream=None):
@@ -122,6 +157,30 @@ def gemv_wmma(segs, x, ncol, mode=0, stream=None):
     """gemv.h:36: the reference's T-invariant matrix-core GEMV; here the (T-invariant) multi GEMV,
     mode accepted and ignored."""
     gemv_multi(segs, x, ncol, stream)
+
+
+def gemv_splitk(fmt, W, x, part, N, K, ksplit, ncol, stream=None):
+    """gemv.h:55: part[(c*ksplit + ks)][N] = W . x over the ks-th range of 256-weight blocks."""
+    _dev(W, torch.uint8, "W"); _dev(part, torch.float32, "part")
+    check(_lib.lib().qmm_gemv_splitk(fmt, _p(W), x.c(), _p(part), N, K, ksplit, ncol, _stream(stream)), "gemv_splitk")
+
+
+def hc_up_fused(W, part, ksplit, y, N, T, stream=None):
+    """gemv.h:52: y[t] = W (Q8_0_SOA [N][320]) . q8(silu(sum_k part[t][k] / 4))."""
+    _dev(W, torch.uint8, "W"); _dev(part, torch.float32, "part"); _dev(y, torch.float32, "y")
+    check(_lib.lib().qmm_hc_up_fused(_p(W), _p(part), ksplit, _p(y), N, T, _stream(stream)), "hc_up_fused")
+
+
+def quantize_x_q8k(x, out, ncol, K, stream=None):
+    """gemv.h:34: x f32 [ncol][K] -> out (XQ8KBuf): one scale per 256, int16 sums per 32."""
+    _dev(x, torch.float32, "x")
+    check(_lib.lib().qmm_quantize_x_q8k(_p(x), out.c(), ncol, K, _stream(stream)), "quantize_x_q8k")
+
+
+def gemv_wmma_q8k(segs, x, ncol, ks_mode=0, stream=None):
+    """gemv.h:35: segs = [(fmt, W, y, N, K), ...] on Q8_K activations (x an XQ8KBuf); ks_mode accepted."""
+    arr = _segs(segs)
+    check(_lib.lib().qmm_gemv_q8k(arr, len(segs), x.c(), ncol, _stream(stream)), "gemv_wmma_q8k")
 
 
 def gemv_q8_f32x(fmt, W, x, y, N, K, ncol, stream=None):
@@ -237,6 +296,11 @@ def gemm_bf16(A, W, D, M, N, K, stream=None):
     check(_lib.lib().qmm_gemm_bf16(_p(A), _p(W), _p(D), M, N, K, _stream(stream)), "gemm_bf16")
 
 
+def gemm_bf16_ld(A, lda, W, ldw, D, M, N, K, stream=None):
+    """BlasLt::gemm_ld (gemm.h:29): as gemm_bf16 with row strides lda / ldw (elements); A and W may be views."""
+    check(_lib.lib().qmm_gemm_bf16_ld(_p(A), lda, _p(W), ldw, _p(D), M, N, K, _stream(stream)), "gemm_bf16_ld")
+
+
 def f32_to_bf16(x, out, n, stream=None):
     check(_lib.lib().qmm_f32_to_bf16(_p(x), _p(out), n, _stream(stream)), "f32_to_bf16")
 
@@ -283,3 +347,10 @@ def moe_gemm_gate_up_bf16(fmt, shared_fmt, Wg, Wgsh, Wu, Wush, ebytes, tiles, co
 
 def moe_silu_bf16(gate, up, h, n, stream=None):
     check(_lib.lib().qmm_moe_silu_bf16(_p(gate), _p(up), _p(h), n, _stream(stream)), "moe_silu_bf16")
+
+
+def moe_gemm(fmt, shared_fmt, W, Wsh, ebytes, tiles, ntiles, stiles, nstiles, ct, rowtab, x, y, N, K, stream=None):
+    """moe_gemm (gemv.h:49-50) with the reference's signature: q8 activations (x an XQ8Buf), routed tiles
+    tiles[:ntiles] and shared tiles stiles[:nstiles] with host counts; y[k][N] f32, the q8 arithmetic."""
+    check(_lib.lib().qmm_moe_gemm_q8(fmt, shared_fmt, _p(W), _p(Wsh), ebytes, _p(tiles), ntiles, _p(stiles), nstiles, ct,
+                                     _p(rowtab), x.c(), _p(y), N, K, _stream(stream)), "moe_gemm")

@@ -3,8 +3,8 @@
  *
  * This is the drop-in boundary for the dzannotti/hipster engine's quantized matmul path.  Every
  * entry point is the `extern "C"` twin of a reference function (cited per declaration as
- * file:line in the reference repo); a header-only C++ shim (hipster_amd/csrc/shim/) restores the
- * reference's `namespace hip` names and signatures on top of it, so the engine's callers compile
+ * file:line in the reference repo); a header-only C++ shim (include/hipster_qmm_shim.hpp) restores
+ * the reference's `namespace hip` names and signatures on top of it, so the engine's callers compile
  * unchanged.
  *
  * Conventions (same as the reference unless stated):
@@ -34,19 +34,32 @@ enum {
     QMM_ERR_NULL = -3,      /* a required pointer is NULL */
     QMM_ERR_LAUNCH = -4,    /* the HIP runtime rejected the launch */
     QMM_ERR_WORKSPACE = -5, /* workspace missing or too small */
-    QMM_ERR_ARG = -6        /* other invalid argument (mode, tpr, ...) */
+    QMM_ERR_ARG = -6,       /* other invalid argument (mode, tpr, alignment, ...) */
+    QMM_ERR_LAYOUT = -7,    /* a weight layout this library does not read (the reference's experimental
+                               interleaved layouts) */
+    QMM_ERR_IO = -8,        /* a GGUF file is missing, truncated, not GGUF v3 or has a tensor past its end */
+    QMM_ERR_NOT_FOUND = -9  /* no tensor / key of that name in the GGUF */
 };
 
 /* ---- weight formats: values of the reference's `enum class WFmt` (engine/kernels/gemv.h:13),
  * plus QMM_Q6_K, the GGUF-native 210-byte Q6_K block read without a repack (this build). ---- */
 enum {
-    QMM_Q4_K = 0,      /* GGUF block_q4_K, 144 B / 256 weights (engine/src/quant.h:22) */
-    QMM_Q5_K = 1,      /* GGUF block_q5_K, 176 B / 256 weights (quant.h:23); GEMV only */
-    QMM_IQ4_XS = 2,    /* GGUF block_iq4_xs, 136 B / 256 weights (quant.h:30); GEMV only */
-    QMM_Q6_K_SOA = 3,  /* Q6_K rows repacked [ql K/2][qh K/4][sc K/16][d K/128] (gemv.h:15) */
-    QMM_Q8_0_SOA = 4,  /* Q8_0 rows repacked [qs K][d K/32 x f16] (gemv.h:16); GEMV only */
-    QMM_Q5_1_SOA = 5,  /* Q5_1 / Q5_0 rows repacked [qs K/2][qh K/8][d K/32][m K/32] (gemv.h:17-18); GEMV only */
-    QMM_Q6_K = 6       /* GGUF block_q6_K, 210 B / 256 weights (quant.h:24) */
+    QMM_Q4_K = 0,      /* GGUF block_q4_K, 144 B / 256 weights (engine/src/quant.h:22).  Every entry point;
+                          K granule 256 */
+    QMM_Q5_K = 1,      /* GGUF block_q5_K, 176 B / 256 weights (quant.h:23).  GEMVs (q8, multi, splitk, q8k),
+                          gemv_moe, dequant_bf16, gemm_wq, moe_gemm_bf16, moe_gemm_q8; K granule 256 */
+    QMM_IQ4_XS = 2,    /* GGUF block_iq4_xs, 136 B / 256 weights (quant.h:30).  The same entry points as
+                          QMM_Q5_K; K granule 256 */
+    QMM_Q6_K_SOA = 3,  /* Q6_K rows repacked [ql K/2][qh K/4][sc K/16][d K/128] (gemv.h:15).  GEMVs (q8,
+                          multi; splitk and q8k with K % 512), dequant_bf16, gemm_wq (K % 512); K granule 256 */
+    QMM_Q8_0_SOA = 4,  /* Q8_0 rows repacked [qs K][d K/32 x f16] (gemv.h:16).  GEMVs (q8, multi, splitk; q8k
+                          with K % 256), hc_up_fused, gemv_moe (routed or shared), dequant_bf16, gemm_wq
+                          (K % 128), moe_gemm_bf16, moe_gemm_q8; K granule 64 */
+    QMM_Q5_1_SOA = 5,  /* Q5_1 / Q5_0 rows repacked [qs K/2][qh K/8][d K/32][m K/32] (gemv.h:17-18).  GEMVs (q8,
+                          multi, splitk), gemv_moe, dequant_bf16, gemm_wq (K % 128), moe_gemm_bf16, moe_gemm_q8;
+                          K granule 32 */
+    QMM_Q6_K = 6       /* GGUF block_q6_K, 210 B / 256 weights (quant.h:24).  GEMVs (q8, multi) and
+                          dequant_bf16; K granule 256 */
 };
 
 /* ---- POD structs, byte-compatible with the reference's (gemv.h:8,27,43,48) ---- */
@@ -59,6 +72,59 @@ typedef struct { int32_t fmt; const void* w; float* y; int32_t N, K; } qmm_gemv_
 typedef struct { const void* w[2]; const void* shared[2]; float* y[2]; size_t ebytes; const float* slotw; } qmm_moe_segs;
 /* a tile of <= 16*ct expert-sorted columns (reference: MoeTile, gemv.h:48) */
 typedef struct { int32_t expert, k0, ncols; } qmm_moe_tile;
+/* x quantised per 256 ("Q8_K"): q [ncol][K] int8, d [K/256][16] f32, bs [K/256][16][8] int16 sums of the q
+ * of each 32 (reference: XQ8K, gemv.h:33) */
+typedef struct { int8_t* q; float* d; int16_t* bs; } qmm_xq8k;
+
+/* ---- GGUF (the on-disk format of the weights; reference: engine/src/gguf.h, gguf.cpp) ---- */
+/* ggml tensor types (the reference's GType numbering, gguf.h:12-17) */
+enum {
+    QMM_GGML_F32 = 0, QMM_GGML_F16 = 1, QMM_GGML_Q4_0 = 2, QMM_GGML_Q4_1 = 3, QMM_GGML_Q5_0 = 6, QMM_GGML_Q5_1 = 7,
+    QMM_GGML_Q8_0 = 8, QMM_GGML_Q8_1 = 9, QMM_GGML_Q2_K = 10, QMM_GGML_Q3_K = 11, QMM_GGML_Q4_K = 12, QMM_GGML_Q5_K = 13,
+    QMM_GGML_Q6_K = 14, QMM_GGML_Q8_K = 15, QMM_GGML_IQ4_NL = 20, QMM_GGML_IQ3_S = 21, QMM_GGML_IQ4_XS = 23,
+    QMM_GGML_I8 = 24, QMM_GGML_I32 = 26, QMM_GGML_BF16 = 30
+};
+/* kinds of KV values (the reference's GValue kinds, gguf.h:37-41: every integer width collapses to one
+ * signed and one unsigned kind, f32/f64 to FLOAT) */
+enum { QMM_GGUF_KV_UINT = 0, QMM_GGUF_KV_INT = 1, QMM_GGUF_KV_FLOAT = 2, QMM_GGUF_KV_BOOL = 3, QMM_GGUF_KV_STRING = 4,
+       QMM_GGUF_KV_ARRAY = 5 };
+/* an opened model (one file, or every shard of a split) */
+typedef struct qmm_gguf qmm_gguf;
+/* one tensor (reference: GTensor, gguf.h:26-35): ne[0] is the contiguous (K) dimension; data points into
+ * the read-only mapping of shard `shard`, at file offset file_off; name valid until qmm_gguf_close */
+typedef struct {
+    const char* name; int32_t type; uint32_t n_dims; uint64_t ne[4]; size_t nbytes; const uint8_t* data;
+    int32_t shard; uint64_t file_off;
+} qmm_gguf_tensor;
+/* (elements, bytes) per block of a ggml type (reference: gtype_block, gguf.h:20, gguf.cpp:26-42) */
+int qmm_gtype_block(int type, uint32_t* block_elems, uint32_t* block_bytes);
+/* open a GGUF v3 file and map it read-only; a path <base>-0000i-of-0000N.gguf opens all N shards and joins
+ * their tensor tables (reference: GGUF::GGUF / open_one, gguf.cpp:71-129); KV keys of later shards replace
+ * earlier ones except split.*; data starts at the next multiple of general.alignment (default 32) */
+int qmm_gguf_open(const char* path, qmm_gguf** out);
+void qmm_gguf_close(qmm_gguf* g);
+int64_t qmm_gguf_n_tensors(const qmm_gguf* g);
+size_t qmm_gguf_mapped_bytes(const qmm_gguf* g);
+int qmm_gguf_tensor_at(const qmm_gguf* g, int64_t i, qmm_gguf_tensor* out);
+/* tensor by name (reference: GGUF::find / get, gguf.cpp:131-137); QMM_ERR_NOT_FOUND when absent */
+int qmm_gguf_find(const qmm_gguf* g, const char* name, qmm_gguf_tensor* out);
+/* KV lookups (reference: kv, kv_u32, kv_f32, kv_str, gguf.cpp:138-143); the string stays valid until close */
+int qmm_gguf_kv_kind(const qmm_gguf* g, const char* key, int* kind);
+int qmm_gguf_kv_u32(const qmm_gguf* g, const char* key, uint32_t* out);
+int qmm_gguf_kv_f32(const qmm_gguf* g, const char* key, float* out);
+int qmm_gguf_kv_str(const qmm_gguf* g, const char* key, const char** out);
+int qmm_gguf_kv_array_len(const qmm_gguf* g, const char* key, uint64_t* out);
+/* copy a tensor's bytes into a host buffer with pread, then drop them from the page cache (reference:
+ * GGUF::read_tensor, gguf.cpp:148-156) */
+int qmm_gguf_read_tensor(const qmm_gguf* g, const char* name, void* dst, size_t dst_bytes);
+/* the layout the kernels read for a GGUF weight type, and its row bytes (reference: to_lin,
+ * qwen4exp.cpp:34-65): Q4_K, Q5_K, IQ4_XS as stored; Q6_K -> QMM_Q6_K_SOA; Q8_0 -> QMM_Q8_0_SOA;
+ * Q5_1 and Q5_0 -> QMM_Q5_1_SOA; F32, F16, BF16 -> QMM_Q8_0_SOA (requantised); others QMM_ERR_FORMAT */
+int qmm_weight_format(int gtype, int K, int* wfmt, size_t* row_bytes);
+/* N rows of K weights of GGUF type gtype -> that layout in dst (N * row_bytes bytes): a copy, the row
+ * repacks above, or for F32/F16/BF16 the reference's quantize_row_q8_0_soa (quant.h:174-183: d =
+ * f16(amax/127) with quant.h's own f32->f16 rounding, q = rint(x/d)); rows split over nthreads host threads */
+int qmm_prepare_weight(int gtype, const uint8_t* src, int N, int K, uint8_t* dst, int nthreads);
 
 /* ---- library / host helpers ---- */
 const char* qmm_version(void);
@@ -77,6 +143,18 @@ int qmm_repack_row_q5_1(const uint8_t* src, uint8_t* dst, int K);
 /* one GGUF Q5_0 row (22 B / 32) -> QMM_Q5_1_SOA (K*24/32 bytes) with m = f16(-16 d), exact
  * (reference: repack_row_q5_0, gemv.h:18, gemv.hip:1448-1457); K % 32 == 0 */
 int qmm_repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K);
+/* the reference's experimental 8-row block interleave (reference: repack_interleave8, gemv.h:21,
+ * gemv.hip:1442-1447): block b of row r moves to ((r/8)*8*nb + b*8 + r%8) blocks; fmt Q4_K, Q5_K or
+ * IQ4_XS, N % 8 == 0, K % 256 == 0.  Host only; the GEMVs here do not read this layout
+ * (qmm_gemv_q8 with rpt 5 returns QMM_ERR_LAYOUT). */
+int qmm_repack_interleave8(int fmt, const uint8_t* src, uint8_t* dst, int N, int K);
+/* bytes of the reference's 16-row chunk-major layout (reference: wmma_il_bytes, gemv.h:37,
+ * gemv.hip:1280): ceil(N/16) * (K/256) * 16 * block bytes (Q4_K 144, Q5_K 176, IQ4_XS 136, Q6_K_SOA 210,
+ * Q8_0_SOA 272); 0 for other formats or K % 256 != 0 */
+size_t qmm_wmma_il_bytes(int fmt, int N, int K);
+/* that layout (reference: repack_wmma_il, gemv.h:38, gemv.hip:1281-1303), byte for byte; host only
+ * (qmm_gemv_q8 with rpt 4, tpr 3 returns QMM_ERR_LAYOUT) */
+int qmm_repack_wmma_il(int fmt, const uint8_t* src, uint8_t* dst, int N, int K);
 
 /* ---- activation quantiser (reference: quantize_x_q8, gemv.h:10, gemv.hip:36-51,1333-1336) ----
  * per 32 values: d = amax/127, q = round-half-even(x*127/amax), s = d*sum(q); x f32 [ncol][K]. */
@@ -93,6 +171,22 @@ int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int n
  * segments, all with the same K, any ncol (8 columns per pass).  Results are bitwise those of
  * qmm_gemv_q8 on each segment. */
 int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void* stream);
+/* split-K GEMV for skinny weights (reference: gemv_splitk, gemv.h:55, gemv.hip:1397-1441):
+ * part[(c*ksplit + ks)*N + n] = W[n][K range ks] . x[c][K range ks], the K range of split ks being the
+ * 256-weight blocks [ks*nb/ksplit, (ks+1)*nb/ksplit), nb = ceil(K/256), as the reference's; the consumer
+ * sums the partials in a fixed order.  fmt: Q4_K, Q5_K, IQ4_XS, Q6_K_SOA (K % 512), Q8_0_SOA (K % 64),
+ * Q5_1_SOA (K % 32); 1 <= ksplit <= nb; any ncol (8 per launch). */
+int qmm_gemv_splitk(int fmt, const void* W, qmm_xq8 x, float* part, int N, int K, int ksplit, int ncol, void* stream);
+/* the hyper-connection up-projection with its prologue (reference: hc_up_fused, gemv.h:52,
+ * gemv.hip:976-1005): per t < T, x = silu(sum_k part[(t*ksplit + k)*320 + i] / 4) (k in order), quantised
+ * per 32, then y[t*N + n] = W[n] . x with W Q8_0_SOA [N][320]. */
+int qmm_hc_up_fused(const void* W, const float* part, int ksplit, float* y, int N, int T, void* stream);
+/* x -> Q8_K (reference: quantize_x_q8k, gemv.h:34, gemv.hip:686-705): per 256, d = amax/127,
+ * q = round-half-even(x*127/amax) (0 when amax == 0), bs = sum of each 32 q; ncol <= 16, K % 256 == 0 */
+int qmm_quantize_x_q8k(const float* x, qmm_xq8k out, int ncol, int K, void* stream);
+/* GEMV on Q8_K activations (reference: gemv_wmma_q8k, gemv.h:35, gemv.hip:706-794,1259-1271): y[c][n] for each
+ * segment, c < ncol <= 16; fmt Q4_K, Q5_K, IQ4_XS, Q6_K_SOA (K % 512), Q8_0_SOA; K % 256 == 0, equal K. */
+int qmm_gemv_q8k(const qmm_gemv_seg* segs, int nseg, qmm_xq8k x, int ncol, void* stream);
 /* qmm_quantize_x_q8 followed by qmm_gemv_q8, in one launch and bit for bit the same y: x is f32
  * [ncol][K], quantised to q8 per 32 inside the GEMV (no q8 buffer).  No reference counterpart (the
  * reference quantises in the producing kernel, e.g. add_rmsnorm_quant, ops.hip:79-98).
@@ -163,6 +257,10 @@ int qmm_gemm_wq(int fmt, const void* W, const uint16_t* A, float* D, int M, int 
  * gemm.h:27, gemm.hip:125-160; here an own MFMA kernel, no hipBLASLt: the fused GEMM's kernel with bf16
  * rows as its weight source when K % 128 == 0).  K % 64 == 0. */
 int qmm_gemm_bf16(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, void* stream);
+/* the same with row strides (elements) for A and W (reference: BlasLt::gemm_ld, gemm.h:29,
+ * gemm.hip:125-160; the split-K halves of qwen35.cpp:230-231): A[m][k] at A[m*lda + k], W[n][k] at
+ * W[n*ldw + k]; D [M][N] dense.  lda, ldw >= K and multiples of 8, A and W 16-byte aligned. */
+int qmm_gemm_bf16_ld(const uint16_t* A, int lda, const uint16_t* W, int ldw, uint16_t* D, int M, int N, int K, void* stream);
 /* bf16 helpers (reference: gemm.h:14-20, gemm.hip:77-95) */
 int qmm_f32_to_bf16(const float* x, uint16_t* out, size_t n, void* stream);
 int qmm_bf16_to_f32(const uint16_t* x, float* out, size_t n, void* stream);
@@ -196,6 +294,16 @@ int qmm_moe_gemm_bf16(int fmt, int shared_fmt, const void* W, const void* Wsh, s
 int qmm_moe_gemm_gate_up_bf16(int fmt, int shared_fmt, const void* Wg, const void* Wgsh, const void* Wu, const void* Wush,
                               size_t ebytes, const qmm_moe_tile* tiles, const int* counts, int max_tiles, const int* rowtab,
                               const uint16_t* A, uint16_t* H, int N, int K, void* stream);
+/* Grouped expert GEMM with the reference's own signature and q8 activations (reference: moe_gemm,
+ * gemv.h:49-50, gemv.hip:909-969,1377-1381; called at qwen4exp.cpp:647-650): routed tiles tiles[0..ntiles)
+ * in format fmt (W + expert*ebytes) and shared-expert tiles stiles[0..nstiles) in shared_fmt (Wsh), tile
+ * counts from the host; for every tile column r < ncols, y[(k0 + r)*N + n] = W_e[n] . x[row] with row =
+ * rowtab[k0 + r] (or k0 + r when rowtab is NULL): the reference's q8 arithmetic per row (integer dot per
+ * sub-block, f32 fix-up), not bf16.  ct (the reference's 16-column tiles per block, >= 1) is accepted and
+ * not needed: tiles of any width work.  fmt / shared_fmt: Q4_K, Q5_K, IQ4_XS, Q8_0_SOA, Q5_1_SOA. */
+int qmm_moe_gemm_q8(int fmt, int shared_fmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles, int ntiles,
+                    const qmm_moe_tile* stiles, int nstiles, int ct, const int* rowtab, qmm_xq8 x, float* y, int N, int K,
+                    void* stream);
 /* h = bf16(silu(gate) * up), n elements (the bf16-path counterpart of fn::moe_silu_quant, fn.hip:206-211) */
 int qmm_moe_silu_bf16(const float* gate, const float* up, uint16_t* h, size_t n, void* stream);
 

@@ -7,7 +7,12 @@
 //  - errors (unsupported format, bad shape, launch failure) throw std::runtime_error carrying the
 //    library's status string, where the reference calls abort() or misbehaves silently;
 //  - gemv_wmma / gemv_wmma_ok map onto the library's T-invariant GEMV (any ncol gives every column
-//    the same reduction order), so `mode` is accepted and ignored;
+//    the same reduction order), so `mode` is accepted and ignored, except mode 3 (the experimental
+//    16-row interleaved layout), which this library does not read: it throws;
+//  - the experiment knobs g_persist_blocks, g_moe_tpr and g_moe_fake exist and are ignored (launch
+//    shapes here depend on the tensor shape only);
+//  - moe_gemm keeps its signature and q8 arithmetic on VALU kernels; the engine's fast prefill path
+//    is moe_sort + moe_gemm_gate_up_bf16 + moe_gemm_bf16 (bf16 MFMA);
 //  - BlasLt::gemm runs the library's own bf16 MFMA GEMM (no hipBLASLt, no autotune, no workspace);
 //  - fn::moe_combine_sorted takes the row width from the hidden size E of the caller's model: the
 //    reference fixes E = 2560 at compile time; here it is the template argument (default 2560).
@@ -30,13 +35,18 @@ inline void ck(int status, const char* what) {
 }  // namespace detail
 
 // ---- gemv.h -------------------------------------------------------------------------------
+inline int g_persist_blocks = 0;   // gemv.h:6 (accepted, not used)
+inline int g_moe_tpr = 0;          // gemv.h:53 (accepted, not used)
+inline int g_moe_fake = 0;         // gemv.h:54 (accepted, not used)
 struct XQ8 { int8_t* q; float* d; float* s; float2* ds = nullptr; };                         // gemv.h:8
+struct XQ8K { int8_t* q; float* d; int16_t* bs; };                                            // gemv.h:33
 enum class WFmt { Q4_K, Q5_K, IQ4_XS, Q6_K_SOA, Q8_0_SOA, Q5_1_SOA };                           // gemv.h:13
 struct GemvSeg { WFmt fmt; const void* w; float* y; int N, K; };                                 // gemv.h:27
 struct MoeSegs { const void* w[2]; const void* shared[2]; float* y[2]; size_t ebytes; const float* slotw = nullptr; };  // gemv.h:43
 struct MoeTile { int expert, k0, ncols; };                                                      // gemv.h:48
 
 inline qmm_xq8 to_c(const XQ8& x) { return qmm_xq8{x.q, x.d, x.s, (void*)x.ds}; }
+inline qmm_xq8k to_c(const XQ8K& x) { return qmm_xq8k{x.q, x.d, x.bs}; }
 
 inline void quantize_x_q8(const float* x, XQ8 out, int ncol, int K, hipStream_t s) {
     detail::ck(qmm_quantize_x_q8(x, to_c(out), ncol, K, (void*)s), "quantize_x_q8");
@@ -54,6 +64,13 @@ inline void repack_row_q5_1(const uint8_t* src, uint8_t* dst, int K) {          
 inline void repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K) {                       // gemv.h:18
     detail::ck(qmm_repack_row_q5_0(src, dst, K), "repack_row_q5_0");
 }
+inline void repack_interleave8(WFmt f, const uint8_t* src, uint8_t* dst, int N, int K) {           // gemv.h:21
+    detail::ck(qmm_repack_interleave8((int)f, src, dst, N, K), "repack_interleave8");
+}
+inline size_t wmma_il_bytes(WFmt f, int N, int K) { return qmm_wmma_il_bytes((int)f, N, K); }       // gemv.h:37
+inline void repack_wmma_il(WFmt f, const uint8_t* src, uint8_t* dst, int N, int K) {               // gemv.h:38
+    detail::ck(qmm_repack_wmma_il((int)f, src, dst, N, K), "repack_wmma_il");
+}
 inline void gemv_q8(WFmt f, const void* W, XQ8 x, float* y, int N, int K, int ncol, int tpr, int rpt, hipStream_t s) {
     detail::ck(qmm_gemv_q8((int)f, W, to_c(x), y, N, K, ncol, tpr, rpt, (void*)s), "gemv_q8");
 }
@@ -63,14 +80,36 @@ inline void gemv_multi(const GemvSeg* segs, int nseg, XQ8 x, int ncol, hipStream
     for (int i = 0; i < nseg; ++i) c[i] = qmm_gemv_seg{(int32_t)segs[i].fmt, segs[i].w, segs[i].y, segs[i].N, segs[i].K};
     detail::ck(qmm_gemv_multi(c, nseg, to_c(x), ncol, (void*)s), "gemv_multi");
 }
+// gemv.hip:1272-1275: every format but Q5_1_SOA, K % 256 == 0, one K
 inline bool gemv_wmma_ok(const GemvSeg* segs, int nseg) {
     if (nseg < 1 || nseg > 4) return false;
     for (int i = 0; i < nseg; ++i)
-        if ((segs[i].fmt != WFmt::Q4_K && segs[i].fmt != WFmt::Q6_K_SOA) || segs[i].K % 256 != 0) return false;
+        if (segs[i].fmt == WFmt::Q5_1_SOA || segs[i].K % 256 != 0 || segs[i].K != segs[0].K) return false;
     return true;
 }
-inline void gemv_wmma(const GemvSeg* segs, int nseg, XQ8 x, int ncol, int /*mode*/, hipStream_t s) {
+inline void gemv_wmma(const GemvSeg* segs, int nseg, XQ8 x, int ncol, int mode, hipStream_t s) {    // gemv.h:36
+    if (mode == 3) detail::ck(QMM_ERR_LAYOUT, "gemv_wmma");
     gemv_multi(segs, nseg, x, ncol, s);
+}
+inline void quantize_x_q8k(const float* x, XQ8K out, int ncol, int K, hipStream_t s) {                // gemv.h:34
+    detail::ck(qmm_quantize_x_q8k(x, to_c(out), ncol, K, (void*)s), "quantize_x_q8k");
+}
+inline void gemv_wmma_q8k(const GemvSeg* segs, int nseg, XQ8K x, int ncol, int /*ks_mode*/, hipStream_t s) {   // gemv.h:35
+    if (nseg < 1) detail::ck(QMM_ERR_SHAPE, "gemv_wmma_q8k");
+    for (int i0 = 0; i0 < nseg; i0 += 4) {
+        qmm_gemv_seg c[4];
+        const int n = nseg - i0 < 4 ? nseg - i0 : 4;
+        for (int i = 0; i < n; ++i) c[i] = qmm_gemv_seg{(int32_t)segs[i0 + i].fmt, segs[i0 + i].w, segs[i0 + i].y, segs[i0 + i].N, segs[i0 + i].K};
+        detail::ck(qmm_gemv_q8k(c, n, to_c(x), ncol, (void*)s), "gemv_wmma_q8k");
+    }
+}
+// split-K partials part[(c*ksplit + ks)][N] (gemv.h:55)
+inline void gemv_splitk(WFmt f, const void* W, XQ8 x, float* part, int N, int K, int ksplit, int ncol, hipStream_t s) {
+    detail::ck(qmm_gemv_splitk((int)f, W, to_c(x), part, N, K, ksplit, ncol, (void*)s), "gemv_splitk");
+}
+// hyper-connection up-projection with the silu + q8 prologue (gemv.h:52)
+inline void hc_up_fused(const void* W, const float* part, int ksplit, float* y, int N, int T, hipStream_t s) {
+    detail::ck(qmm_hc_up_fused(W, part, ksplit, y, N, T, (void*)s), "hc_up_fused");
 }
 inline void gemv_moe(WFmt f, WFmt fs, const MoeSegs& a, int nseg, const int* ids, int nexp, XQ8 x, int N, int K, int T,
                      bool xrow_te, hipStream_t s) {
@@ -82,6 +121,15 @@ inline void gemv_moe(WFmt f, WFmt fs, const MoeSegs& a, int nseg, const int* ids
 }
 inline void gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int ncol, int tpr, hipStream_t s) {
     detail::ck(qmm_gemv_q4_K_f32(W, x, y, N, K, ncol, tpr, (void*)s), "gemv_q4_K_f32");
+}
+// grouped expert GEMM with the reference's signature and q8 activations (gemv.h:49-50): routed tiles
+// then shared-expert tiles, counts from the host, y[k][N] f32
+inline void moe_gemm(WFmt f, WFmt fs, const void* W, const void* Wsh, size_t ebytes, const MoeTile* tiles, int ntiles,
+                     const MoeTile* stiles, int nstiles, int ct, const int* rowtab, XQ8 x, float* y, int N, int K, hipStream_t s) {
+    static_assert(sizeof(MoeTile) == sizeof(qmm_moe_tile), "MoeTile layout");
+    detail::ck(qmm_moe_gemm_q8((int)f, (int)fs, W, Wsh, ebytes, reinterpret_cast<const qmm_moe_tile*>(tiles), ntiles,
+                               reinterpret_cast<const qmm_moe_tile*>(stiles), nstiles, ct, rowtab, to_c(x), y, N, K, (void*)s),
+               "moe_gemm");
 }
 
 // ---- gemm.h -------------------------------------------------------------------------------
@@ -105,6 +153,10 @@ public:
     // D[M][N] bf16 = A[M][K] bf16 . W[N][K]^T bf16, f32 accumulate (gemm.h:27)
     void gemm(const uint16_t* A, const uint16_t* W, uint16_t* D, int M, int N, int K, hipStream_t s) {
         detail::ck(qmm_gemm_bf16(A, W, D, M, N, K, (void*)s), "BlasLt::gemm");
+    }
+    // the same with row strides lda / ldw in elements: split-K over column halves (gemm.h:29)
+    void gemm_ld(const uint16_t* A, int lda, const uint16_t* W, int ldw, uint16_t* D, int M, int N, int K, hipStream_t s) {
+        detail::ck(qmm_gemm_bf16_ld(A, lda, W, ldw, D, M, N, K, (void*)s), "BlasLt::gemm_ld");
     }
     // D[M][N] f32 = A[M][K] f32 . W[N][K]^T f32: the prefill router (gemm.h:31)
     void gemm_f32(const float* A, const float* W, float* D, int M, int N, int K, hipStream_t s) {

@@ -14,12 +14,14 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(_HERE, "liboracle.so")
 REF_LIB = os.path.join(_HERE, "_ref", "libqmm_ref.so")
 REF_GEMV_LIB = os.path.join(_HERE, "_ref", "libqmm_ref_gemv.so")
+REF_GGUF_LIB = os.path.join(_HERE, "_ref", "libgguf_ref.so")
 
 Q4_K, Q5_K, IQ4_XS, Q6_K_SOA, Q8_0_SOA, Q5_1_SOA, Q6_K = 0, 1, 2, 3, 4, 5, 6
 Q8_0, Q5_1, Q5_0 = 8, 9, 10
 _o = None
 _r = None
 _rg = None
+_rgg = None
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -57,6 +59,7 @@ def lib():
             "qo_dequant_row": [I, P, P, I],
             "qo_dequant_matrix": [I, P, I, I, P, I], "qo_dequant_matrix_bf16": [I, P, I, I, P, I],
             "qo_quantize_x_q8": [P, I, P, P, P], "qo_q8_to_f32": [P, P, I, P],
+            "qo_quantize_x_q8k": [P, I, I, P, P, P],
             "qo_silu_mul": [P, P, ctypes.c_size_t, P],
             "qo_add_rmsnorm_quant": [P, P, P, P, P, P, P, I, I, ctypes.c_float],
             "qo_add_rmsnorm_bf16": [P, P, P, P, I, I, ctypes.c_float],
@@ -90,6 +93,10 @@ def ref_lib():
         L.ref_get_scale_min_k4.restype = None
         L.ref_dequant_row.argtypes = [I, P, P, ctypes.c_uint64]
         L.ref_dequant_row.restype = None
+        L.ref_f32_to_f16.restype = ctypes.c_uint16
+        L.ref_f32_to_f16.argtypes = [ctypes.c_float]
+        L.ref_quantize_row_q8_0_soa.argtypes = [P, P, ctypes.c_uint64]
+        L.ref_quantize_row_q8_0_soa.restype = None
         _r = L
     return _r
 
@@ -128,6 +135,24 @@ def quantize_x_q8(x):
     for c in range(ncol):
         lib().qo_quantize_x_q8(_ptr(x[c]), K, _ptr(q[c]), _ptr(d[c]), _ptr(s[c]))
     return q, d, s
+
+
+def quantize_x_q8k(x):
+    """x f32 [ncol <= 16][K] -> (q int8 [ncol][K], d f32 [K/256][16], bs int16 [K/256][16][8]) (gemv.hip:686-705)."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    ncol, K = x.shape
+    q = np.zeros((ncol, K), dtype=np.int8)
+    d = np.zeros((K // 256, 16), dtype=np.float32)
+    bs = np.zeros((K // 256, 16, 8), dtype=np.int16)
+    lib().qo_quantize_x_q8k(_ptr(x), K, ncol, _ptr(q), _ptr(d), _ptr(bs))
+    return q, d, bs
+
+
+def q8k_to_f32(q, d):
+    """The value each q8k entry stands for, q * (its 256-block's d), f32 [ncol][K]."""
+    ncol, K = q.shape
+    scale = np.repeat(d[:, :ncol].T, 256, axis=1)
+    return (q.astype(np.float32) * scale).astype(np.float32)
 
 
 def add_rmsnorm_quant(x, y, w, eps):
@@ -315,5 +340,31 @@ def ref_gemv_lib():
         for n in ("refg_repack_row_q6_K", "refg_repack_row_q8_0", "refg_repack_row_q5_1", "refg_repack_row_q5_0"):
             getattr(L, n).argtypes = [P, P, I]
             getattr(L, n).restype = None
+        for n in ("refg_repack_interleave8", "refg_repack_wmma_il"):
+            getattr(L, n).argtypes = [I, P, P, I, I]
+            getattr(L, n).restype = None
+        L.refg_wmma_il_bytes.restype = ctypes.c_size_t
+        L.refg_wmma_il_bytes.argtypes = [I, I, I]
         _rg = L
     return _rg
+
+
+def ref_gguf_lib():
+    """The reference's GGUF v3 reader (engine/src/gguf.cpp) compiled by oracle/Makefile, or None when it
+    was not built (no reference checkout)."""
+    global _rgg
+    if _rgg is None and os.path.exists(REF_GGUF_LIB):
+        L = ctypes.CDLL(REF_GGUF_LIB)
+        L.refgg_open.restype = P
+        L.refgg_open.argtypes = [ctypes.c_char_p]
+        L.refgg_close.argtypes = [P]
+        L.refgg_close.restype = None
+        L.refgg_n_tensors.restype = ctypes.c_long
+        L.refgg_n_tensors.argtypes = [P]
+        L.refgg_tensor.argtypes = [P, ctypes.c_long, ctypes.c_char_p, I, P, P, P, P, P]
+        L.refgg_read.argtypes = [P, ctypes.c_char_p, P]
+        L.refgg_kv_u32.argtypes = [P, ctypes.c_char_p, P]
+        L.refgg_kv_f32.argtypes = [P, ctypes.c_char_p, P]
+        L.refgg_kv_str.argtypes = [P, ctypes.c_char_p, ctypes.c_char_p, I]
+        _rgg = L
+    return _rgg

@@ -363,6 +363,27 @@ void qo_quantize_x_q8(const float* x, int K, int8_t* q, float* d, float* s) {
         d[b] = dd; s[b] = dd * (float)sum;
     }
 }
+/* gemv.hip:686-705 (quantize_x_q8k): one scale per 256 values, d = amax/127 over the 256, q = rne(x * 127/amax)
+ * (0 when amax == 0), bs = the int16 sum of each 32 q.  Column c of ncol <= 16: q at q + c*K, d[b*16 + c],
+ * bs[(b*16 + c)*8 + j] (the reference's XQ8K layout, gemv.h:33). */
+void qo_quantize_x_q8k(const float* x, int K, int ncol, int8_t* q, float* d, int16_t* bs) {
+    for (int c = 0; c < ncol; ++c)
+        for (int b = 0; b < K / 256; ++b) {
+            const float* xb = x + (size_t)c * K + (size_t)b * 256;
+            float amax = 0.f;
+            for (int l = 0; l < 256; ++l) amax = fmaxf(amax, fabsf(xb[l]));
+            const float dd = amax / 127.f, id = amax > 0 ? 127.f / amax : 0.f;
+            for (int j = 0; j < 8; ++j) {
+                int sum = 0;
+                for (int l = 0; l < 32; ++l) {
+                    const int qi = (int)nearbyintf(xb[32 * j + l] * id);
+                    q[(size_t)c * K + (size_t)b * 256 + 32 * j + l] = (int8_t)qi; sum += qi;
+                }
+                bs[((size_t)b * 16 + c) * 8 + j] = (int16_t)sum;
+            }
+            d[(size_t)b * 16 + c] = dd;
+        }
+}
 void qo_q8_to_f32(const int8_t* q, const float* d, int K, float* xr) {
     for (int k = 0; k < K; ++k) xr[k] = (float)q[k] * d[k / 32];
 }

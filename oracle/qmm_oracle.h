@@ -60,6 +60,7 @@ int qo_dequant_matrix_bf16(int wfmt, const uint8_t* W, int N, int K, uint16_t* o
 /* ---- activations ---- */
 /* per 32: d = amax/127, q = rne(x*127/amax), s = d*sum(q)  (engine/bench/bench_gemv.cpp:17-25) */
 void qo_quantize_x_q8(const float* x, int K, int8_t* q, float* d, float* s);
+void qo_quantize_x_q8k(const float* x, int K, int ncol, int8_t* q, float* d, int16_t* bs);   /* gemv.hip:686-705 */
 /* xr[k] = q[k] * d[k/32]  (bench_gemv.cpp:89, the "same-math" x the q8 kernels are gated against) */
 void qo_q8_to_f32(const int8_t* q, const float* d, int K, float* xr);
 /* silu(g)*u per element, then the q8 quantiser over rows of n (fn.hip:206-211) */

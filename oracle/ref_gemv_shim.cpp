@@ -12,4 +12,8 @@ void refg_repack_row_q6_K(const uint8_t* s, uint8_t* d, int K) { hip::repack_row
 void refg_repack_row_q8_0(const uint8_t* s, uint8_t* d, int K) { hip::repack_row_q8_0(s, d, K); }
 void refg_repack_row_q5_1(const uint8_t* s, uint8_t* d, int K) { hip::repack_row_q5_1(s, d, K); }
 void refg_repack_row_q5_0(const uint8_t* s, uint8_t* d, int K) { hip::repack_row_q5_0(s, d, K); }
+// the experimental interleaved layouts (gemv.hip:1442-1447,1280-1303)
+void refg_repack_interleave8(int f, const uint8_t* s, uint8_t* d, int N, int K) { hip::repack_interleave8((hip::WFmt)f, s, d, N, K); }
+size_t refg_wmma_il_bytes(int f, int N, int K) { return hip::wmma_il_bytes((hip::WFmt)f, N, K); }
+void refg_repack_wmma_il(int f, const uint8_t* s, uint8_t* d, int N, int K) { hip::repack_wmma_il((hip::WFmt)f, s, d, N, K); }
 }

@@ -12,6 +12,12 @@ Q5_0 rows.  Run from the repo root after `make -C oracle`:
 
     python tests/golden/make_golden.py             # quant_golden.npz
     python tests/golden/make_golden.py --formats   # quant_golden_fmt.npz
+    python tests/golden/make_golden.py --loadtime  # loadtime_golden.npz
+
+loadtime_golden.npz holds what the reference's load path writes: repack_row_q6_K rows (gemv.hip:
+1341-1350), the experimental interleaved layouts repack_interleave8 / repack_wmma_il (gemv.hip:1280-1303,
+1442-1447), the load-time f32 -> f16 rounding (quant.h:150-155) and quantize_row_q8_0_soa of F32, F16
+and BF16 rows (quant.h:174-199), all computed by the reference's own code.
 """
 import ctypes
 import os
@@ -131,9 +137,69 @@ def main_formats():
     print("wrote quant_golden_fmt.npz:", {k: v.shape for k, v in out.items()})
 
 
+def main_loadtime():
+    ref, refg = oracle.ref_lib(), oracle.ref_gemv_lib()
+    if ref is None or refg is None:
+        sys.exit("oracle/_ref libraries not built (needs the reference checkout): make -C oracle")
+    vp = ctypes.c_void_p
+    out = {}
+    # Q6_K rows -> SoA (K = 512 and 1280)
+    for K in (512, 1280):
+        rows = synth.q6k_blocks(synth.rng(20300 + K), 3 * (K // 256)).reshape(3, -1)
+        dst = np.zeros_like(rows)
+        for r in range(3):
+            src = np.ascontiguousarray(rows[r])
+            refg.refg_repack_row_q6_K(vp(src.ctypes.data), vp(dst[r].ctypes.data), K)
+        out[f"q6k_K{K}_src"], out[f"q6k_K{K}_dst"] = rows, dst
+    # interleaved layouts: 8-row block interleave (Q4_K, Q5_K, IQ4_XS) and the 16-row piece-major layout
+    # (those three plus Q6_K_SOA and Q8_0_SOA rows); N = 16 / 20 (a partial 16-row group), K = 512
+    K = 512
+    for name, fmt in (("q4k", synth.Q4_K), ("q5k", synth.Q5_K), ("iq4xs", synth.IQ4_XS), ("q6ksoa", synth.Q6_K_SOA),
+                      ("q8_0soa", synth.Q8_0_SOA)):
+        for N in (16, 20):
+            W = np.ascontiguousarray(synth.matrix(20310 + fmt + N, fmt, N, K))
+            if fmt in (synth.Q4_K, synth.Q5_K, synth.IQ4_XS) and N % 8 == 0:
+                d8 = np.zeros_like(W)
+                refg.refg_repack_interleave8(fmt, vp(W.ctypes.data), vp(d8.ctypes.data), N, K)
+                out[f"il8_{name}_N{N}_src"], out[f"il8_{name}_N{N}_dst"] = W, d8
+            nb = refg.refg_wmma_il_bytes(fmt, N, K)
+            d16 = np.zeros(nb, np.uint8)
+            refg.refg_repack_wmma_il(fmt, vp(W.ctypes.data), vp(d16.ctypes.data), N, K)
+            out[f"il16_{name}_N{N}_src"], out[f"il16_{name}_N{N}_dst"] = W, d16
+    # f32 -> f16 at load time: ties, subnormal range, overflow, signed zero, random
+    g = synth.rng(20320)
+    tie = np.array([1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 2.0 ** -14 * (1 + 2.0 ** -11), 2.0 ** -24 * 1.5, 2.0 ** -25,
+                    2.0 ** -25 * 1.0001, 2.0 ** -26, 65504.0, 65519.0, 65520.0, 1e9, 0.0, -0.0, 6.1e-5, 5.96e-8,
+                    -1.0 - 2.0 ** -11, 3.0e-6], np.float32)
+    f32 = np.concatenate([tie, g.standard_normal(2000).astype(np.float32) * np.float32(10.0) ** g.integers(-9, 5, 2000)])
+    out["f16_in"] = f32.astype(np.float32)
+    out["f16_out"] = np.array([ref.ref_f32_to_f16(float(v)) for v in out["f16_in"]], np.uint16)
+    # quantize_row_q8_0_soa of F32 / F16 / BF16 rows (K = 256, 8 rows; a zero block and large values included)
+    K = 256
+    x = (g.standard_normal((8, K)) * 3).astype(np.float32)
+    x[1, 32:64] = 0
+    x[2, :32] *= 1e3
+    x[3, 64:96] = 1e-6
+    src16 = x.astype(np.float16).view(np.uint16)
+    srcbf = synth.to_bf16_bits(x)
+    for name, gtype, src in (("f32", 0, x), ("f16", 1, src16), ("bf16", 30, srcbf)):
+        src = np.ascontiguousarray(src)
+        dst = np.zeros((8, K + K // 16), np.uint8)
+        row = np.zeros(K, np.float32)
+        for r in range(8):
+            sr = np.ascontiguousarray(src[r])
+            ref.ref_dequant_row(gtype, vp(sr.ctypes.data), vp(row.ctypes.data), K)
+            ref.ref_quantize_row_q8_0_soa(vp(row.ctypes.data), vp(dst[r].ctypes.data), K)
+        out[f"q8_0_{name}_src"], out[f"q8_0_{name}_dst"] = src, dst
+    np.savez_compressed(os.path.join(HERE, "loadtime_golden.npz"), **out)
+    print("wrote loadtime_golden.npz:", len(out), "arrays")
+
+
 def main():
     if "--formats" in sys.argv:
         return main_formats()
+    if "--loadtime" in sys.argv:
+        return main_loadtime()
     ref = oracle.ref_lib()
     if ref is None:
         sys.exit("oracle/_ref/libqmm_ref.so not built (needs the reference checkout): make -C oracle")

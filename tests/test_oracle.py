@@ -331,3 +331,32 @@ def test_gemm_wq_ref_matches_numpy():
     # the bf16 dequant is the RNE of the (golden-pinned) f32 dequant
     Wf = oracle.dequant_rows(oracle.Q4_K, W, K)
     assert np.array_equal(oracle.dequant_rows_bf16(oracle.Q4_K, W, K), synth.to_bf16_bits(Wf))
+
+
+def test_quantize_x_q8k_pinned_to_q8():
+    """Q8_K (one scale per 256) reduces to the pinned per-32 quantiser when every 32-sub-block of a 256-block
+    holds the block's amax: then q, d agree with qo_quantize_x_q8 exactly and bs is the per-32 integer sum.
+    Plus the closed forms: an all-zero block gives d = 0, q = 0; amax maps to +-127."""
+    g = np.random.default_rng(5)
+    K, ncol = 1024, 3
+    x = g.standard_normal((ncol, K)).astype(np.float32)
+    for c in range(ncol):
+        for b in range(K // 256):
+            blk = x[c, b * 256:(b + 1) * 256]
+            amax = np.float32(np.abs(blk).max() * 1.5 + 0.25)
+            for j in range(8):
+                blk[32 * j + (j * 5) % 32] = amax if (j + b + c) % 2 else -amax
+    x[2, 256:512] = 0.0                                  # an all-zero block
+    q, d, bs = oracle.quantize_x_q8k(x)
+    q8, d8, s8 = oracle.quantize_x_q8(x)
+    assert np.array_equal(q, q8)
+    for c in range(ncol):
+        for b in range(K // 256):
+            assert np.all(d8[c, 8 * b:8 * b + 8] == d[b, c])
+            assert np.array_equal(bs[b, c], q8[c, 256 * b:256 * (b + 1)].reshape(8, 32).astype(np.int64).sum(axis=1))
+    assert d[1, 2] == 0 and not q[2, 256:512].any() and not bs[1, 2].any()
+    assert np.abs(q).max() == 127
+    # columns beyond ncol untouched, and a column alone gives the same bits
+    assert not d[:, ncol:].any()
+    q1, d1, bs1 = oracle.quantize_x_q8k(x[1:2])
+    assert np.array_equal(q1[0], q[1]) and np.array_equal(d1[:, 0], d[:, 1]) and np.array_equal(bs1[:, 0], bs[:, 1])

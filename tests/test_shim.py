@@ -15,9 +15,11 @@ SRC = r'''
 #include "hipster_qmm_shim.hpp"
 #include <cstdio>
 int main() {
-    hip::GemvSeg seg{hip::WFmt::Q5_K, nullptr, nullptr, 16, 256};
-    hip::GemvSeg ok4{hip::WFmt::Q4_K, nullptr, nullptr, 16, 256};
-    if (hip::gemv_wmma_ok(&seg, 1) || !hip::gemv_wmma_ok(&ok4, 1)) return 2;
+    // gemv_wmma_ok as the reference's (gemv.hip:1272-1275): not Q5_1_SOA, K % 256 == 0, one K
+    hip::GemvSeg seg{hip::WFmt::Q5_1_SOA, nullptr, nullptr, 16, 256};
+    hip::GemvSeg ok4[2] = {{hip::WFmt::Q4_K, nullptr, nullptr, 16, 256}, {hip::WFmt::Q5_K, nullptr, nullptr, 16, 256}};
+    hip::GemvSeg badk[2] = {{hip::WFmt::Q4_K, nullptr, nullptr, 16, 256}, {hip::WFmt::Q4_K, nullptr, nullptr, 16, 512}};
+    if (hip::gemv_wmma_ok(&seg, 1) || !hip::gemv_wmma_ok(ok4, 2) || hip::gemv_wmma_ok(badk, 2)) return 2;
     if (hip::wfmt_row_bytes(hip::WFmt::Q4_K, 5120) != 20 * 144) return 3;
     int caught = 0;
     try {
@@ -29,7 +31,25 @@ int main() {
     try {   // ncol above the fused kernel's limit
         hip::gemv_q8_f32x(hip::WFmt::Q4_K, (void*)16, (const float*)16, (float*)16, 16, 256, 5, nullptr);
     } catch (const std::runtime_error&) { ++caught; }
-    if (caught != 3) return 4;
+    try {   // the reference's experimental interleaved layouts are not read here
+        hip::gemv_q8(hip::WFmt::Q4_K, (void*)16, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, (float*)16, 16, 256, 1, 4, 5, nullptr);
+    } catch (const std::runtime_error&) { ++caught; }
+    try {
+        hip::GemvSeg g{hip::WFmt::Q4_K, (void*)16, (float*)16, 16, 256};
+        hip::gemv_wmma(&g, 1, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, 1, 3, nullptr);
+    } catch (const std::runtime_error&) { ++caught; }
+    try {   // moe_gemm: Q6_K_SOA experts are not a moe_gemm format
+        hip::moe_gemm(hip::WFmt::Q6_K_SOA, hip::WFmt::Q8_0_SOA, (void*)16, (void*)16, 1024, (const hip::MoeTile*)16, 1, nullptr, 0,
+                      1, nullptr, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, (float*)16, 16, 256, nullptr);
+    } catch (const std::runtime_error&) { ++caught; }
+    try {   // gemv_splitk: more splits than 256-weight blocks
+        hip::gemv_splitk(hip::WFmt::Q8_0_SOA, (void*)16, hip::XQ8{(int8_t*)16, (float*)16, (float*)16}, (float*)16, 16, 512, 3, 1, nullptr);
+    } catch (const std::runtime_error&) { ++caught; }
+    try {   // gemm_ld: lda smaller than K
+        hip::BlasLt b; b.gemm_ld((const uint16_t*)16, 64, (const uint16_t*)16, 128, (uint16_t*)16, 16, 16, 128, nullptr);
+    } catch (const std::runtime_error&) { ++caught; }
+    hip::g_persist_blocks = 4; hip::g_moe_tpr = 8;    // the experiment knobs exist (and are ignored)
+    if (caught != 8) return 4;
     {   // the load-time repacks of the other formats (gemv.h:16-18), host only
         uint8_t src[34 * 2] = {0}, dst[34 * 2];
         src[0] = 0x00; src[1] = 0x3c;                      // Q8_0 block 0: d = 1
