@@ -50,6 +50,9 @@ def parse():
     p.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
     p.add_argument("--only-extra", choices=["activation_producers", "formats", "router"], default=None,
                    help="only run one of the extra measurements and print its JSON (for profiling it alone)")
+    p.add_argument("--roofs", action="store_true",
+                   help="only run the roof microbenchmarks (streaming read of the GEMV's 50 MB over a >= 1 GiB rotation, "
+                        "asymptotic 1 GiB read, matrix-instruction issue rates) and print their JSON")
     p.add_argument("--calib-copy", action="store_true",
                    help="only run 10 plain device copies of 256 MiB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
@@ -66,6 +69,69 @@ def calib_copy():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"calib_copy_bytes_read": n, "calib_copy_bytes_written": n, "dispatches": 10}), flush=True)
+
+
+def roofs(torch):
+    """MI355X roofs re-measured by libhipster_roofs.so (hipster_amd/csrc/roofs/roofs.hip, the method of the
+    reference's bench/roofline/bandwidth.hip and wmma_rate.hip): streaming-read GB/s of config 0's
+    50,135,040 weight bytes rotated over >= 1 GiB of copies (grid-stride loop as bandwidth.hip, and one-shot
+    bursts of U loads per thread as the GEMV issues them, plain and nontemporal), the asymptotic read of one
+    1 GiB buffer, and the issue rate of independent matrix instructions (TFLOP/s, TOP/s)."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "hipster_amd", "lib", "libhipster_roofs.so"))
+    lib.qmm_roof_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                  ctypes.c_void_p]
+    lib.qmm_roof_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda")
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+
+    def read_us(bufs, nbytes, variant, grid, unroll, reps=3):
+        def one(b):
+            return lambda: lib.qmm_roof_read(ctypes.c_void_p(b.data_ptr()), nbytes, variant, grid, unroll,
+                                             ctypes.c_void_p(sink.data_ptr()), st())
+        return graph_us(torch, [one(b) for b in bufs], reps=reps) / len(bufs)
+
+    nbytes = 50135040                                     # config 0's Q4_K weight bytes
+    ncopy = -(-ROTATE_BYTES // nbytes)
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_() for _ in range(ncopy)]
+    r50 = {}
+    for grid in (1024, 2048, 4096, 8192):
+        us = read_us(bufs, nbytes, 0, grid, 0)
+        r50[f"stride_grid{grid}"] = {"us": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1)}
+    for variant, tag in ((1, "burst"), (2, "burst_nt")):
+        for u in (4, 8, 16):
+            us = read_us(bufs, nbytes, variant, 0, u)
+            r50[f"{tag}_u{u}"] = {"us": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1)}
+    best = max(v["GB_s"] for v in r50.values())
+    out["read_50MB_rotated"] = dict(r50, best_GB_s=best, pct_of_8TBs=round(100 * best / HBM_PEAK_GBS, 1),
+                                    copies=ncopy)
+    del bufs
+    torch.cuda.empty_cache()
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").random_()
+    r1g = {}
+    for grid in (4096, 16384, 65536):
+        us = read_us([big], 1 << 30, 0, grid, 0, reps=5)
+        r1g[f"stride_grid{grid}"] = {"us": round(us, 1), "GB_s": round((1 << 30) / us / 1e3, 1)}
+    us = read_us([big], 1 << 30, 1, 0, 16, reps=5)
+    r1g["burst_u16"] = {"us": round(us, 1), "GB_s": round((1 << 30) / us / 1e3, 1)}
+    out["read_1GiB"] = r1g
+    del big
+    torch.cuda.empty_cache()
+    ops = {0: ("mfma_f32_32x32x16_bf16", 2 * 32 * 32 * 16, 2500.0), 1: ("mfma_f32_16x16x32_bf16", 2 * 16 * 16 * 32, 2500.0),
+           2: ("mfma_i32_32x32x32_i8", 2 * 32 * 32 * 32, 5000.0), 3: ("mfma_f32_32x32x2_f32", 2 * 32 * 32 * 2, 157.3),
+           4: ("mfma_i32_16x16x64_i8", 2 * 16 * 16 * 64, 5000.0)}
+    iters = 4096
+    for op, (name, flop, peak) in ops.items():
+        res = {}
+        for grid in (256, 512, 1024):                     # 8 waves per workgroup: 2, 4, 8 waves per SIMD
+            us = graph_us(torch, [lambda: lib.qmm_roof_mfma(op, iters, grid, ctypes.c_void_p(sink.data_ptr()), st())], reps=3)
+            tf = grid * 8 * iters * 4 * flop / us / 1e6
+            res[f"waves_per_simd{grid * 8 // 1024}"] = round(tf, 1)
+        res["best_TFLOPS"] = max(res.values())
+        res["pct_of_peak"] = round(100 * res["best_TFLOPS"] / peak, 1)
+        out[name] = res
+    return out
 
 
 def capture(torch, launches):
@@ -385,6 +451,9 @@ def main():
         sys.exit(2)
     if args.calib_copy:
         calib_copy()
+        return
+    if args.roofs:
+        print(json.dumps({"roofs": roofs(torch)}), flush=True)
         return
     if args.only_extra:
         fn = {"activation_producers": extra_act, "formats": extra_formats, "router": extra_router}[args.only_extra]

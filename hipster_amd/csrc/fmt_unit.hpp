@@ -1,7 +1,9 @@
 // fmt_unit.hpp -- per-format "units" of the q8-activation GEMV: the raw weight bytes of one scale's
 // worth of weights, their load, the matching activations and the unit's contribution to one
 // column, in the reference's arithmetic (block decoders engine/kernels/gemv.hip:58-268; formats
-// engine/src/quant.h:22-100).  Shared by the decode GEMV of the other formats (gemv_fmt.hip) and the
+// engine/src/quant.h:22-100).  The unit arithmetic and the lane accumulation are compiled without
+// floating-point contraction (explicit fmaf where one is meant), so every kernel built on them
+// rounds the same way and their results agree bit for bit.  Shared by the decode GEMV of the other formats (gemv_fmt.hip) and the
 // compatibility entry points (compat.hip: split-K GEMV, grouped q8 expert GEMM, Q8_K GEMV).
 // Device code only.
 #pragma once
@@ -88,6 +90,7 @@ template <> struct FmtUnit<QMM_Q8_0_SOA> {            // row = [qs K][d (K/32) x
     template <class XS>
     static __device__ __forceinline__ void xload(const XS& xs, int u, X& x) { xs.sub(u, x); }
     static __device__ __forceinline__ float col(const Raw& r, const X& x, int) {
+#pragma clang fp contract(off)
         const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
         return h2f(r.d) * x.d * (float)dot32(w, x.a, x.b);
     }
@@ -105,6 +108,7 @@ template <> struct FmtUnit<QMM_Q5_1_SOA> {            // row = [qs K/2][qh K/8][
     template <class XS>
     static __device__ __forceinline__ void xload(const XS& xs, int u, X& x) { xs.sub(u, x); }
     static __device__ __forceinline__ float col(const Raw& r, const X& x, int) {
+#pragma clang fp contract(off)
         // weight j (< 16): low nibble of qs byte j, fifth bit = qh bit j; weight j + 16: high nibble,
         // qh bit j + 16 (quant.h:82-88)
         const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
@@ -129,6 +133,7 @@ template <> struct FmtUnit<QMM_IQ4_XS> {              // block = {f16 d, u16 sca
     template <class XS>
     static __device__ __forceinline__ void xload(const XS& xs, int u, X& x) { xs.sub(u, x); }
     static __device__ __forceinline__ float col(const Raw& r, const X& x, int u) {
+#pragma clang fp contract(off)
         const int ib = u & 7;
         const int ls = (int)((r.hd.y >> (4 * ib)) & 0xfu) | (int)(((r.hd.x >> (16 + 2 * ib)) & 3u) << 4);
         const float dl = h2f(r.hd.x) * (float)(ls - 32);
@@ -160,6 +165,7 @@ template <> struct FmtUnit<QMM_Q5_K> {                // block = {f16 d, dmin, s
         xs.sub(2 * u + 1, x.hi);
     }
     static __device__ __forceinline__ float col(const Raw& r, const X& x, int u) {
+#pragma clang fp contract(off)
         // pair j of block b: weights 64j + l (sub-block 2j) = low nibble of qs[32j + l] with bit 2j of
         // qh[l] as the fifth bit, 64j + 32 + l (sub-block 2j + 1) = high nibble with bit 2j + 1
         const int j = u & 3;
@@ -195,6 +201,7 @@ template <> struct FmtUnit<QMM_Q4_K> {                // block = {f16 d, dmin, s
         xs.sub(2 * u + 1, x.hi);
     }
     static __device__ __forceinline__ float col(const Raw& r, const X& x, int u) {
+#pragma clang fp contract(off)
         // pair j of block b (quant.h:44-53): weights 64j + l = low nibble of qs[32j + l] (sub-block
         // 2j), 64j + 32 + l = its high nibble (sub-block 2j + 1)
         const int j = u & 3;
@@ -240,6 +247,7 @@ template <> struct FmtUnit<QMM_Q6_K_SOA> {            // row = [ql K/2][qh K/4][
         }
     }
     static __device__ __forceinline__ float col(const Raw& q, const X& x, int u) {
+#pragma clang fp contract(off)
         const int lh = u & 1;
         const uint32_t A[4] = {q.a.x, q.a.y, q.a.z, q.a.w}, B[4] = {q.b.x, q.b.y, q.b.z, q.b.w}, H[4] = {q.h.x, q.h.y, q.h.z, q.h.w};
         // scales sc[lh + 2g] of the unit's 8-byte run {sc0, sc1}: bytes lh, lh+2, lh+4, lh+6
@@ -274,6 +282,7 @@ template <> struct FmtUnit<QMM_Q6_K_SOA> {            // row = [ql K/2][qh K/4][
 template <int F, int NCOL, int NIT, int RPW, class XS>
 __device__ __forceinline__ void fmt_rows(const uint8_t* __restrict__ W, int row0, int N, int K, const XS (&xs)[NCOL],
                                          float (&acc)[RPW][NCOL], int ub, int ue, size_t rb = 0) {
+#pragma clang fp contract(off)
     typedef FmtUnit<F> FU;
     const int lane = threadIdx.x & 63;
     if (rb == 0) rb = fmt_row_bytes<F>(K);
