@@ -48,7 +48,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
-    p.add_argument("--only-extra", choices=["activation_producers", "formats", "router"], default=None,
+    p.add_argument("--only-extra", choices=["activation_producers", "formats", "router", "moe_decode"], default=None,
                    help="only run one of the extra measurements and print its JSON (for profiling it alone)")
     p.add_argument("--roofs", action="store_true",
                    help="only run the roof microbenchmarks (streaming read of the GEMV's 50 MB over a >= 1 GiB rotation, "
@@ -331,7 +331,8 @@ def moe_tables(torch):
 
 def extra_cfg2(torch, tb):
     """MoE decode step (route, gate|up gather GEMV, silu*up q8, down + combine)
-    at T = 1, 4, 8 over 512 Q4_K experts + shared; each replayed step routes different logits."""
+    at T = 1, 4, 8 over 512 Q4_K experts + shared; each replayed step routes different logits.  The step
+    is qmm_moe_decode (two launches); the four-launch sequence it replaces is timed beside it."""
     import numpy as np
     from hipster_amd import qmm, synth
     H, F, NE = 2048, 512, 11
@@ -357,11 +358,18 @@ def extra_cfg2(torch, tb):
                 qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [tb["Wd"]], [tb["Sd"]], [y], tb["Wd"][0].numel(), ids[r], NE, hq, H, F, T,
                              True, slotw=w[r])
             return f
-        us = graph_us(torch, [step(r) for r in range(R)], reps=2) / R
+        us4 = graph_us(torch, [step(r) for r in range(R)], reps=2) / R
+        ws = torch.zeros(qmm.moe_decode_ws_bytes(T, 10, F) // 4, device="cuda")
+        y2 = torch.zeros((T, H), device="cuda")
+
+        def fused(r):      # the same step in two launches (routing in the gather, silu -> q8 in the down staging)
+            return lambda: qmm.moe_decode(synth.Q4_K, tb["Wg"], tb["Wu"], tb["Wd"], tb["Wg"][0].numel(), tb["Wd"][0].numel(), tb["Sg"],
+                                          tb["Su"], tb["Sd"], lg[r], 513, 512, 10, xb, T, H, F, ids[r], w[r], ws, y2)
+        us = graph_us(torch, [fused(r) for r in range(R)], reps=2) / R
         distinct = float(np.mean([len(np.unique(i.cpu().numpy())) for i in ids]))   # includes the shared slot (-1)
         byts = distinct * per_expert
-        out[f"T{T}"] = {"us_per_step": round(us, 1), "distinct_experts_incl_shared": distinct,
-                        "GB_s": round(byts / us / 1e3, 1)}
+        out[f"T{T}"] = {"us_per_step": round(us, 1), "four_launch_us_per_step": round(us4, 1),
+                        "distinct_experts_incl_shared": distinct, "GB_s": round(byts / us / 1e3, 1)}
     return out
 
 
@@ -456,7 +464,8 @@ def main():
         print(json.dumps({"roofs": roofs(torch)}), flush=True)
         return
     if args.only_extra:
-        fn = {"activation_producers": extra_act, "formats": extra_formats, "router": extra_router}[args.only_extra]
+        fn = {"activation_producers": extra_act, "formats": extra_formats, "router": extra_router,
+              "moe_decode": lambda t: extra_cfg2(t, moe_tables(t))}[args.only_extra]
         print(json.dumps({args.only_extra: fn(torch)}), flush=True)
         return
     from hipster_amd import _lib

@@ -27,6 +27,7 @@ namespace qmm {
 namespace {
 
 constexpr int kMaxCols = 8;        // columns per pass of the gather GEMV
+constexpr int kMaxSlots = 16;      // slots per token
 
 // ------------------------------------------------------------------------------------------
 // Routing (fn.hip:157-205).  One wave per token (4 tokens per workgroup), VPL logits per lane (expert
@@ -71,12 +72,10 @@ __device__ __forceinline__ int wave_min64(int v) {
 
 constexpr int kRouteMaxK = 16, kRouteMaxExp = 1024;
 
+// one wave routes the token whose logits start at l: ids / weights of its topk + 1 slots to idt / wt
 template <int VPL>
-__global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ logits, int* __restrict__ ids,
-                                                   float* __restrict__ w, int T, int nexp, int stride, int topk) {
-    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T) return;                                  // wave-uniform
-    const float* l = logits + (size_t)t * stride;
+__device__ __forceinline__ void route_token(const float* __restrict__ l, int nexp, int topk, int* idt, float* wt) {
+    const int lane = threadIdx.x & 63;
     float v[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {                      // unconditional (clamped) loads: no wait per load
@@ -136,10 +135,16 @@ __global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ log
                 if (p[j] > bv) { bv = p[j]; bj = j; }
         }
     }
-    int* idt = ids + (size_t)t * (topk + 1);
-    float* wt = w + (size_t)t * (topk + 1);
     if (lane < topk) { idt[lane] = isel; wt[lane] = psel / wsum; }
     if (lane == topk) { idt[topk] = -1; wt[topk] = 1.f / (1.f + __expf(-gate)); }
+}
+
+template <int VPL>
+__global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ logits, int* __restrict__ ids,
+                                                   float* __restrict__ w, int T, int nexp, int stride, int topk) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;                                  // wave-uniform
+    route_token<VPL>(logits + (size_t)t * stride, nexp, topk, ids + (size_t)t * (topk + 1), w + (size_t)t * (topk + 1));
 }
 
 // ------------------------------------------------------------------------------------------
@@ -174,10 +179,8 @@ __global__ void __launch_bounds__(256) k_moe_silu_quant(const float* __restrict_
 // Expert gather GEMV, Q4_K experts and shared expert.  grid = (row blocks, slots, segments).
 // Row block = 4 waves x (64 / LPR) rows.  I = pair iterations per row (ceil(4 K/256 / LPR)).
 template <int LPR, int I, int NC, bool EXACT>
-__device__ __forceinline__ void moe_cols(const uint8_t* rp, int t, int j, int ntask, uint8_t* smem, int K, int N, int row,
+__device__ __forceinline__ void moe_cols(const Q4kPairs<I>& A, int t, int j, int ntask, uint8_t* smem, int K, int N, int row,
                                          const int* cols, float* __restrict__ y) {
-    Q4kPairs<I> A;
-    q4k_load_pairs<I, LPR>(rp, t, j, ntask, 0, A);
     XPairSrc<true> xs[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) xs[c] = XPairSrc<true>{smem + (size_t)c * (K + (K >> 2)), nullptr, nullptr, K};
@@ -209,20 +212,13 @@ __device__ __forceinline__ void stage_gather(uint8_t* lds, const int8_t* __restr
     }
 }
 
+// the gather of slot te's expert for the columns s_cols[0..ncols) (after the dedup): weights of
+// expert id (segment seg), x rows xrow_te ? slot : slot / nexp
 template <int LPR, int I>
-__global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
-                                                      const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                                      const float* __restrict__ xsum, int N, int K, int nslot, int xrow_te) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int s_cols[64 + kMaxCols];
-    __shared__ int s_n, s_dup;
-    const int te = blockIdx.y, seg = blockIdx.z, tid = threadIdx.x;
-    const int id = ids[te];
-    if (tid < 64) moe_slot_columns(ids, nslot, te, id, s_cols, &s_n, &s_dup);
-    __syncthreads();
-    if (s_dup) return;
-    const int ncols = s_n;
-    const int nb = K >> 8, ntask = 4 * nb;
+__device__ __forceinline__ void gather_expert(const qmm_moe_segs& a, int seg, int id, int ncols, const int* s_cols, uint8_t* smem,
+                                              const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                              const float* __restrict__ xsum, int N, int K, int nexp, int xrow_te) {
+    const int nb = K >> 8, ntask = 4 * nb, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, t = lane & (LPR - 1), j = t & 3;
     constexpr int RPW = 64 / LPR;
     const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
@@ -230,6 +226,9 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
     const uint8_t* rp = wbase + (size_t)min(row, N - 1) * ((size_t)nb * 144);
     float* y = a.y[seg];
     const bool exact = (ntask % LPR) == 0;
+    // the expert's rows are loaded once, before the x staging, so both latencies overlap
+    Q4kPairs<I> A;
+    q4k_load_pairs<I, LPR>(rp, t, j, ntask, 0, A);
     for (int c0 = 0; c0 < ncols; c0 += kMaxCols) {
         const int nc = min(kMaxCols, ncols - c0);
         int xrow[kMaxCols];
@@ -244,8 +243,8 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
         const int* cols = s_cols + c0;
 #define QMM_MOE_NC(NCV)                                                                                    \
     case NCV:                                                                                              \
-        if (exact) moe_cols<LPR, I, NCV, true>(rp, t, j, ntask, smem, K, N, row, cols, y);                 \
-        else moe_cols<LPR, I, NCV, false>(rp, t, j, ntask, smem, K, N, row, cols, y);                      \
+        if (exact) moe_cols<LPR, I, NCV, true>(A, t, j, ntask, smem, K, N, row, cols, y);                  \
+        else moe_cols<LPR, I, NCV, false>(A, t, j, ntask, smem, K, N, row, cols, y);                       \
         break;
         switch (nc) {
             QMM_MOE_NC(1) QMM_MOE_NC(2) QMM_MOE_NC(3) QMM_MOE_NC(4)
@@ -255,43 +254,96 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
     }
 }
 
-// ------------------------------------------------------------------------------------------
-// Down projection + weighted combine: grid = (row blocks of 64/LPR rows, tokens).  Wave w takes
-// the slots e = w, w+4, ...; per-slot row results go to LDS; lane r of wave 0 sums row r over the
-// slots in order.
-constexpr int kMaxSlots = 16;
-
 template <int LPR, int I>
-__global__ void __launch_bounds__(256) k_gemv_moe_down_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
-                                                           const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                                           const float* __restrict__ xsum, int N, int K) {
+__global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
+                                                      const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                      const float* __restrict__ xsum, int N, int K, int nslot, int xrow_te) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int RPW = 64 / LPR;
+    __shared__ int s_cols[64 + kMaxCols];
+    __shared__ int s_n, s_dup;
+    const int te = blockIdx.y, seg = blockIdx.z, tid = threadIdx.x;
+    const int id = ids[te];
+    if (tid < 64) moe_slot_columns(ids, nslot, te, id, s_cols, &s_n, &s_dup);
+    __syncthreads();
+    if (s_dup) return;
+    gather_expert<LPR, I>(a, seg, id, s_n, s_cols, smem, xq, xd, xsum, N, K, nexp, xrow_te);
+}
+
+// ------------------------------------------------------------------------------------------
+// The MoE decode step (qmm_moe_decode).  At T = 1, launch 1 routes inside the gather: every
+// workgroup of the gate|up gather first routes the token itself (route_token, the arithmetic of
+// k_moe_route, so ids and weights are the same bits), then deduplicates and gathers exactly as
+// k_gemv_moe_q4k; workgroup (0, 0, 0) writes ids and weights out.  At T = 2..8 the routing work
+// would repeat in each of the T * (topk + 1) * rowblocks workgroups, so k_moe_route runs once first
+// and k_gemv_moe_q4k gathers.  The last launch stages h = silu(gate) * up of the token's slot rows, quantised per 32, straight into the
+// down GEMV's LDS layout (the arithmetic of k_moe_silu_quant: the same q8 bits), then runs the down
+// projection and the slot-ordered combine of k_gemv_moe_down_q4k.  The four-launch sequence
+// moe_route, gemv_moe (gate|up), moe_silu_quant, gemv_moe (down) gives the same y bit for bit.
+constexpr int kDecMaxTok = 8;
+
+template <int LPR, int I, int VPL>
+__global__ void __launch_bounds__(256) k_moe_route_gather(qmm_moe_segs a, const float* __restrict__ logits, int stride, int nexp_total,
+                                                          int topk, int* __restrict__ ids_out, float* __restrict__ w_out,
+                                                          const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                          const float* __restrict__ xsum, int N, int K, int T) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_ids[kDecMaxTok * kMaxSlots];
+    __shared__ float s_w[kDecMaxTok * kMaxSlots];
+    __shared__ int s_cols[64 + kMaxCols];
+    __shared__ int s_n, s_dup;
+    const int tid = threadIdx.x, wave = tid >> 6, nexp = topk + 1, nslot = T * nexp;
+    for (int t = wave; t < T; t += 4)                              // wave-uniform
+        route_token<VPL>(logits + (size_t)t * stride, nexp_total, topk, s_ids + t * nexp, s_w + t * nexp);
+    __syncthreads();
+    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && tid < nslot) {
+        ids_out[tid] = s_ids[tid];
+        w_out[tid] = s_w[tid];
+    }
+    const int te = blockIdx.y, seg = blockIdx.z;
+    const int id = s_ids[te];
+    if (tid < 64) moe_slot_columns(s_ids, nslot, te, id, s_cols, &s_n, &s_dup);
+    __syncthreads();
+    if (s_dup) return;
+    gather_expert<LPR, I>(a, seg, id, s_n, s_cols, smem, xq, xd, xsum, N, K, nexp, 0);
+}
+
+// the down projection of one token's slots: wave w takes the slots e = w, w + 4, ... (at most
+// kMaxSlots / 4 of them); their weight rows are loaded before the caller stages x (stage(), then a
+// barrier), per-slot row results go to LDS and lane r of wave 0 sums row r over the slots in order
+template <int LPR, int I, typename Stage>
+__device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __restrict__ ids, int nexp, uint8_t* smem, int N, int K,
+                                           Stage stage) {
+    constexpr int RPW = 64 / LPR, SPW = kMaxSlots / 4;
     __shared__ float vres[kMaxSlots][RPW];
     const int tok = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, t = lane & (LPR - 1), j = t & 3;
     const int nb = K >> 8, ntask = 4 * nb;
     const int rloc = lane / LPR, row = blockIdx.x * RPW + rloc;
-    // stage the nexp slot rows of this token
-    int xrow[kMaxSlots];
+    Q4kPairs<I> A[SPW];
 #pragma unroll
-    for (int e = 0; e < kMaxSlots; ++e) xrow[e] = tok * nexp + min(e, nexp - 1);
-    stage_gather(smem, xq, xd, xsum, xrow, nexp, K);
+    for (int i = 0; i < SPW; ++i) {
+        const int e = wave + 4 * i;
+        if (e < nexp) {                                  // wave-uniform
+            const int id = ids[tok * nexp + e];
+            const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[0] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[0];
+            q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, N - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[i]);
+        }
+    }
+    stage();
     __syncthreads();
     const Q4kPairDecode dc(j);
     const bool exact = (ntask % LPR) == 0;
-    for (int e = wave; e < nexp; e += 4) {
-        const int id = ids[tok * nexp + e];
-        const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[0] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[0];
-        const uint8_t* rp = wbase + (size_t)min(row, N - 1) * ((size_t)nb * 144);
-        Q4kPairs<I> A;
-        q4k_load_pairs<I, LPR>(rp, t, j, ntask, 0, A);
-        XPairSrc<true> xs[1] = {XPairSrc<true>{smem + (size_t)e * (K + (K >> 2)), nullptr, nullptr, K}};
-        float acc[1] = {0.f};
-        if (exact) q4k_pairs_compute<1, I, true, true, LPR>(A, dc, t, ntask, 0, xs, acc);
-        else q4k_pairs_compute<1, I, true, false, LPR>(A, dc, t, ntask, 0, xs, acc);
-        acc[0] = group_sum(acc[0], LPR);
-        if (t == 0) vres[e][rloc] = acc[0];
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+        const int e = wave + 4 * i;
+        if (e < nexp) {
+            XPairSrc<true> xs[1] = {XPairSrc<true>{smem + (size_t)e * (K + (K >> 2)), nullptr, nullptr, K}};
+            float acc[1] = {0.f};
+            if (exact) q4k_pairs_compute<1, I, true, true, LPR>(A[i], dc, t, ntask, 0, xs, acc);
+            else q4k_pairs_compute<1, I, true, false, LPR>(A[i], dc, t, ntask, 0, xs, acc);
+            acc[0] = group_sum(acc[0], LPR);
+            if (t == 0) vres[e][rloc] = acc[0];
+        }
     }
     __syncthreads();
     if (tid < RPW && blockIdx.x * RPW + tid < N) {
@@ -299,6 +351,48 @@ __global__ void __launch_bounds__(256) k_gemv_moe_down_q4k(qmm_moe_segs a, const
         for (int e = 0; e < nexp; ++e) acc += a.slotw[tok * nexp + e] * vres[e][tid];
         a.y[0][(size_t)tok * N + blockIdx.x * RPW + tid] = acc;
     }
+}
+
+// h = silu(g) * u of ncol rows of K (g, u row-major, rows of this token) -> q8 per 32 in the pair layout
+__device__ __forceinline__ void stage_silu_q8(uint8_t* lds, const float* __restrict__ g, const float* __restrict__ u, int ncol, int K) {
+    const int n8 = ncol * (K >> 3);
+    const int lim = (n8 + 255) & ~255;                            // whole quads stay together: n8 % 4 == 0
+    for (int e = threadIdx.x; e < lim; e += 256) {
+        const int ec = min(e, n8 - 1);
+        const float4 g0 = ((const float4*)g)[2 * ec], g1 = ((const float4*)g)[2 * ec + 1];
+        const float4 u0 = ((const float4*)u)[2 * ec], u1 = ((const float4*)u)[2 * ec + 1];
+        const float4 a = make_float4(silu_f(g0.x) * u0.x, silu_f(g0.y) * u0.y, silu_f(g0.z) * u0.z, silu_f(g0.w) * u0.w);
+        const float4 b = make_float4(silu_f(g1.x) * u1.x, silu_f(g1.y) * u1.y, silu_f(g1.z) * u1.z, silu_f(g1.w) * u1.w);
+        stagef_store_one(lds, K, a, b, e, n8);
+    }
+}
+
+template <int LPR, int I>
+__global__ void __launch_bounds__(256) k_moe_silu_down(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
+                                                       const float* __restrict__ gate, const float* __restrict__ up, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tok = blockIdx.y;
+    down_slots<LPR, I>(a, ids, nexp, smem, N, K, [&] {
+        stage_silu_q8(smem, gate + (size_t)tok * nexp * K, up + (size_t)tok * nexp * K, nexp, K);
+    });
+}
+
+// ------------------------------------------------------------------------------------------
+// Down projection + weighted combine: grid = (row blocks of 64/LPR rows, tokens), down_slots over
+// the token's slot rows of q8 x.
+
+template <int LPR, int I>
+__global__ void __launch_bounds__(256) k_gemv_moe_down_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
+                                                           const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                           const float* __restrict__ xsum, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tok = blockIdx.y;
+    down_slots<LPR, I>(a, ids, nexp, smem, N, K, [&] {   // the nexp slot rows of this token
+        int xrow[kMaxSlots];
+#pragma unroll
+        for (int e = 0; e < kMaxSlots; ++e) xrow[e] = tok * nexp + min(e, nexp - 1);
+        stage_gather(smem, xq, xd, xsum, xrow, nexp, K);
+    });
 }
 
 // ------------------------------------------------------------------------------------------
@@ -368,7 +462,88 @@ int launch_down(const qmm_moe_segs& a, const int* ids, int nexp, qmm_xq8 x, int 
     return QMM_OK;
 }
 
+// the two launches of qmm_moe_decode (shapes checked by the caller)
+template <int LPR, int VPL>
+int launch_decode_gather(const qmm_moe_segs& a, const float* logits, int stride, int nexp_total, int topk, int* ids, float* w,
+                         qmm_xq8 x, int F, int H, int T, hipStream_t s) {
+    const int iters = (H / 256 * 4 + LPR - 1) / LPR;
+    const dim3 grid((F + 4 * (64 / LPR) - 1) / (4 * (64 / LPR)), T * (topk + 1), 2);
+    const size_t lds = (size_t)kMaxCols * (H + H / 4);
+#define QMM_G(IV) case IV: hipLaunchKernelGGL((k_moe_route_gather<LPR, IV, VPL>), grid, dim3(256), lds, s, a, logits, stride, nexp_total, \
+                                              topk, ids, w, x.q, x.d, x.s, F, H, T); break;
+    switch (iters) {
+        QMM_G(1) QMM_G(2) QMM_G(3) QMM_G(4) QMM_G(5) QMM_G(6)
+        default: return QMM_ERR_SHAPE;
+    }
+#undef QMM_G
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+template <int LPR>
+int launch_decode_down(const qmm_moe_segs& a, const int* ids, int nexp, const float* gate, const float* up, int H, int F, int T,
+                       hipStream_t s) {
+    const int iters = (F / 256 * 4 + LPR - 1) / LPR;
+    const dim3 grid((H + (64 / LPR) - 1) / (64 / LPR), T);
+    const size_t lds = (size_t)nexp * (F + F / 4);
+#define QMM_D(IV) case IV: hipLaunchKernelGGL((k_moe_silu_down<LPR, IV>), grid, dim3(256), lds, s, a, ids, nexp, gate, up, H, F); break;
+    switch (iters) {
+        QMM_D(1) QMM_D(2) QMM_D(3) QMM_D(4) QMM_D(5) QMM_D(6)
+        default: return QMM_ERR_SHAPE;
+    }
+#undef QMM_D
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+template <int VPL>
+int decode_gather_vpl(const qmm_moe_segs& a, const float* logits, int stride, int nexp_total, int topk, int* ids, float* w, qmm_xq8 x,
+                      int F, int H, int T, hipStream_t s) {
+    return moe_lpr(H) == 8 ? launch_decode_gather<8, VPL>(a, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
+                           : launch_decode_gather<16, VPL>(a, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s);
+}
+
 }  // namespace
+
+// checks shared by qmm_moe_decode and the workspace-free variant; 0 when the call can run
+int moe_decode_check(int fmt, const void* Wg, const void* Wu, const void* Wd, const void* Sg, const void* Su, const void* Sd,
+                     const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H, int F, const int* ids,
+                     const float* w, const float* y) {
+    if (fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+    if (!Wg || !Wu || !Wd || !Sg || !Su || !Sd || !logits || !x.q || !x.d || !x.s || !ids || !w || !y) return QMM_ERR_NULL;
+    if (T < 0 || T > kDecMaxTok || nexp_total < 1 || nexp_total > kRouteMaxExp || topk < 1 || topk + 1 > kMaxSlots ||
+        topk > nexp_total || stride < nexp_total + 1 || H <= 0 || F <= 0 || H % 256 || F % 256 || H > 6144 || F > 6144)
+        return QMM_ERR_SHAPE;
+    return QMM_OK;
+}
+
+// the two launches, gate / up rows in gu (2 * T * (topk + 1) * F floats)
+int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg, const void* Su,
+                   const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H, int F, int* ids,
+                   float* w, float* gu, float* y, hipStream_t s) {
+    if (T == 0) return QMM_OK;
+    const int nexp = topk + 1;
+    float* gate = gu;
+    float* up = gu + (size_t)T * nexp * F;
+    const qmm_moe_segs ga = {{Wg, Wu}, {Sg, Su}, {gate, up}, ebytes_gu, nullptr};
+    int rc;
+    if (T == 1) {
+        rc = nexp_total <= 128 ? decode_gather_vpl<2>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
+           : nexp_total <= 256 ? decode_gather_vpl<4>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
+           : nexp_total <= 512 ? decode_gather_vpl<8>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
+                               : decode_gather_vpl<16>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s);
+    } else {
+        // every gather workgroup would route all T tokens again: route once instead
+        rc = qmm_moe_route_n(logits, ids, w, T, nexp_total, stride, topk, s);
+        if (rc == QMM_OK)
+            rc = moe_lpr(H) == 8 ? launch_gather<8>(ga, 2, ids, nexp, x, F, H, T, 0, s) : launch_gather<16>(ga, 2, ids, nexp, x, F, H, T, 0, s);
+    }
+    if (rc != QMM_OK) return rc;
+    const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
+    return moe_lpr(F) == 8 ? launch_decode_down<8>(da, ids, nexp, gate, up, H, F, T, s)
+                           : launch_decode_down<16>(da, ids, nexp, gate, up, H, F, T, s);
+}
+
 }  // namespace qmm
 
 using namespace qmm;
@@ -428,6 +603,20 @@ int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const
     }
     return moe_lpr(K) == 8 ? launch_gather<8>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s)
                            : launch_gather<16>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s);
+}
+
+int qmm_moe_decode(int fmt, const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg,
+                   const void* Su, const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H,
+                   int F, int* ids, float* w, float* ws, size_t ws_bytes, float* y, void* stream) {
+    if (int e = moe_decode_check(fmt, Wg, Wu, Wd, Sg, Su, Sd, logits, stride, nexp_total, topk, x, T, H, F, ids, w, y)) return e;
+    if (!ws) return QMM_ERR_NULL;
+    if (ws_bytes < qmm_moe_decode_ws_bytes(T, topk, F)) return QMM_ERR_WORKSPACE;
+    return moe_decode_run(Wg, Wu, Wd, ebytes_gu, ebytes_d, Sg, Su, Sd, logits, stride, nexp_total, topk, x, T, H, F, ids, w, ws, y,
+                          (hipStream_t)stream);
+}
+
+size_t qmm_moe_decode_ws_bytes(int T, int topk, int F) {
+    return T <= 0 || topk < 1 || F <= 0 ? 0 : (size_t)2 * T * (topk + 1) * F * sizeof(float);
 }
 
 int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, float* y, int T, int nexp, int E, void* stream) {

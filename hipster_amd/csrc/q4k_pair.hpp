@@ -186,38 +186,43 @@ __device__ __forceinline__ int quad_xor(int v) {
     return __builtin_amdgcn_mov_dpp(v, M == 1 ? 0xB1 : 0x4E, 0xf, 0xf, false);
 }
 
-template <int NCOL, int U, int BS = kPairBlock>
-__device__ __forceinline__ void stagef_store(uint8_t* lds, int K, const XStageF<NCOL, U>& S) {
-    const int k8 = K >> 3, n8 = NCOL * k8, kq = K >> 6;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int e = (int)threadIdx.x + BS * u;              // n8 is a multiple of 4: quads share e < n8
-        const float4 a = S.v[u][0], b = S.v[u][1];
-        float amax = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                           fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
-        amax = fmaxf(amax, __int_as_float(quad_xor<1>(__float_as_int(amax))));
-        amax = fmaxf(amax, __int_as_float(quad_xor<2>(__float_as_int(amax))));
-        const float dd = amax / 127.f, id = amax > 0.f ? 127.f / amax : 0.f;
-        const int q0 = __float2int_rn(a.x * id), q1 = __float2int_rn(a.y * id), q2 = __float2int_rn(a.z * id);
-        const int q3 = __float2int_rn(a.w * id), q4 = __float2int_rn(b.x * id), q5 = __float2int_rn(b.y * id);
-        const int q6 = __float2int_rn(b.z * id), q7 = __float2int_rn(b.w * id);
-        int sum = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7));
-        sum += quad_xor<1>(sum);
-        sum += quad_xor<2>(sum);
-        if (e < n8) {
-            const int c = e / k8, f = e - c * k8, un = f >> 1;   // 16-byte unit un, half f & 1
-            uint8_t* base = lds + (size_t)c * (K + (K >> 2));
-            const uint32_t lo = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)q3 << 24);
-            const uint32_t hi = (uint32_t)(q4 & 0xff) | ((uint32_t)(q5 & 0xff) << 8) | ((uint32_t)(q6 & 0xff) << 16) | ((uint32_t)q7 << 24);
-            *(uint2*)(base + (size_t)((un & 3) * kq + (un >> 2)) * 16 + (f & 1) * 8) = make_uint2(lo, hi);
-            if ((f & 3) == 0) {
-                const int sb = f >> 2;
-                float* dsq = (float*)(base + (size_t)K + (size_t)(sb >> 1) * 16);
-                dsq[sb & 1] = dd;
-                dsq[2 + (sb & 1)] = dd * (float)sum;
-            }
+// One slot of the staging below: the 8 values {a, b} are floats 8e..8e+7 of the column-major [ncol][K]
+// array; the 4 lanes of a quad hold one 32-value q8 block.  All 4 lanes of a quad must be active (the
+// quad reductions are DPP permutations); e >= n8 computes and stores nothing.
+__device__ __forceinline__ void stagef_store_one(uint8_t* lds, int K, float4 a, float4 b, int e, int n8) {
+    const int k8 = K >> 3, kq = K >> 6;
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                       fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    amax = fmaxf(amax, __int_as_float(quad_xor<1>(__float_as_int(amax))));
+    amax = fmaxf(amax, __int_as_float(quad_xor<2>(__float_as_int(amax))));
+    const float dd = amax / 127.f, id = amax > 0.f ? 127.f / amax : 0.f;
+    const int q0 = __float2int_rn(a.x * id), q1 = __float2int_rn(a.y * id), q2 = __float2int_rn(a.z * id);
+    const int q3 = __float2int_rn(a.w * id), q4 = __float2int_rn(b.x * id), q5 = __float2int_rn(b.y * id);
+    const int q6 = __float2int_rn(b.z * id), q7 = __float2int_rn(b.w * id);
+    int sum = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7));
+    sum += quad_xor<1>(sum);
+    sum += quad_xor<2>(sum);
+    if (e < n8) {
+        const int c = e / k8, f = e - c * k8, un = f >> 1;   // 16-byte unit un, half f & 1
+        uint8_t* base = lds + (size_t)c * (K + (K >> 2));
+        const uint32_t lo = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)q3 << 24);
+        const uint32_t hi = (uint32_t)(q4 & 0xff) | ((uint32_t)(q5 & 0xff) << 8) | ((uint32_t)(q6 & 0xff) << 16) | ((uint32_t)q7 << 24);
+        *(uint2*)(base + (size_t)((un & 3) * kq + (un >> 2)) * 16 + (f & 1) * 8) = make_uint2(lo, hi);
+        if ((f & 3) == 0) {
+            const int sb = f >> 2;
+            float* dsq = (float*)(base + (size_t)K + (size_t)(sb >> 1) * 16);
+            dsq[sb & 1] = dd;
+            dsq[2 + (sb & 1)] = dd * (float)sum;
         }
     }
+}
+
+template <int NCOL, int U, int BS = kPairBlock>
+__device__ __forceinline__ void stagef_store(uint8_t* lds, int K, const XStageF<NCOL, U>& S) {
+    const int n8 = NCOL * (K >> 3);
+#pragma unroll
+    for (int u = 0; u < U; ++u)                               // n8 is a multiple of 4: quads share e < n8
+        stagef_store_one(lds, K, S.v[u][0], S.v[u][1], (int)threadIdx.x + BS * u, n8);
 }
 
 // Same layout, loop form for any K (used when the whole x does not fit the register batch).

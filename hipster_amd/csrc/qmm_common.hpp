@@ -240,6 +240,14 @@ int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K,
 int launch_moe_gemm_fmt(int fmt, int sfmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles,
                         const int* counts, int max_tiles, const int* rowtab, const uint16_t* A, float* D, int N, int K,
                         hipStream_t s);
+// the MoE decode step of qmm_moe_decode (moe.hip): argument checks, and the two launches with the gate /
+// up rows in gu (2 * T * (topk + 1) * F floats)
+int moe_decode_check(int fmt, const void* Wg, const void* Wu, const void* Wd, const void* Sg, const void* Su, const void* Sd,
+                     const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H, int F, const int* ids,
+                     const float* w, const float* y);
+int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg, const void* Su,
+                   const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H, int F, int* ids,
+                   float* w, float* gu, float* y, hipStream_t s);
 // MoE decode gather / down (qmm_gemv_moe) for the routed formats other than all-Q4_K (gemv_fmt.hip)
 int moe_fmt_dispatch(int fmt, int sfmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x, int N, int K,
                      int T, int xrow_te, hipStream_t s);

@@ -232,6 +232,21 @@ int qmm_moe_router(const float* Wr, const float* x, float* logits, int* ids, flo
  * (a different, equally exact, Q4_K decode). */
 int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x,
                  int N, int K, int T, int xrow_te, void* stream);
+/* The whole MoE decode step in two launches at T = 1, three at T = 2..8 (no reference counterpart as one
+ * function: the reference runs fn::moe_route, gemv_moe gate|up, fn::moe_silu_quant and gemv_moe down,
+ * qwen4exp.cpp:345-354): at T = 1 the routing of logits [T][stride] (nexp_total experts, the shared gate
+ * at column nexp_total, top-k) runs inside the gate|up gather (at T > 1 it runs once before it), and
+ * silu(gate) * up is quantised inside the down projection's staging.
+ * Outputs: ids / w [T][topk+1] as qmm_moe_route_n writes them, y [T][H] = the slot-ordered combine.  The
+ * gate and up rows go to the caller's workspace ws (qmm_moe_decode_ws_bytes(T, topk, F) bytes).  Bitwise
+ * the four calls qmm_moe_route_n, qmm_gemv_moe (gate|up), qmm_moe_silu_quant, qmm_gemv_moe (down).
+ * fmt Q4_K for routed and shared experts (gate, up [F][H] at Wg / Wu + e * ebytes_gu; down [H][F] at
+ * Wd + e * ebytes_d; shared Sg, Su, Sd); x q8 [T][H]; T <= 8, topk + 1 <= 16, H and F multiples of 256,
+ * at most 6144. */
+int qmm_moe_decode(int fmt, const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg,
+                   const void* Su, const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H,
+                   int F, int* ids, float* w, float* ws, size_t ws_bytes, float* y, void* stream);
+size_t qmm_moe_decode_ws_bytes(int T, int topk, int F);
 /* h = silu(gate) * up quantised per 32 into xq, rows x n (reference: fn::moe_silu_quant, fn.h:48,
  * fn.hip:206-211,305) */
 int qmm_moe_silu_quant(const float* gate, const float* up, qmm_xq8 xq, int rows, int n, void* stream);

@@ -210,3 +210,48 @@ def test_moe_combine_sorted(gpu):
     qmm.moe_combine_sorted(dev(down), dev(w), dev(kpos), y, T, nexp, E)
     ref = np.einsum("te,ted->td", w.astype(np.float64), down[kpos.reshape(T, nexp)].astype(np.float64))
     assert rel_l2(host(y), ref) <= 1e-6
+
+
+@pytest.mark.parametrize("T,n_exp", [(1, 512), (4, 512), (8, 512), (3, 40)])
+def test_moe_decode_two_launches_bitwise(gpu, T, n_exp):
+    """qmm_moe_decode (routing inside the gate|up gather, silu*up -> q8 inside the down staging) against the
+    four-launch sequence it replaces on the same inputs: ids, weights and y bit for bit.  Then y against the
+    oracle's down projection + combine fed with the device's q8 h and routing (1e-5: every stage after the
+    device exp of silu pinned)."""
+    print(f"moe_decode T={T} n_exp={n_exp}", flush=True)
+    nexp = 11
+    Wg_h, Wu_h, Wd_h = experts(1260, n_exp, F, H), experts(1261, n_exp, F, H), experts(1262, n_exp, H, F)
+    Sg_h, Su_h, Sd_h = (synth.matrix(1263 + i, synth.Q4_K, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
+    W = [dev(a) for a in (Wg_h, Wu_h, Wd_h, Sg_h, Su_h, Sd_h)]
+    x = synth.normal_f32(1266 + T, (T, H))
+    lg = dev(synth.router_logits(1267 + T, T, n_exp))
+    xb = qmm.XQ8Buf(T, H)
+    qmm.quantize_x_q8(dev(x), xb, T, H)
+    # four launches
+    ids = torch.zeros((T, nexp), dtype=torch.int32, device="cuda")
+    w = torch.zeros((T, nexp), dtype=torch.float32, device="cuda")
+    qmm.moe_route_n(lg, ids, w, T, n_exp, n_exp + 1, 10)
+    g = torch.zeros((T * nexp, F), device="cuda"); u = torch.zeros((T * nexp, F), device="cuda")
+    qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [W[0], W[1]], [W[3], W[4]], [g, u], Wg_h[0].nbytes, ids, nexp, xb, F, H, T, False)
+    hq = qmm.XQ8Buf(T * nexp, F)
+    qmm.moe_silu_quant(g, u, hq, T * nexp, F)
+    y = torch.zeros((T, H), device="cuda")
+    qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [W[2]], [W[5]], [y], Wd_h[0].nbytes, ids, nexp, hq, H, F, T, True, slotw=w)
+    # two launches
+    ids2 = torch.full((T, nexp), -7, dtype=torch.int32, device="cuda")
+    w2 = torch.zeros((T, nexp), dtype=torch.float32, device="cuda")
+    ws = torch.zeros(qmm.moe_decode_ws_bytes(T, 10, F) // 4, dtype=torch.float32, device="cuda")
+    y2 = torch.full((T, H), float("nan"), device="cuda")
+    qmm.moe_decode(synth.Q4_K, W[0], W[1], W[2], Wg_h[0].nbytes, Wd_h[0].nbytes, W[3], W[4], W[5], lg, n_exp + 1, n_exp, 10, xb,
+                   T, H, F, ids2, w2, ws, y2)
+    assert np.array_equal(host(ids2), host(ids))
+    assert np.array_equal(host(w2).view(np.uint32), host(w).view(np.uint32))
+    assert np.array_equal(host(y2).view(np.uint32), host(y).view(np.uint32))
+    # the gate / up rows in the workspace are the gather's
+    gu = host(ws).reshape(2, T * nexp, F)
+    assert np.array_equal(gu[0].view(np.uint32), host(g).view(np.uint32)) and np.array_equal(gu[1].view(np.uint32), host(u).view(np.uint32))
+    _, y_ref = oracle.moe_down_q8(synth.Q4_K, Wd_h, Sd_h, host(hq.q), host(hq.d), host(ids), host(w), H, F)
+    assert rel_l2(host(y2), y_ref) <= 1e-5
+    with pytest.raises(qmm.QmmError, match="WORKSPACE"):
+        qmm.moe_decode(synth.Q4_K, W[0], W[1], W[2], Wg_h[0].nbytes, Wd_h[0].nbytes, W[3], W[4], W[5], lg, n_exp + 1, n_exp, 10,
+                       xb, T, H, F, ids2, w2, ws[:8], y2)
