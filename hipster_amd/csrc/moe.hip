@@ -6,6 +6,7 @@
 //   qmm_gemv_moe                      hip::gemv_moe        engine/kernels/gemv.hip:1075-1129,1385-1394
 //   qmm_moe_silu_quant                fn::moe_silu_quant   engine/kernels/fn.hip:206-211,305
 //   qmm_moe_combine_sorted            fn::moe_combine_sorted engine/kernels/fn.hip:126-132,295-297
+//   qmm_moe_decode                    (route, gate|up, silu-q8, down: qwen4exp.cpp:345-354 in one call)
 //
 // Expert gather (gate|up, or any call without slot weights): the reference launches one thread
 // group per (token, slot, row block), so an expert picked by several tokens, and the shared expert
@@ -274,8 +275,8 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
 // workgroup of the gate|up gather first routes the token itself (route_token, the arithmetic of
 // k_moe_route, so ids and weights are the same bits), then deduplicates and gathers exactly as
 // k_gemv_moe_q4k; workgroup (0, 0, 0) writes ids and weights out.  At T = 2..8 the routing work
-// would repeat in each of the T * (topk + 1) * rowblocks workgroups, so k_moe_route runs once first
-// and k_gemv_moe_q4k gathers.  The last launch stages h = silu(gate) * up of the token's slot rows, quantised per 32, straight into the
+// would repeat in each of the T * (topk + 1) * rowblocks workgroups, so the step is the four
+// launches k_moe_route, k_gemv_moe_q4k, k_moe_silu_quant, k_gemv_moe_down_q4k.  At T = 1 the last launch stages h = silu(gate) * up of the token's slot rows, quantised per 32, straight into the
 // down GEMV's LDS layout (the arithmetic of k_moe_silu_quant: the same q8 bits), then runs the down
 // projection and the slot-ordered combine of k_gemv_moe_down_q4k.  The four-launch sequence
 // moe_route, gemv_moe (gate|up), moe_silu_quant, gemv_moe (down) gives the same y bit for bit.
@@ -517,7 +518,7 @@ int moe_decode_check(int fmt, const void* Wg, const void* Wu, const void* Wd, co
     return QMM_OK;
 }
 
-// the two launches, gate / up rows in gu (2 * T * (topk + 1) * F floats)
+// the launches, gate / up rows in gu (2 * T * (topk + 1) * F floats, then at T > 1 the q8 of h)
 int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg, const void* Su,
                    const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H, int F, int* ids,
                    float* w, float* gu, float* y, hipStream_t s) {
@@ -533,10 +534,17 @@ int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes
            : nexp_total <= 512 ? decode_gather_vpl<8>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
                                : decode_gather_vpl<16>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s);
     } else {
-        // every gather workgroup would route all T tokens again: route once instead
+        // every gather workgroup would route all T tokens again, and every down workgroup would
+        // redo silu-q8 of all the token's rows: route once, quantise h once (the four launches)
         rc = qmm_moe_route_n(logits, ids, w, T, nexp_total, stride, topk, s);
         if (rc == QMM_OK)
             rc = moe_lpr(H) == 8 ? launch_gather<8>(ga, 2, ids, nexp, x, F, H, T, 0, s) : launch_gather<16>(ga, 2, ids, nexp, x, F, H, T, 0, s);
+        const size_t nh = (size_t)T * nexp * F;
+        const qmm_xq8 h = {(int8_t*)(up + nh), up + nh + nh / 4, up + nh + nh / 4 + nh / 32};
+        if (rc == QMM_OK) rc = qmm_moe_silu_quant(gate, up, h, T * nexp, F, s);
+        if (rc != QMM_OK) return rc;
+        const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
+        return moe_lpr(F) == 8 ? launch_down<8>(da, ids, nexp, h, H, F, T, s) : launch_down<16>(da, ids, nexp, h, H, F, T, s);
     }
     if (rc != QMM_OK) return rc;
     const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
@@ -616,7 +624,9 @@ int qmm_moe_decode(int fmt, const void* Wg, const void* Wu, const void* Wd, size
 }
 
 size_t qmm_moe_decode_ws_bytes(int T, int topk, int F) {
-    return T <= 0 || topk < 1 || F <= 0 ? 0 : (size_t)2 * T * (topk + 1) * F * sizeof(float);
+    // gate and up rows (f32); at T > 1 also h = silu(gate) * up as q8 (bytes, then d and s per 32)
+    const size_t nh = T <= 0 || topk < 1 || F <= 0 ? 0 : (size_t)T * (topk + 1) * F;
+    return nh * 2 * sizeof(float) + (T > 1 ? nh + nh / 32 * 2 * sizeof(float) : 0);
 }
 
 int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, float* y, int T, int nexp, int E, void* stream) {

@@ -23,11 +23,11 @@ void ref_quantize_row_q8_0_soa(const float* x, uint8_t* dst, uint64_t K) { hip::
 // nthreads std::threads as the engine's parallel_rows (qwen4exp.cpp:27-31).  The row body is compiled
 // for the host's best vector ISA at run time (target_clones), the -march=native equivalent for a
 // library built here and run on another host.
+// (w: the thread's dequantised row, allocated by the caller: no library templates inside the clones)
 __attribute__((target_clones("arch=x86-64-v4", "arch=x86-64-v3", "default")))
-static void rows_f32(int type, const uint8_t* W, size_t rb, int K, const float* x, float* y, int r0, int r1) {
-    std::vector<float> w((size_t)K);
+static void rows_f32(int type, const uint8_t* W, size_t rb, int K, const float* x, float* y, int r0, int r1, float* w) {
     for (int r = r0; r < r1; ++r) {
-        hip::dequant_row(type, W + (size_t)r * rb, w.data(), (uint64_t)K);
+        hip::dequant_row(type, W + (size_t)r * rb, w, (uint64_t)K);
         float acc = 0.f;
         for (int k = 0; k < K; ++k) acc += w[k] * x[k];
         y[r] = acc;
@@ -35,9 +35,11 @@ static void rows_f32(int type, const uint8_t* W, size_t rb, int K, const float* 
 }
 int ref_gemv_f32_threads(int type, const uint8_t* W, size_t row_bytes, int N, int K, const float* x, float* y, int nthreads) {
     if (nthreads < 1) nthreads = 1;
+    std::vector<float> rowbuf((size_t)K * nthreads);
     std::vector<std::thread> th;
     for (int i = 0; i < nthreads; ++i)
-        th.emplace_back(rows_f32, type, W, row_bytes, K, x, y, (int)((long long)N * i / nthreads), (int)((long long)N * (i + 1) / nthreads));
+        th.emplace_back(rows_f32, type, W, row_bytes, K, x, y, (int)((long long)N * i / nthreads), (int)((long long)N * (i + 1) / nthreads),
+                        rowbuf.data() + (size_t)K * i);
     for (auto& t : th) t.join();
     return 0;
 }

@@ -213,9 +213,10 @@ def test_moe_combine_sorted(gpu):
 
 
 @pytest.mark.parametrize("T,n_exp", [(1, 512), (4, 512), (8, 512), (3, 40)])
-def test_moe_decode_two_launches_bitwise(gpu, T, n_exp):
-    """qmm_moe_decode (routing inside the gate|up gather, silu*up -> q8 inside the down staging) against the
-    four-launch sequence it replaces on the same inputs: ids, weights and y bit for bit.  Then y against the
+def test_moe_decode_step_bitwise(gpu, T, n_exp):
+    """qmm_moe_decode (T = 1: routing inside the gate|up gather, silu*up -> q8 inside the down staging; T > 1:
+    the four launches) against the four-launch sequence of separate calls on the same inputs: ids, weights
+    and y bit for bit.  Then y against the
     oracle's down projection + combine fed with the device's q8 h and routing (1e-5: every stage after the
     device exp of silu pinned)."""
     print(f"moe_decode T={T} n_exp={n_exp}", flush=True)
@@ -248,8 +249,13 @@ def test_moe_decode_two_launches_bitwise(gpu, T, n_exp):
     assert np.array_equal(host(w2).view(np.uint32), host(w).view(np.uint32))
     assert np.array_equal(host(y2).view(np.uint32), host(y).view(np.uint32))
     # the gate / up rows in the workspace are the gather's
-    gu = host(ws).reshape(2, T * nexp, F)
+    NS = T * nexp
+    gu = host(ws)[:2 * NS * F].reshape(2, NS, F)
     assert np.array_equal(gu[0].view(np.uint32), host(g).view(np.uint32)) and np.array_equal(gu[1].view(np.uint32), host(u).view(np.uint32))
+    if T > 1:   # then the q8 of h, as moe_silu_quant writes it
+        hb = host(ws)[2 * NS * F:].view(np.uint8)
+        assert np.array_equal(hb[:NS * F].view(np.int8), host(hq.q).reshape(-1))
+        assert np.array_equal(hb[NS * F:].view(np.float32), np.concatenate([host(hq.d).reshape(-1), host(hq.s).reshape(-1)]))
     _, y_ref = oracle.moe_down_q8(synth.Q4_K, Wd_h, Sd_h, host(hq.q), host(hq.d), host(ids), host(w), H, F)
     assert rel_l2(host(y2), y_ref) <= 1e-5
     with pytest.raises(qmm.QmmError, match="WORKSPACE"):
