@@ -93,6 +93,9 @@ SIGNATURES = {
     "qmm_moe_decode": (c_int, [c_int, c_vp, c_vp, c_vp, ctypes.c_size_t, ctypes.c_size_t, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int,
                                XQ8, c_int, c_int, c_int, c_vp, c_vp, c_vp, ctypes.c_size_t, c_vp, c_vp]),
     "qmm_moe_decode_ws_bytes": (ctypes.c_size_t, [c_int, c_int, c_int]),
+    "qmm_moe_decode_noalloc": (c_int, [c_int, c_vp, c_vp, c_vp, ctypes.c_size_t, ctypes.c_size_t, c_vp, c_vp, c_vp, c_vp, c_int, c_int,
+                                       c_int, XQ8, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp]),
+    "qmm_moe_decode_scratch_max": (ctypes.c_size_t, []),
     "qmm_moe_combine_sorted": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     "qmm_dequant_bf16": (c_int, [c_int, c_vp, c_vp, c_int, c_int, c_vp]),
     "qmm_moe_sort": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),

@@ -6,7 +6,7 @@
 //   qmm_gemv_moe                      hip::gemv_moe        engine/kernels/gemv.hip:1075-1129,1385-1394
 //   qmm_moe_silu_quant                fn::moe_silu_quant   engine/kernels/fn.hip:206-211,305
 //   qmm_moe_combine_sorted            fn::moe_combine_sorted engine/kernels/fn.hip:126-132,295-297
-//   qmm_moe_decode                    (route, gate|up, silu-q8, down: qwen4exp.cpp:345-354 in one call)
+//   qmm_moe_decode / _noalloc         (route, gate|up, silu-q8, down: qwen4exp.cpp:345-354 in one call)
 //
 // Expert gather (gate|up, or any call without slot weights): the reference launches one thread
 // group per (token, slot, row block), so an expert picked by several tokens, and the shared expert
@@ -23,6 +23,14 @@
 #include "qmm_common.hpp"
 
 #include <hip/hip_runtime.h>
+
+#include <mutex>
+
+// Workspace of qmm_moe_decode_noalloc: one copy per GPU, held until the process ends.  Host code
+// never passes this name to a kernel or a copy (on the host it is only a stand-in for the symbol):
+// moe_scratch() looks up each device's address once and every use goes through that pointer.
+constexpr size_t kDecScratchBytes = (size_t)2 << 20;
+static __device__ __align__(256) uint8_t scratch[kDecScratchBytes];
 
 namespace qmm {
 namespace {
@@ -552,6 +560,23 @@ int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes
                            : launch_decode_down<16>(da, ids, nexp, gate, up, H, F, T, s);
 }
 
+// the device address of `scratch` on the current device, looked up on the first call per device
+int moe_scratch(void** out) {
+    constexpr int kMaxDev = 64;
+    static std::mutex mu;
+    static void* ptr[kMaxDev] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return QMM_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return QMM_ERR_LAUNCH;
+        ptr[dev] = p;
+    }
+    *out = ptr[dev];
+    return QMM_OK;
+}
+
 }  // namespace qmm
 
 using namespace qmm;
@@ -621,6 +646,22 @@ int qmm_moe_decode(int fmt, const void* Wg, const void* Wu, const void* Wd, size
     if (ws_bytes < qmm_moe_decode_ws_bytes(T, topk, F)) return QMM_ERR_WORKSPACE;
     return moe_decode_run(Wg, Wu, Wd, ebytes_gu, ebytes_d, Sg, Su, Sd, logits, stride, nexp_total, topk, x, T, H, F, ids, w, ws, y,
                           (hipStream_t)stream);
+}
+
+size_t qmm_moe_decode_scratch_max(void) { return kDecScratchBytes; }
+
+int qmm_moe_decode_noalloc(int fmt, const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg,
+                           const void* Su, const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T,
+                           int H, int F, int* ids, float* w, float* y, void* stream) {
+    if (int e = moe_decode_check(fmt, Wg, Wu, Wd, Sg, Su, Sd, logits, stride, nexp_total, topk, x, T, H, F, ids, w, y)) return e;
+    if (qmm_moe_decode_ws_bytes(T, topk, F) > kDecScratchBytes) return QMM_ERR_WORKSPACE;
+    if (T == 0) return QMM_OK;
+    void* ws = nullptr;
+    if (int e = moe_scratch(&ws)) return e;
+    // every byte of the workspace that the step reads it has written first in the same call: nothing
+    // to clear.  Calls that overlap on one GPU (other streams, other threads) share it and race.
+    return moe_decode_run(Wg, Wu, Wd, ebytes_gu, ebytes_d, Sg, Su, Sd, logits, stride, nexp_total, topk, x, T, H, F, ids, w, (float*)ws,
+                          y, (hipStream_t)stream);
 }
 
 size_t qmm_moe_decode_ws_bytes(int T, int topk, int F) {

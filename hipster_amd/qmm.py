@@ -229,6 +229,18 @@ def moe_decode(fmt, Wg, Wu, Wd, ebytes_gu, ebytes_d, Sg, Su, Sd, logits, stride,
                                     _p(y), _stream(stream)), "moe_decode")
 
 
+def moe_decode_noalloc(fmt, Wg, Wu, Wd, ebytes_gu, ebytes_d, Sg, Su, Sd, logits, stride, nexp_total, topk, x, T, H, F, ids, w, y,
+                       stream=None):
+    """moe_decode with its workspace in the library's static per-GPU array (no allocation; calls that
+    overlap on one GPU race); QmmError(-5) when moe_decode_ws_bytes(T, topk, F) > moe_decode_scratch_max()."""
+    check(_lib.lib().qmm_moe_decode_noalloc(fmt, _p(Wg), _p(Wu), _p(Wd), ebytes_gu, ebytes_d, _p(Sg), _p(Su), _p(Sd), _p(logits),
+                                            stride, nexp_total, topk, x.c(), T, H, F, _p(ids), _p(w), _p(y), _stream(stream)),
+          "moe_decode_noalloc")
+
+
+def moe_decode_scratch_max():
+    return _lib.lib().qmm_moe_decode_scratch_max()
+
 
 def moe_combine_sorted(down, w, kpos, y, T, nexp, E, stream=None):
     """fn.h:38: y[t][d] = sum_e w[t*nexp+e] * down[kpos[t*nexp+e]][d] (E is an argument here)."""

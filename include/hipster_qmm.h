@@ -249,6 +249,16 @@ int qmm_moe_decode(int fmt, const void* Wg, const void* Wu, const void* Wd, size
                    const void* Su, const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H,
                    int F, int* ids, float* w, float* ws, size_t ws_bytes, float* y, void* stream);
 size_t qmm_moe_decode_ws_bytes(int T, int topk, int F);
+/* qmm_moe_decode without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The workspace is a static device array of qmm_moe_decode_scratch_max() bytes (2 MiB) per
+ * GPU, held until the process ends; QMM_ERR_WORKSPACE when qmm_moe_decode_ws_bytes(T, topk, F) exceeds
+ * it.  Allocates nothing.  Calls that overlap on one GPU (other streams or threads) share the array and
+ * race: serialise them.  Same arguments, limits and bits as qmm_moe_decode. */
+int qmm_moe_decode_noalloc(int fmt, const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d,
+                           const void* Sg, const void* Su, const void* Sd, const float* logits, int stride, int nexp_total,
+                           int topk, qmm_xq8 x, int T, int H, int F, int* ids, float* w, float* y, void* stream);
+size_t qmm_moe_decode_scratch_max(void);
 /* h = silu(gate) * up quantised per 32 into xq, rows x n (reference: fn::moe_silu_quant, fn.h:48,
  * fn.hip:206-211,305) */
 int qmm_moe_silu_quant(const float* gate, const float* up, qmm_xq8 xq, int rows, int n, void* stream);
