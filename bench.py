@@ -16,8 +16,9 @@ Prints ONE JSON line:
   value        -- whole-step throughput: algorithmic bytes (W + x f32 + y f32 = 50,225,152 B/step) / time
   roofline     -- the dominant kernel (the Q4_K GEMV) alone: the same algorithmic bytes / its average
                   launch duration (a graph of K back-to-back launches, HIP events), against 8 TB/s
-  cpu_baseline -- the oracle's restatement of the reference host path (per-row dequant_q4_K + fp32 dot),
-                  threaded over rows on this host, timed over a bounded sample (--cpu-seconds)
+  cpu_baseline -- the reference host path (per-row dequant_q4_K + fp32 dot) built from the reference's
+                  quant.h (the oracle's restatement when that is absent), on all host cores and on one,
+                  timed over a bounded sample (--cpu-seconds); the MoE configs get CPU legs under "extra"
 
 The other BASELINE configurations are measured too and reported under "extra" (parity-test
 shapes, not the headline): the dense decode layer at M = 1, 4, 8 (config 1), the MoE decode step at
@@ -321,12 +322,21 @@ def extra_cfg1(torch):
     return out
 
 
-def moe_tables(torch):
+def moe_tables(torch, keep_host=False):
+    """512 Q4_K experts (gate, up [512][F][H], down [512][H][F]) + the shared expert, on the device;
+    with keep_host the host arrays too (under "host", for the CPU legs)."""
     from hipster_amd import synth
     H, F, n_exp = 2048, 512, 512
-    gen = lambda i, N, K: torch.from_numpy(synth.experts(synth.SEEDS["cfg4"] + i, synth.Q4_K, n_exp, N, K)).cuda()
-    one = lambda i, N, K: torch.from_numpy(synth.matrix(synth.SEEDS["cfg4"] + 10 + i, synth.Q4_K, N, K)).cuda()
-    return dict(Wg=gen(0, F, H), Wu=gen(1, F, H), Wd=gen(2, H, F), Sg=one(0, F, H), Su=one(1, F, H), Sd=one(2, H, F))
+    hst = dict(Wg=synth.experts(synth.SEEDS["cfg4"], synth.Q4_K, n_exp, F, H),
+               Wu=synth.experts(synth.SEEDS["cfg4"] + 1, synth.Q4_K, n_exp, F, H),
+               Wd=synth.experts(synth.SEEDS["cfg4"] + 2, synth.Q4_K, n_exp, H, F),
+               Sg=synth.matrix(synth.SEEDS["cfg4"] + 10, synth.Q4_K, F, H),
+               Su=synth.matrix(synth.SEEDS["cfg4"] + 11, synth.Q4_K, F, H),
+               Sd=synth.matrix(synth.SEEDS["cfg4"] + 12, synth.Q4_K, H, F))
+    tb = {k: torch.from_numpy(v).cuda() for k, v in hst.items()}
+    if keep_host:
+        tb["host"] = hst
+    return tb
 
 
 def extra_cfg2(torch, tb):
@@ -429,21 +439,90 @@ def extra_cfg4(torch, tb):
             "distinct_experts_incl_shared": int(len(np.unique(ids.cpu().numpy())))}
 
 
-def cpu_baseline_gemv(W, x, N, K, seconds):
-    """The oracle's restatement of the reference host path (dequant_row + fp32 dot per row), threaded."""
-    import oracle
-    threads = min(16, os.cpu_count() or 1)
-    oracle.gemv_f32(0, W[:64], 64, K, x, nthreads=1)   # warm up code and pages
+def host_threads():
+    """All host cores this process may use, capped by the box's CPU share (OMP_NUM_THREADS, at most 16)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    try:
+        cap = int(os.environ.get("OMP_NUM_THREADS", "16"))
+    except ValueError:
+        cap = 16
+    return max(1, min(n, cap, 16))
+
+
+def timed_calls(fn, seconds):
     calls, t0 = 0, time.perf_counter()
     while True:
-        oracle.gemv_f32(0, W, N, K, x, nthreads=threads)
+        fn()
         calls += 1
         el = time.perf_counter() - t0
         if el >= seconds and calls >= 2:
-            break
-    return dict(value=round((W.nbytes + K * 4 + N * 4) * calls / el / 1e9, 2), unit="GB/s", cores=threads, kind="port",
-                sample=f"{calls} full calls of the 17408x5120 Q4_K GEMV at M=1 in {el:.1f} s (mean rate), oracle "
-                       f"qo_gemv_f32: per-row dequant_q4_K + fp32 dot, {threads} host threads")
+            return calls, el
+
+
+def cpu_baseline_gemv(W, x, N, K, seconds):
+    """The reference host path (bench_gemv.cpp:95-104: quant.h dequant_row + fp32 dot per row) on all
+    host cores and on one, compiled from the reference's own quant.h (oracle/_ref, kind "reference");
+    the oracle's restatement (kind "port") when that library was not built."""
+    import oracle
+    threads = host_threads()
+    if oracle.ref_lib() is not None:
+        kind, what = "reference", "reference quant.h dequant_row + f32 dot (oracle/_ref, ISA clones up to x86-64-v4)"
+        run = lambda nt: oracle.ref_gemv_f32(12, W, N, K, x, nthreads=nt)
+    else:
+        kind, what = "port", "oracle qo_gemv_f32: per-row dequant_q4_K + f32 dot"
+        run = lambda nt: oracle.gemv_f32(0, W, N, K, x, nthreads=nt)
+    run(threads)                                   # warm up code and pages
+    byts = W.nbytes + K * 4 + N * 4
+    calls, el = timed_calls(lambda: run(threads), seconds * 0.6)
+    c1, e1 = timed_calls(lambda: run(1), seconds * 0.4)
+    return dict(value=round(byts * calls / el / 1e9, 2), unit="GB/s", cores=threads, kind=kind,
+                single_thread={"value": round(byts * c1 / e1 / 1e9, 3), "unit": "GB/s", "cores": 1},
+                host_cpu_count=os.cpu_count(),
+                sample=f"{calls} full calls of the 17408x5120 Q4_K GEMV at M=1 in {el:.1f} s on {threads} threads, "
+                       f"{c1} in {e1:.1f} s on 1 (mean rates): {what}")
+
+
+def cpu_moe_legs(tb, seconds):
+    """CPU time of configs 2 and 4 on bounded samples, with the oracle's restatement of the reference's
+    host MoE (kind "port"): routing (softmax + top-10), then per slot dequant . dot for gate, up and
+    down and the slot-ordered combine; config 4 runs a sample of its 2048 tokens on all host cores."""
+    import numpy as np
+    import oracle
+    from hipster_amd import synth
+    hst = tb["host"]
+    H, F = 2048, 512
+    out = {}
+    lg = synth.router_logits(synth.SEEDS["cfg2"] + 100, 1, 512)
+    x = synth.normal_f32(synth.SEEDS["cfg2"] + 1, (1, H))
+
+    def dec():
+        ids, w = oracle.moe_route(lg, 512, 10)
+        oracle.moe_decode(0, hst["Wg"], hst["Wu"], hst["Wd"], hst["Sg"], hst["Su"], hst["Sd"], x, ids, w, H, F)
+    dec()
+    calls, el = timed_calls(dec, seconds * 0.4)
+    out["cfg2_T1"] = {"us_per_step": round(el / calls * 1e6, 1), "cores": 1, "kind": "port",
+                      "sample": f"{calls} T=1 steps (route + 11 slots of gate/up/down + combine) in {el:.1f} s"}
+    T, ntok = 2048, 64
+    logits = synth.router_logits(synth.SEEDS["cfg4"], T, 512, 1.1)
+    ids, w = oracle.moe_route(logits, 512, 10)
+    xb = (synth.normal_f32(synth.SEEDS["cfg4"] + 5, (T, H)).view(np.uint32) >> 16).astype(np.uint16)
+    toks = np.arange(0, T, T // ntok, dtype=np.int32)[:ntok]
+    threads = host_threads()
+    lgs = logits[toks]
+
+    def pre():     # the sample's routing, then its slots (ids / w of the full batch are the same rows)
+        oracle.moe_route(lgs, 512, 10)
+        oracle.moe_prefill_tokens(0, hst["Wg"], hst["Wu"], hst["Wd"], hst["Sg"], hst["Su"], hst["Sd"], xb, ids, w, H, F, toks,
+                                  nthreads=threads)
+    calls, el = timed_calls(pre, seconds * 0.6)
+    per_tok = el / calls / ntok
+    out["cfg4_T2048"] = {"ms_per_step_est": round(per_tok * T * 1e3, 1), "cores": threads, "kind": "port",
+                         "sample": f"{calls} passes over {ntok} of the 2048 tokens (every 32nd; route + per-slot "
+                                   f"dequant . dot + combine) in {el:.1f} s, scaled to 2048 tokens"}
+    return out
 
 
 def main():
@@ -511,9 +590,13 @@ def main():
         torch.cuda.empty_cache()
         extra = {"cfg1_dense_decode_layer": extra_cfg1(torch)}
         torch.cuda.empty_cache()
-        tb = moe_tables(torch)
+        tb = moe_tables(torch, keep_host=not args.no_cpu)
         extra["cfg2_moe_decode"] = extra_cfg2(torch, tb)
         extra["cfg4_moe_prefill"] = extra_cfg4(torch, tb)
+        if not args.no_cpu:
+            cpu = cpu_moe_legs(tb, args.cpu_seconds)
+            extra["cfg2_moe_decode"]["cpu_baseline_T1"] = cpu["cfg2_T1"]
+            extra["cfg4_moe_prefill"]["cpu_baseline"] = cpu["cfg4_T2048"]
         del tb
         torch.cuda.empty_cache()
         extra["cfg3_dense_prefill"] = extra_cfg3(torch)

@@ -56,6 +56,8 @@ const char* qmm_status_string(int status) {
         case QMM_ERR_WORKSPACE: return "workspace missing or too small";
         case QMM_ERR_ARG: return "invalid argument";
         case QMM_ERR_LAYOUT: return "weight layout not supported (the reference's experimental interleaved layouts)";
+        case QMM_ERR_IO: return "GGUF file missing, truncated, not GGUF v3, or a tensor past its end";
+        case QMM_ERR_NOT_FOUND: return "tensor or key not found";
         default: return "unknown status";
     }
 }

@@ -408,11 +408,12 @@ __global__ void __launch_bounds__(256) k_gemv_moe_down_q4k(qmm_moe_segs a, const
 // prefill combine over expert-sorted rows (fn.hip:126-132): y[t][d] = sum_e w[t*nexp+e] * down[kpos[t*nexp+e]][d]
 // one workgroup per token; thread i sums float4 columns i, i+256, ... in slot order
 __global__ void __launch_bounds__(256) k_moe_combine_sorted(const float* __restrict__ down, const float* __restrict__ w,
-                                                            const int* __restrict__ kpos, float* __restrict__ y, int nexp, int E) {
+                                                            const int* __restrict__ kpos, float* __restrict__ y, int nexp, int E,
+                                                            bool vec4) {
     const int t = blockIdx.x;
     const int* kp = kpos + (size_t)t * nexp;
     const float* wt = w + (size_t)t * nexp;
-    if ((E & 3) == 0) {
+    if (vec4) {                                          // E % 4 == 0, down and y 16-byte aligned
         const int E4 = E >> 2;
         for (int d4 = threadIdx.x; d4 < E4; d4 += 256) {
             float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -674,7 +675,8 @@ int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, f
     if (!down || !w || !kpos || !y) return QMM_ERR_NULL;
     if (T < 0 || nexp < 1 || E <= 0) return QMM_ERR_SHAPE;
     if (T == 0) return QMM_OK;
-    hipLaunchKernelGGL(k_moe_combine_sorted, dim3(T), dim3(256), 0, (hipStream_t)stream, down, w, kpos, y, nexp, E);
+    const bool vec4 = E % 4 == 0 && ((uintptr_t)down & 15) == 0 && ((uintptr_t)y & 15) == 0;
+    hipLaunchKernelGGL(k_moe_combine_sorted, dim3(T), dim3(256), 0, (hipStream_t)stream, down, w, kpos, y, nexp, E, vec4);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }

@@ -71,8 +71,12 @@ __device__ __forceinline__ void wave_range(int lo, int hi, int wave, int& wlo, i
     whi = min(hi, wlo + per);
 }
 
+// the sort key of an id: id + 1 (0 = the shared expert), ids outside [-1, nkeys - 2] clamped into
+// that range, so a bad router output sorts wrongly but never indexes outside the count tables
+__device__ __forceinline__ int sort_key(int id, int nkeys) { return min(max(id + 1, 0), nkeys - 1); }
+
 // pass 1: key counts of the wave's slots into cnt[wave * nkeys + key] (LDS, zeroed by the caller).
-// ids outside [-1, nkeys-2] are rejected by the host check; the kernel trusts them.  The ids are
+// The ids are
 // loaded kSortBatch per lane at a time, so the loads overlap instead of each waiting behind the
 // previous LDS atomic.
 __device__ __forceinline__ void sort_count(const int* __restrict__ ids, int lo, int hi, int nkeys, int* cnt) {
@@ -82,7 +86,7 @@ __device__ __forceinline__ void sort_count(const int* __restrict__ ids, int lo, 
 #pragma unroll
         for (int u = 0; u < kSortBatch; ++u) {      // unconditional (clamped) loads: no wait per load
             const int i = c0 + 64 * u + lane;
-            const int v = ids[min(i, hi - 1)] + 1;
+            const int v = sort_key(ids[min(i, hi - 1)], nkeys);
             kk[u] = i < hi ? v : -1;
         }
 #pragma unroll
@@ -103,7 +107,7 @@ __device__ __forceinline__ void sort_scatter(const int* __restrict__ ids, int lo
 #pragma unroll
         for (int u = 0; u < kSortBatch; ++u) {
             const int i = b0 + 64 * u + lane;
-            const int v = ids[min(i, hi - 1)] + 1;
+            const int v = sort_key(ids[min(i, hi - 1)], nkeys);
             kk[u] = i < hi ? v : 0;
         }
 #pragma unroll
@@ -276,7 +280,7 @@ __global__ void __launch_bounds__(kSortThreads) k_moe_sort_scatter(const int* __
 // 4-byte stores issued from the one sorting workgroup would all queue on a single CU)
 __global__ void __launch_bounds__(256) k_moe_rowtok(const int* __restrict__ kpos, int* __restrict__ rowtok, int ns, int nslot) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < ns) rowtok[kpos[i]] = i / nslot;
+    if (i < ns && (unsigned)kpos[i] < (unsigned)ns) rowtok[kpos[i]] = i / nslot;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -854,7 +858,7 @@ extern "C" {
 int qmm_moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* kpos, int* rowtok, qmm_moe_tile* tiles,
                  int* counts, void* stream) {
     if (!ids || !kpos || !rowtok || !tiles || !counts) return QMM_ERR_NULL;
-    if (T < 0 || nslot < 1 || nexperts < 1 || nexperts + 1 > kMaxKeys || maxc < 1) return QMM_ERR_SHAPE;
+    if (T < 0 || nslot < 1 || nexperts < 1 || nexperts + 1 > kMaxKeys || maxc < 1 || maxc > QMM_MOE_MAX_TILE_ROWS) return QMM_ERR_SHAPE;
     const int nkeys = nexperts + 1, ns = T * nslot;
     hipStream_t st = (hipStream_t)stream;
     // G workgroups of at least 1024 slots each, their counts (G x nkeys) held in rowtok until the

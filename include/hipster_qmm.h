@@ -296,12 +296,15 @@ int qmm_bf16_to_f32_seg(const uint16_t* x, int Nt, int off, int N, float* out, i
 int qmm_bf16_to_f32_seg2(const uint16_t* x, const uint16_t* x2, int Nt, int off, int N, float* out, int M, void* stream);
 
 /* ---- MoE prefill ---- */
+#define QMM_MOE_MAX_TILE_ROWS 128   /* rows per tile of the grouped GEMMs: qmm_moe_sort's maxc limit */
 /* Device-side replacement of the host sort of engine/src/qwen4exp.cpp:628-645: slots te = t*nslot + e
  * of ids [T][nslot] (id -1 = shared expert, else 0..nexperts-1) ordered by (id, te), stable.
  * kpos[te] = sorted position, rowtok[k] = token of sorted position k, tiles = tiles of <= maxc
  * consecutive positions of one expert, routed experts first (ascending id) then the shared expert
  * (expert -1); counts[0] = routed tiles, counts[1] = shared tiles (both written on the device: no
- * host sync).  tiles needs room for ceil(T*nslot/maxc) + nexperts + 1 entries.  nexperts <= 1024. */
+ * host sync).  tiles needs room for ceil(T*nslot/maxc) + nexperts + 1 entries.  nexperts <= 1024;
+ * 1 <= maxc <= QMM_MOE_MAX_TILE_ROWS.  Ids outside [-1, nexperts-1] are clamped into that range on
+ * the device (no host check: the ids live on the device). */
 int qmm_moe_sort(const int* ids, int T, int nslot, int nexperts, int maxc, int* kpos, int* rowtok, qmm_moe_tile* tiles,
                  int* counts, void* stream);
 /* Grouped expert GEMM over sorted rows (reference: moe_gemm, gemv.h:49-50, gemv.hip:909-969,1377-1381,

@@ -97,6 +97,8 @@ def ref_lib():
         L.ref_f32_to_f16.argtypes = [ctypes.c_float]
         L.ref_quantize_row_q8_0_soa.argtypes = [P, P, ctypes.c_uint64]
         L.ref_quantize_row_q8_0_soa.restype = None
+        L.ref_gemv_f32_threads.argtypes = [I, P, ctypes.c_size_t, I, I, P, P, I]
+        L.ref_gemv_f32_threads.restype = I
         _r = L
     return _r
 
@@ -230,6 +232,20 @@ def gemv_f32(fmt, W, N, K, x, nthreads=1):
     y = np.empty((x.shape[0], N), dtype=np.float32)
     if lib().qo_gemv_f32(fmt, _ptr(W), N, K, _ptr(x), x.shape[0], _ptr(y), nthreads) != 0:
         raise ValueError("gemv_f32")
+    return y
+
+
+def ref_gemv_f32(gtype, W, N, K, x, nthreads=1):
+    """The CPU baseline on the reference's own code (ref_shim.cpp: quant.h dequant_row + a sequential
+    f32 dot per row, rows over nthreads threads); gtype is the GGUF type id (12 = Q4_K).  None when
+    oracle/_ref was not built."""
+    L = ref_lib()
+    if L is None:
+        return None
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    y = np.empty(N, dtype=np.float32)
+    L.ref_gemv_f32_threads(gtype, _ptr(W), W.nbytes // N, N, K, _ptr(x), _ptr(y), nthreads)
     return y
 
 

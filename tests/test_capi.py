@@ -32,6 +32,9 @@ def test_version_and_status_strings():
     assert b"gfx950" in L.qmm_version()
     assert L.qmm_status_string(0) == b"ok"
     assert L.qmm_status_string(-1) == b"unsupported weight format"
+    for code in range(-9, 0):     # every status the header defines has its own text
+        assert L.qmm_status_string(code) != b"unknown status", code
+    assert L.qmm_status_string(-10) == b"unknown status"
 
 
 def test_row_bytes_and_repack_match_oracle():

@@ -210,6 +210,12 @@ def test_moe_combine_sorted(gpu):
     qmm.moe_combine_sorted(dev(down), dev(w), dev(kpos), y, T, nexp, E)
     ref = np.einsum("te,ted->td", w.astype(np.float64), down[kpos.reshape(T, nexp)].astype(np.float64))
     assert rel_l2(host(y), ref) <= 1e-6
+    # views 4 bytes off a 16-byte boundary take the scalar path: the same bits
+    dbuf = torch.zeros(NS * E + 1, device="cuda")
+    dbuf[1:] = dev(down).reshape(-1)
+    ybuf = torch.full((T * E + 1,), float("nan"), device="cuda")
+    qmm.moe_combine_sorted(dbuf[1:], dev(w), dev(kpos), ybuf[1:], T, nexp, E)
+    assert np.array_equal(host(ybuf[1:]).reshape(T, E).view(np.uint32), host(y).view(np.uint32))
 
 
 @pytest.mark.parametrize("T,n_exp", [(1, 512), (4, 512), (8, 512), (3, 40)])

@@ -55,6 +55,28 @@ def test_moe_sort_degenerate_routing(gpu):
     assert np.array_equal(host(tiles)[:c[0] + c[1]], np.concatenate([tl, st]))
 
 
+def test_moe_sort_refuses_tiles_over_128_rows(gpu):
+    ids = torch.zeros((4, 11), dtype=torch.int32, device="cuda")
+    with pytest.raises(qmm.QmmError, match="SHAPE"):
+        sort_on_gpu(host(ids), 512, maxc=qmm.MOE_TILE_ROWS + 1)
+    assert qmm.MOE_TILE_ROWS == 128
+
+
+def test_moe_sort_clamps_out_of_range_ids(gpu):
+    """ids outside [-1, n_exp-1] (a corrupt router output) sort as the nearest valid id: no index
+    leaves the buffers, and the result is the oracle's sort of the clamped ids"""
+    n_exp = 64
+    ids_h, _ = oracle.moe_route(synth.router_logits(1490, 300, n_exp, None), n_exp, 10)
+    bad = ids_h.copy()
+    bad[::7, 3] = 5000
+    bad[::11, 5] = -9
+    kpos, rowtok, tiles, counts, _ = sort_on_gpu(bad, n_exp)
+    kp, rt, tl, st = oracle.moe_sort(np.clip(bad, -1, n_exp - 1), qmm.MOE_TILE_ROWS)
+    c = host(counts)
+    assert np.array_equal(host(kpos), kp) and np.array_equal(host(rowtok), rt)
+    assert np.array_equal(host(tiles)[:c[0] + c[1]], np.concatenate([tl, st]))
+
+
 def dequant_experts_f32(Wd, n_exp, N, K):
     out = torch.zeros((n_exp, N, K), dtype=torch.int16, device="cuda")
     for e in range(n_exp):

@@ -184,6 +184,11 @@ def test_gemv_ref_linear_and_rows_variant():
     assert np.array_equal(yr, y[:, rows])
     yf = oracle.gemv_f32(oracle.Q4_K, W, 64, 1024, x, nthreads=3)
     np.testing.assert_allclose(yf, y, rtol=2e-5, atol=2e-5 * np.abs(y).max())
+    # the reference-code CPU baseline (quant.h dequant_row + f32 dot, threaded) computes the same GEMV
+    if oracle.ref_lib() is not None:
+        for nt in (1, 3):
+            yr = oracle.ref_gemv_f32(12, W, 64, 1024, x[0], nthreads=nt)
+            np.testing.assert_allclose(yr, y[0], rtol=2e-5, atol=2e-5 * np.abs(y[0]).max())
 
 
 # ----------------------------------------------------------------------------- routing / sort
