@@ -814,9 +814,17 @@ int check_gemv_shape(int fmt, int N, int K) {
 
 }  // namespace
 
+// Q4_K calls with at least this many columns run on the matrix cores (gemv_mfma.hip: the same bits;
+// at 17408 x 5120 it is the faster kernel from 4 columns on)
+int g_mfma_min_ncol = 4;
+
 int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
     if (fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA)
         return gemv_fmt_dispatch(fmt, W, x, y, N, K, ncol, s);
+    if (fmt == QMM_Q4_K && ncol >= g_mfma_min_ncol && ncol <= 16 && gemv_q4k_mfma_lds(K, ncol) <= kMfmaLdsMax) {
+        const qmm_gemv_seg seg = {QMM_Q4_K, W, y, N, K};
+        return gemv_q4k_mfma(&seg, 1, x, K, ncol, s);
+    }
     switch (ncol) {
         case 1: return launch_gemv_q8_ncol<1>(fmt, W, x, y, N, K, s);
         case 2: return launch_gemv_q8_ncol<2>(fmt, W, x, y, N, K, s);
@@ -830,11 +838,23 @@ int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, 
     }
 }
 
+int gemv_q8_dispatch_segs(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s) {
+    for (int i = 0; i < nseg; ++i)
+        if (int e = gemv_q8_dispatch(segs[i].fmt, segs[i].w, x, segs[i].y, segs[i].N, K, ncol, s)) return e;
+    return QMM_OK;
+}
+
 }  // namespace qmm
 
 using namespace qmm;
 
 extern "C" {
+
+int qmm_set_gemv_mfma_min_ncol(int n) {
+    const int prev = g_mfma_min_ncol;
+    g_mfma_min_ncol = n < 1 ? 1 : n;
+    return prev;
+}
 
 int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream) {
     if (!x || !out.q || !out.d || !out.s) return QMM_ERR_NULL;
@@ -889,6 +909,27 @@ int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void
         if (segs[i].K != segs[0].K) return QMM_ERR_SHAPE;
     }
     const int K = segs[0].K;
+    bool all_q4k = true;
+    for (int i = 0; i < nseg; ++i) all_q4k = all_q4k && segs[i].fmt == QMM_Q4_K;
+    // columns per launch: 16 (8, 4 when x of 16 columns does not fit the LDS budget)
+    int cpl = 16;
+    while (cpl > 1 && gemv_q4k_mfma_lds(K, cpl) > kMfmaLdsMax) cpl /= 2;
+    if (all_q4k && ncol >= g_mfma_min_ncol && cpl >= 2) {      // every segment in one launch per cpl columns
+        for (int c0 = 0; c0 < ncol; c0 += cpl) {
+            const int nc = ncol - c0 < cpl ? ncol - c0 : cpl;
+            qmm_xq8 xc = {x.q + (size_t)c0 * K, x.d + (size_t)c0 * (K / 32), x.s + (size_t)c0 * (K / 32), nullptr};
+            qmm_gemv_seg sc[4];
+            for (int i = 0; i < nseg; ++i) {
+                sc[i] = segs[i];
+                sc[i].y = segs[i].y + (size_t)c0 * segs[i].N;
+            }
+            // a tail pass of one column keeps the one-column kernel (the same bits)
+            const int e = nc >= g_mfma_min_ncol ? gemv_q4k_mfma(sc, nseg, xc, K, nc, (hipStream_t)stream)
+                                                : gemv_q8_dispatch_segs(sc, nseg, xc, K, nc, (hipStream_t)stream);
+            if (e) return e;
+        }
+        return QMM_OK;
+    }
     for (int c0 = 0; c0 < ncol; c0 += 8) {
         const int nc = ncol - c0 < 8 ? ncol - c0 : 8;
         qmm_xq8 xc = {x.q + (size_t)c0 * K, x.d + (size_t)c0 * (K / 32), x.s + (size_t)c0 * (K / 32), nullptr};

@@ -1,0 +1,244 @@
+// gemv_mfma.hip -- Q4_K decode GEMV for 2..16 columns on the int8 matrix cores of gfx950.
+//
+// Replaces, for Q4_K weights, the per-column dot4 work of the reference's gemv_q8 / gemv_multi /
+// gemv_wmma (engine/kernels/gemv.hip:602-682 is the reference's int8 WMMA form for gfx1151).
+//
+// v_mfma_i32_16x16x32_i8 multiplies A [16 x 32] by B [32 x 16]: lane l supplies A row l%16 and B
+// column l%16, k = 8(l/16)..8(l/16)+7 of each, and gets D[i][l%16] for i = 4(l/16)..+3.  Here A holds
+// x (rows = token slots) and B one 32-weight sub-block of 16 weight rows: a Q4_K pair j (qs bytes
+// 32j..32j+31 of a block) is two instructions, its low nibbles against sub-block 2j of x and its high
+// nibbles against sub-block 2j+1, on the same 8 bytes of row l%16 in lane l.  The int32 results are the
+// exact sub-block dots ia, ib of the dot4 kernels.
+//
+// Bitwise the dot4 kernels (q4k_pair.hpp): there, lane t of a row's 16 lanes adds the values of pair
+// tasks t, t+16, t+32, ... (task = 4 * block + j) in that order, and the 16 partial sums meet in the
+// xor butterfly 8, 4, 2, 1.  Here wave w of a workgroup takes blocks w, w+4, w+8, ... of one 16-row
+// tile, which are exactly the tasks of partial sums t = 4w + j, in the same order; each value is
+// q4k_pair_value of the same scales, x pair scales and integer dots; the 16 partial sums are then
+// combined in LDS in the butterfly's association order.  So every column is the same float as the
+// one-column kernels give, whatever the number of columns (T-invariant with them).
+//
+// Token slots: with MV = 1, 2 or 4 slots per lane group (ncol <= 4, 8, 16), token c sits in A row
+// 4(c / MV) + c % MV, so lane l's D values v < MV are tokens MV(l/16) + v: the float epilogue costs
+// MV evaluations per pair per lane whatever the slot rows left empty.
+#include "q4k_pair.hpp"
+#include "qmm_common.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace qmm {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaMaxSeg = 4;
+constexpr int kScaleRegs = 4;      // x pair-scale quadruples each thread loads ahead of the weights
+
+struct MSegs {
+    const uint8_t* w[kMfmaMaxSeg];
+    float* y[kMfmaMaxSeg];
+    int N[kMfmaMaxSeg];
+    int t0[kMfmaMaxSeg + 1];       // first 16-row tile of each segment; t0[nseg] = all tiles
+    int nseg;
+};
+
+__device__ __forceinline__ uint2 ld8(const void* p) { return *(const uint2*)p; }
+__device__ __forceinline__ long as_long(uint2 v) { return (long)(((unsigned long)v.y << 32) | v.x); }
+
+// One block (256 weights) of the lane's row: its header and 16 qs bytes of each pair couple (pairs
+// 2c, 2c+1 = qs bytes 64c..64c+63): lane group h reads bytes 64c + 16h..+15, whole 16-byte pieces.
+// A permlane32 swap of their second halves (groups 0, 1) with the first halves of groups 2, 3 leaves
+// every lane 8 bytes of pair 2c and 8 of pair 2c+1, at k offsets 8 kperm(h) within the pair,
+// kperm = {0, 2, 1, 3}; the A operand (x) is read at the same k offsets, so each MFMA sums the same
+// products as with k in order.
+struct MBlk {
+    uint4 hd;
+    uint4 q[2];
+    uint4 x[4];        // x of the lane's token slot, bytes 64j + 16h..+15 of the block (pair j)
+};
+
+__device__ __forceinline__ int kperm(int h) { return ((h & 1) << 1) | (h >> 1); }
+
+typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+
+// x through a buffer resource over the call's x: lanes of empty token slots use an offset past its
+// end, which reads zeros without touching memory
+__device__ __forceinline__ uint4 xload(__amdgpu_buffer_rsrc_t rx, uint32_t off) {
+    const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ void mblk_load(MBlk& B, const uint8_t* rp, __amdgpu_buffer_rsrc_t rx, uint32_t xo, int b, int h) {
+    const uint8_t* bp = rp + (size_t)b * 144;
+    B.hd = ld16(bp);
+    B.q[0] = ld16(bp + 16 + 16 * h);
+    B.q[1] = ld16(bp + 80 + 16 * h);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) B.x[j] = xload(rx, xo + (uint32_t)(b * 256 + 64 * j));
+}
+
+// {lane's 8 bytes of pair 2c, lane's 8 bytes of pair 2c+1} from the couple's 16-byte piece
+__device__ __forceinline__ void couple_split(const uint4 v, uint2& p0, uint2& p1) {
+    const auto sx = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+    const auto sy = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+    p0 = make_uint2(sx[0], sy[0]);
+    p1 = make_uint2(sx[1], sy[1]);
+}
+
+// adds block b's pair values to acc; a block past the row's end (live = false, b clamped by the
+// caller) adds +0, which leaves every partial sum unchanged (a sum started at +0 is never -0)
+// The x piece of pair j (sub-block 2j = bytes 0..31, 2j+1 = bytes 32..63) splits the same way as a
+// weight couple: after the swap the lane holds 8 bytes of each sub-block at k offsets 8 kperm(h).
+template <int MV>
+__device__ __forceinline__ void mblk_compute(const MBlk& B, int b, int h, bool live, const float4* __restrict__ sds,
+                                             float (&acc)[4][MV]) {
+    constexpr int NS = 4 * MV;
+    uint2 q[4];
+    couple_split(B.q[0], q[0], q[1]);
+    couple_split(B.q[1], q[2], q[3]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint2 lo = make_uint2(q[j].x & 0x0f0f0f0fu, q[j].y & 0x0f0f0f0fu);
+        const uint2 hi = make_uint2((q[j].x >> 4) & 0x0f0f0f0fu, (q[j].y >> 4) & 0x0f0f0f0fu);
+        uint2 x0, x1;
+        couple_split(B.x[j], x0, x1);
+        const i32x4 z = {0, 0, 0, 0};
+        const i32x4 ca = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(x0), as_long(lo), z, 0, 0, 0);
+        const i32x4 cb = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(x1), as_long(hi), z, 0, 0, 0);
+        const Q4kPairScales sc = q4k_pair_scales(B.hd, Q4kPairDecode(j));
+        const float4* dsp = sds + (size_t)(4 * b + j) * NS + h * MV;
+#pragma unroll
+        for (int v = 0; v < MV; ++v) acc[j][v] += live ? q4k_pair_value(sc, dsp[v], ca[v], cb[v]) : 0.f;
+    }
+}
+
+constexpr int kMfmaMaxK = 32768;
+
+// grid = all 16-row tiles of all segments, 256 threads; LDS: x pair scales [K/64][4 MV] float4, after
+// the main loop reused for the partial sums [16][4 MV][16] float
+template <int MV>
+__global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                       const float* __restrict__ xs, int K, int ncol) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NS = 4 * MV;
+    const int tile = blockIdx.x;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < kMfmaMaxSeg; ++i)
+        if (i < sg.nseg && tile >= sg.t0[i]) si = i;
+    const int N = sg.N[si], row0 = (tile - sg.t0[si]) * 16;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = lane & 15, h = lane >> 4;
+    const int nb = K >> 8, nsb = K >> 5, npair = K >> 6;
+    const uint8_t* rp = sg.w[si] + (size_t)min(row0 + r, N - 1) * ((size_t)nb * 144);
+    float4* sds = (float4*)smem;
+    float* part = (float*)smem;
+    // A operand source of this lane: x of the token in slot r (zeros for an empty slot), 16-byte
+    // piece h of each pair
+    const int ca = (r >> 2) * MV + (r & 3);
+    const bool aval = (r & 3) < MV && ca < ncol;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, ncol * K, 0x00020000);
+    const uint32_t xo = aval ? (uint32_t)(ca * K + 16 * h) : 0x40000000u;
+
+    // x pair scales {d[2p], d[2p+1], s[2p], s[2p+1]} of every (pair, token): item e = c * npair + p,
+    // thread tid taking items tid + 256 u, loaded (unconditionally, clamped) before the first weights
+    // so that their LDS stores wait for them only (loads retire in issue order).  c = e / npair by a
+    // float reciprocal, exact for these small integers.
+    const int nitem = npair * ncol;
+    const float inv_np = 1.f / (float)npair;
+    float4 sv[kScaleRegs];
+#pragma unroll
+    for (int u = 0; u < kScaleRegs; ++u) {
+        const int e = min(tid + 256 * u, nitem - 1), c = (int)(((float)e + 0.5f) * inv_np), pp = e - c * npair;
+        const float2 dd = *(const float2*)(xd + (size_t)c * nsb + 2 * pp), ss = *(const float2*)(xs + (size_t)c * nsb + 2 * pp);
+        sv[u] = make_float4(dd.x, dd.y, ss.x, ss.y);
+    }
+    // every load below is unconditional (block indices clamped to the last block): with the same
+    // loads on every path the wait counts stay exact and each prefetch stays in flight
+    MBlk A, B;
+    mblk_load(A, rp, rx, xo, min(wave, nb - 1), h);
+#pragma unroll
+    for (int u = 0; u < kScaleRegs; ++u) {
+        const int e = tid + 256 * u, c = (int)(((float)e + 0.5f) * inv_np), pp = e - c * npair;
+        if (e < nitem) sds[pp * NS + c] = sv[u];
+    }
+    for (int e = tid + 256 * kScaleRegs; e < nitem; e += 256) {     // K * ncol > 128 K: the rest in a loop
+        const int c = (int)(((float)e + 0.5f) * inv_np), pp = e - c * npair;
+        const float2 dd = *(const float2*)(xd + (size_t)c * nsb + 2 * pp), ss = *(const float2*)(xs + (size_t)c * nsb + 2 * pp);
+        sds[pp * NS + c] = make_float4(dd.x, dd.y, ss.x, ss.y);
+    }
+    lds_barrier();
+
+    float acc[4][MV];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < MV; ++v) acc[j][v] = 0.f;
+    // two register sets in turn; no branch around a load or a compute (the compiler would sink the
+    // prefetch into it), and scheduling barriers keep each prefetch ahead of the compute it overlaps
+    for (int b = wave; b < nb; b += 8) {                  // wave-uniform
+        mblk_load(B, rp, rx, xo, min(b + 4, nb - 1), h);
+        __builtin_amdgcn_sched_barrier(0);
+        mblk_compute<MV>(A, b, h, true, sds, acc);
+        mblk_load(A, rp, rx, xo, min(b + 8, nb - 1), h);
+        __builtin_amdgcn_sched_barrier(0);
+        mblk_compute<MV>(B, min(b + 4, nb - 1), h, b + 4 < nb, sds, acc);
+    }
+    __syncthreads();                                      // every wave is done with the scales
+    // partial sum t = 4 wave + j of token MV h + v, row r
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < MV; ++v) part[((4 * wave + j) * NS + h * MV + v) * 16 + r] = acc[j][v];
+    __syncthreads();
+    const int orow = tid & 15, oc = tid >> 4;
+    if (oc < ncol && row0 + orow < N) {
+        float a[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) a[t] = part[(t * NS + oc) * 16 + orow];
+        // the association order of the xor butterfly 8, 4, 2, 1 (group_sum over 16 lanes)
+        float q[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) q[t] = a[t] + a[t + 8];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) q[t] = q[t] + q[t + 4];
+        q[0] = q[0] + q[2];
+        q[1] = q[1] + q[3];
+        sg.y[si][(size_t)oc * N + row0 + orow] = q[0] + q[1];
+    }
+}
+
+}  // namespace
+
+size_t gemv_q4k_mfma_lds(int K, int ncol) {
+    const int mv = ncol <= 4 ? 1 : ncol <= 8 ? 2 : 4;
+    const size_t scales = (size_t)(K / 64) * (4 * mv) * 16, parts = (size_t)16 * (4 * mv) * 16 * 4;
+    return K > kMfmaMaxK ? SIZE_MAX : scales > parts ? scales : parts;
+}
+
+// ncol (1..16) columns of q8 x against nseg (1..4) Q4_K segments sharing K, in one launch.  Shapes are
+// checked by the caller (K % 256 == 0, N > 0).
+int gemv_q4k_mfma(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s) {
+    if (nseg < 1 || nseg > kMfmaMaxSeg || ncol < 1 || ncol > 16) return QMM_ERR_SHAPE;
+    MSegs sg = {};
+    sg.nseg = nseg;
+    sg.t0[0] = 0;
+    for (int i = 0; i < nseg; ++i) {
+        sg.w[i] = (const uint8_t*)segs[i].w;
+        sg.y[i] = segs[i].y;
+        sg.N[i] = segs[i].N;
+        sg.t0[i + 1] = sg.t0[i] + (segs[i].N + 15) / 16;
+    }
+    const int mv = ncol <= 4 ? 1 : ncol <= 8 ? 2 : 4;
+    const size_t lds = gemv_q4k_mfma_lds(K, ncol);
+    if (lds > kMfmaLdsMax) return QMM_ERR_SHAPE;
+    const dim3 grid((unsigned)sg.t0[nseg]);
+    switch (mv) {
+        case 1: hipLaunchKernelGGL(k_gemv_q4k_mfma<1>, grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
+        case 2: hipLaunchKernelGGL(k_gemv_q4k_mfma<2>, grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
+        default: hipLaunchKernelGGL(k_gemv_q4k_mfma<4>, grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
+    }
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+}  // namespace qmm

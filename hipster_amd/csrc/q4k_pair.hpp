@@ -84,6 +84,27 @@ struct Q4kPairDecode {
     }
 };
 
+// The scales of pair j of a block header: dA, dB = d * sc[2j], d * sc[2j+1]; mA, mB = dmin * m[2j],
+// dmin * m[2j+1] (quant.h:37-40 decode).
+struct Q4kPairScales { float dA, dB, mA, mB; };
+__device__ __forceinline__ Q4kPairScales q4k_pair_scales(const uint4 hd, const Q4kPairDecode& dc) {
+    const uint32_t scw = (((hd.y >> dc.sh0) & dc.m0) | (hd.w & dc.m2)) >> dc.bsh;
+    const uint32_t mw = (((hd.z >> dc.sh0) & dc.m0) | ((hd.w >> 4) & dc.m2)) >> dc.bsh;
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    return {d * (float)(scw & 0xffu), d * (float)((scw >> 8) & 0xffu), dmin * (float)(mw & 0xffu),
+            dmin * (float)((mw >> 8) & 0xffu)};
+}
+
+// One pair's contribution to one column, ds = {dx[2p], dx[2p+1], sx[2p], sx[2p+1]} of x and ia, ib the
+// exact integer dots of sub-blocks 2j, 2j+1.  Evaluated in a fixed order (explicit fma, no contraction
+// left to the compiler), so every kernel that adds a row's pair values in the same order -- the dot4
+// kernels here, the matrix-core kernel of gemv_mfma.hip -- gets the same bits.
+__device__ __forceinline__ float q4k_pair_value(const Q4kPairScales& s, const float4 ds, int ia, int ib) {
+#pragma clang fp contract(off)
+    const float t = __builtin_fmaf(s.dB, ds.y * (float)ib, s.dA * (ds.x * (float)ia));
+    return t - __builtin_fmaf(s.mB, ds.w, s.mA * ds.z);
+}
+
 template <int NCOL, int I, bool XLDS, bool EXACT, int LPR = 16>
 __device__ __forceinline__ void q4k_pairs_compute(const Q4kPairs<I>& B, const Q4kPairDecode& dc, int t, int ntask, int it0,
                                                   const XPairSrc<XLDS>* xs, float* acc) {
@@ -91,11 +112,7 @@ __device__ __forceinline__ void q4k_pairs_compute(const Q4kPairs<I>& B, const Q4
     for (int i = 0; i < I; ++i) {
         const int task = t + LPR * (it0 + i);
         const uint4 hd = B.h[i], w0 = B.q0[i], w1 = B.q1[i];
-        const uint32_t scw = (((hd.y >> dc.sh0) & dc.m0) | (hd.w & dc.m2)) >> dc.bsh;
-        const uint32_t mw = (((hd.z >> dc.sh0) & dc.m0) | ((hd.w >> 4) & dc.m2)) >> dc.bsh;
-        const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-        const float dA = d * (float)(scw & 0xffu), dB = d * (float)((scw >> 8) & 0xffu);
-        const float mA = dmin * (float)(mw & 0xffu), mB = dmin * (float)((mw >> 8) & 0xffu);
+        const Q4kPairScales sc = q4k_pair_scales(hd, dc);
         const uint32_t a0 = w0.x & 0x0f0f0f0fu, a1 = w0.y & 0x0f0f0f0fu, a2 = w0.z & 0x0f0f0f0fu, a3 = w0.w & 0x0f0f0f0fu;
         const uint32_t a4 = w1.x & 0x0f0f0f0fu, a5 = w1.y & 0x0f0f0f0fu, a6 = w1.z & 0x0f0f0f0fu, a7 = w1.w & 0x0f0f0f0fu;
         const uint32_t b0 = (w0.x >> 4) & 0x0f0f0f0fu, b1 = (w0.y >> 4) & 0x0f0f0f0fu, b2 = (w0.z >> 4) & 0x0f0f0f0fu, b3 = (w0.w >> 4) & 0x0f0f0f0fu;
@@ -109,7 +126,7 @@ __device__ __forceinline__ void q4k_pairs_compute(const Q4kPairs<I>& B, const Q4
             ia = sdot4(a4, u1.x, ia); ia = sdot4(a5, u1.y, ia); ia = sdot4(a6, u1.z, ia); ia = sdot4(a7, u1.w, ia);
             int ib = sdot4(b0, u2.x, 0); ib = sdot4(b1, u2.y, ib); ib = sdot4(b2, u2.z, ib); ib = sdot4(b3, u2.w, ib);
             ib = sdot4(b4, u3.x, ib); ib = sdot4(b5, u3.y, ib); ib = sdot4(b6, u3.z, ib); ib = sdot4(b7, u3.w, ib);
-            const float v = dA * (ds.x * (float)ia) + dB * (ds.y * (float)ib) - (mA * ds.z + mB * ds.w);
+            const float v = q4k_pair_value(sc, ds, ia, ib);
             acc[c] += (EXACT || task < ntask) ? v : 0.f;
         }
     }

@@ -240,6 +240,15 @@ int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K,
 int launch_moe_gemm_fmt(int fmt, int sfmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles,
                         const int* counts, int max_tiles, const int* rowtab, const uint16_t* A, float* D, int N, int K,
                         hipStream_t s);
+// Q4_K GEMV of 1..16 columns over 1..4 segments sharing K on the int8 matrix cores, one launch
+// (gemv_mfma.hip); bitwise the dot4 kernels.  The dispatch of gemv.hip sends Q4_K calls of at least
+// g_mfma_min_ncol columns there.
+int gemv_q4k_mfma(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s);
+size_t gemv_q4k_mfma_lds(int K, int ncol);     // its LDS bytes; it runs when they are <= kMfmaLdsMax
+constexpr size_t kMfmaLdsMax = 120 * 1024;
+int gemv_q8_dispatch_segs(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s);
+extern int g_mfma_min_ncol;
+
 // the MoE decode step of qmm_moe_decode (moe.hip): argument checks, and the two launches with the gate /
 // up rows in gu (2 * T * (topk + 1) * F floats)
 int moe_decode_check(int fmt, const void* Wg, const void* Wu, const void* Wd, const void* Sg, const void* Su, const void* Sd,

@@ -1,0 +1,103 @@
+"""The Q4_K decode GEMV on the int8 matrix cores (gemv_mfma.hip), through the C ABI.
+
+Bars: every column bitwise equal to the one-column dot4 kernel's result for the same x (so a column's
+bits do not depend on ncol, 1..16, nor on which kernel ran), at the headline shape and at shapes whose
+block count is not a multiple of 4 or whose rows are not a multiple of 16; several segments in one
+launch equal separate calls; and the result against the oracle within the GEMV bar (1e-5).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hipster_amd import _lib, qmm, synth
+from tests.gpu_util import dev, host, max_rel_mag, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def q8_on_gpu(x):
+    ncol, K = x.shape
+    xb = qmm.XQ8Buf(ncol, K)
+    qmm.quantize_x_q8(dev(x), xb, ncol, K)
+    return xb
+
+
+class min_ncol:
+    """qmm_set_gemv_mfma_min_ncol for the duration of a block"""
+
+    def __init__(self, n):
+        self.n = n
+
+    def __enter__(self):
+        self.prev = _lib.lib().qmm_set_gemv_mfma_min_ncol(self.n)
+
+    def __exit__(self, *a):
+        _lib.lib().qmm_set_gemv_mfma_min_ncol(self.prev)
+
+
+def multi(Wd, xb, N, K, ncol):
+    y = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+    qmm.gemv_multi([(synth.Q4_K, Wd, y, N, K)], xb, ncol)
+    torch.cuda.synchronize()
+    return host(y)
+
+
+def test_columns_equal_one_column_kernel_ncol_1_to_16(gpu):
+    """17408 x 5120: for ncol = 1..16 every column is bitwise the one-column kernel's"""
+    N, K = 17408, 5120
+    print(f"mfma T-invariance N={N} K={K}", flush=True)
+    Wd = dev(synth.matrix(700, synth.Q4_K, N, K))
+    x = synth.normal_f32(701, (16, K))
+    xb = q8_on_gpu(x)
+    single = []
+    for c in range(16):
+        xc = q8_on_gpu(x[c:c + 1])
+        single.append(multi(Wd, xc, N, K, 1)[0])
+    single = np.stack(single)
+    for ncol in range(1, 17):
+        y = multi(Wd, xb, N, K, ncol)
+        assert np.array_equal(y.view(np.uint32), single[:ncol].view(np.uint32)), ncol
+    q, d, _ = oracle.quantize_x_q8(x)
+    ref, mag = oracle.gemv_ref(synth.Q4_K, host(Wd), N, K, oracle.q8_to_f32(q, d))
+    assert rel_l2(single, ref) <= 1e-5
+    assert max_rel_mag(single, ref, mag) < 1e-5
+
+
+@pytest.mark.parametrize("N,K", [(4099, 5120), (77, 768), (300, 1280), (16, 256), (1000, 17408), (33, 2048)])
+def test_mfma_equals_dot4_same_ncol(gpu, N, K):
+    """the same call with the matrix-core kernel switched off (dot4 kernels) and on: the same bits"""
+    print(f"mfma vs dot4 N={N} K={K}", flush=True)
+    Wd = dev(synth.matrix(710 + N, synth.Q4_K, N, K))
+    x = synth.normal_f32(711 + K, (16, K))
+    xb = q8_on_gpu(x)
+    for ncol in (2, 3, 4, 5, 8, 9, 16):
+        with min_ncol(17):
+            y0 = multi(Wd, xb, N, K, ncol)
+        with min_ncol(2):
+            y1 = multi(Wd, xb, N, K, ncol)
+        assert np.all(np.isfinite(y1))
+        assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32)), ncol
+    # gemv_q8 (up to 8 columns) takes the same route
+    y = torch.zeros((8, N), dtype=torch.float32, device="cuda")
+    qmm.gemv_q8(synth.Q4_K, Wd, xb, y, N, K, 8)
+    assert np.array_equal(host(y).view(np.uint32), y1[:8].view(np.uint32))
+
+
+@pytest.mark.parametrize("ncol", [2, 6, 16, 21])
+def test_segments_in_one_launch_equal_separate_calls(gpu, ncol):
+    K = 2048
+    Ns = [1024, 77, 513]
+    x = synth.normal_f32(720, (ncol, K))
+    xb = q8_on_gpu(x)
+    segs, ref = [], []
+    for i, N in enumerate(Ns):
+        Wh = synth.matrix(721 + i, synth.Q4_K, N, K)
+        W = dev(Wh)
+        y = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+        segs.append((synth.Q4_K, W, y, N, K))
+        ref.append(np.stack([multi(W, q8_on_gpu(x[c:c + 1]), N, K, 1)[0] for c in range(ncol)]))
+    qmm.gemv_multi(segs, xb, ncol)
+    torch.cuda.synchronize()
+    for (_, _, y, _, _), r in zip(segs, ref):
+        assert np.array_equal(host(y).view(np.uint32), r.view(np.uint32))
