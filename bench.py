@@ -221,6 +221,15 @@ def extra_formats(torch):
                           reps=2) / ncopy
             r[f"M{M}"] = {"us": round(us, 2), "GB_s": round(W.nbytes / us / 1e3, 1)}
         out[name] = r
+        if fmt == synth.Q4_K:      # the reference's f32-x GEMV (gemv_q4_K_f32) on the same weights
+            rf = {}
+            for M in (1, 4):
+                x = torch.randn((M, K), device="cuda")
+                y = torch.zeros((M, N), device="cuda")
+                us = graph_us(torch, [(lambda i: (lambda: qmm.gemv_q4_K_f32(Wd[i], x, y, N, K, M)))(i) for i in range(ncopy)],
+                              reps=2) / ncopy
+                rf[f"M{M}"] = {"us": round(us, 2), "GB_s": round(W.nbytes / us / 1e3, 1)}
+            out["Q4_K_gemv_q4_K_f32"] = rf
         del Wd, Wt
         torch.cuda.empty_cache()
     return out

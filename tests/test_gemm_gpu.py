@@ -126,6 +126,22 @@ def test_gemm_wq_other_formats(gpu, fmt, M, N, K):
     assert err <= 2e-3
 
 
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 768, 2048)])
+def test_gemm_wq_q4k_is_the_bf16_gemm_of_its_dequantisation(gpu, M, N, K):
+    """the fused Q4_K GEMM feeds the matrix cores exactly qmm_dequant_bf16's weights: rounded to bf16 its
+    f32 output equals, bit for bit, the bf16 GEMM (the same kernel body and K order) on the dequantised
+    rows"""
+    W = dev(synth.matrix(1460 + N, synth.Q4_K, N, K))
+    A = bf16_dev(synth.to_bf16_bits(synth.normal_f32(1461 + M, (M, K))))
+    D = torch.full((M, N), float("nan"), device="cuda")
+    qmm.gemm_wq(synth.Q4_K, W, A, D, M, N, K)
+    Wb = torch.zeros((N, K), dtype=torch.int16, device="cuda")
+    qmm.dequant_bf16(synth.Q4_K, W, Wb, N, K)
+    Db = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
+    qmm.gemm_bf16(A, Wb.view(torch.bfloat16), Db, M, N, K)
+    assert np.array_equal(synth.to_bf16_bits(host(D)), host(Db.view(torch.int16)).view(np.uint16))
+
+
 def test_gemm_deterministic(gpu):
     M, N, K = 512, 384, 1024
     W = dev(synth.matrix(1400, synth.Q4_K, N, K))
