@@ -651,7 +651,9 @@ constexpr bool kAsDeferStores = false;
 // f32 store the compiler does not see (address = wave-uniform base in SGPRs + per-lane 32-bit byte
 // offset): its waits for the weight loads issued before it are then computed over loads only (loads
 // complete in order, so such a wait can only last longer), instead of the full vmcnt(0) it places
-// once loads and stores are both outstanding.
+// once loads and stores are both outstanding.  Unlike the DMA helpers it carries no s_nop guard (64
+// stores per weight block): its base is only ever advanced by scalar adds, never reloaded by a VALU
+// instruction, which tests/test_asm_hazards.py checks on the compiled code.
 __device__ __forceinline__ void st_f32_nc(const uint8_t* base, uint32_t voff, float v) {
     asm volatile("global_store_dword %0, %1, %2" : : "v"(voff), "v"(v), "s"(base) : "memory");
 }

@@ -76,13 +76,21 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // LDS read, which waits for the DMA just issued for a later step and serialises the prefetch.  The
 // callers order DMA and LDS reads themselves (s_waitcnt vmcnt(n), then a barrier).  Loads the
 // compiler issues itself stay correct: a vmcnt it computes without counting these only waits longer.
+//
+// Every inline-assembly memory instruction here starts with s_nop 4 (5 wait states).  The compiler
+// cannot see that the assembly is a vector memory instruction, so it does not insert the wait states
+// the ISA requires between a VALU write of an SGPR and a vector memory instruction reading it (5),
+// or between an SALU write of M0 and an LDS DMA (1).  Without them a base address the compiler has
+// just reloaded with v_readlane (an SGPR spill) or moved into M0 can be read stale: a garbage global
+// address or LDS slot.
+#define QMM_VMEM_ASM_GUARD "s_nop 4\n\t"
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+    asm volatile(QMM_VMEM_ASM_GUARD "global_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 // The same with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset: per-step
 // address changes then cost scalar adds only.  base and lds must be wave-uniform.
 __device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
-    asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
+    asm volatile(QMM_VMEM_ASM_GUARD "global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 // A value the optimiser cannot see through (keeps a byte mask from being folded into the
