@@ -345,24 +345,22 @@ struct WRawQ4KHalf {
         q0 = ld16(bp + 16 + 32 * j);
         q1 = ld16(bp + 32 + 32 * j);
     }
-    // thread t: row t/2, sub-block 2j + (t&1): 32 bf16 -> chunks 4*(t&1)..+3 of the row
+    // thread t: row t/2, sub-block 2j + (t&1): 32 bf16 -> chunks 4*(t&1)..+3 of the row, each weight
+    // bf16(fmaf(dl, q, -ml)) through v_fma_mix_f32 (q4_bf16x8_mix: the low nibbles with dl * 2^24, the
+    // high ones in place with dl * 2^20)
     __device__ __forceinline__ void store(uint4* Lb, int k0) const {
         const int t = threadIdx.x, h = t & 1, row = t >> 1;
         const int sbi = 2 * ((k0 >> 6) & 3) + h;
         const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
         const Q4kScaleBytes sb = q4k_scale_bytes(hd.y, hd.z, hd.w);
         const float dl = d * (float)byte8(sb.sc_lo, sb.sc_hi, sbi), ml = dmin * (float)byte8(sb.m_lo, sb.m_hi, sbi);
+        const float s24 = dl * (h ? 1048576.f : 16777216.f);
+        const uint32_t m = h ? 0x00f000f0u : 0x000f000fu;
         const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            __bf16 v[8];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const uint32_t u = (h ? (qw[2 * c + e] >> 4) : qw[2 * c + e]) & 0x0f0f0f0fu;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) v[4 * e + b] = (__bf16)(dl * (float)((u >> (8 * b)) & 0xffu) - ml);
-            }
-            Lb[swz(row, 4 * h + c)] = *(const uint4*)v;
+            const qmm_bf16x8 v = q4_bf16x8_mix(qw[2 * c], qw[2 * c + 1], m, s24, -ml);
+            Lb[swz(row, 4 * h + c)] = __builtin_bit_cast(uint4, v);
         }
     }
 };

@@ -269,6 +269,38 @@ int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes
 int moe_fmt_dispatch(int fmt, int sfmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x, int N, int K,
                      int T, int xrow_te, hipStream_t s);
 
+// ------------------------------------------------------------------------------------------
+// Q4_K nibbles -> bf16 through v_fma_mix_f32 (the grouped and dense prefill GEMMs)
+typedef __bf16 qmm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// fma(value of the f16 half, s, c) -- v_fma_mix_f32.  A half whose bits are a small integer q
+// (exponent field 0) is the subnormal q * 2^-24, exactly, so with s = x * 2^24 the product is
+// exactly q * x and the result is the single rounding of q * x + c: fmaf(x, q, c) bit for bit.
+__device__ __forceinline__ float mix_lo(uint32_t v, float s, float c) {
+    return __builtin_fmaf((float)__builtin_bit_cast(f16x2, v)[0], s, c);
+}
+__device__ __forceinline__ float mix_hi(uint32_t v, float s, float c) {
+    return __builtin_fmaf((float)__builtin_bit_cast(f16x2, v)[1], s, c);
+}
+// 8 weights bf16(fma(dl, q, -ml)) from the nibbles of bytes 0..7 of {u0, u1} (k order = byte
+// order).  m = 0x000f000f takes the low nibbles (s24 = dl * 2^24), m = 0x00f000f0 the high ones in
+// place, 16q (s24 = dl * 2^20).  Bit for bit the dequantisation bf16(fmaf(dl, (float)q, -ml)) (RNE),
+// in 17 VALU per 8 weights (byte-to-float conversions, fma and packing take 22).  Relies on f16
+// subnormals being kept, the kernels' default mode (float_denorm_mode_16_64 = 3).
+__device__ __forceinline__ qmm_bf16x8 q4_bf16x8_mix(uint32_t u0, uint32_t u1, uint32_t m, float s24, float c) {
+    const uint32_t e0 = u0 & m, o0 = (u0 >> 8) & m, e1 = u1 & m, o1 = (u1 >> 8) & m;
+    qmm_bf16x8 r;
+    r[0] = (__bf16)mix_lo(e0, s24, c);
+    r[1] = (__bf16)mix_lo(o0, s24, c);
+    r[2] = (__bf16)mix_hi(e0, s24, c);
+    r[3] = (__bf16)mix_hi(o0, s24, c);
+    r[4] = (__bf16)mix_lo(e1, s24, c);
+    r[5] = (__bf16)mix_lo(o1, s24, c);
+    r[6] = (__bf16)mix_hi(e1, s24, c);
+    r[7] = (__bf16)mix_hi(o1, s24, c);
+    return r;
+}
+
 }  // namespace qmm
 
 // Host-side launch check shared by the C-ABI wrappers.
