@@ -78,12 +78,14 @@ def roofs(torch):
     reference's bench/roofline/bandwidth.hip and wmma_rate.hip): streaming-read GB/s of config 0's
     50,135,040 weight bytes rotated over >= 1 GiB of copies (grid-stride loop as bandwidth.hip, and one-shot
     bursts of U loads per thread as the GEMV issues them, plain and nontemporal), the asymptotic read of one
-    1 GiB buffer, and the issue rate of independent matrix instructions (TFLOP/s, TOP/s)."""
+    1 GiB buffer, the issue rate of independent matrix instructions (TFLOP/s, TOP/s) and the LDS read
+    rate of ds_read_b128 per CU."""
     import ctypes
     lib = ctypes.CDLL(os.path.join(ROOT, "hipster_amd", "lib", "libhipster_roofs.so"))
     lib.qmm_roof_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                   ctypes.c_void_p]
     lib.qmm_roof_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.qmm_roof_lds.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     sink = torch.zeros(64, dtype=torch.int32, device="cuda")
     st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     out = {}
@@ -133,6 +135,15 @@ def roofs(torch):
         res["best_TFLOPS"] = max(res.values())
         res["pct_of_peak"] = round(100 * res["best_TFLOPS"] / peak, 1)
         out[name] = res
+    # LDS read rate: one workgroup per CU, 4 / 8 / 16 waves; bytes per CU per second, and per clock at the
+    # nominal 2.4 GHz
+    res = {}
+    iters, cus = 2000, 256
+    for waves in (4, 8, 16):
+        us = graph_us(torch, [lambda: lib.qmm_roof_lds(waves, iters, cus, ctypes.c_void_p(sink.data_ptr()), st())], reps=3)
+        per_cu = iters * 16 * 1024 * waves / us / 1e3          # GB/s per CU
+        res[f"waves{waves}"] = {"TB_s": round(per_cu * cus / 1e3, 1), "B_per_clk_per_CU_at_2.4GHz": round(per_cu / 2.4, 1)}
+    out["lds_read_b128"] = res
     return out
 
 

@@ -83,6 +83,26 @@ __global__ void __launch_bounds__(512) k_mfma(float* __restrict__ out, int iters
     if (t == 12345.f) out[0] = t;
 }
 
+// LDS read rate: WAVES waves per workgroup (one workgroup per CU: 128 KiB of LDS), each issuing
+// ds_read_b128 of 16 consecutive bytes per lane (conflict-free: a wave reads 1 KiB of consecutive
+// addresses), 16 reads per iteration folded into registers stored only on an impossible value
+template <int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) k_lds_read(uint32_t* __restrict__ sink, int iters) {
+    __shared__ __align__(16) uint4 lds[8192];
+    for (int i = threadIdx.x; i < 8192; i += 64 * WAVES) lds[i] = make_uint4(i, 3 * i, 5 * i, 7 * i);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint4 acc = make_uint4(0, 0, 0, 0);
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const uint4 v = lds[((it * 16 + u) * 64 + wave * 1024 + lane) & 8191];
+            acc.x ^= v.x; acc.y += v.y; acc.z ^= v.z; acc.w += v.w;
+        }
+    }
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x12345678u) sink[0] = acc.x;
+}
+
 }  // namespace
 
 extern "C" {
@@ -121,6 +141,19 @@ int qmm_roof_mfma(int op, int iters, int grid, float* sink, void* stream) {
         case 2: hipLaunchKernelGGL(k_mfma<2>, dim3(grid), dim3(512), 0, s, sink, iters); break;
         case 3: hipLaunchKernelGGL(k_mfma<3>, dim3(grid), dim3(512), 0, s, sink, iters); break;
         case 4: hipLaunchKernelGGL(k_mfma<4>, dim3(grid), dim3(512), 0, s, sink, iters); break;
+        default: return -1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// grid workgroups of `waves` waves (4, 8 or 16), iters rounds of 16 ds_read_b128 per wave
+int qmm_roof_lds(int waves, int iters, int grid, uint32_t* sink, void* stream) {
+    if (!sink || iters < 1 || grid < 1) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    switch (waves) {
+        case 4: hipLaunchKernelGGL(k_lds_read<4>, dim3(grid), dim3(256), 0, s, sink, iters); break;
+        case 8: hipLaunchKernelGGL(k_lds_read<8>, dim3(grid), dim3(512), 0, s, sink, iters); break;
+        case 16: hipLaunchKernelGGL(k_lds_read<16>, dim3(grid), dim3(1024), 0, s, sink, iters); break;
         default: return -1;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
