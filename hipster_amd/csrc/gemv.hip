@@ -498,6 +498,85 @@ __global__ void __launch_bounds__(kBlock) k_gemv_q6k_u(const uint8_t* __restrict
     }
 }
 
+// Several columns at once (NCOL >= 5): x of all NCOL columns staged once per workgroup of 16 rows
+// (1024 threads, one row per wave, so the x copy is paid once per 16 rows instead of once per 4 rows
+// and per pass of k_gemv_q6k_u's 64 KiB budget).  Column c at c * 9K/8: the x units as k_gemv_q6k_u
+// lays them out, then its q8 scales d as they are in memory (the float4 of unit u is the one of unit
+// pair u / 2, at K + 16 (u / 2)).  Same per-lane arithmetic and reduction as k_gemv_q6k_u, so every
+// column is bitwise the one-column kernel's.  Needs NCOL * 9K/8 bytes of LDS.
+constexpr int kQ6WideWaves = 16;
+inline size_t q6w_lds_bytes(int ncol, int K) { return (size_t)ncol * ((size_t)K + K / 8); }
+
+template <int F, int NCOL, int NIT>
+__global__ void __launch_bounds__(64 * kQ6WideWaves) k_gemv_q6k_w(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                                  const float* __restrict__ xd, float* __restrict__ y, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nb = K >> 8, U = K >> 6, nsb = K >> 5, ccol = K + (K >> 3);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * kQ6WideWaves + wave;
+    const uint8_t* rp = W + (size_t)min(row, N - 1) * ((size_t)nb * 210);
+    Q6Unit P[NIT];
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) q6k_load_unit<F>(rp, nb, min(lane + 64 * i, U - 1), P[i]);   // weights first
+    {
+        const int nx = 4 * U;
+        for (int v = threadIdx.x; v < NCOL * nx; v += 64 * kQ6WideWaves) {
+            const int c = v / nx, r = v - c * nx, g = r / U, u = r - g * U;
+            const int b = u >> 2, n = (u >> 1) & 1, lh = u & 1;
+            *(uint4*)(smem + (size_t)c * ccol + (size_t)(g * U + u) * 16) =
+                ld16(xq + (size_t)c * K + (size_t)b * 256 + 128 * n + 32 * g + 16 * lh);
+        }
+        const int nd = nsb >> 2;                                    // float4 of d per column
+        for (int v = threadIdx.x; v < NCOL * nd; v += 64 * kQ6WideWaves) {
+            const int c = v / nd, w = v - c * nd;
+            *(float4*)(smem + (size_t)c * ccol + (size_t)K + (size_t)w * 16) = *(const float4*)(xd + (size_t)c * nsb + 4 * w);
+        }
+    }
+    lds_barrier();
+    float acc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+        const int u = lane + 64 * i, uc = min(u, U - 1), lh = uc & 1;
+        const Q6Unit& q = P[i];
+        const uint32_t A[4] = {q.a.x, q.a.y, q.a.z, q.a.w}, B[4] = {q.b.x, q.b.y, q.b.z, q.b.w}, H[4] = {q.h.x, q.h.y, q.h.z, q.h.w};
+        const uint32_t scr = __builtin_amdgcn_perm(q.sc1, q.sc0, lh ? 0x07050301u : 0x06040200u);
+        uint32_t qw[4][4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            qw[0][w] = q6_signed((A[w] & 0x0f0f0f0fu) | ((H[w] << 4) & 0x30303030u));
+            qw[1][w] = q6_signed((B[w] & 0x0f0f0f0fu) | ((H[w] << 2) & 0x30303030u));
+            qw[2][w] = q6_signed(((A[w] >> 4) & 0x0f0f0f0fu) | (H[w] & 0x30303030u));
+            qw[3][w] = q6_signed(((B[w] >> 4) & 0x0f0f0f0fu) | ((H[w] >> 2) & 0x30303030u));
+        }
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) {
+            const uint8_t* xc = smem + (size_t)c * ccol;
+            const float4 xs4 = *(const float4*)(xc + (size_t)K + (size_t)(uc >> 1) * 16);
+            const float xsg[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+            float v = 0.f;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint4 xv = *(const uint4*)(xc + (size_t)(g * U + uc) * 16);
+                int is = sdot4(qw[g][0], xv.x, 0);
+                is = sdot4(qw[g][1], xv.y, is);
+                is = sdot4(qw[g][2], xv.z, is);
+                is = sdot4(qw[g][3], xv.w, is);
+                const int scg = (int)(int8_t)((scr >> (8 * g)) & 0xffu);
+                v = __builtin_fmaf(q.d * xsg[g], (float)(scg * is), v);
+            }
+            acc[c] += u < U ? v : 0.f;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = wave_sum(acc[c]);
+    if (lane == 0 && row < N) {
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row] = acc[c];
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // Q4_K x f32 GEMV (gemv.hip:1177-1216 semantics): acc += dA*sum(x*qA) + dB*sum(x*qB) - the min
 // terms once per sub-block, with f32 x and per-sub-block sums of x staged in LDS when they fit.
@@ -646,6 +725,20 @@ template <int F, int NCOL>
 int launch_q6k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
     const size_t per_col = (size_t)K + K / 4;
     const int g = (int)std::min<size_t>(NCOL, kXLdsBudget / per_col);
+    if constexpr (NCOL >= 5) {     // measured at 5120 x 17408: 3 columns faster, 4 equal in the unit kernel
+      if (K <= 64 * 64 * 6 && q6w_lds_bytes(NCOL, K) <= 160 * 1024) {   // all columns in one pass
+        const int grid = (N + kQ6WideWaves - 1) / kQ6WideWaves;
+        const size_t lds_w = q6w_lds_bytes(NCOL, K);
+#define QMM_Q6W(IV) case IV: hipLaunchKernelGGL((k_gemv_q6k_w<F, NCOL, IV>), dim3(grid), dim3(64 * kQ6WideWaves), lds_w, s, (const uint8_t*)W, x.q, x.d, y, N, K); break;
+        switch ((K / 64 + 63) / 64) {
+            QMM_Q6W(1) QMM_Q6W(2) QMM_Q6W(3) QMM_Q6W(4) QMM_Q6W(5) QMM_Q6W(6)
+            default: return QMM_ERR_SHAPE;
+        }
+#undef QMM_Q6W
+        QMM_LAUNCH_CHECK();
+        return QMM_OK;
+      }
+    }
     if (g >= 1 && K <= 64 * 64 * 6) {                       // unit kernel: at most 6 units per lane
         const int grid = (N + kWavesPerBlock - 1) / kWavesPerBlock;
         const size_t lds_u = (size_t)g * per_col;

@@ -73,8 +73,11 @@ def test_gemv_q8_parity(gpu, fmt, N, K):
         assert max_rel_mag(y, ref[:ncol], mag[:ncol]) < TOL
 
 
-@pytest.mark.parametrize("fmt,N,K", [(synth.Q4_K, 4099, 5120), (synth.Q6_K, 1031, 5120), (synth.Q6_K_SOA, 515, 2048)])
+@pytest.mark.parametrize("fmt,N,K", [(synth.Q4_K, 4099, 5120), (synth.Q6_K, 1031, 5120), (synth.Q6_K_SOA, 515, 2048),
+                                     (synth.Q6_K_SOA, 5120, 17408), (synth.Q6_K, 1037, 17408)])
 def test_gemv_q8_t_invariant_and_deterministic(gpu, fmt, N, K):
+    """every column bitwise the same for ncol 1..8 (Q6_K from 5 columns on: all columns staged at once
+    per 16-row workgroup, the config-1 down shape included)"""
     W = synth.matrix(400 + N, fmt, N, K)
     x = synth.normal_f32(401, (8, K))
     Wd = dev(W)
