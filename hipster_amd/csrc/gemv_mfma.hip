@@ -89,10 +89,20 @@ __device__ __forceinline__ void couple_split(const uint4 v, uint2& p0, uint2& p1
 // caller) adds +0, which leaves every partial sum unchanged (a sum started at +0 is never -0)
 // The x piece of pair j (sub-block 2j = bytes 0..31, 2j+1 = bytes 32..63) splits the same way as a
 // weight couple: after the swap the lane holds 8 bytes of each sub-block at k offsets 8 kperm(h).
+// The four lane groups of a row need the same scales: lane (r, h) decodes those of pair j = h only and
+// the row's four quadruples meet in the wave's LDS slot (DS instructions of a wave run in order, so the
+// reads see the writes; the compiler barriers keep them in program order), then every lane reads the
+// four.  The same floats as decoding all four in every lane.
 template <int MV>
-__device__ __forceinline__ void mblk_compute(const MBlk& B, int b, int h, bool live, const float4* __restrict__ sds,
-                                             float (&acc)[4][MV]) {
+__device__ __forceinline__ void mblk_compute(const MBlk& B, int b, int h, int r, bool live, const float4* __restrict__ sds,
+                                             float4* __restrict__ sslot, float (&acc)[4][MV]) {
     constexpr int NS = 4 * MV;
+    {
+        const Q4kPairScales own = q4k_pair_scales(B.hd, Q4kPairDecode(h));
+        asm volatile("" ::: "memory");
+        sslot[r * 4 + h] = make_float4(own.dA, own.dB, own.mA, own.mB);
+        asm volatile("" ::: "memory");
+    }
     uint2 q[4];
     couple_split(B.q[0], q[0], q[1]);
     couple_split(B.q[1], q[2], q[3]);
@@ -105,7 +115,8 @@ __device__ __forceinline__ void mblk_compute(const MBlk& B, int b, int h, bool l
         const i32x4 z = {0, 0, 0, 0};
         const i32x4 ca = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(x0), as_long(lo), z, 0, 0, 0);
         const i32x4 cb = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(x1), as_long(hi), z, 0, 0, 0);
-        const Q4kPairScales sc = q4k_pair_scales(B.hd, Q4kPairDecode(j));
+        const float4 sj = sslot[r * 4 + j];
+        const Q4kPairScales sc = {sj.x, sj.y, sj.z, sj.w};
         const float4* dsp = sds + (size_t)(4 * b + j) * NS + h * MV;
 #pragma unroll
         for (int v = 0; v < MV; ++v) acc[j][v] += live ? q4k_pair_value(sc, dsp[v], ca[v], cb[v]) : 0.f;
@@ -113,6 +124,14 @@ __device__ __forceinline__ void mblk_compute(const MBlk& B, int b, int h, bool l
 }
 
 constexpr int kMfmaMaxK = 32768;
+
+// LDS of the x pair scales [K/64][4 MV] float4, reused for the partial sums [16][4 MV][16] float; the
+// per-wave scale-exchange slots (4 waves x 2 sets x 16 rows x 4 pairs float4) follow
+__host__ __device__ inline size_t gemv_q4k_mfma_main_lds(int K, int mv) {
+    const size_t scales = (size_t)(K / 64) * (4 * mv) * 16, parts = (size_t)16 * (4 * mv) * 16 * 4;
+    return scales > parts ? scales : parts;
+}
+constexpr size_t kScaleSlotBytes = 4 * 2 * 16 * 4 * 16;
 
 // grid = all 16-row tiles of all segments, 256 threads; LDS: x pair scales [K/64][4 MV] float4, after
 // the main loop reused for the partial sums [16][4 MV][16] float
@@ -132,6 +151,8 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
     const uint8_t* rp = sg.w[si] + (size_t)min(row0 + r, N - 1) * ((size_t)nb * 144);
     float4* sds = (float4*)smem;
     float* part = (float*)smem;
+    // per wave two scale-exchange slots (register sets A, B) of 16 rows x 4 pairs, after the scales
+    float4* sslot = (float4*)(smem + gemv_q4k_mfma_main_lds(K, MV)) + wave * 128;
     // A operand source of this lane: x of the token in slot r (zeros for an empty slot), 16-byte
     // piece h of each pair
     const int ca = (r >> 2) * MV + (r & 3);
@@ -178,10 +199,10 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
     for (int b = wave; b < nb; b += 8) {                  // wave-uniform
         mblk_load(B, rp, rx, xo, min(b + 4, nb - 1), h);
         __builtin_amdgcn_sched_barrier(0);
-        mblk_compute<MV>(A, b, h, true, sds, acc);
+        mblk_compute<MV>(A, b, h, r, true, sds, sslot, acc);
         mblk_load(A, rp, rx, xo, min(b + 8, nb - 1), h);
         __builtin_amdgcn_sched_barrier(0);
-        mblk_compute<MV>(B, min(b + 4, nb - 1), h, b + 4 < nb, sds, acc);
+        mblk_compute<MV>(B, min(b + 4, nb - 1), h, r, b + 4 < nb, sds, sslot + 64, acc);
     }
     __syncthreads();                                      // every wave is done with the scales
     // partial sum t = 4 wave + j of token MV h + v, row r
@@ -211,8 +232,7 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
 
 size_t gemv_q4k_mfma_lds(int K, int ncol) {
     const int mv = ncol <= 4 ? 1 : ncol <= 8 ? 2 : 4;
-    const size_t scales = (size_t)(K / 64) * (4 * mv) * 16, parts = (size_t)16 * (4 * mv) * 16 * 4;
-    return K > kMfmaMaxK ? SIZE_MAX : scales > parts ? scales : parts;
+    return K > kMfmaMaxK ? SIZE_MAX : gemv_q4k_mfma_main_lds(K, mv) + kScaleSlotBytes;
 }
 
 // ncol (1..16) columns of q8 x against nseg (1..4) Q4_K segments sharing K, in one launch.  Shapes are
