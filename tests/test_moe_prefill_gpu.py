@@ -140,6 +140,33 @@ def test_moe_gate_up_fused_equals_unfused(gpu, T, N, K, maxc):
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("N,K", [(F, H), (640, 768)])
+def test_moe_gemm_bf16_tile_size_invariant(gpu, N, K):
+    """the sorted positions do not depend on the tile size, and neither do the results: every output
+    element is the same MFMA sequence whether its tile has 128, 64 or 32 rows (four, two or one 32-row
+    MFMA blocks) -- bit for bit, gate/up fused as well"""
+    T, n_exp = 700, 24
+    W_h, S_h = synth.experts(1450 + N, synth.Q4_K, n_exp, N, K), synth.matrix(1451 + N, synth.Q4_K, N, K)
+    U_h, SU_h = synth.experts(1452 + N, synth.Q4_K, n_exp, N, K), synth.matrix(1453 + N, synth.Q4_K, N, K)
+    ids_h, _ = oracle.moe_route(synth.router_logits(1454 + N, T, n_exp, 1.1), n_exp, 10)
+    A = bf16_dev(synth.to_bf16_bits(synth.normal_f32(1455, (T, K))))
+    Wd, Sd, Ud, SUd = dev(W_h), dev(S_h), dev(U_h), dev(SU_h)
+    outs, hs = [], []
+    for maxc in (128, 64, 32):
+        kpos, rowtok, tiles, counts, cap = sort_on_gpu(ids_h, n_exp, maxc)
+        D = torch.full((T * NE, N), float("nan"), device="cuda")
+        qmm.moe_gemm_bf16(synth.Q4_K, synth.Q4_K, Wd, Sd, W_h[0].nbytes, tiles, counts, cap, rowtok, A, D, N, K)
+        h = torch.full((T * NE, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+        qmm.moe_gemm_gate_up_bf16(synth.Q4_K, synth.Q4_K, Wd, Sd, Ud, SUd, W_h[0].nbytes, tiles, counts, cap, rowtok, A, h, N, K)
+        outs.append(host(D).view(np.int32))
+        hs.append(host(h.view(torch.int16)))
+        print(f"tile-size invariance N={N} K={K} maxc={maxc}: "
+              f"{int((outs[-1] != outs[0]).sum())} / {int((hs[-1] != hs[0]).sum())} differing", flush=True)
+    assert not np.isnan(host(D)).any()
+    for o, hh in zip(outs[1:], hs[1:]):
+        assert np.array_equal(o, outs[0]) and np.array_equal(hh, hs[0])
+
+
 def test_moe_prefill_config4_pipeline(gpu):
     """2048 tokens, hidden 2048, 512 Q4_K experts + shared, top-10 with the Zipf
     bias.  Device pipeline: route -> sort -> gate/up/silu (one launch) -> down -> combine; 12 sampled tokens
