@@ -49,7 +49,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
-    p.add_argument("--only-extra", choices=["activation_producers", "formats", "router", "moe_decode", "moe_prefill", "dense_prefill"],
+    p.add_argument("--only-extra", choices=["activation_producers", "formats", "router", "dense_decode", "moe_decode", "moe_prefill",
+                                            "dense_prefill"],
                    default=None,
                    help="only run one of the extra measurements and print its JSON (for profiling it alone)")
     p.add_argument("--roofs", action="store_true",
@@ -564,7 +565,7 @@ def main():
         print(json.dumps({"roofs": roofs(torch)}), flush=True)
         return
     if args.only_extra:
-        fn = {"activation_producers": extra_act, "formats": extra_formats, "router": extra_router,
+        fn = {"activation_producers": extra_act, "formats": extra_formats, "router": extra_router, "dense_decode": extra_cfg1,
               "moe_decode": lambda t: extra_cfg2(t, moe_tables(t)), "moe_prefill": lambda t: extra_cfg4(t, moe_tables(t)),
               "dense_prefill": extra_cfg3}[args.only_extra]
         print(json.dumps({args.only_extra: fn(torch)}), flush=True)

@@ -910,6 +910,9 @@ int check_gemv_shape(int fmt, int N, int K) {
 // Q4_K calls with at least this many columns run on the matrix cores (gemv_mfma.hip: the same bits;
 // at 17408 x 5120 it is the faster kernel from 4 columns on)
 int g_mfma_min_ncol = 4;
+// Q6_K_SOA calls with at least this many columns (and at most 8) run on the matrix cores (measured at
+// 5120 x 17408: 2 columns 26.5 us on the dot4 kernel against 33, 3 columns 35 against 33, 4 43 against 33)
+int g_q6_mfma_min_ncol = 3;
 
 int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
     if (fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA)
@@ -918,6 +921,9 @@ int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, 
         const qmm_gemv_seg seg = {QMM_Q4_K, W, y, N, K};
         return gemv_q4k_mfma(&seg, 1, x, K, ncol, s);
     }
+    if (fmt == QMM_Q6_K_SOA && ncol >= g_q6_mfma_min_ncol && ncol <= 8 && K >= 512 && K % 512 == 0 &&
+        (size_t)ncol * K <= 262144 && ((uintptr_t)x.d & 15) == 0)
+        return gemv_q6k_mfma(W, x, y, N, K, ncol, s);
     switch (ncol) {
         case 1: return launch_gemv_q8_ncol<1>(fmt, W, x, y, N, K, s);
         case 2: return launch_gemv_q8_ncol<2>(fmt, W, x, y, N, K, s);
@@ -946,6 +952,12 @@ extern "C" {
 int qmm_set_gemv_mfma_min_ncol(int n) {
     const int prev = g_mfma_min_ncol;
     g_mfma_min_ncol = n < 1 ? 1 : n;
+    return prev;
+}
+
+int qmm_set_gemv_q6k_mfma_min_ncol(int n) {
+    const int prev = g_q6_mfma_min_ncol;
+    g_q6_mfma_min_ncol = n < 1 ? 1 : n;
     return prev;
 }
 

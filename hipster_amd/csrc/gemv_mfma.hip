@@ -228,6 +228,195 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
     }
 }
 
+
+// ------------------------------------------------------------------------------------------
+// Q6_K_SOA GEMV for 2..8 columns on the int8 matrix cores, bitwise the unit kernel of gemv.hip
+// (k_gemv_q6k_u / k_gemv_q6k_w: lane l of a row's wave adds the values of quarter-block units l,
+// l+64, ... in that order, each value the fma chain over the unit's four 16-weight groups g of
+// (d * xd[g]) * (float)(sc[g] * isum_g), and the 64 partial sums meet in the xor butterfly 32, 16,
+// 8, 4, 2, 1).  Unit u = 4b + 2n + lh holds weights 256b + 128n + 16lh + l' + 32g, l' < 16: group g
+// is the low (g < 2) or high nibble of ql run A (g even, ql[64n + l]) or run B (g odd, ql[64n + 32 +
+// l]) with bits 2g, 2g+1 of qh[32n + l], l = 16lh + l' (quant.h:65-80).
+//
+// v_mfma_i32_16x16x64_i8, one instruction per group g and 4 tokens: lane (j, q) = (l % 16, l / 16)
+// supplies 16 bytes of A row j and of B column j, the same 16 k for both.  B column j is weight row j
+// of the 16-row tile and lane group q supplies group g of unit q of the block, so every lane loads
+// bytes of its own (ql runs A and B and qh of its unit: three 16-byte loads per block, none
+// repeated).  A row 4t + s is token t against unit s alone (its x of group g in the lanes of group
+// q = s, zeros elsewhere), so D[4t + s][j] is the exact integer isum of unit s, group g, and lane
+// (j, q) receives D[4q + v][j], v = 0..3: token q (q + 4 in the second token block), units 0..3.
+// A workgroup is 16 rows x 4 waves; wave w takes blocks b = w + 4m, whose units 4b + v belong to the
+// unit kernel's lanes 4w + v + 16k, k = m % 4, in the same order: acc[k][v] is lane (4w + v + 16k)'s
+// partial sum.  The 64 partials of each (row, token) meet in LDS in the butterfly's association order.
+struct Q6MBlk {
+    uint4 a, b, h;      // the lane's unit: 16 bytes of ql run A, of run B and of qh
+    uint4 sc;           // the block's 16 scale bytes
+    uint32_t d;         // the block's f16 d
+};
+
+template <int NT>
+__device__ __forceinline__ void q6m_load(Q6MBlk& B, uint4 (&X)[NT][4], const uint8_t* qlp, const uint8_t* qhp, const uint8_t* scp,
+                                         const uint16_t* dp, __amdgpu_buffer_rsrc_t rx, const uint32_t (&xo)[NT], int b) {
+    B.a = ld16_a4(qlp + b * 128);
+    B.b = ld16_a4(qlp + b * 128 + 32);
+    B.h = ld16_a4(qhp + b * 64);
+    B.sc = ld16_a4(scp + b * 16);
+    B.d = dp[b];
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) X[i][g] = xload(rx, xo[i] + (uint32_t)(b * 256 + 32 * g));
+}
+
+// the block's unit values for the lane's tokens q + 4i added to acc[v][i] (live = false adds +0)
+template <int NT>
+__device__ __forceinline__ void q6m_compute(const Q6MBlk& B, const uint4 (&X)[NT][4], int b, int q, const float* sxd, int nsb,
+                                            int ncol, bool live, float (&acc)[4][NT]) {
+    const uint32_t aw[4] = {B.a.x, B.a.y, B.a.z, B.a.w}, bw[4] = {B.b.x, B.b.y, B.b.z, B.b.w};
+    const uint32_t hw[4] = {B.h.x, B.h.y, B.h.z, B.h.w};
+    i32x4 bop[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        bop[0][w] = (int)q6_signed((aw[w] & 0x0f0f0f0fu) | ((hw[w] << 4) & 0x30303030u));
+        bop[1][w] = (int)q6_signed((bw[w] & 0x0f0f0f0fu) | ((hw[w] << 2) & 0x30303030u));
+        bop[2][w] = (int)q6_signed(((aw[w] >> 4) & 0x0f0f0f0fu) | (hw[w] & 0x30303030u));
+        bop[3][w] = (int)q6_signed(((bw[w] >> 4) & 0x0f0f0f0fu) | ((hw[w] >> 2) & 0x30303030u));
+    }
+    const float d = h2f(B.d);
+    const uint32_t scw[4] = {B.sc.x, B.sc.y, B.sc.z, B.sc.w};
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        i32x4 c[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const i32x4 a = {(int)X[i][g].x, (int)X[i][g].y, (int)X[i][g].z, (int)X[i][g].w};
+            const i32x4 z = {0, 0, 0, 0};
+            c[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bop[g], z, 0, 0, 0);
+        }
+        const float* xs = sxd + (size_t)min(q + 4 * i, ncol - 1) * nsb + 8 * b;
+        const float4 x0 = *(const float4*)xs, x1 = *(const float4*)(xs + 4);
+        const float xsn[2][4] = {{x0.x, x0.y, x0.z, x0.w}, {x1.x, x1.y, x1.z, x1.w}};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {              // unit v = (n, lh) = (v >> 1, v & 1)
+            const int n = v >> 1, lh = v & 1;
+            float val = 0.f;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int si = 8 * n + lh + 2 * g;  // scale byte of the unit's group g
+                const int scg = (int)(int8_t)((scw[si >> 2] >> (8 * (si & 3))) & 0xffu);
+                val = __builtin_fmaf(d * xsn[n][g], (float)(scg * c[g][v]), val);
+            }
+            acc[v][i] += live ? val : 0.f;
+        }
+    }
+}
+
+constexpr int kQ6MWaves = 4;
+constexpr int kQ6MScaleRegs = 8;      // x-scale float4 per thread loaded ahead of the weights
+
+// LDS: x scales [ncol][K/32] float, after the main loop reused for the partials [64][4 NT][16] float
+__host__ __device__ inline size_t gemv_q6k_mfma_lds(int K, int ncol) {
+    const size_t xs = (size_t)ncol * (K / 32) * 4, parts = (size_t)64 * (ncol <= 4 ? 4 : 8) * 16 * 4;
+    return xs > parts ? xs : parts;
+}
+
+template <int NT>
+__global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                                 const float* __restrict__ xd, float* __restrict__ y, int N, int K,
+                                                                 int ncol) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int NS = 4 * NT;
+    const int nb = K >> 8, nsb = K >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, q = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: a scalar block loop
+    const int row0 = blockIdx.x * 16;
+    const uint8_t* rp = W + (size_t)min(row0 + j, N - 1) * ((size_t)nb * 210);
+    const int un = q >> 1, ulh = q & 1;                      // the lane's unit (n, lh) = q of each block
+    const uint8_t* qlp = rp + 64 * un + 16 * ulh;
+    const uint8_t* qhp = rp + (size_t)nb * 128 + 32 * un + 16 * ulh;
+    const uint8_t* scp = rp + (size_t)nb * 192;
+    const uint16_t* dp = (const uint16_t*)(rp + (size_t)nb * 208);
+    // A source: token 4i + (j >> 2) against unit s = j & 3 of the block, from the lanes of group q = s
+    // only (an offset past the end of x reads zeros)
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, ncol * K, 0x00020000);
+    uint32_t xo[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int t = 4 * i + (j >> 2), sv = j & 3;
+        xo[i] = (sv == q && t < ncol) ? (uint32_t)(t * K + 128 * (sv >> 1) + 16 * (sv & 1)) : 0x40000000u;
+    }
+    // x scales of every column to LDS, kQ6MScaleRegs float4 per thread (the launcher checks that they
+    // cover them), loaded before the weights: loads retire in issue order, so their LDS stores wait
+    // for them only
+    float* sxd = (float*)smem;
+    const int nx4 = ncol * (nsb >> 2);
+    float4 sv[kQ6MScaleRegs];
+#pragma unroll
+    for (int r = 0; r < kQ6MScaleRegs; ++r) sv[r] = ((const float4*)xd)[min(tid + 64 * kQ6MWaves * r, nx4 - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    const int nm = (nb - wave + kQ6MWaves - 1) / kQ6MWaves;  // blocks b = wave + 4m of this wave (may be 0)
+    auto blk = [&](int m) { return min(wave + kQ6MWaves * min(m, max(nm - 1, 0)), nb - 1); };
+    // two blocks in flight (weights three blocks ahead measured no faster); every load unconditional
+    // (clamped block), so the wait counts stay exact
+    Q6MBlk R[2];
+    uint4 X[2][NT][4];
+    q6m_load<NT>(R[0], X[0], qlp, qhp, scp, dp, rx, xo, blk(0));
+    q6m_load<NT>(R[1], X[1], qlp, qhp, scp, dp, rx, xo, blk(1));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < kQ6MScaleRegs; ++r)                 // no branch: a clamped item stores its own value
+        ((float4*)sxd)[min(tid + 64 * kQ6MWaves * r, nx4 - 1)] = sv[r];
+    lds_barrier();
+    float acc[4][4][NT];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int i = 0; i < NT; ++i) acc[k][v][i] = 0.f;
+    // at least one pass: a loop that might not run would let the compiler sink the ring's loads past
+    // the barrier into its entry
+    int m0 = 0;
+    do {                                                     // wave-uniform
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int m = m0 + k;
+            q6m_compute<NT>(R[k & 1], X[k & 1], blk(m), q, sxd, nsb, ncol, m < nm, acc[k]);
+            // the refill stays right here: the scheduler would otherwise move the ring's loads next to
+            // their uses and drain the queue
+            __builtin_amdgcn_sched_barrier(0);
+            q6m_load<NT>(R[k & 1], X[k & 1], qlp, qhp, scp, dp, rx, xo, blk(m + 2));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        m0 += 4;
+    } while (m0 < nm);
+    lds_barrier();                                           // every wave is done with the x scales
+    float* part = (float*)smem;                              // [slot l][token][row]
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int i = 0; i < NT; ++i) part[((4 * wave + v + 16 * k) * NS + 4 * i + q) * 16 + j] = acc[k][v][i];
+    lds_barrier();
+    for (int e = tid; e < 16 * ncol; e += 64 * kQ6MWaves) {
+        const int orow = e & 15, oc = e >> 4;
+        if (row0 + orow >= N) continue;
+        // the association order of the butterfly over the 64 lanes of the unit kernel's row wave
+        float a[32];
+#pragma unroll
+        for (int t = 0; t < 32; ++t) a[t] = part[(t * NS + oc) * 16 + orow] + part[((t + 32) * NS + oc) * 16 + orow];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) a[t] = a[t] + a[t + 16];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) a[t] = a[t] + a[t + 8];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[t] = a[t] + a[t + 4];
+        a[0] = a[0] + a[2];
+        a[1] = a[1] + a[3];
+        y[(size_t)oc * N + row0 + orow] = a[0] + a[1];
+    }
+}
 }  // namespace
 
 size_t gemv_q4k_mfma_lds(int K, int ncol) {
@@ -257,6 +446,22 @@ int gemv_q4k_mfma(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol
         case 2: hipLaunchKernelGGL(k_gemv_q4k_mfma<2>, grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
         default: hipLaunchKernelGGL(k_gemv_q4k_mfma<4>, grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
     }
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+// ncol (1..8) columns of q8 x against a Q6_K_SOA matrix (K % 512 == 0, 512 <= K, ncol * K <= 262144),
+// bitwise the unit kernel's columns
+int gemv_q6k_mfma(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    if (ncol < 1 || ncol > 8 || K < 512 || K % 512 || N < 1) return QMM_ERR_SHAPE;
+    if ((size_t)ncol * (K / 128) > (size_t)64 * kQ6MWaves * kQ6MScaleRegs) return QMM_ERR_SHAPE;   // x scales in one pass
+    const size_t lds = gemv_q6k_mfma_lds(K, ncol);
+    if (lds > kMfmaLdsMax) return QMM_ERR_SHAPE;
+    const dim3 grid((unsigned)((N + 15) / 16));
+    if (ncol <= 4)
+        hipLaunchKernelGGL(k_gemv_q6k_mfma<1>, grid, dim3(64 * kQ6MWaves), lds, s, (const uint8_t*)W, x.q, x.d, y, N, K, ncol);
+    else
+        hipLaunchKernelGGL(k_gemv_q6k_mfma<2>, grid, dim3(64 * kQ6MWaves), lds, s, (const uint8_t*)W, x.q, x.d, y, N, K, ncol);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }

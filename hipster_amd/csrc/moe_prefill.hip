@@ -298,10 +298,14 @@ __global__ void __launch_bounds__(256) k_moe_rowtok(const int* __restrict__ kpos
 // 2, 3), h = l/32.  A (gathered bf16 rows, DMA issued by waves 0-3) streams global -> LDS with
 // global_load_lds_dwordx4 through a ring of XST = 5 stages issued four steps ahead; the weight rows'
 // Q4_K blocks (144 contiguous bytes per row, so one DMA instruction covers about 7 rows: coalesced)
-// stream through a ring of two block stages, one block (4 K steps) ahead, DMA issued by waves 4-7.
-// The raw bytes of step t+1 are dequantised while the MFMAs of step t run.  A stage: 128 rows x 8
+// stream through a ring of block stages, DMA issued by waves 4-7: two stages (one block of 4 K steps
+// ahead) for tiles of 65-128 rows, three (two blocks ahead) for tiles of at most 64 rows, whose
+// smaller A stages leave the room.  A tile of few rows spends little time per step, so one block in
+// flight per CU would bound its weight stream at about 37 KB per memory latency.
+// The raw bytes of step t+1 are dequantised while the MFMAs of step t run.  A stage: 32 NRB rows x 8
 // chunks of 16 B, chunk c of row r in slot r*8 + (c ^ ((r >> 1) & 7)) (conflict-free fragment
-// reads); block stage: 256 rows x 144 B, row-major.
+// reads); block stage: 256 rows x 144 B, row-major.  The A ring comes first in LDS, then the weight
+// ring.
 // Gate/up mode: the 256 weight rows of a workgroup are 128 gate rows (waves 0-3) and the same 128
 // up rows (waves 4-7); the up waves hand their results over through LDS and the gate waves write
 // h = bf16(silu(g) * u).
@@ -309,6 +313,13 @@ constexpr int XBM = 128, XBW = 256, XBK = 64, XST = 5, XTHREADS = 512;
 constexpr int kXA = XBM * XBK / 8;                          // 16-byte chunks per A stage (1024)
 constexpr int kXW = 9 * XBW;                                // chunks per weight block stage (2304)
 constexpr size_t kXLds = ((size_t)XST * kXA + 2 * (size_t)kXW) * 16;   // 155,648 B
+// ring geometry for tiles of NRB row blocks: chunks per A stage, weight block stages
+template <int NRB>
+struct XRing {
+    static constexpr int kA = 256 * NRB;
+    static constexpr int WST = NRB <= 2 ? 3 : 2;
+    static_assert(((size_t)XST * kA + (size_t)WST * kXW) * 16 <= kXLds, "ring exceeds the launch's LDS");
+};
 
 // s_waitcnt immediate for "vmcnt <= v" (expcnt, lgkmcnt unconstrained)
 constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >> 4) << 14); }
@@ -354,11 +365,12 @@ __device__ __forceinline__ StepScl q4k_step_scales(const uint4 hd, int j) {
 }
 
 template <bool GU, int NRB>
-__device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile tl, int n0, uint4* As, uint4* Ws,
-                                              const int* rows) {
+__device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile tl, int n0, uint4* As, const int* rows) {
+    constexpr int kA = XRing<NRB>::kA, WST = XRing<NRB>::WST;
+    uint4* const Ws = As + XST * kA;
     const int lane = threadIdx.x & 63, fr = lane & 31, h = lane >> 5, fx = (fr >> 1) & 7;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), team = wave >> 2, wq = wave & 3;
-    const int K = a.K, N = a.N, nk = K / XBK;
+    const int K = a.K, N = a.N, nk = K / XBK, nblk = K >> 8;
     const uint32_t rowbytes = (uint32_t)(K >> 8) * 144u;
     const uint8_t* w0 = tl.expert >= 0 ? a.w0 + (size_t)tl.expert * a.ebytes : a.w0sh;
     const uint8_t* w1 = GU ? (tl.expert >= 0 ? a.w1 + (size_t)tl.expert * a.ebytes : a.w1sh) : w0;
@@ -382,14 +394,14 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
     auto issue = [&](int p, int st) {       // A of step p (waves 0-3)
         if (team == 0) {
             const uint8_t* abase = (const uint8_t*)a.A + (size_t)p * (XBK * 2);
-            const uint32_t la = lA + (uint32_t)(st * kXA * 16);
+            const uint32_t la = lA + (uint32_t)(st * kA * 16);
 #pragma unroll
             for (int q = 0; q < NRB; ++q) dma16s(abase, aoff[q], la + (uint32_t)((wq + 4 * q) * 1024));
         }
     };
-    auto issue_w = [&](int b) {             // weight block b into block stage b & 1 (waves 4-7)
+    auto issue_w = [&](int b) {             // weight block b into block stage b % WST (waves 4-7)
         if (team == 1) {
-            const uint32_t lw = lW + (uint32_t)((b & 1) * kXW * 16);
+            const uint32_t lw = lW + (uint32_t)((b % WST) * kXW * 16);
 #pragma unroll
             for (int q = 0; q < 9; ++q) {
                 const int k = 9 * wq + q;
@@ -415,7 +427,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
     // raw weight bytes of one step for the lane's weight row, and their decode
     struct Raw { uint4 hd; uint2 q0, q1; };
     auto rawread = [&](int p, Raw& r) {     // step p: block p / 4, qs pair p % 4
-        const uint8_t* rp = (const uint8_t*)(Ws + ((p >> 2) & 1) * kXW) + c0 * 144;
+        const uint8_t* rp = (const uint8_t*)(Ws + ((p >> 2) % WST) * kXW) + c0 * 144;
         const int j = p & 3;
         r.hd = *(const uint4*)rp;
         r.q0 = *(const uint2*)(rp + 16 + 32 * j + 8 * h);
@@ -427,19 +439,23 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
         const uint2 q = (s & 1) ? r.q1 : r.q0;
         return s < 2 ? q4_bf16x8_mix(q.x, q.y, 0x000f000fu, c.sa, -c.ma) : q4_bf16x8_mix(q.x, q.y, 0x00f000f0u, c.sb, -c.mb);
     };
-    // before dequantising step p (waves 4-7 hold at most one block in flight: the next one is
-    // issued at the first step of the current block, after this wait)
+    // before dequantising step p (waves 4-7 hold at most WST - 1 blocks in flight: block b + WST - 1
+    // is issued at the first step of block b, after this wait, into the stage block b - 1 used)
     auto wait_rem = [&](int rem, int p) {
         if (team == 0) wait_steps<NRB>(rem);
-        else if ((p & 3) == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        else if ((p & 3) == 0) {
+            if (WST == 3 && (p >> 2) + 1 < nblk) __builtin_amdgcn_s_waitcnt(vmcnt_imm(9));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
     };
-    // prologue (K % 256 == 0, so nk >= 4): A steps 0..3 and weight block 0 in flight, wait for A
-    // steps 0, 1 and block 0
+    // prologue (K % 256 == 0, so nk >= 4): A steps 0..3 and weight blocks 0 (and 1) in flight, wait
+    // for A steps 0, 1 and block 0
     issue(0, 0);
     issue(1, 1);
     issue(2, 2);
     issue(3, 3);
     issue_w(0);
+    if (WST == 3 && nblk > 1) issue_w(1);
     wait_rem(2, 0);
     lds_barrier();
     bf16x8 wa[4], wb[4], af0[NRB];
@@ -461,7 +477,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
             lds_barrier();
         }
         __builtin_amdgcn_sched_barrier(0);
-        const uint4* la = As + st * kXA;
+        const uint4* la = As + st * kA;
         Raw r;
         rawread(t + 1, r);
         StepScl c;
@@ -472,10 +488,10 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
         for (int s = 0; s < 4; ++s) {
             if (s == 1) {       // DMA for step t+4 (its stage was last read in step t-1) after chunk 0's MFMAs
                 if (t + 4 < nk) issue(t + 4, st4);
-                if ((t & 3) == 0 && t + 4 < nk) issue_w((t >> 2) + 1);
+                if ((t & 3) == 0 && (t >> 2) + WST - 1 < nblk) issue_w((t >> 2) + WST - 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            afrag(s < 3 ? la : As + st1 * kXA, s < 3 ? s + 1 : 0, afn);
+            afrag(s < 3 ? la : As + st1 * kA, s < 3 ? s + 1 : 0, afn);
             if (s == 0) c = q4k_step_scales(r.hd, (t + 1) & 3);
             nxt[s] = deq(r, c, s);
             asm volatile("" : : "v"(nxt[s]));   // keeps the dequantisation inside this chunk
@@ -512,7 +528,7 @@ __device__ __forceinline__ void moe_gemm_tile(const XArgs& a, const qmm_moe_tile
     {   // steps nk-2 and nk-1
         const int s1 = st == XST - 1 ? 0 : st + 1;
         step(nk - 2, st, s1, 0, wa, wb);
-        const uint4* la = As + s1 * kXA;
+        const uint4* la = As + s1 * kA;
         bf16x8 af[NRB];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -583,13 +599,12 @@ __global__ void __launch_bounds__(XTHREADS) k_moe_gemm_x(XArgs a) {
     }
     __syncthreads();
     uint4* const As = (uint4*)smem_raw;
-    uint4* const Ws = As + XST * kXA;
     const int n0 = nbi * (GU ? XBW / 2 : XBW);
     switch ((tl.ncols + 31) >> 5) {
-        case 1: moe_gemm_tile<GU, 1>(a, tl, n0, As, Ws, rows); break;
-        case 2: moe_gemm_tile<GU, 2>(a, tl, n0, As, Ws, rows); break;
-        case 3: moe_gemm_tile<GU, 3>(a, tl, n0, As, Ws, rows); break;
-        default: moe_gemm_tile<GU, 4>(a, tl, n0, As, Ws, rows); break;
+        case 1: moe_gemm_tile<GU, 1>(a, tl, n0, As, rows); break;
+        case 2: moe_gemm_tile<GU, 2>(a, tl, n0, As, rows); break;
+        case 3: moe_gemm_tile<GU, 3>(a, tl, n0, As, rows); break;
+        default: moe_gemm_tile<GU, 4>(a, tl, n0, As, rows); break;
     }
 }
 

@@ -256,6 +256,11 @@ size_t gemv_q4k_mfma_lds(int K, int ncol);     // its LDS bytes; it runs when th
 constexpr size_t kMfmaLdsMax = 120 * 1024;
 int gemv_q8_dispatch_segs(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s);
 extern int g_mfma_min_ncol;
+// Q6_K_SOA GEMV of 2..8 columns on the int8 matrix cores (gemv_mfma.hip), bitwise the unit kernel;
+// the dispatch sends Q6_K_SOA calls of at least g_q6_mfma_min_ncol columns there (K % 512 == 0,
+// 16-byte aligned x scales)
+int gemv_q6k_mfma(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s);
+extern int g_q6_mfma_min_ncol;
 
 // the MoE decode step of qmm_moe_decode (moe.hip): argument checks, and the two launches with the gate /
 // up rows in gu (2 * T * (topk + 1) * F floats)

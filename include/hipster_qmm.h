@@ -168,16 +168,20 @@ int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream
  * tpr in {0,1,2,4,8,16,32} and rpt in {0,1,2,3} for compatibility. */
 int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, int tpr, int rpt, void* stream);
 /* several weights sharing x (reference: gemv_multi, gemv.h:28, gemv.hip:1355-1369); up to 4
- * segments, all with the same K, any ncol.  When every segment is Q4_K and ncol >= 2 all segments
- * run in one launch per 16 columns on the int8 matrix cores; otherwise one launch per segment and 8
- * columns.  Results are bitwise those of qmm_gemv_q8 on each segment, and a Q4_K column's bits do
+ * segments, all with the same K, any ncol.  When every segment is Q4_K and ncol >= 4 (the knob below)
+ * all segments run in one launch per 16 columns on the int8 matrix cores; otherwise one launch per
+ * segment and 8 columns.  Results are bitwise those of qmm_gemv_q8 on each segment, and a Q4_K column's bits do
  * not depend on ncol (the matrix-core kernel adds the same values in the same order as the
  * one-column kernel). */
 int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void* stream);
 /* Tuning knob (no reference counterpart, like the reference's bench knobs): Q4_K GEMV calls with at
- * least n columns use the matrix-core kernel (default 2; n > 16 keeps every call on the dot4
+ * least n columns use the matrix-core kernel (default 4; n > 16 keeps every call on the dot4
  * kernels).  Returns the previous value.  Results are the same bits either way. */
 int qmm_set_gemv_mfma_min_ncol(int n);
+/* Tuning knob (no reference counterpart): Q6_K_SOA GEMV calls of n..8 columns (K % 512 == 0,
+ * ncol * K <= 262144, x.d 16-byte aligned) use the int8 matrix-core kernel (default 3; n > 8 keeps
+ * every call on the dot4 kernels).  Returns the previous value.  Results are the same bits either way. */
+int qmm_set_gemv_q6k_mfma_min_ncol(int n);
 /* split-K GEMV for skinny weights (reference: gemv_splitk, gemv.h:55, gemv.hip:1397-1441):
  * part[(c*ksplit + ks)*N + n] = W[n][K range ks] . x[c][K range ks], the K range of split ks being the
  * 256-weight blocks [ks*nb/ksplit, (ks+1)*nb/ksplit), nb = ceil(K/256), as the reference's; the consumer

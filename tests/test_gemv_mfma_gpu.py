@@ -1,4 +1,4 @@
-"""The Q4_K decode GEMV on the int8 matrix cores (gemv_mfma.hip), through the C ABI.
+"""The Q4_K and Q6_K_SOA decode GEMVs on the int8 matrix cores (gemv_mfma.hip), through the C ABI.
 
 Bars: every column bitwise equal to the one-column dot4 kernel's result for the same x (so a column's
 bits do not depend on ncol, 1..16, nor on which kernel ran), at the headline shape and at shapes whose
@@ -101,3 +101,68 @@ def test_segments_in_one_launch_equal_separate_calls(gpu, ncol):
     torch.cuda.synchronize()
     for (_, _, y, _, _), r in zip(segs, ref):
         assert np.array_equal(host(y).view(np.uint32), r.view(np.uint32))
+
+
+class q6_min_ncol:
+    """qmm_set_gemv_q6k_mfma_min_ncol for the duration of a block"""
+
+    def __init__(self, n):
+        self.n = n
+
+    def __enter__(self):
+        self.prev = _lib.lib().qmm_set_gemv_q6k_mfma_min_ncol(self.n)
+
+    def __exit__(self, *a):
+        _lib.lib().qmm_set_gemv_q6k_mfma_min_ncol(self.prev)
+
+
+def q6_gemv(Wd, xb, N, K, ncol):
+    y = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+    qmm.gemv_q8(synth.Q6_K_SOA, Wd, xb, y, N, K, ncol)
+    torch.cuda.synchronize()
+    return host(y)
+
+
+@pytest.mark.parametrize("N,K", [(5120, 17408), (129, 512), (515, 2048), (77, 1024), (1000, 5120)])
+def test_q6k_matrix_cores_bitwise_dot4(gpu, N, K):
+    """Q6_K_SOA on the int8 matrix cores (forced from one column on) against the dot4 kernels (the
+    matrix cores switched off): every column bitwise equal, ncol 1..8; rows not a multiple of 16,
+    K = 512 (two blocks: two of the four waves have none) and block counts not a multiple of 4"""
+    print(f"q6k mfma vs dot4 N={N} K={K}", flush=True)
+    Wd = dev(synth.matrix(720 + N, synth.Q6_K_SOA, N, K))
+    x = synth.normal_f32(721, (8, K))
+    xb = q8_on_gpu(x)
+    for ncol in range(1, 9):
+        with q6_min_ncol(9):
+            ref = q6_gemv(Wd, xb, N, K, ncol)
+        with q6_min_ncol(1):
+            got = q6_gemv(Wd, xb, N, K, ncol)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), ncol
+
+
+def test_q6k_matrix_cores_against_oracle(gpu):
+    """the matrix-core Q6_K_SOA GEMV at 4 and 8 columns against the oracle within the GEMV bar"""
+    N, K = 333, 5120
+    W = synth.matrix(730, synth.Q6_K_SOA, N, K)
+    x = synth.normal_f32(731, (8, K))
+    q, d, _ = oracle.quantize_x_q8(x)
+    ref, mag = oracle.gemv_ref(synth.Q6_K_SOA, W, N, K, oracle.q8_to_f32(q, d))
+    xb = q8_on_gpu(x)
+    Wd = dev(W)
+    with q6_min_ncol(1):
+        for ncol in (4, 8):
+            y = q6_gemv(Wd, xb, N, K, ncol)
+            assert rel_l2(y, ref[:ncol]) <= 1e-5
+            assert max_rel_mag(y, ref[:ncol], mag[:ncol]) < 1e-5
+
+
+def test_q6k_matrix_cores_large_k_falls_back(gpu):
+    """ncol * K above the kernel's x-scale staging (8 x 65536) runs the dot4 kernels: the same bits"""
+    N, K = 64, 65536
+    Wd = dev(synth.matrix(740, synth.Q6_K_SOA, N, K))
+    xb = q8_on_gpu(synth.normal_f32(741, (8, K)))
+    with q6_min_ncol(9):
+        ref = q6_gemv(Wd, xb, N, K, 8)
+    with q6_min_ncol(1):
+        got = q6_gemv(Wd, xb, N, K, 8)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
