@@ -68,13 +68,17 @@ __device__ __forceinline__ uint4 xload(__amdgpu_buffer_rsrc_t rx, uint32_t off) 
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// XL: x comes from LDS at compute time (only the weights are loaded here)
+template <bool XL>
 __device__ __forceinline__ void mblk_load(MBlk& B, const uint8_t* rp, __amdgpu_buffer_rsrc_t rx, uint32_t xo, int b, int h) {
     const uint8_t* bp = rp + (size_t)b * 144;
     B.hd = ld16(bp);
     B.q[0] = ld16(bp + 16 + 16 * h);
     B.q[1] = ld16(bp + 80 + 16 * h);
+    if constexpr (!XL) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) B.x[j] = xload(rx, xo + (uint32_t)(b * 256 + 64 * j));
+        for (int j = 0; j < 4; ++j) B.x[j] = xload(rx, xo + (uint32_t)(b * 256 + 64 * j));
+    }
 }
 
 // {lane's 8 bytes of pair 2c, lane's 8 bytes of pair 2c+1} from the couple's 16-byte piece
@@ -93,9 +97,10 @@ __device__ __forceinline__ void couple_split(const uint4 v, uint2& p0, uint2& p1
 // the row's four quadruples meet in the wave's LDS slot (DS instructions of a wave run in order, so the
 // reads see the writes; the compiler barriers keep them in program order), then every lane reads the
 // four.  The same floats as decoding all four in every lane.
-template <int MV>
+// XL: the x piece of pair j is the 16 bytes at xl + 64 j (LDS)
+template <int MV, bool XL>
 __device__ __forceinline__ void mblk_compute(const MBlk& B, int b, int h, int r, bool live, const float4* __restrict__ sds,
-                                             float4* __restrict__ sslot, float (&acc)[4][MV]) {
+                                             float4* __restrict__ sslot, const uint8_t* xl, float (&acc)[4][MV]) {
     constexpr int NS = 4 * MV;
     {
         const Q4kPairScales own = q4k_pair_scales(B.hd, Q4kPairDecode(h));
@@ -111,7 +116,8 @@ __device__ __forceinline__ void mblk_compute(const MBlk& B, int b, int h, int r,
         const uint2 lo = make_uint2(q[j].x & 0x0f0f0f0fu, q[j].y & 0x0f0f0f0fu);
         const uint2 hi = make_uint2((q[j].x >> 4) & 0x0f0f0f0fu, (q[j].y >> 4) & 0x0f0f0f0fu);
         uint2 x0, x1;
-        couple_split(B.x[j], x0, x1);
+        if constexpr (XL) couple_split(*(const uint4*)(xl + 64 * j), x0, x1);
+        else couple_split(B.x[j], x0, x1);
         const i32x4 z = {0, 0, 0, 0};
         const i32x4 ca = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(x0), as_long(lo), z, 0, 0, 0);
         const i32x4 cb = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(x1), as_long(hi), z, 0, 0, 0);
@@ -132,10 +138,17 @@ __host__ __device__ inline size_t gemv_q4k_mfma_main_lds(int K, int mv) {
     return scales > parts ? scales : parts;
 }
 constexpr size_t kScaleSlotBytes = 4 * 2 * 16 * 4 * 16;
+// x staged in LDS (XL) for ncol <= 4 and ncol * K <= kXlMax: token c at c * (K + 64) (the 64-byte skew
+// spreads the tokens over the banks), then 256 bytes of zeros read by the empty token slots; staged
+// by kXlRegs 16-byte pieces per thread, loaded before the first weights
+constexpr int kXlRegs = 8;
+constexpr int kXlMax = 256 * 16 * kXlRegs;
+__host__ __device__ inline size_t gemv_q4k_mfma_xl_bytes(int K, int ncol) { return (size_t)ncol * (K + 64) + 256; }
 
 // grid = all 16-row tiles of all segments, 256 threads; LDS: x pair scales [K/64][4 MV] float4, after
-// the main loop reused for the partial sums [16][4 MV][16] float
-template <int MV>
+// the main loop reused for the partial sums [16][4 MV][16] float; the scale-exchange slots; with XL the
+// staged x.  XL takes the x loads out of the main loop (fewer load instructions, 32 fewer VGPRs).
+template <int MV, bool XL>
 __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                        const float* __restrict__ xs, int K, int ncol) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -159,6 +172,11 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
     const bool aval = (r & 3) < MV && ca < ncol;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, ncol * K, 0x00020000);
     const uint32_t xo = aval ? (uint32_t)(ca * K + 16 * h) : 0x40000000u;
+    // XL: the lane's x in LDS for block b at xlb + b * xls (the zero area for an empty slot)
+    uint8_t* const xlds = smem + gemv_q4k_mfma_main_lds(K, MV) + kScaleSlotBytes;
+    const int kp = K + 64;
+    const uint8_t* const xlb = aval ? xlds + ca * kp + 16 * h : xlds + ncol * kp + 16 * h;
+    const int xls = aval ? 256 : 0;
 
     // x pair scales {d[2p], d[2p+1], s[2p], s[2p+1]} of every (pair, token): item e = c * npair + p,
     // thread tid taking items tid + 256 u, loaded (unconditionally, clamped) before the first weights
@@ -173,10 +191,19 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
         const float2 dd = *(const float2*)(xd + (size_t)c * nsb + 2 * pp), ss = *(const float2*)(xs + (size_t)c * nsb + 2 * pp);
         sv[u] = make_float4(dd.x, dd.y, ss.x, ss.y);
     }
+    // XL: the x of every column, 16-byte piece e = c * (K / 16) + o (token c by a float reciprocal,
+    // exact for these small integers), loaded (clamped) ahead of the weights as well
+    const int nxq = XL ? ncol * (K >> 4) : 1;
+    const float inv_kq = 1.f / (float)(K >> 4);
+    uint4 xv[XL ? kXlRegs : 1];
+    if constexpr (XL) {
+#pragma unroll
+        for (int u = 0; u < kXlRegs; ++u) xv[u] = ld16(xq + (size_t)min(tid + 256 * u, nxq - 1) * 16);
+    }
     // every load below is unconditional (block indices clamped to the last block): with the same
     // loads on every path the wait counts stay exact and each prefetch stays in flight
     MBlk A, B;
-    mblk_load(A, rp, rx, xo, min(wave, nb - 1), h);
+    mblk_load<XL>(A, rp, rx, xo, min(wave, nb - 1), h);
 #pragma unroll
     for (int u = 0; u < kScaleRegs; ++u) {
         const int e = tid + 256 * u, c = (int)(((float)e + 0.5f) * inv_np), pp = e - c * npair;
@@ -186,6 +213,14 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
         const int c = (int)(((float)e + 0.5f) * inv_np), pp = e - c * npair;
         const float2 dd = *(const float2*)(xd + (size_t)c * nsb + 2 * pp), ss = *(const float2*)(xs + (size_t)c * nsb + 2 * pp);
         sds[pp * NS + c] = make_float4(dd.x, dd.y, ss.x, ss.y);
+    }
+    if constexpr (XL) {
+#pragma unroll
+        for (int u = 0; u < kXlRegs; ++u) {               // no branch: a clamped piece stores its own value
+            const int e = min(tid + 256 * u, nxq - 1), c = (int)(((float)e + 0.5f) * inv_kq), o = e - c * (K >> 4);
+            *(uint4*)(xlds + c * kp + 16 * o) = xv[u];
+        }
+        if (tid < 16) *(uint4*)(xlds + ncol * kp + 16 * tid) = make_uint4(0, 0, 0, 0);
     }
     lds_barrier();
 
@@ -197,12 +232,12 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
     // two register sets in turn; no branch around a load or a compute (the compiler would sink the
     // prefetch into it), and scheduling barriers keep each prefetch ahead of the compute it overlaps
     for (int b = wave; b < nb; b += 8) {                  // wave-uniform
-        mblk_load(B, rp, rx, xo, min(b + 4, nb - 1), h);
+        mblk_load<XL>(B, rp, rx, xo, min(b + 4, nb - 1), h);
         __builtin_amdgcn_sched_barrier(0);
-        mblk_compute<MV>(A, b, h, r, true, sds, sslot, acc);
-        mblk_load(A, rp, rx, xo, min(b + 8, nb - 1), h);
+        mblk_compute<MV, XL>(A, b, h, r, true, sds, sslot, xlb + b * xls, acc);
+        mblk_load<XL>(A, rp, rx, xo, min(b + 8, nb - 1), h);
         __builtin_amdgcn_sched_barrier(0);
-        mblk_compute<MV>(B, min(b + 4, nb - 1), h, r, b + 4 < nb, sds, sslot + 64, acc);
+        mblk_compute<MV, XL>(B, min(b + 4, nb - 1), h, r, b + 4 < nb, sds, sslot + 64, xlb + min(b + 4, nb - 1) * xls, acc);
     }
     __syncthreads();                                      // every wave is done with the scales
     // partial sum t = 4 wave + j of token MV h + v, row r
@@ -419,9 +454,14 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
 }
 }  // namespace
 
+// x in LDS: up to 4 columns whose x fits the staging registers
+static bool gemv_q4k_mfma_xl(int K, int ncol) { return ncol <= 4 && ncol * K <= kXlMax; }
+
 size_t gemv_q4k_mfma_lds(int K, int ncol) {
     const int mv = ncol <= 4 ? 1 : ncol <= 8 ? 2 : 4;
-    return K > kMfmaMaxK ? SIZE_MAX : gemv_q4k_mfma_main_lds(K, mv) + kScaleSlotBytes;
+    return K > kMfmaMaxK ? SIZE_MAX
+                         : gemv_q4k_mfma_main_lds(K, mv) + kScaleSlotBytes +
+                               (gemv_q4k_mfma_xl(K, ncol) ? gemv_q4k_mfma_xl_bytes(K, ncol) : 0);
 }
 
 // ncol (1..16) columns of q8 x against nseg (1..4) Q4_K segments sharing K, in one launch.  Shapes are
@@ -442,9 +482,14 @@ int gemv_q4k_mfma(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol
     if (lds > kMfmaLdsMax) return QMM_ERR_SHAPE;
     const dim3 grid((unsigned)sg.t0[nseg]);
     switch (mv) {
-        case 1: hipLaunchKernelGGL(k_gemv_q4k_mfma<1>, grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
-        case 2: hipLaunchKernelGGL(k_gemv_q4k_mfma<2>, grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
-        default: hipLaunchKernelGGL(k_gemv_q4k_mfma<4>, grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
+        case 1:
+            if (gemv_q4k_mfma_xl(K, ncol))
+                hipLaunchKernelGGL((k_gemv_q4k_mfma<1, true>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol);
+            else
+                hipLaunchKernelGGL((k_gemv_q4k_mfma<1, false>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol);
+            break;
+        case 2: hipLaunchKernelGGL((k_gemv_q4k_mfma<2, false>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
+        default: hipLaunchKernelGGL((k_gemv_q4k_mfma<4, false>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
     }
     QMM_LAUNCH_CHECK();
     return QMM_OK;
