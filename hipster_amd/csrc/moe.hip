@@ -279,41 +279,76 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
 }
 
 // ------------------------------------------------------------------------------------------
-// The MoE decode step (qmm_moe_decode).  At T = 1, launch 1 routes inside the gather: every
-// workgroup of the gate|up gather first routes the token itself (route_token, the arithmetic of
-// k_moe_route, so ids and weights are the same bits), then deduplicates and gathers exactly as
-// k_gemv_moe_q4k; workgroup (0, 0, 0) writes ids and weights out.  At T = 2..8 the routing work
-// would repeat in each of the T * (topk + 1) * rowblocks workgroups, so the step is the four
-// launches k_moe_route, k_gemv_moe_q4k, k_moe_silu_quant, k_gemv_moe_down_q4k.  At T = 1 the last launch stages h = silu(gate) * up of the token's slot rows, quantised per 32, straight into the
-// down GEMV's LDS layout (the arithmetic of k_moe_silu_quant: the same q8 bits), then runs the down
-// projection and the slot-ordered combine of k_gemv_moe_down_q4k.  The four-launch sequence
-// moe_route, gemv_moe (gate|up), moe_silu_quant, gemv_moe (down) gives the same y bit for bit.
+// The MoE decode step (qmm_moe_decode).  At T = 1 two launches: k_moe_route_gu_q8 (routing, the
+// gate|up rows and h = silu(g) * u as q8) and k_gemv_moe_down_q4k (the down projection and the
+// slot-ordered combine).  At T = 2..8 the routing would repeat in every workgroup, so the step is the
+// four launches k_moe_route, k_gemv_moe_q4k, k_moe_silu_quant, k_gemv_moe_down_q4k.  Either way the
+// four-launch sequence moe_route, gemv_moe (gate|up), moe_silu_quant, gemv_moe (down) gives the same
+// ids, weights and y bit for bit.
 constexpr int kDecMaxTok = 8;
 
+// The T = 1 step's first launch: workgroup (32-row block rb, slot e) routes the token (wave 0,
+// route_token: the arithmetic of k_moe_route) while the other waves stage x, then computes rows
+// rb*32..rb*32+31 of slot e's gate (waves 0-3) and up (waves 4-7) projections with the gather's
+// per-row arithmetic (q4k pairs over LPR lanes per row, the same floats as k_gemv_moe_q4k), meets them
+// in LDS and writes h = silu(g) * u quantised per 32 (half_wave_quant32: the q8 bits of
+// k_moe_silu_quant).  The second launch is then the plain q8 down projection (k_gemv_moe_down_q4k).
+constexpr int kGuWaves = 8;
+
 template <int LPR, int I, int VPL>
-__global__ void __launch_bounds__(256) k_moe_route_gather(qmm_moe_segs a, const float* __restrict__ logits, int stride, int nexp_total,
-                                                          int topk, int* __restrict__ ids_out, float* __restrict__ w_out,
-                                                          const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                                          const float* __restrict__ xsum, int N, int K, int T) {
+__global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs a, const float* __restrict__ logits,
+                                                                  int nexp_total, int topk, int* __restrict__ ids_out,
+                                                                  float* __restrict__ w_out, const int8_t* __restrict__ xq,
+                                                                  const float* __restrict__ xd, const float* __restrict__ xsum,
+                                                                  int F, int H, int8_t* __restrict__ hq, float* __restrict__ hd,
+                                                                  float* __restrict__ hs) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int s_ids[kDecMaxTok * kMaxSlots];
-    __shared__ float s_w[kDecMaxTok * kMaxSlots];
-    __shared__ int s_cols[64 + kMaxCols];
-    __shared__ int s_n, s_dup;
-    const int tid = threadIdx.x, wave = tid >> 6, nexp = topk + 1, nslot = T * nexp;
-    for (int t = wave; t < T; t += 4)                              // wave-uniform
-        route_token<VPL>(logits + (size_t)t * stride, nexp_total, topk, s_ids + t * nexp, s_w + t * nexp);
+    __shared__ int s_ids[kMaxSlots];
+    __shared__ float s_w[kMaxSlots];
+    __shared__ float s_gu[2][32];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (wave == 0) {
+        route_token<VPL>(logits, nexp_total, topk, s_ids, s_w);
+    } else {   // x (token 0) in the pair layout of stage_gather, column 0
+        const int nu = H >> 4, kq = H >> 6;
+        for (int v = tid - 64; v < nu; v += 64 * (kGuWaves - 1)) {
+            const int pp = v >> 2, q = v & 3;
+            *(uint4*)(smem + (size_t)(q * kq + pp) * 16) = ld16(xq + (size_t)v * 16);
+        }
+        for (int v = tid - 64; v < kq; v += 64 * (kGuWaves - 1)) {
+            const float2 dd = *(const float2*)(xd + 2 * v), ss = *(const float2*)(xsum + 2 * v);
+            *(float4*)(smem + (size_t)H + (size_t)v * 16) = make_float4(dd.x, dd.y, ss.x, ss.y);
+        }
+    }
     __syncthreads();
-    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && tid < nslot) {
+    const int e = blockIdx.y, rb = blockIdx.x, nexp = topk + 1;
+    if (rb == 0 && e == 0 && tid < nexp) {
         ids_out[tid] = s_ids[tid];
         w_out[tid] = s_w[tid];
     }
-    const int te = blockIdx.y, seg = blockIdx.z;
-    const int id = s_ids[te];
-    if (tid < 64) moe_slot_columns(s_ids, nslot, te, id, s_cols, &s_n, &s_dup);
+    const int id = s_ids[e], seg = wave >> 2;
+    constexpr int RPW = 64 / LPR, NP = 8 / RPW;          // rows per wave pass; passes for the wave's 8 rows
+    const int nb = H >> 8, ntask = 4 * nb, t = lane & (LPR - 1), j = t & 3;
+    const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[seg] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[seg];
+    Q4kPairs<I> A[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const int row = rb * 32 + (wave & 3) * 8 + p * RPW + lane / LPR;
+        q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, F - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[p]);
+    }
+    const Q4kPairDecode dc(j);
+    const XPairSrc<true> xs[1] = {XPairSrc<true>{smem, nullptr, nullptr, H}};
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        float acc[1] = {0.f};
+        if ((ntask % LPR) == 0) q4k_pairs_compute<1, I, true, true, LPR>(A[p], dc, t, ntask, 0, xs, acc);
+        else q4k_pairs_compute<1, I, true, false, LPR>(A[p], dc, t, ntask, 0, xs, acc);
+        acc[0] = group_sum(acc[0], LPR);
+        if (t == 0) s_gu[seg][(wave & 3) * 8 + p * RPW + lane / LPR] = acc[0];
+    }
     __syncthreads();
-    if (s_dup) return;
-    gather_expert<LPR, I>(a, seg, id, s_n, s_cols, smem, xq, xd, xsum, N, K, nexp, 0);
+    if (wave == 0 && lane < 32)
+        half_wave_quant32(silu_f(s_gu[0][lane]) * s_gu[1][lane], hq, hd, hs, (size_t)e * (F / 32) + rb, lane);
 }
 
 // the down projection of one token's slots: wave w takes the slots e = w, w + 4, ... (at most
@@ -360,30 +395,6 @@ __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __r
         for (int e = 0; e < nexp; ++e) acc += a.slotw[tok * nexp + e] * vres[e][tid];
         a.y[0][(size_t)tok * N + blockIdx.x * RPW + tid] = acc;
     }
-}
-
-// h = silu(g) * u of ncol rows of K (g, u row-major, rows of this token) -> q8 per 32 in the pair layout
-__device__ __forceinline__ void stage_silu_q8(uint8_t* lds, const float* __restrict__ g, const float* __restrict__ u, int ncol, int K) {
-    const int n8 = ncol * (K >> 3);
-    const int lim = (n8 + 255) & ~255;                            // whole quads stay together: n8 % 4 == 0
-    for (int e = threadIdx.x; e < lim; e += 256) {
-        const int ec = min(e, n8 - 1);
-        const float4 g0 = ((const float4*)g)[2 * ec], g1 = ((const float4*)g)[2 * ec + 1];
-        const float4 u0 = ((const float4*)u)[2 * ec], u1 = ((const float4*)u)[2 * ec + 1];
-        const float4 a = make_float4(silu_f(g0.x) * u0.x, silu_f(g0.y) * u0.y, silu_f(g0.z) * u0.z, silu_f(g0.w) * u0.w);
-        const float4 b = make_float4(silu_f(g1.x) * u1.x, silu_f(g1.y) * u1.y, silu_f(g1.z) * u1.z, silu_f(g1.w) * u1.w);
-        stagef_store_one(lds, K, a, b, e, n8);
-    }
-}
-
-template <int LPR, int I>
-__global__ void __launch_bounds__(256) k_moe_silu_down(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
-                                                       const float* __restrict__ gate, const float* __restrict__ up, int N, int K) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int tok = blockIdx.y;
-    down_slots<LPR, I>(a, ids, nexp, smem, N, K, [&] {
-        stage_silu_q8(smem, gate + (size_t)tok * nexp * K, up + (size_t)tok * nexp * K, nexp, K);
-    });
 }
 
 // ------------------------------------------------------------------------------------------
@@ -472,15 +483,15 @@ int launch_down(const qmm_moe_segs& a, const int* ids, int nexp, qmm_xq8 x, int 
     return QMM_OK;
 }
 
-// the two launches of qmm_moe_decode (shapes checked by the caller)
+// the T = 1 step's first launch (k_moe_route_gu_q8): q8 of h into hq / hd / hs
 template <int LPR, int VPL>
-int launch_decode_gather(const qmm_moe_segs& a, const float* logits, int stride, int nexp_total, int topk, int* ids, float* w,
-                         qmm_xq8 x, int F, int H, int T, hipStream_t s) {
+int launch_decode_gu_q8(const qmm_moe_segs& a, const float* logits, int nexp_total, int topk, int* ids, float* w, qmm_xq8 x, int F,
+                        int H, qmm_xq8 h, hipStream_t s) {
     const int iters = (H / 256 * 4 + LPR - 1) / LPR;
-    const dim3 grid((F + 4 * (64 / LPR) - 1) / (4 * (64 / LPR)), T * (topk + 1), 2);
-    const size_t lds = (size_t)kMaxCols * (H + H / 4);
-#define QMM_G(IV) case IV: hipLaunchKernelGGL((k_moe_route_gather<LPR, IV, VPL>), grid, dim3(256), lds, s, a, logits, stride, nexp_total, \
-                                              topk, ids, w, x.q, x.d, x.s, F, H, T); break;
+    const dim3 grid(F / 32, topk + 1);
+    const size_t lds = (size_t)H + H / 4;
+#define QMM_G(IV) case IV: hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL>), grid, dim3(64 * kGuWaves), lds, s, a, logits, nexp_total, \
+                                              topk, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s); break;
     switch (iters) {
         QMM_G(1) QMM_G(2) QMM_G(3) QMM_G(4) QMM_G(5) QMM_G(6)
         default: return QMM_ERR_SHAPE;
@@ -490,27 +501,11 @@ int launch_decode_gather(const qmm_moe_segs& a, const float* logits, int stride,
     return QMM_OK;
 }
 
-template <int LPR>
-int launch_decode_down(const qmm_moe_segs& a, const int* ids, int nexp, const float* gate, const float* up, int H, int F, int T,
-                       hipStream_t s) {
-    const int iters = (F / 256 * 4 + LPR - 1) / LPR;
-    const dim3 grid((H + (64 / LPR) - 1) / (64 / LPR), T);
-    const size_t lds = (size_t)nexp * (F + F / 4);
-#define QMM_D(IV) case IV: hipLaunchKernelGGL((k_moe_silu_down<LPR, IV>), grid, dim3(256), lds, s, a, ids, nexp, gate, up, H, F); break;
-    switch (iters) {
-        QMM_D(1) QMM_D(2) QMM_D(3) QMM_D(4) QMM_D(5) QMM_D(6)
-        default: return QMM_ERR_SHAPE;
-    }
-#undef QMM_D
-    QMM_LAUNCH_CHECK();
-    return QMM_OK;
-}
-
 template <int VPL>
-int decode_gather_vpl(const qmm_moe_segs& a, const float* logits, int stride, int nexp_total, int topk, int* ids, float* w, qmm_xq8 x,
-                      int F, int H, int T, hipStream_t s) {
-    return moe_lpr(H) == 8 ? launch_decode_gather<8, VPL>(a, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
-                           : launch_decode_gather<16, VPL>(a, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s);
+int decode_gu_q8_vpl(const qmm_moe_segs& a, const float* logits, int nexp_total, int topk, int* ids, float* w, qmm_xq8 x, int F, int H,
+                     qmm_xq8 h, hipStream_t s) {
+    return moe_lpr(H) == 8 ? launch_decode_gu_q8<8, VPL>(a, logits, nexp_total, topk, ids, w, x, F, H, h, s)
+                           : launch_decode_gu_q8<16, VPL>(a, logits, nexp_total, topk, ids, w, x, F, H, h, s);
 }
 
 }  // namespace
@@ -527,7 +522,8 @@ int moe_decode_check(int fmt, const void* Wg, const void* Wu, const void* Wd, co
     return QMM_OK;
 }
 
-// the launches, gate / up rows in gu (2 * T * (topk + 1) * F floats, then at T > 1 the q8 of h)
+// the launches; workspace gu: at T = 1 the q8 of h, at T > 1 the gate / up rows (2 * T * (topk + 1) * F
+// floats), then the q8 of h
 int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg, const void* Su,
                    const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H, int F, int* ids,
                    float* w, float* gu, float* y, hipStream_t s) {
@@ -538,10 +534,16 @@ int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes
     const qmm_moe_segs ga = {{Wg, Wu}, {Sg, Su}, {gate, up}, ebytes_gu, nullptr};
     int rc;
     if (T == 1) {
-        rc = nexp_total <= 128 ? decode_gather_vpl<2>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
-           : nexp_total <= 256 ? decode_gather_vpl<4>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
-           : nexp_total <= 512 ? decode_gather_vpl<8>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s)
-                               : decode_gather_vpl<16>(ga, logits, stride, nexp_total, topk, ids, w, x, F, H, T, s);
+        // h as q8 at the start of the workspace (the gate / up rows are not kept at T = 1)
+        const size_t nh = (size_t)nexp * F;
+        const qmm_xq8 h = {(int8_t*)gu, gu + nh / 4, gu + nh / 4 + nh / 32};
+        rc = nexp_total <= 128 ? decode_gu_q8_vpl<2>(ga, logits, nexp_total, topk, ids, w, x, F, H, h, s)
+           : nexp_total <= 256 ? decode_gu_q8_vpl<4>(ga, logits, nexp_total, topk, ids, w, x, F, H, h, s)
+           : nexp_total <= 512 ? decode_gu_q8_vpl<8>(ga, logits, nexp_total, topk, ids, w, x, F, H, h, s)
+                               : decode_gu_q8_vpl<16>(ga, logits, nexp_total, topk, ids, w, x, F, H, h, s);
+        if (rc != QMM_OK) return rc;
+        const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
+        return moe_lpr(F) == 8 ? launch_down<8>(da, ids, nexp, h, H, F, T, s) : launch_down<16>(da, ids, nexp, h, H, F, T, s);
     } else {
         // every gather workgroup would route all T tokens again, and every down workgroup would
         // redo silu-q8 of all the token's rows: route once, quantise h once (the four launches)
@@ -555,10 +557,6 @@ int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes
         const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
         return moe_lpr(F) == 8 ? launch_down<8>(da, ids, nexp, h, H, F, T, s) : launch_down<16>(da, ids, nexp, h, H, F, T, s);
     }
-    if (rc != QMM_OK) return rc;
-    const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
-    return moe_lpr(F) == 8 ? launch_decode_down<8>(da, ids, nexp, gate, up, H, F, T, s)
-                           : launch_decode_down<16>(da, ids, nexp, gate, up, H, F, T, s);
 }
 
 // the device address of `scratch` on the current device, looked up on the first call per device

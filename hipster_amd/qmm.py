@@ -221,9 +221,9 @@ def moe_decode_ws_bytes(T, topk, F):
 
 def moe_decode(fmt, Wg, Wu, Wd, ebytes_gu, ebytes_d, Sg, Su, Sd, logits, stride, nexp_total, topk, x, T, H, F, ids, w, ws, y,
                stream=None):
-    """The MoE decode step in one call (T = 1: two launches, routing inside the gate|up gather and silu * up
-    -> q8 inside the down projection; T > 1: the four launches); ids / w [T][topk+1] and y [T][H] out, bitwise moe_route + gemv_moe + moe_silu_quant +
-    gemv_moe.  ws: a device buffer of moe_decode_ws_bytes(T, topk, F) bytes."""
+    """The MoE decode step in one call (T = 1: two launches, routing + gate|up + silu * up -> q8, then the
+    down projection; T > 1: the four launches); ids / w [T][topk+1] and y [T][H] out, bitwise moe_route + gemv_moe +
+    moe_silu_quant + gemv_moe.  ws: a device buffer of moe_decode_ws_bytes(T, topk, F) bytes."""
     check(_lib.lib().qmm_moe_decode(fmt, _p(Wg), _p(Wu), _p(Wd), ebytes_gu, ebytes_d, _p(Sg), _p(Su), _p(Sd), _p(logits), stride,
                                     nexp_total, topk, x.c(), T, H, F, _p(ids), _p(w), _p(ws), ws.numel() * ws.element_size(),
                                     _p(y), _stream(stream)), "moe_decode")
