@@ -91,19 +91,37 @@ __device__ __forceinline__ void stage_xq8(uint8_t* lds, const int8_t* __restrict
     __syncthreads();
 }
 
+// Q4_K weights sharing x and K in one launch (the reference's k_gemv_multi, gemv.hip:1042-1067):
+// workgroup (16-row tile) i belongs to segment s when t0[s] <= i < t0[s + 1]
+constexpr int kQSegMax = 4;
+struct QSegs {
+    const uint8_t* w[kQSegMax];
+    float* y[kQSegMax];
+    int N[kQSegMax];
+    int t0[kQSegMax + 1];
+    int nseg;
+};
+
 // ILOAD pair iterations per load batch; NITER > 0: the row is exactly NITER iterations and is
 // loaded in one batch, with x staged from registers loaded ahead of the weights (XU units per
-// thread); NITER == 0: any length, streamed in double-buffered batches of ILOAD.
+// thread); NITER == 0: any length, streamed in double-buffered batches of ILOAD.  The rows of every
+// segment get the same arithmetic as alone.
 template <int NCOL, int ILOAD, int NITER, bool XLDS>
-__global__ void __launch_bounds__(kBlock) k_gemv_q4k_q8(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
-                                                        const float* __restrict__ xd, const float* __restrict__ xs,
-                                                        float* __restrict__ y, int N, int K) {
+__global__ void __launch_bounds__(kBlock) k_gemv_q4k_q8(QSegs sg, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                        const float* __restrict__ xs, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int XU = (NITER > 0 && XLDS && NCOL <= QMM_Q4K_XFIRST_NCOL) ? 2 * NCOL : 0;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < kQSegMax; ++i)
+        if (i < sg.nseg && (int)blockIdx.x >= sg.t0[i]) si = i;
+    const uint8_t* __restrict__ W = sg.w[si];
+    float* __restrict__ y = sg.y[si];
+    const int N = sg.N[si];
     const int nb = K >> 8, ntask = 4 * nb, nsb = K >> 5;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = lane & 15, j = t & 3;
-    const int row = (blockIdx.x * kWavesPerBlock + wave) * 4 + (lane >> 4);
+    const int row = (((int)blockIdx.x - sg.t0[si]) * kWavesPerBlock + wave) * 4 + (lane >> 4);
     const uint8_t* rp = W + (size_t)min(row, N - 1) * ((size_t)nb * 144);
     Q4kPairs<ILOAD> A, B;
     XPairSrc<XLDS> xsrc[NCOL];
@@ -666,27 +684,62 @@ inline int persistent_grid(int N) {
 // depends on (N, K) only, never on ncol (T-invariance).  x goes to LDS when NCOL columns fit in
 // kXLdsBudget (5K/4 bytes per column).
 template <int NCOL, int ILOAD, int NITER>
-int launch_q4k_q8_i(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+int launch_q4k_q8_i(const QSegs& sg, qmm_xq8 x, int K, hipStream_t s) {
     const size_t lds = (size_t)NCOL * (K + K / 4);
-    const int grid = (N + 4 * kWavesPerBlock - 1) / (4 * kWavesPerBlock);
+    const int grid = sg.t0[sg.nseg];
     if (lds <= kXLdsBudget)
-        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, ILOAD, NITER, true>), dim3(grid), dim3(kBlock), lds, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
+        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, ILOAD, NITER, true>), dim3(grid), dim3(kBlock), lds, s, sg, x.q, x.d, x.s, K);
     else
-        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, ILOAD, NITER, false>), dim3(grid), dim3(kBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K);
+        hipLaunchKernelGGL((k_gemv_q4k_q8<NCOL, ILOAD, NITER, false>), dim3(grid), dim3(kBlock), 0, s, sg, x.q, x.d, x.s, K);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }
 
 template <int NCOL>
-int launch_q4k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+int launch_q4k_q8_segs(const QSegs& sg, qmm_xq8 x, int K, hipStream_t s) {
     switch ((K / 256 * 4 + 15) / 16) {   // pair iterations per lane
-        case 1: return launch_q4k_q8_i<NCOL, 1, 1>(W, x, y, N, K, s);
-        case 2: return launch_q4k_q8_i<NCOL, 2, 2>(W, x, y, N, K, s);
-        case 3: return launch_q4k_q8_i<NCOL, 3, 3>(W, x, y, N, K, s);
-        case 4: return launch_q4k_q8_i<NCOL, 4, 4>(W, x, y, N, K, s);
-        case 5: return launch_q4k_q8_i<NCOL, 5, 5>(W, x, y, N, K, s);
-        case 6: return launch_q4k_q8_i<NCOL, 6, 6>(W, x, y, N, K, s);
-        default: return launch_q4k_q8_i<NCOL, 4, 0>(W, x, y, N, K, s);
+        case 1: return launch_q4k_q8_i<NCOL, 1, 1>(sg, x, K, s);
+        case 2: return launch_q4k_q8_i<NCOL, 2, 2>(sg, x, K, s);
+        case 3: return launch_q4k_q8_i<NCOL, 3, 3>(sg, x, K, s);
+        case 4: return launch_q4k_q8_i<NCOL, 4, 4>(sg, x, K, s);
+        case 5: return launch_q4k_q8_i<NCOL, 5, 5>(sg, x, K, s);
+        case 6: return launch_q4k_q8_i<NCOL, 6, 6>(sg, x, K, s);
+        default: return launch_q4k_q8_i<NCOL, 4, 0>(sg, x, K, s);
+    }
+}
+
+// segments (Q4_K, one K) as a tile table
+inline QSegs q4k_segs(const qmm_gemv_seg* segs, int nseg, int c0) {
+    QSegs sg = {};
+    sg.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) {
+        sg.w[i] = (const uint8_t*)segs[i].w;
+        sg.y[i] = segs[i].y + (size_t)c0 * segs[i].N;
+        sg.N[i] = segs[i].N;
+        sg.t0[i + 1] = sg.t0[i] + (segs[i].N + 4 * kWavesPerBlock - 1) / (4 * kWavesPerBlock);
+    }
+    return sg;
+}
+
+template <int NCOL>
+int launch_q4k_q8(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    const qmm_gemv_seg seg = {QMM_Q4_K, W, y, N, K};
+    return launch_q4k_q8_segs<NCOL>(q4k_segs(&seg, 1, 0), x, K, s);
+}
+
+// ncol (1..8) columns against nseg Q4_K segments sharing x and K on the dot4 kernel, one launch
+int gemv_q4k_q8_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, int c0, hipStream_t s) {
+    const QSegs sg = q4k_segs(segs, nseg, c0);
+    switch (ncol) {
+        case 1: return launch_q4k_q8_segs<1>(sg, x, K, s);
+        case 2: return launch_q4k_q8_segs<2>(sg, x, K, s);
+        case 3: return launch_q4k_q8_segs<3>(sg, x, K, s);
+        case 4: return launch_q4k_q8_segs<4>(sg, x, K, s);
+        case 5: return launch_q4k_q8_segs<5>(sg, x, K, s);
+        case 6: return launch_q4k_q8_segs<6>(sg, x, K, s);
+        case 7: return launch_q4k_q8_segs<7>(sg, x, K, s);
+        case 8: return launch_q4k_q8_segs<8>(sg, x, K, s);
+        default: return QMM_ERR_SHAPE;
     }
 }
 
@@ -937,12 +990,6 @@ int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, 
     }
 }
 
-int gemv_q8_dispatch_segs(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s) {
-    for (int i = 0; i < nseg; ++i)
-        if (int e = gemv_q8_dispatch(segs[i].fmt, segs[i].w, x, segs[i].y, segs[i].N, K, ncol, s)) return e;
-    return QMM_OK;
-}
-
 }  // namespace qmm
 
 using namespace qmm;
@@ -1028,10 +1075,18 @@ int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void
                 sc[i] = segs[i];
                 sc[i].y = segs[i].y + (size_t)c0 * segs[i].N;
             }
-            // a tail pass of one column keeps the one-column kernel (the same bits)
+            // a tail pass of fewer columns runs the dot4 kernel, all segments in one launch (the same bits)
             const int e = nc >= g_mfma_min_ncol ? gemv_q4k_mfma(sc, nseg, xc, K, nc, (hipStream_t)stream)
-                                                : gemv_q8_dispatch_segs(sc, nseg, xc, K, nc, (hipStream_t)stream);
+                                                : gemv_q4k_q8_multi(segs, nseg, xc, K, nc, c0, (hipStream_t)stream);
             if (e) return e;
+        }
+        return QMM_OK;
+    }
+    if (all_q4k) {                                           // the dot4 kernel, all segments in one launch per 8 columns
+        for (int c0 = 0; c0 < ncol; c0 += 8) {
+            const int nc = ncol - c0 < 8 ? ncol - c0 : 8;
+            qmm_xq8 xc = {x.q + (size_t)c0 * K, x.d + (size_t)c0 * (K / 32), x.s + (size_t)c0 * (K / 32), nullptr};
+            if (int e = gemv_q4k_q8_multi(segs, nseg, xc, K, nc, c0, (hipStream_t)stream)) return e;
         }
         return QMM_OK;
     }

@@ -254,7 +254,6 @@ int launch_moe_gemm_fmt(int fmt, int sfmt, const void* W, const void* Wsh, size_
 int gemv_q4k_mfma(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s);
 size_t gemv_q4k_mfma_lds(int K, int ncol);     // its LDS bytes; it runs when they are <= kMfmaLdsMax
 constexpr size_t kMfmaLdsMax = 120 * 1024;
-int gemv_q8_dispatch_segs(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s);
 extern int g_mfma_min_ncol;
 // Q6_K_SOA GEMV of 2..8 columns on the int8 matrix cores (gemv_mfma.hip), bitwise the unit kernel;
 // the dispatch sends Q6_K_SOA calls of at least g_q6_mfma_min_ncol columns there (K % 512 == 0,

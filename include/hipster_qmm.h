@@ -168,9 +168,9 @@ int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream
  * tpr in {0,1,2,4,8,16,32} and rpt in {0,1,2,3} for compatibility. */
 int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, int tpr, int rpt, void* stream);
 /* several weights sharing x (reference: gemv_multi, gemv.h:28, gemv.hip:1355-1369); up to 4
- * segments, all with the same K, any ncol.  When every segment is Q4_K and ncol >= 4 (the knob below)
- * all segments run in one launch per 16 columns on the int8 matrix cores; otherwise one launch per
- * segment and 8 columns.  Results are bitwise those of qmm_gemv_q8 on each segment, and a Q4_K column's bits do
+ * segments, all with the same K, any ncol.  When every segment is Q4_K all segments run in one launch:
+ * per 16 columns on the int8 matrix cores from 4 columns on (the knob below), else per 8 columns on the
+ * dot4 kernel; other formats run one launch per segment and 8 columns.  Results are bitwise those of qmm_gemv_q8 on each segment, and a Q4_K column's bits do
  * not depend on ncol (the matrix-core kernel adds the same values in the same order as the
  * one-column kernel). */
 int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void* stream);

@@ -125,6 +125,32 @@ def test_gemv_multi_equals_separate_calls(gpu):
         assert torch.equal(y, y1)
 
 
+@pytest.mark.parametrize("K", [5120, 17408, 768])
+def test_gemv_multi_q4k_one_launch_equals_separate_calls(gpu, K):
+    """all-Q4_K segments in one dot4 launch (ncol 1..3; ncol 17: a matrix-core pass of 16 columns, then the
+    17th on the dot4 kernel) bitwise the separate one-segment calls; ragged row counts, K = 17408 takes the
+    streamed long-row form"""
+    Ns = [1000, 77, 4099, 16]
+    x = synth.normal_f32(620, (17, K))
+    xb = q8_on_gpu(x)
+    Ws = [dev(synth.matrix(630 + i + K, synth.Q4_K, N, K)) for i, N in enumerate(Ns)]
+    for ncol in (1, 2, 3, 17):
+        print(f"gemv_multi q4k K={K} ncol={ncol}", flush=True)
+        segs, ref = [], []
+        for W, N in zip(Ws, Ns):
+            y = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+            y1 = torch.zeros((ncol, N), dtype=torch.float32, device="cuda")
+            for c0 in range(0, ncol, 8):
+                nc = min(8, ncol - c0)
+                xc = qmm.XQ8Buf(nc, K)
+                xc.q.copy_(xb.q[c0:c0 + nc]); xc.d.copy_(xb.d[c0:c0 + nc]); xc.s.copy_(xb.s[c0:c0 + nc])
+                qmm.gemv_q8(synth.Q4_K, W, xc, y1[c0:c0 + nc], N, K, nc)
+            segs.append((synth.Q4_K, W, y, N, K)); ref.append(y1)
+        qmm.gemv_multi(segs, xb, ncol)
+        for (_, _, y, _, _), y1 in zip(segs, ref):
+            assert np.array_equal(host(y).view(np.uint32), host(y1).view(np.uint32)), ncol
+
+
 @pytest.mark.parametrize("N,K", [(17408, 5120), (999, 256), (4096, 2048), (77, 768), (300, 17408)])
 def test_gemv_q4_K_f32_parity(gpu, N, K):
     """f32 x (the 1e-5 semantics of gemv.hip:1177-1216) against the oracle; column 0 is bitwise the
