@@ -279,55 +279,98 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
 }
 
 // ------------------------------------------------------------------------------------------
-// The MoE decode step (qmm_moe_decode).  At T = 1 two launches: k_moe_route_gu_q8 (routing, the
+// The MoE decode step (qmm_moe_decode), T <= 8, two launches: k_moe_route_gu_q8 (routing, the
 // gate|up rows and h = silu(g) * u as q8) and k_gemv_moe_down_q4k (the down projection and the
-// slot-ordered combine).  At T = 2..8 the routing would repeat in every workgroup, so the step is the
-// four launches k_moe_route, k_gemv_moe_q4k, k_moe_silu_quant, k_gemv_moe_down_q4k.  Either way the
-// four-launch sequence moe_route, gemv_moe (gate|up), moe_silu_quant, gemv_moe (down) gives the same
-// ids, weights and y bit for bit.
+// slot-ordered combine).  The four-launch sequence moe_route, gemv_moe (gate|up), moe_silu_quant,
+// gemv_moe (down) gives the same ids, weights, q8 of h and y bit for bit.
 constexpr int kDecMaxTok = 8;
 
-// The T = 1 step's first launch: workgroup (32-row block rb, slot e) routes the token (wave 0,
-// route_token: the arithmetic of k_moe_route) while the other waves stage x, then computes rows
-// rb*32..rb*32+31 of slot e's gate (waves 0-3) and up (waves 4-7) projections with the gather's
-// per-row arithmetic (q4k pairs over LPR lanes per row, the same floats as k_gemv_moe_q4k), meets them
-// in LDS and writes h = silu(g) * u quantised per 32 (half_wave_quant32: the q8 bits of
-// k_moe_silu_quant).  The second launch is then the plain q8 down projection (k_gemv_moe_down_q4k).
+// The step's first launch (T <= 8): workgroup (32-row block rb, slot e) routes the T tokens (wave t
+// routes token t, route_token: the arithmetic of k_moe_route) while the other waves stage the tokens'
+// x; then, if e is the first slot holding its expert (the gather's dedup, moe_slot_columns), it
+// computes rows rb*32..rb*32+31 of that expert's gate (waves 0-3) and up (waves 4-7) projections for
+// every slot holding it (the columns, in slot order) with the gather's per-row arithmetic (q4k pairs
+// over LPR lanes per row: the same floats as k_gemv_moe_q4k), meets them in LDS and writes, one
+// half-wave per column, h = silu(g) * u quantised per 32 (half_wave_quant32: the q8 bits of
+// k_moe_silu_quant).  The second launch is the plain q8 down projection (k_gemv_moe_down_q4k).
 constexpr int kGuWaves = 8;
 
-template <int LPR, int I, int VPL>
-__global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs a, const float* __restrict__ logits,
-                                                                  int nexp_total, int topk, int* __restrict__ ids_out,
+template <int NC, int LPR, int I>
+__device__ __forceinline__ void gu_rows(const Q4kPairs<I> (&A)[8 / (64 / LPR)], const uint8_t* smem, const int* cols, int nexp, int H,
+                                        int t, int j, int ntask, int rbase, float (*s_g)[kDecMaxTok]) {
+    constexpr int RPW = 64 / LPR, NP = 8 / RPW;
+    XPairSrc<true> xs[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) xs[c] = XPairSrc<true>{smem + (size_t)(cols[c] / nexp) * (H + (H >> 2)), nullptr, nullptr, H};
+    const Q4kPairDecode dc(j);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        float acc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[c] = 0.f;
+        if ((ntask % LPR) == 0) q4k_pairs_compute<NC, I, true, true, LPR>(A[p], dc, t, ntask, 0, xs, acc);
+        else q4k_pairs_compute<NC, I, true, false, LPR>(A[p], dc, t, ntask, 0, xs, acc);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[c] = group_sum(acc[c], LPR);
+        if (t == 0) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) s_g[rbase + p * RPW][c] = acc[c];
+        }
+    }
+}
+
+// ROUTE false: the ids come from ids_out (k_moe_route ran before), nothing is routed or written there
+template <int LPR, int I, int VPL, bool ROUTE>
+__global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs a, const float* __restrict__ logits, int stride,
+                                                                  int nexp_total, int topk, int T, int* __restrict__ ids_out,
                                                                   float* __restrict__ w_out, const int8_t* __restrict__ xq,
                                                                   const float* __restrict__ xd, const float* __restrict__ xsum,
                                                                   int F, int H, int8_t* __restrict__ hq, float* __restrict__ hd,
                                                                   float* __restrict__ hs) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int s_ids[kMaxSlots];
-    __shared__ float s_w[kMaxSlots];
-    __shared__ float s_gu[2][32];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    if (wave == 0) {
-        route_token<VPL>(logits, nexp_total, topk, s_ids, s_w);
-    } else {   // x (token 0) in the pair layout of stage_gather, column 0
-        const int nu = H >> 4, kq = H >> 6;
-        for (int v = tid - 64; v < nu; v += 64 * (kGuWaves - 1)) {
-            const int pp = v >> 2, q = v & 3;
-            *(uint4*)(smem + (size_t)(q * kq + pp) * 16) = ld16(xq + (size_t)v * 16);
+    __shared__ int s_ids[kDecMaxTok * kMaxSlots];
+    __shared__ float s_w[kDecMaxTok * kMaxSlots];
+    __shared__ int s_cols[64 + kMaxCols];
+    __shared__ int s_n, s_dup;
+    __shared__ float s_gu[2][32][kDecMaxTok];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nexp = topk + 1, nslot = T * nexp;
+    // x of the T tokens in the pair layout of stage_gather, token c at c * 5H/4
+    auto stage = [&](int first, int step) {
+        const int nu = H >> 4, kq = H >> 6, nsb = H >> 5;
+        for (int v = first; v < T * nu; v += step) {
+            const int c = v / nu, u = v - c * nu, pp = u >> 2, q = u & 3;
+            *(uint4*)(smem + (size_t)c * (H + (H >> 2)) + (size_t)(q * kq + pp) * 16) = ld16(xq + (size_t)c * H + (size_t)u * 16);
         }
-        for (int v = tid - 64; v < kq; v += 64 * (kGuWaves - 1)) {
-            const float2 dd = *(const float2*)(xd + 2 * v), ss = *(const float2*)(xsum + 2 * v);
-            *(float4*)(smem + (size_t)H + (size_t)v * 16) = make_float4(dd.x, dd.y, ss.x, ss.y);
+        for (int v = first; v < T * kq; v += step) {
+            const int c = v / kq, pp = v - c * kq;
+            const float2 dd = *(const float2*)(xd + (size_t)c * nsb + 2 * pp), ss = *(const float2*)(xsum + (size_t)c * nsb + 2 * pp);
+            *(float4*)(smem + (size_t)c * (H + (H >> 2)) + (size_t)H + (size_t)pp * 16) = make_float4(dd.x, dd.y, ss.x, ss.y);
         }
+    };
+    const int e = blockIdx.y, rb = blockIdx.x;
+    if constexpr (ROUTE) {
+        if (wave < T) route_token<VPL>(logits + (size_t)wave * stride, nexp_total, topk, s_ids + wave * nexp, s_w + wave * nexp);
+        else stage(tid - 64 * T, 64 * (kGuWaves - T));
+        __syncthreads();
+        if (T == kGuWaves) {                                 // every wave routed: stage now
+            stage(tid, 64 * kGuWaves);
+            __syncthreads();
+        }
+        if (rb == 0 && e == 0 && tid < nslot) {
+            ids_out[tid] = s_ids[tid];
+            w_out[tid] = s_w[tid];
+        }
+    } else {
+        if (tid < nslot) s_ids[tid] = ids_out[tid];
+        stage(tid, 64 * kGuWaves);
+        __syncthreads();
     }
+    const int id = s_ids[e];
+    if (tid < 64) moe_slot_columns(s_ids, nslot, e, id, s_cols, &s_n, &s_dup);
     __syncthreads();
-    const int e = blockIdx.y, rb = blockIdx.x, nexp = topk + 1;
-    if (rb == 0 && e == 0 && tid < nexp) {
-        ids_out[tid] = s_ids[tid];
-        w_out[tid] = s_w[tid];
-    }
-    const int id = s_ids[e], seg = wave >> 2;
-    constexpr int RPW = 64 / LPR, NP = 8 / RPW;          // rows per wave pass; passes for the wave's 8 rows
+    if (s_dup) return;                                       // an earlier slot computes this expert
+    const int seg = wave >> 2, ncols = min(s_n, kMaxCols);     // at most T <= 8: a token holds an expert once
+    constexpr int RPW = 64 / LPR, NP = 8 / RPW;              // rows per wave pass; passes for the wave's 8 rows
     const int nb = H >> 8, ntask = 4 * nb, t = lane & (LPR - 1), j = t & 3;
     const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[seg] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[seg];
     Q4kPairs<I> A[NP];
@@ -336,19 +379,17 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
         const int row = rb * 32 + (wave & 3) * 8 + p * RPW + lane / LPR;
         q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, F - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[p]);
     }
-    const Q4kPairDecode dc(j);
-    const XPairSrc<true> xs[1] = {XPairSrc<true>{smem, nullptr, nullptr, H}};
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        float acc[1] = {0.f};
-        if ((ntask % LPR) == 0) q4k_pairs_compute<1, I, true, true, LPR>(A[p], dc, t, ntask, 0, xs, acc);
-        else q4k_pairs_compute<1, I, true, false, LPR>(A[p], dc, t, ntask, 0, xs, acc);
-        acc[0] = group_sum(acc[0], LPR);
-        if (t == 0) s_gu[seg][(wave & 3) * 8 + p * RPW + lane / LPR] = acc[0];
+    const int rbase = (wave & 3) * 8 + lane / LPR;
+    switch (ncols) {
+#define QMM_GU(NCV) case NCV: gu_rows<NCV, LPR, I>(A, smem, s_cols, nexp, H, t, j, ntask, rbase, s_gu[seg]); break;
+        QMM_GU(1) QMM_GU(2) QMM_GU(3) QMM_GU(4) QMM_GU(5) QMM_GU(6) QMM_GU(7) QMM_GU(8)
+#undef QMM_GU
     }
     __syncthreads();
-    if (wave == 0 && lane < 32)
-        half_wave_quant32(silu_f(s_gu[0][lane]) * s_gu[1][lane], hq, hd, hs, (size_t)e * (F / 32) + rb, lane);
+    if (tid < 32 * ncols) {                                  // one half-wave per column: its slot's q8 block
+        const int c = tid >> 5, l = tid & 31;
+        half_wave_quant32(silu_f(s_gu[0][l][c]) * s_gu[1][l][c], hq, hd, hs, (size_t)s_cols[c] * (F / 32) + rb, l);
+    }
 }
 
 // the down projection of one token's slots: wave w takes the slots e = w, w + 4, ... (at most
@@ -483,15 +524,21 @@ int launch_down(const qmm_moe_segs& a, const int* ids, int nexp, qmm_xq8 x, int 
     return QMM_OK;
 }
 
-// the T = 1 step's first launch (k_moe_route_gu_q8): q8 of h into hq / hd / hs
+// the step's first launch (k_moe_route_gu_q8): q8 of h into hq / hd / hs
 template <int LPR, int VPL>
-int launch_decode_gu_q8(const qmm_moe_segs& a, const float* logits, int nexp_total, int topk, int* ids, float* w, qmm_xq8 x, int F,
-                        int H, qmm_xq8 h, hipStream_t s) {
+int launch_decode_gu_q8(const qmm_moe_segs& a, const float* logits, int stride, int nexp_total, int topk, int T, int* ids, float* w,
+                        qmm_xq8 x, int F, int H, qmm_xq8 h, hipStream_t s) {
     const int iters = (H / 256 * 4 + LPR - 1) / LPR;
-    const dim3 grid(F / 32, topk + 1);
-    const size_t lds = (size_t)H + H / 4;
-#define QMM_G(IV) case IV: hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL>), grid, dim3(64 * kGuWaves), lds, s, a, logits, nexp_total, \
-                                              topk, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s); break;
+    const dim3 grid(F / 32, T * (topk + 1));
+    const size_t lds = (size_t)T * (H + H / 4);
+#define QMM_G(IV) case IV:                                                                                                   \
+        if (T == 1)                                                                                                          \
+            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL, true>), grid, dim3(64 * kGuWaves), lds, s, a, logits, stride,  \
+                               nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                              \
+        else                                                                                                                 \
+            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL, false>), grid, dim3(64 * kGuWaves), lds, s, a, logits, stride, \
+                               nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                              \
+        break;
     switch (iters) {
         QMM_G(1) QMM_G(2) QMM_G(3) QMM_G(4) QMM_G(5) QMM_G(6)
         default: return QMM_ERR_SHAPE;
@@ -502,10 +549,10 @@ int launch_decode_gu_q8(const qmm_moe_segs& a, const float* logits, int nexp_tot
 }
 
 template <int VPL>
-int decode_gu_q8_vpl(const qmm_moe_segs& a, const float* logits, int nexp_total, int topk, int* ids, float* w, qmm_xq8 x, int F, int H,
-                     qmm_xq8 h, hipStream_t s) {
-    return moe_lpr(H) == 8 ? launch_decode_gu_q8<8, VPL>(a, logits, nexp_total, topk, ids, w, x, F, H, h, s)
-                           : launch_decode_gu_q8<16, VPL>(a, logits, nexp_total, topk, ids, w, x, F, H, h, s);
+int decode_gu_q8_vpl(const qmm_moe_segs& a, const float* logits, int stride, int nexp_total, int topk, int T, int* ids, float* w,
+                     qmm_xq8 x, int F, int H, qmm_xq8 h, hipStream_t s) {
+    return moe_lpr(H) == 8 ? launch_decode_gu_q8<8, VPL>(a, logits, stride, nexp_total, topk, T, ids, w, x, F, H, h, s)
+                           : launch_decode_gu_q8<16, VPL>(a, logits, stride, nexp_total, topk, T, ids, w, x, F, H, h, s);
 }
 
 }  // namespace
@@ -522,41 +569,26 @@ int moe_decode_check(int fmt, const void* Wg, const void* Wu, const void* Wd, co
     return QMM_OK;
 }
 
-// the launches; workspace gu: at T = 1 the q8 of h, at T > 1 the gate / up rows (2 * T * (topk + 1) * F
-// floats), then the q8 of h
+// the two launches; workspace gu: the q8 of h (T * (topk + 1) * F bytes, then d and s per 32)
 int moe_decode_run(const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg, const void* Su,
                    const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H, int F, int* ids,
                    float* w, float* gu, float* y, hipStream_t s) {
     if (T == 0) return QMM_OK;
     const int nexp = topk + 1;
-    float* gate = gu;
-    float* up = gu + (size_t)T * nexp * F;
-    const qmm_moe_segs ga = {{Wg, Wu}, {Sg, Su}, {gate, up}, ebytes_gu, nullptr};
-    int rc;
-    if (T == 1) {
-        // h as q8 at the start of the workspace (the gate / up rows are not kept at T = 1)
-        const size_t nh = (size_t)nexp * F;
-        const qmm_xq8 h = {(int8_t*)gu, gu + nh / 4, gu + nh / 4 + nh / 32};
-        rc = nexp_total <= 128 ? decode_gu_q8_vpl<2>(ga, logits, nexp_total, topk, ids, w, x, F, H, h, s)
-           : nexp_total <= 256 ? decode_gu_q8_vpl<4>(ga, logits, nexp_total, topk, ids, w, x, F, H, h, s)
-           : nexp_total <= 512 ? decode_gu_q8_vpl<8>(ga, logits, nexp_total, topk, ids, w, x, F, H, h, s)
-                               : decode_gu_q8_vpl<16>(ga, logits, nexp_total, topk, ids, w, x, F, H, h, s);
-        if (rc != QMM_OK) return rc;
-        const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
-        return moe_lpr(F) == 8 ? launch_down<8>(da, ids, nexp, h, H, F, T, s) : launch_down<16>(da, ids, nexp, h, H, F, T, s);
-    } else {
-        // every gather workgroup would route all T tokens again, and every down workgroup would
-        // redo silu-q8 of all the token's rows: route once, quantise h once (the four launches)
-        rc = qmm_moe_route_n(logits, ids, w, T, nexp_total, stride, topk, s);
-        if (rc == QMM_OK)
-            rc = moe_lpr(H) == 8 ? launch_gather<8>(ga, 2, ids, nexp, x, F, H, T, 0, s) : launch_gather<16>(ga, 2, ids, nexp, x, F, H, T, 0, s);
-        const size_t nh = (size_t)T * nexp * F;
-        const qmm_xq8 h = {(int8_t*)(up + nh), up + nh + nh / 4, up + nh + nh / 4 + nh / 32};
-        if (rc == QMM_OK) rc = qmm_moe_silu_quant(gate, up, h, T * nexp, F, s);
-        if (rc != QMM_OK) return rc;
-        const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
-        return moe_lpr(F) == 8 ? launch_down<8>(da, ids, nexp, h, H, F, T, s) : launch_down<16>(da, ids, nexp, h, H, F, T, s);
+    const qmm_moe_segs ga = {{Wg, Wu}, {Sg, Su}, {nullptr, nullptr}, ebytes_gu, nullptr};
+    // h as q8 at the start of the workspace
+    const size_t nh = (size_t)T * nexp * F;
+    const qmm_xq8 h = {(int8_t*)gu, gu + nh / 4, gu + nh / 4 + nh / 32};
+    if (T > 1) {   // T routing waves in every workgroup cost more than a launch: route once first
+        if (int e = qmm_moe_route_n(logits, ids, w, T, nexp_total, stride, topk, s)) return e;
     }
+    const int rc = nexp_total <= 128 ? decode_gu_q8_vpl<2>(ga, logits, stride, nexp_total, topk, T, ids, w, x, F, H, h, s)
+                 : nexp_total <= 256 ? decode_gu_q8_vpl<4>(ga, logits, stride, nexp_total, topk, T, ids, w, x, F, H, h, s)
+                 : nexp_total <= 512 ? decode_gu_q8_vpl<8>(ga, logits, stride, nexp_total, topk, T, ids, w, x, F, H, h, s)
+                                     : decode_gu_q8_vpl<16>(ga, logits, stride, nexp_total, topk, T, ids, w, x, F, H, h, s);
+    if (rc != QMM_OK) return rc;
+    const qmm_moe_segs da = {{Wd, nullptr}, {Sd, nullptr}, {y, nullptr}, ebytes_d, w};
+    return moe_lpr(F) == 8 ? launch_down<8>(da, ids, nexp, h, H, F, T, s) : launch_down<16>(da, ids, nexp, h, H, F, T, s);
 }
 
 // the device address of `scratch` on the current device, looked up on the first call per device
@@ -664,9 +696,9 @@ int qmm_moe_decode_noalloc(int fmt, const void* Wg, const void* Wu, const void* 
 }
 
 size_t qmm_moe_decode_ws_bytes(int T, int topk, int F) {
-    // gate and up rows (f32); at T > 1 also h = silu(gate) * up as q8 (bytes, then d and s per 32)
+    // h = silu(gate) * up as q8: the bytes, then d and s per 32
     const size_t nh = T <= 0 || topk < 1 || F <= 0 ? 0 : (size_t)T * (topk + 1) * F;
-    return nh * 2 * sizeof(float) + (T > 1 ? nh + nh / 32 * 2 * sizeof(float) : 0);
+    return nh + nh / 32 * 2 * sizeof(float);
 }
 
 int qmm_moe_combine_sorted(const float* down, const float* w, const int* kpos, float* y, int T, int nexp, int E, void* stream) {

@@ -245,13 +245,12 @@ int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const
                  int N, int K, int T, int xrow_te, void* stream);
 /* The whole MoE decode step in one call (no reference counterpart as one function: the reference runs
  * fn::moe_route, gemv_moe gate|up, fn::moe_silu_quant and gemv_moe down, qwen4exp.cpp:345-354).  At
- * T = 1 two launches: the first routes logits [T][stride] (nexp_total experts, the shared gate at column
- * nexp_total, top-k), computes the slots' gate and up rows and writes h = silu(gate) * up as q8; the
- * second is the down projection with the slot-ordered combine.  At T = 2..8 those four launches (the
- * fused forms would repeat the routing in every workgroup).
+ * two launches: the first routes logits [T][stride] (nexp_total experts, the shared gate at column
+ * nexp_total, top-k), computes each distinct expert's gate and up rows once for the slots holding it and
+ * writes h = silu(gate) * up as q8; the second is the down projection with the slot-ordered combine.
  * Outputs: ids / w [T][topk+1] as qmm_moe_route_n writes them, y [T][H] = the slot-ordered combine.  The
- * caller's workspace ws (qmm_moe_decode_ws_bytes(T, topk, F) bytes) holds at T = 1 the q8 of h, at T > 1
- * the gate and up rows, then the q8 of h.  Bitwise
+ * caller's workspace ws (qmm_moe_decode_ws_bytes(T, topk, F) bytes) holds the q8 of h (T*(topk+1)*F
+ * bytes, then d and s per 32).  Bitwise
  * the four calls qmm_moe_route_n, qmm_gemv_moe (gate|up), qmm_moe_silu_quant, qmm_gemv_moe (down).
  * fmt Q4_K for routed and shared experts (gate, up [F][H] at Wg / Wu + e * ebytes_gu; down [H][F] at
  * Wd + e * ebytes_d; shared Sg, Su, Sd); x q8 [T][H]; T <= 8, topk + 1 <= 16, H and F multiples of 256,
