@@ -278,10 +278,16 @@ template <> struct FmtUnit<QMM_Q6_K_SOA> {            // row = [ql K/2][qh K/4][
 // [ub, ue): lane l takes units ub + l, ub + l + 64, ..., NIT at a time, every load of a pass issued
 // before its arithmetic.  xs[c] is column c's activation source; acc[r][c] is the lane's partial
 // (the caller reduces over the wave).  Rows of format F start rb bytes apart (0 = the format's own
-// row size for K).
-template <int F, int NCOL, int NIT, int RPW, class XS>
+// row size for K).  pre() runs once, after the first pass's weight loads are issued and before its x
+// is read (a caller that stages x in LDS finishes the staging there, so its weights are already in
+// flight); FmtNoPre does nothing.
+struct FmtNoPre {
+    static constexpr bool active = false;
+    __device__ __forceinline__ void operator()() const {}
+};
+template <int F, int NCOL, int NIT, int RPW, class XS, class Pre = FmtNoPre>
 __device__ __forceinline__ void fmt_rows(const uint8_t* __restrict__ W, int row0, int N, int K, const XS (&xs)[NCOL],
-                                         float (&acc)[RPW][NCOL], int ub, int ue, size_t rb = 0) {
+                                         float (&acc)[RPW][NCOL], int ub, int ue, size_t rb = 0, const Pre& pre = Pre()) {
 #pragma clang fp contract(off)
     typedef FmtUnit<F> FU;
     const int lane = threadIdx.x & 63;
@@ -297,6 +303,12 @@ __device__ __forceinline__ void fmt_rows(const uint8_t* __restrict__ W, int row0
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
             for (int i = 0; i < NIT; ++i) FU::load(W + (size_t)min(row0 + r, N - 1) * rb, K, min(base + lane + 64 * i, ue - 1), R[r][i]);
+        if constexpr (Pre::active) {
+            if (base == ub) {
+                __builtin_amdgcn_sched_barrier(0);
+                pre();
+            }
+        }
 #pragma unroll
         for (int c = 0; c < NCOL; ++c) {
 #pragma unroll

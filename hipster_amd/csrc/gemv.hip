@@ -74,22 +74,6 @@ __global__ void __launch_bounds__(256) k_quantize_x_q8(const float* __restrict__
     }
 }
 
-// ------------------------------------------------------------------------------------------
-// Stage q8 x of NCOL columns into LDS: [xq NCOL*K][xd NCOL*K/32][xs NCOL*K/32].
-template <int NCOL>
-__device__ __forceinline__ void stage_xq8(uint8_t* lds, const int8_t* __restrict__ xq, const float* __restrict__ xd,
-                                          const float* __restrict__ xs, int K) {
-    const int nq = NCOL * K / 16, ns = NCOL * (K / 32) / 4;
-    uint4* dq = (uint4*)lds;
-    for (int i = threadIdx.x; i < nq; i += blockDim.x) dq[i] = ld16(xq + (size_t)i * 16);
-    float4* dd = (float4*)(lds + (size_t)NCOL * K);
-    float4* dsv = dd + ns;
-    for (int i = threadIdx.x; i < ns; i += blockDim.x) {
-        dd[i] = *(const float4*)(xd + (size_t)i * 4);
-        dsv[i] = *(const float4*)(xs + (size_t)i * 4);
-    }
-    __syncthreads();
-}
 
 // Q4_K weights sharing x and K in one launch (the reference's k_gemv_multi, gemv.hip:1042-1067):
 // workgroup (16-row tile) i belongs to segment s when t0[s] <= i < t0[s + 1]

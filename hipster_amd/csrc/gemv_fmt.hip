@@ -7,8 +7,9 @@
 // RPW rows per wave (4; 2 for Q5_K).  A unit is one scale's worth of weights -- 32 (one sub-block) for IQ4_XS,
 // Q8_0_SOA and Q5_1_SOA, 64 for Q5_K (the two sub-blocks sharing one 32-byte qs pair) -- and lane l
 // takes units l, l + 64, ... of the row, NIT at a time, with all of a pass's weight loads issued
-// before its compute.  The q8 x of a unit (32 bytes per sub-block, its d and s) is read from
-// global memory (L1) once per wave and used for all of the wave's rows.  Per sub-block the
+// before its compute.  The q8 x of a unit (32 bytes per sub-block, its d and s) is read once per
+// wave and used for all of the wave's rows, from LDS (x staged once per workgroup) or from global
+// memory (L1), whichever the format and width measured faster.  Per sub-block the
 // weights become int8 lanes of a dword, the integer dot with the q8 x uses v_dot4_i32_i8, and the
 // reference's fix-up follows:
 //   Q5_K    acc += (d sc) xd isum - (dmin m) xs          (q = nibble | fifth bit << 4, 0..31)
@@ -24,22 +25,73 @@
 #include <hip/hip_runtime.h>
 
 namespace qmm {
+extern int g_fmt_xlds;
 namespace {
 
 constexpr int kFmtBlock = 256, kFmtWaves = kFmtBlock / 64;
+constexpr size_t kFmtXLds = 64 * 1024;   // bytes of LDS the plain GEMV may use for staged x
 
-template <int F, int NCOL, int NIT, int RPW>
+// x of NCOL columns staged in LDS as [xq NCOL*K][xd NCOL*K/32][xs NCOL*K/32] (the layout of
+// stage_xq8), read ahead of the weights: load() issues the thread's 16-byte pieces (element e =
+// threadIdx.x + 256u, clamped to the last element, so every store is unconditional and duplicates
+// write the same bytes), the weight loads follow, and operator() -- called by fmt_rows once they
+// are issued -- stores the pieces (waiting for the x loads only: loads retire in issue order) and
+// meets the workgroup at an LDS-only barrier.
+constexpr int kXFirstU = 4;                    // pieces per thread: 16 KiB of staged x
+template <int NU>
+struct FmtXFirst {
+    static constexpr bool active = true;
+    uint4 v[NU];
+    uint4* lds;
+    int n;
+    __device__ __forceinline__ void load(const int8_t* xq, const float* xd, const float* xs, int ncol, int K) {
+        const int nq = ncol * K / 16, ns = ncol * (K / 32) / 4;
+        n = nq + 2 * ns;
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int e = min((int)threadIdx.x + kFmtBlock * u, n - 1);
+            const void* src = e < nq ? (const void*)(xq + (size_t)e * 16)
+                            : e < nq + ns ? (const void*)(xd + (size_t)(e - nq) * 4) : (const void*)(xs + (size_t)(e - nq - ns) * 4);
+            v[u] = ld16(src);
+        }
+    }
+    __device__ __forceinline__ void operator()() const {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) lds[min((int)threadIdx.x + kFmtBlock * u, n - 1)] = v[u];
+        lds_barrier();
+    }
+};
+
+// XS: 0 = x read from global memory (L1) by every wave, 1 = staged in LDS before the weights are
+// loaded, 2 = staged in LDS from registers loaded ahead of the first weight loads (FmtXFirst).
+// The arithmetic is the same in all three, so are the results.
+template <int F, int NCOL, int NIT, int RPW, int XS>
 __global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                         const float* __restrict__ xd, const float* __restrict__ xs,
                                                         float* __restrict__ y, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * kFmtWaves + wave) * RPW;
     const int nsb = K / 32;
     XSrcQ8 xsrc[NCOL];
-#pragma unroll
-    for (int c = 0; c < NCOL; ++c) xsrc[c] = XSrcQ8{xq + (size_t)c * K, xd + (size_t)c * nsb, xs + (size_t)c * nsb};
     float acc[RPW][NCOL];
-    fmt_rows<F, NCOL, NIT, RPW>(W, row0, N, K, xsrc, acc, 0, fmt_units<F>(K));
+    if constexpr (XS > 0) {
+        const float* sd = (const float*)(smem + (size_t)NCOL * K);
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) xsrc[c] = XSrcQ8{(const int8_t*)smem + (size_t)c * K, sd + (size_t)c * nsb, sd + (size_t)(NCOL + c) * nsb};
+    } else {
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) xsrc[c] = XSrcQ8{xq + (size_t)c * K, xd + (size_t)c * nsb, xs + (size_t)c * nsb};
+    }
+    if constexpr (XS == 2) {
+        FmtXFirst<kXFirstU> st;
+        st.lds = (uint4*)smem;
+        st.load(xq, xd, xs, NCOL, K);
+        fmt_rows<F, NCOL, NIT, RPW>(W, row0, N, K, xsrc, acc, 0, fmt_units<F>(K), 0, st);
+    } else {
+        if constexpr (XS == 1) stage_xq8<NCOL>(smem, xq, xd, xs, K);
+        fmt_rows<F, NCOL, NIT, RPW>(W, row0, N, K, xsrc, acc, 0, fmt_units<F>(K));
+    }
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
@@ -175,7 +227,27 @@ int launch_fmt(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) 
     constexpr int RPW = (F == QMM_Q5_K || NCOL == 1) ? 2 : 4;
     const int grid = (N + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
     const int per_lane = (fmt_units<F>(K) + 63) / 64;
-#define QMM_FMTL(IV) hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV, RPW>), dim3(grid), dim3(kFmtBlock), 0, s, (const uint8_t*)W, x.q, x.d, x.s, y, N, K)
+    // Where x comes from (measured at 17408 x 5120, M = 1..8): staged once per workgroup in LDS for
+    // Q5_K and Q5_1_SOA at every width (Q5_K M = 4: 30.6 -> 23.6 us, M = 8: 52.5 -> 35.2 us), for
+    // IQ4_XS at 2..4 columns and Q8_0_SOA at 1..2; read from global memory otherwise (there each wave's
+    // L1 reads cost less than the staging).  Staged x is loaded ahead of the weights into registers
+    // when it is at most 16 KiB and the kernel is one column or a row-SoA format (M = 1: Q5_K 17.7 ->
+    // 16.8 us), else copied before them.  Needs K % 128 == 0 (the float4 copy of the scales).
+    constexpr bool lds_pays = F == QMM_Q5_K || F == QMM_Q5_1_SOA || (F == QMM_IQ4_XS && NCOL >= 2 && NCOL <= 4) ||
+                              (F == QMM_Q8_0_SOA && NCOL <= 2);
+    constexpr bool xfirst_pays = NCOL == 1 || F == QMM_Q8_0_SOA || F == QMM_Q5_1_SOA;
+    const size_t xl = (size_t)NCOL * (K + K / 4);
+    const int xmode = !g_fmt_xlds || !lds_pays || K % 128 != 0 || xl > kFmtXLds ? 0
+                    : xfirst_pays && xl <= (size_t)kXFirstU * kFmtBlock * 16 ? 2 : 1;
+#define QMM_FMTL(IV)                                                                                                     \
+    do {                                                                                                                \
+        if (xmode == 2) hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV, RPW, 2>), dim3(grid), dim3(kFmtBlock), xl, s,       \
+                                           (const uint8_t*)W, x.q, x.d, x.s, y, N, K);                                  \
+        else if (xmode == 1) hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV, RPW, 1>), dim3(grid), dim3(kFmtBlock), xl, s,  \
+                                                (const uint8_t*)W, x.q, x.d, x.s, y, N, K);                             \
+        else hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV, RPW, 0>), dim3(grid), dim3(kFmtBlock), 0, s,                   \
+                                (const uint8_t*)W, x.q, x.d, x.s, y, N, K);                                            \
+    } while (0)
     // units per lane and pass: all of them when they are few, else passes of two (registers: RPW
     // rows x NIT units of raw weights are live at once)
     if (per_lane <= 1) QMM_FMTL(1);
@@ -198,6 +270,8 @@ int launch_fmt_ncol(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, h
 }
 
 }  // namespace
+
+int g_fmt_xlds = 1;
 
 int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
     switch (ncol) {
@@ -238,3 +312,9 @@ int moe_fmt_dispatch(int fmt, int sfmt, const qmm_moe_segs* a, int nseg, const i
 }
 
 }  // namespace qmm
+
+extern "C" int qmm_set_gemv_fmt_xlds(int on) {
+    const int prev = qmm::g_fmt_xlds;
+    qmm::g_fmt_xlds = on != 0;
+    return prev;
+}

@@ -114,6 +114,22 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// Stage q8 x of NCOL columns into LDS: [xq NCOL*K][xd NCOL*K/32][xs NCOL*K/32].
+template <int NCOL>
+__device__ __forceinline__ void stage_xq8(uint8_t* lds, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                          const float* __restrict__ xs, int K) {
+    const int nq = NCOL * K / 16, ns = NCOL * (K / 32) / 4;
+    uint4* dq = (uint4*)lds;
+    for (int i = threadIdx.x; i < nq; i += blockDim.x) dq[i] = ld16(xq + (size_t)i * 16);
+    float4* dd = (float4*)(lds + (size_t)NCOL * K);
+    float4* dsv = dd + ns;
+    for (int i = threadIdx.x; i < ns; i += blockDim.x) {
+        dd[i] = *(const float4*)(xd + (size_t)i * 4);
+        dsv[i] = *(const float4*)(xs + (size_t)i * 4);
+    }
+    __syncthreads();
+}
+
 // ---- wave reductions (wave64) ----
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

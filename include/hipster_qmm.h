@@ -182,6 +182,11 @@ int qmm_set_gemv_mfma_min_ncol(int n);
  * ncol * K <= 262144, x.d 16-byte aligned) use the int8 matrix-core kernel (default 3; n > 8 keeps
  * every call on the dot4 kernels).  Returns the previous value.  Results are the same bits either way. */
 int qmm_set_gemv_q6k_mfma_min_ncol(int n);
+/* Tuning knob (no reference counterpart): the Q5_K / IQ4_XS / Q8_0_SOA / Q5_1_SOA GEMV stages x once
+ * per workgroup in LDS where that measured faster (on = 1, the default; needs K % 128 == 0 and the
+ * columns' x within 64 KiB) or always reads it from global memory (0).  Returns the previous value.
+ * Results are the same bits either way. */
+int qmm_set_gemv_fmt_xlds(int on);
 /* split-K GEMV for skinny weights (reference: gemv_splitk, gemv.h:55, gemv.hip:1397-1441):
  * part[(c*ksplit + ks)*N + n] = W[n][K range ks] . x[c][K range ks], the K range of split ks being the
  * 256-weight blocks [ks*nb/ksplit, (ks+1)*nb/ksplit), nb = ceil(K/256), as the reference's; the consumer

@@ -105,3 +105,30 @@ def test_gemv_multi_mixed_formats_equals_separate_calls(gpu):
     qmm.gemv_multi(segs, xb, 4)
     for (_, _, y, _, _), y1 in zip(segs, ref):
         assert torch.equal(y, y1)
+
+
+@pytest.mark.parametrize("fmt,K", [(synth.Q5_K, 5120), (synth.Q5_K, 17408), (synth.IQ4_XS, 5120), (synth.IQ4_XS, 2048),
+                                   (synth.Q8_0_SOA, 5120), (synth.Q8_0_SOA, 640), (synth.Q5_1_SOA, 5120),
+                                   (synth.Q5_1_SOA, 640), (synth.Q5_1_SOA, 96)])
+def test_gemv_q8_formats_x_in_lds_equals_global(gpu, fmt, K):
+    """x staged in LDS (ahead of the weights or before them, as the launcher picks per format and
+    width) gives the same bits as x read from global memory, at every width 1..8 (knob
+    qmm_set_gemv_fmt_xlds; K = 96 is not a multiple of 128 and always reads global x)."""
+    from hipster_amd import _lib
+    N = 1029
+    W = synth.matrix(1200 + fmt + K, fmt, N, K)
+    x = synth.normal_f32(1201 + K, (8, K))
+    Wd, xb = dev(W), q8_on_gpu(x)
+    L = _lib.lib()
+    try:
+        for ncol in range(1, 9):
+            print(f"fmt={fmt} K={K} ncol={ncol}", flush=True)
+            ys = []
+            for on in (0, 1):
+                L.qmm_set_gemv_fmt_xlds(on)
+                y = torch.zeros((ncol, N), dtype=torch.float32, device="cuda")
+                qmm.gemv_q8(fmt, Wd, xb, y, N, K, ncol)
+                ys.append(host(y))
+            assert np.array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32)), ncol
+    finally:
+        L.qmm_set_gemv_fmt_xlds(1)
