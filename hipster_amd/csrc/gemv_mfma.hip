@@ -132,12 +132,12 @@ __device__ __forceinline__ void mblk_compute(const MBlk& B, int b, int h, int r,
 constexpr int kMfmaMaxK = 32768;
 
 // LDS of the x pair scales [K/64][4 MV] float4, reused for the partial sums [16][4 MV][16] float; the
-// per-wave scale-exchange slots (4 waves x 2 sets x 16 rows x 4 pairs float4) follow
+// per-wave scale-exchange slots (4 waves x 16 rows x 4 pairs float4) follow
 __host__ __device__ inline size_t gemv_q4k_mfma_main_lds(int K, int mv) {
     const size_t scales = (size_t)(K / 64) * (4 * mv) * 16, parts = (size_t)16 * (4 * mv) * 16 * 4;
     return scales > parts ? scales : parts;
 }
-constexpr size_t kScaleSlotBytes = 4 * 2 * 16 * 4 * 16;
+constexpr size_t kScaleSlotBytes = 4 * 16 * 4 * 16;
 // x staged in LDS (XL) for ncol <= 4 and ncol * K <= kXlMax: token c at c * (K + 64) (the 64-byte skew
 // spreads the tokens over the banks), then 256 bytes of zeros read by the empty token slots; staged
 // by kXlRegs 16-byte pieces per thread, loaded before the first weights
@@ -164,8 +164,10 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
     const uint8_t* rp = sg.w[si] + (size_t)min(row0 + r, N - 1) * ((size_t)nb * 144);
     float4* sds = (float4*)smem;
     float* part = (float*)smem;
-    // per wave two scale-exchange slots (register sets A, B) of 16 rows x 4 pairs, after the scales
-    float4* sslot = (float4*)(smem + gemv_q4k_mfma_main_lds(K, MV)) + wave * 128;
+    // per wave one scale-exchange slot of 16 rows x 4 pairs, after the scales: blocks A and B of the
+    // ring share it (a wave's LDS instructions run in order, so block B's writes come after block A's
+    // reads; one slot instead of two keeps x-in-LDS workgroups at 5 per CU instead of 4 for 4 columns)
+    float4* sslot = (float4*)(smem + gemv_q4k_mfma_main_lds(K, MV)) + wave * 64;
     // A operand source of this lane: x of the token in slot r (zeros for an empty slot), 16-byte
     // piece h of each pair
     const int ca = (r >> 2) * MV + (r & 3);
@@ -237,7 +239,7 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
         mblk_compute<MV, XL>(A, b, h, r, true, sds, sslot, xlb + b * xls, acc);
         mblk_load<XL>(A, rp, rx, xo, min(b + 8, nb - 1), h);
         __builtin_amdgcn_sched_barrier(0);
-        mblk_compute<MV, XL>(B, min(b + 4, nb - 1), h, r, b + 4 < nb, sds, sslot + 64, xlb + min(b + 4, nb - 1) * xls, acc);
+        mblk_compute<MV, XL>(B, min(b + 4, nb - 1), h, r, b + 4 < nb, sds, sslot, xlb + min(b + 4, nb - 1) * xls, acc);
     }
     __syncthreads();                                      // every wave is done with the scales
     // partial sum t = 4 wave + j of token MV h + v, row r
