@@ -12,7 +12,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libh
 QMM_OK = 0
 STATUS = {0: "QMM_OK", -1: "QMM_ERR_FORMAT", -2: "QMM_ERR_SHAPE", -3: "QMM_ERR_NULL",
           -4: "QMM_ERR_LAUNCH", -5: "QMM_ERR_WORKSPACE", -6: "QMM_ERR_ARG", -7: "QMM_ERR_LAYOUT", -8: "QMM_ERR_IO",
-          -9: "QMM_ERR_NOT_FOUND"}
+          -9: "QMM_ERR_NOT_FOUND", -10: "QMM_ERR_UNSUPPORTED"}
 QMM_Q4_K, QMM_Q5_K, QMM_IQ4_XS, QMM_Q6_K_SOA, QMM_Q8_0_SOA, QMM_Q5_1_SOA, QMM_Q6_K = 0, 1, 2, 3, 4, 5, 6
 
 c_vp = ctypes.c_void_p

@@ -58,6 +58,7 @@ const char* qmm_status_string(int status) {
         case QMM_ERR_LAYOUT: return "weight layout not supported (the reference's experimental interleaved layouts)";
         case QMM_ERR_IO: return "GGUF file missing, truncated, not GGUF v3, or a tensor past its end";
         case QMM_ERR_NOT_FOUND: return "tensor or key not found";
+        case QMM_ERR_UNSUPPORTED: return "entry point off the quantized matmul path (not provided by this library)";
         default: return "unknown status";
     }
 }

@@ -2,7 +2,7 @@
 // engine and its validators compile and run against this library unchanged:
 //
 //   qmm_gemv_splitk        gemv_splitk     engine/kernels/gemv.h:55, gemv.hip:1397-1441
-//   qmm_hc_up_fused        hc_up_fused     gemv.h:52, gemv.hip:976-1005
+//   qmm_hc_up_fused        hc_up_fused     gemv.h:52 (declared only: returns QMM_ERR_UNSUPPORTED)
 //   qmm_moe_gemm_q8        moe_gemm        gemv.h:49-50, gemv.hip:909-969,1377-1381 (q8 activations)
 //   qmm_quantize_x_q8k     quantize_x_q8k  gemv.h:34, gemv.hip:686-705,1254-1257
 //   qmm_gemv_q8k           gemv_wmma_q8k   gemv.h:35, gemv.hip:706-794,1259-1271
@@ -73,55 +73,6 @@ int launch_splitk(const void* W, qmm_xq8 x, float* part, int N, int K, int kspli
         QMM_LAUNCH_CHECK();
     }
     return QMM_OK;
-}
-
-// ---- hyper-connection up-projection with its silu prologue (gemv.hip:976-1005) -------------------
-// x = silu(sum_k part[(t*ksplit + k)][320] / 4) (partials summed in k order, silu v / (1 + exp(-v))),
-// quantised per 32 into LDS, then y[t][n] = W[n] . x with W Q8_0_SOA [N][320].  Grid = (row
-// blocks of 32, T); 8 lanes per row, lane l of a row takes sub-blocks l and l + 8.
-constexpr int kHcK = 320, kHcSub = kHcK / 32, kHcRows = 32;
-
-__global__ void __launch_bounds__(kCThreads) k_hc_up_fused(const uint8_t* __restrict__ W, const float* __restrict__ part, int ksplit,
-                                                           float* __restrict__ y, int N) {
-    __shared__ __align__(16) int8_t sq[kHcK];
-    __shared__ float sxf[kHcK], sd[kHcSub], ss[kHcSub];
-    const int t = blockIdx.y, tid = threadIdx.x;
-    for (int i = tid; i < kHcK; i += kCThreads) {
-        float v = 0.f;
-        for (int k = 0; k < ksplit; ++k) v += part[((size_t)t * ksplit + k) * kHcK + i];
-        v *= 0.25f;
-        sxf[i] = v / (1.f + __expf(-v));
-    }
-    __syncthreads();
-    {   // q8 per 32, one half-wave per sub-block (the order-free max and integer sum of hw32_quant)
-        const int hw = tid >> 5, l = tid & 31;
-        for (int sb = hw; sb < kHcSub; sb += kCThreads / 32) {
-            const float v = sxf[sb * 32 + l];
-            const float amax = g32_max(fabsf(v));
-            const float dd = amax / 127.f, id = amax > 0.f ? 127.f / amax : 0.f;
-            const int qi = __float2int_rn(v * id);
-            const int sum = g32_isum(qi);
-            sq[sb * 32 + l] = (int8_t)qi;
-            if (l == 0) { sd[sb] = dd; ss[sb] = dd * (float)sum; }
-        }
-    }
-    __syncthreads();
-    const int lane = tid & 63, wave = tid >> 6, l8 = lane & 7;
-    const int row = blockIdx.x * kHcRows + wave * 8 + (lane >> 3);
-    const uint8_t* rp = W + (size_t)min(row, N - 1) * fmt_row_bytes<QMM_Q8_0_SOA>(kHcK);
-    const XSrcQ8 src{sq, sd, ss};
-    typedef FmtUnit<QMM_Q8_0_SOA> FU;
-    FU::Raw r0, r1;
-    FU::load(rp, kHcK, l8, r0);
-    FU::load(rp, kHcK, min(l8 + 8, kHcSub - 1), r1);
-    X32 x0, x1;
-    src.sub(l8, x0);
-    src.sub(min(l8 + 8, kHcSub - 1), x1);
-    float acc = FU::col(r0, x0, l8);
-    const float v1 = FU::col(r1, x1, l8 + 8);
-    acc += l8 + 8 < kHcSub ? v1 : 0.f;
-    acc = group_sum(acc, 8);
-    if (l8 == 0 && row < N) y[(size_t)t * N + row] = acc;
 }
 
 // ---- grouped expert GEMM over sorted slots with q8 activations (moe_gemm, gemv.hip:909-969) -------
@@ -304,15 +255,8 @@ int qmm_gemv_splitk(int fmt, const void* W, qmm_xq8 x, float* part, int N, int K
     }
 }
 
-int qmm_hc_up_fused(const void* W, const float* part, int ksplit, float* y, int N, int T, void* stream) {
-    if (!W || !part || !y) return QMM_ERR_NULL;
-    if (N <= 0 || T < 0 || ksplit < 1) return QMM_ERR_SHAPE;
-    if (T == 0) return QMM_OK;
-    hipLaunchKernelGGL(k_hc_up_fused, dim3((unsigned)((N + kHcRows - 1) / kHcRows), (unsigned)T), dim3(kCThreads), 0,
-                       (hipStream_t)stream, (const uint8_t*)W, part, ksplit, y, N);
-    QMM_LAUNCH_CHECK();
-    return QMM_OK;
-}
+// the Flash-Next hyper-connection prologue is a neighbour of the path, not part of it (declared only)
+int qmm_hc_up_fused(const void*, const float*, int, float*, int, int, void*) { return QMM_ERR_UNSUPPORTED; }
 
 int qmm_moe_gemm_q8(int fmt, int shared_fmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles, int ntiles,
                     const qmm_moe_tile* stiles, int nstiles, int ct, const int* rowtab, qmm_xq8 x, float* y, int N, int K,

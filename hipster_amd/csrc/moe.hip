@@ -284,6 +284,7 @@ __global__ void __launch_bounds__(256) k_gemv_moe_q4k(qmm_moe_segs a, const int*
 // slot-ordered combine).  The four-launch sequence moe_route, gemv_moe (gate|up), moe_silu_quant,
 // gemv_moe (down) gives the same ids, weights, q8 of h and y bit for bit.
 constexpr int kDecMaxTok = 8;
+constexpr size_t kDecDownLds = 64 * 1024;   // dynamic LDS budget of the decode down projection
 
 // The step's first launch (T <= 8): workgroup (32-row block rb, slot e) routes the T tokens (wave t
 // routes token t, route_token: the arithmetic of k_moe_route) while the other waves stage the tokens'
@@ -513,7 +514,7 @@ int launch_down(const qmm_moe_segs& a, const int* ids, int nexp, qmm_xq8 x, int 
     const int iters = (K / 256 * 4 + LPR - 1) / LPR;
     const dim3 grid((N + (64 / LPR) - 1) / (64 / LPR), T);
     const size_t lds = (size_t)nexp * (K + K / 4);
-    if (lds > 64 * 1024) return QMM_ERR_SHAPE;
+    if (lds > kDecDownLds) return QMM_ERR_SHAPE;
 #define QMM_D(IV) case IV: hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV>), grid, dim3(256), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K); break;
     switch (iters) {
         QMM_D(1) QMM_D(2) QMM_D(3) QMM_D(4) QMM_D(5) QMM_D(6)
@@ -566,6 +567,9 @@ int moe_decode_check(int fmt, const void* Wg, const void* Wu, const void* Wd, co
     if (T < 0 || T > kDecMaxTok || nexp_total < 1 || nexp_total > kRouteMaxExp || topk < 1 || topk + 1 > kMaxSlots ||
         topk > nexp_total || stride < nexp_total + 1 || H <= 0 || F <= 0 || H % 256 || F % 256 || H > 6144 || F > 6144)
         return QMM_ERR_SHAPE;
+    // the down launch holds every slot's q8 h row in LDS (launch_down's budget): refuse here, before
+    // the first launch writes ids, w or the workspace
+    if ((size_t)(topk + 1) * (F + F / 4) > kDecDownLds) return QMM_ERR_SHAPE;
     return QMM_OK;
 }
 

@@ -165,12 +165,6 @@ def gemv_splitk(fmt, W, x, part, N, K, ksplit, ncol, stream=None):
     check(_lib.lib().qmm_gemv_splitk(fmt, _p(W), x.c(), _p(part), N, K, ksplit, ncol, _stream(stream)), "gemv_splitk")
 
 
-def hc_up_fused(W, part, ksplit, y, N, T, stream=None):
-    """gemv.h:52: y[t] = W (Q8_0_SOA [N][320]) . q8(silu(sum_k part[t][k] / 4))."""
-    _dev(W, torch.uint8, "W"); _dev(part, torch.float32, "part"); _dev(y, torch.float32, "y")
-    check(_lib.lib().qmm_hc_up_fused(_p(W), _p(part), ksplit, _p(y), N, T, _stream(stream)), "hc_up_fused")
-
-
 def quantize_x_q8k(x, out, ncol, K, stream=None):
     """gemv.h:34: x f32 [ncol][K] -> out (XQ8KBuf): one scale per 256, int16 sums per 32."""
     _dev(x, torch.float32, "x")

@@ -38,7 +38,9 @@ enum {
     QMM_ERR_LAYOUT = -7,    /* a weight layout this library does not read (the reference's experimental
                                interleaved layouts) */
     QMM_ERR_IO = -8,        /* a GGUF file is missing, truncated, not GGUF v3 or has a tensor past its end */
-    QMM_ERR_NOT_FOUND = -9  /* no tensor / key of that name in the GGUF */
+    QMM_ERR_NOT_FOUND = -9, /* no tensor / key of that name in the GGUF */
+    QMM_ERR_UNSUPPORTED = -10 /* an entry point of the reference's call surface that lies off the quantized
+                               matmul path (declared so that the reference's callers compile) */
 };
 
 /* ---- weight formats: values of the reference's `enum class WFmt` (engine/kernels/gemv.h:13),
@@ -193,9 +195,9 @@ int qmm_set_gemv_fmt_xlds(int on);
  * sums the partials in a fixed order.  fmt: Q4_K, Q5_K, IQ4_XS, Q6_K_SOA (K % 512), Q8_0_SOA (K % 64),
  * Q5_1_SOA (K % 32); 1 <= ksplit <= nb; any ncol (8 per launch). */
 int qmm_gemv_splitk(int fmt, const void* W, qmm_xq8 x, float* part, int N, int K, int ksplit, int ncol, void* stream);
-/* the hyper-connection up-projection with its prologue (reference: hc_up_fused, gemv.h:52,
- * gemv.hip:976-1005): per t < T, x = silu(sum_k part[(t*ksplit + k)*320 + i] / 4) (k in order), quantised
- * per 32, then y[t*N + n] = W[n] . x with W Q8_0_SOA [N][320]. */
+/* the Flash-Next hyper-connection up-projection (reference: hc_up_fused, gemv.h:52, gemv.hip:976-1005).
+ * Off the quantized matmul path (a model-specific prologue of one engine): declared so that the
+ * reference's callers compile against the shim, and returns QMM_ERR_UNSUPPORTED without launching. */
 int qmm_hc_up_fused(const void* W, const float* part, int ksplit, float* y, int N, int T, void* stream);
 /* x -> Q8_K (reference: quantize_x_q8k, gemv.h:34, gemv.hip:686-705): per 256, d = amax/127,
  * q = round-half-even(x*127/amax) (0 when amax == 0), bs = sum of each 32 q; ncol <= 16, K % 256 == 0 */
@@ -259,7 +261,9 @@ int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const
  * the four calls qmm_moe_route_n, qmm_gemv_moe (gate|up), qmm_moe_silu_quant, qmm_gemv_moe (down).
  * fmt Q4_K for routed and shared experts (gate, up [F][H] at Wg / Wu + e * ebytes_gu; down [H][F] at
  * Wd + e * ebytes_d; shared Sg, Su, Sd); x q8 [T][H]; T <= 8, topk + 1 <= 16, H and F multiples of 256,
- * at most 6144. */
+ * at most 6144, and (topk + 1) * F * 5/4 <= 65536 (the down projection keeps every slot's q8 h row in
+ * LDS: F <= 4608 at topk 10, F <= 3072 at topk 15).  A shape outside these limits is refused with
+ * QMM_ERR_SHAPE before anything is launched or written. */
 int qmm_moe_decode(int fmt, const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg,
                    const void* Su, const void* Sd, const float* logits, int stride, int nexp_total, int topk, qmm_xq8 x, int T, int H,
                    int F, int* ids, float* w, float* ws, size_t ws_bytes, float* y, void* stream);

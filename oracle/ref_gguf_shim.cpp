@@ -1,6 +1,6 @@
 // ref_gguf_shim.cpp -- exposes the reference's own GGUF v3 reader (engine/src/gguf.cpp, compiled from
 // where it lies in the reference checkout) through a C ABI, so the library's reader
-// (hipster_amd/csrc/gguf.cpp) can be checked against it on the same files.  TEST INFRASTRUCTURE
+// (hipster_amd/csrc/gguf_reader.cpp) can be checked against it on the same files.  TEST INFRASTRUCTURE
 // ONLY: built into oracle/_ref/ (git-ignored) by oracle/Makefile, loaded only by tests/.
 #include <cstring>
 #include <exception>

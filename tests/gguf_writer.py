@@ -1,4 +1,4 @@
-"""GGUF v3 writer for the tests (the reader under test is hipster_amd/csrc/gguf.cpp; the reference's own
+"""GGUF v3 writer for the tests (the reader under test is hipster_amd/csrc/gguf_reader.cpp; the reference's own
 reader, engine/src/gguf.cpp, only reads).
 
 Layout written (ggml's GGUF v3): magic "GGUF", version 3, n_tensors u64, n_kv u64; the KV pairs (key

@@ -32,9 +32,9 @@ def test_version_and_status_strings():
     assert b"gfx950" in L.qmm_version()
     assert L.qmm_status_string(0) == b"ok"
     assert L.qmm_status_string(-1) == b"unsupported weight format"
-    for code in range(-9, 0):     # every status the header defines has its own text
+    for code in range(-10, 0):    # every status the header defines has its own text
         assert L.qmm_status_string(code) != b"unknown status", code
-    assert L.qmm_status_string(-10) == b"unknown status"
+    assert L.qmm_status_string(-11) == b"unknown status"
 
 
 def test_row_bytes_and_repack_match_oracle():
@@ -203,3 +203,12 @@ def test_prefill_argument_validation_without_device_work():
     assert L.qmm_gemv_q8_f32x(q4, d, None, d, 16, 256, 1, None) == -3
     assert L.qmm_gemv_q8_f32x(q4, d, d, d, 16, 256, 5, None) == -2      # ncol above 4
     assert L.qmm_gemv_q8_f32x(q4, d, d, d, 16, 6400, 1, None) == -2     # K above 6144
+
+
+def test_off_path_entry_point_refused():
+    """hc_up_fused (the reference's Flash-Next hyper-connection prologue, gemv.h:52) lies off the
+    quantized matmul path: declared for the reference's callers, refused before any launch."""
+    L = _lib.lib()
+    buf = np.zeros(64, np.float32)
+    assert L.qmm_hc_up_fused(buf.ctypes.data, buf.ctypes.data, 1, buf.ctypes.data, 32, 1, None) == -10
+    assert "off the quantized matmul path" in L.qmm_status_string(-10).decode()

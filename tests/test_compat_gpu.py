@@ -3,7 +3,6 @@ working (compat.hip, gemm.hip), through the C ABI:
 
   gemv_splitk     each partial within 1e-5 of the oracle's double dot over its K range (the reference's
                   256-block split, gemv.hip:1404), and the partials' sum within 1e-5 of the whole GEMV
-  hc_up_fused     equal to silu_mul_quant (same x bits) followed by the q8 GEMV, within 1e-6
   moe_gemm (q8)   every sorted row within 1e-5 of the oracle's q8 GEMV of its expert (the reference's
                   integer arithmetic, not bf16), routed and shared tiles of the reference's widths
   q8k             quantize_x_q8k bit-exact against the oracle; gemv_wmma_q8k within 1e-5 of the double dot
@@ -57,30 +56,6 @@ def test_gemv_splitk(gpu, fmt, N, K, ksplit, ncol):
     for ks in range(ksplit):
         s += p[:, ks]
     assert max_rel_mag(s, full, mag) < TOL
-
-
-@pytest.mark.parametrize("T,ksplit,N", [(1, 8, 10240), (4, 8, 10240), (3, 2, 333)])
-def test_hc_up_fused(gpu, T, ksplit, N):
-    K = 320
-    W = synth.matrix(510 + N, synth.Q8_0_SOA, N, K)
-    part = (synth.normal_f32(511 + T, (T, ksplit, K)) * 2).astype(np.float32)
-    y = torch.zeros((T, N), dtype=torch.float32, device="cuda")
-    Wd = dev(W)
-    qmm.hc_up_fused(Wd, dev(part), ksplit, y, N, T)
-    # the same x the kernel forms: the partials summed in k order in f32, times 1/4, then silu(g) * 1 and q8
-    g = np.zeros((T, K), np.float32)
-    for k in range(ksplit):
-        g = (g + part[:, k]).astype(np.float32)
-    g = (g * np.float32(0.25)).astype(np.float32)
-    xq = qmm.XQ8Buf(T, K)
-    qmm.silu_mul_quant(dev(g), torch.ones((T, K), device="cuda"), xq, T * K)
-    y2 = torch.zeros((T, N), dtype=torch.float32, device="cuda")
-    qmm.gemv_q8(synth.Q8_0_SOA, Wd, xq, y2, N, K, T)
-    assert rel_l2(host(y), host(y2)) <= 1e-6
-    # and against the oracle on the same q8 x
-    xr = oracle.q8_to_f32(host(xq.q), host(xq.d))
-    ref, mag = oracle.gemv_ref(synth.Q8_0_SOA, W, N, K, xr)
-    assert max_rel_mag(host(y), ref, mag) < TOL
 
 
 def _tiles(ids, maxc):

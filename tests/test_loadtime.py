@@ -1,5 +1,5 @@
-"""CPU tests of the on-disk side of the path: the GGUF v3 reader (hipster_amd/csrc/gguf.cpp, reference
-engine/src/gguf.cpp:71-156) and the load-time layout preparation (qwen4exp.cpp:34-65), through the C ABI.
+"""CPU tests of the on-disk side of the path: the GGUF v3 reader (hipster_amd/csrc/gguf_reader.cpp, reference
+engine/src/gguf.cpp:71-156) and the load-time layout preparation (hipster_amd/csrc/loadtime.cpp, qwen4exp.cpp:34-65), through the C ABI.
 
 Pins:
   - bytes the reference's own code wrote (tests/golden/loadtime_golden.npz, tests/golden/make_golden.py
@@ -20,7 +20,7 @@ import pytest
 from hipster_amd import _lib, gguf, qmm, synth
 from hipster_amd._lib import QmmError
 import oracle
-from gguf_writer import ARR, BOOL, F32, I32, STR, U8, U16, U32, U64, write_gguf
+from gguf_writer import ARR, BOOL, F32, F64, I8, I16, I32, I64, STR, U8, U16, U32, U64, write_gguf
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 G = np.load(os.path.join(HERE, "golden", "loadtime_golden.npz"))
@@ -207,6 +207,56 @@ def test_gguf_errors(tmp_path):
     write_gguf(q, [("t", 99, (32,), np.zeros(32, np.uint8))])
     with pytest.raises(QmmError, match="QMM_ERR_FORMAT"):
         gguf.GGUF(q)
+
+
+def test_gguf_dims_overflow(tmp_path):
+    """Dims whose element count wraps 64 bits (here to 0, so the byte count would be 0 and pass any
+    end-of-file check) and an ne[0] beyond int range are refused."""
+    for name, ne, gt in (("wrap", (256, 1 << 56, 1 << 8), 12), ("wrap3", (1 << 32, 1 << 32, 1), 0),
+                         ("ne0", (1 << 32,), 24)):
+        q = str(tmp_path / f"{name}.gguf")
+        write_gguf(q, [("t", gt, ne, np.zeros(64, np.uint8))])
+        with pytest.raises(QmmError, match="QMM_ERR_IO"):
+            gguf.GGUF(q)
+
+
+def test_gguf_value_types(tmp_path):
+    """Every GGUF value type, arrays of strings, nested arrays and an empty array; the tensor after them
+    is found at its offset."""
+    kv = {"v.i8": (I8, -3), "v.i16": (I16, -300), "v.u16": (U16, 65535), "v.i64": (I64, -(1 << 40)),
+          "v.f64": (F64, 2.5), "v.f32": (F32, -0.75), "v.bool": (BOOL, 0), "v.u64": (U64, (1 << 64) - 1),
+          "v.strs": (ARR, (STR, ["", "x" * 300])), "v.nest": (ARR, (ARR, [(U8, [1, 2]), (I64, [5])])),
+          "v.empty": (ARR, (F64, [])), "v.str": (STR, "")}
+    data = np.arange(40, dtype=np.float32)
+    p = str(tmp_path / "v.gguf")
+    write_gguf(p, [("w", 0, (40,), data)], kv)
+    with gguf.GGUF(p) as g:
+        assert g.kv_u32("v.i8") == (-3) & 0xffffffff and g.kv_u32("v.i16") == (-300) & 0xffffffff
+        assert g.kv_u32("v.u16") == 65535 and g.kv_u32("v.i64") == (-(1 << 40)) & 0xffffffff
+        assert g.kv_u32("v.u64") == 0xffffffff and g.kv_u32("v.bool") == 0
+        assert g.kv_f32("v.f64") == 2.5 and g.kv_f32("v.f32") == -0.75
+        assert g.kv_array_len("v.strs") == 2 and g.kv_array_len("v.nest") == 2 and g.kv_array_len("v.empty") == 0
+        assert g.kv_str("v.str") == ""
+        assert np.array_equal(g.read_tensor(g.get("w")).view(np.float32), data)
+    # an unknown value type inside an array is refused
+    raw = open(p, "rb").read()
+    at = raw.index(b"v.empty") + len(b"v.empty") + 4          # past the key and the value type (array)
+    q = str(tmp_path / "badarr.gguf")
+    open(q, "wb").write(raw[:at] + struct.pack("<I", 13) + raw[at + 4:])
+    with pytest.raises(QmmError, match="QMM_ERR_IO"):
+        gguf.GGUF(q)
+
+
+def test_gguf_single_shard_name(tmp_path):
+    """A -00001-of-00001 name opens that one file; a name with non-digits in the index is a plain file."""
+    ts = _tensors()[:2]
+    files = write_gguf(str(tmp_path / "m.gguf"), ts, KV, shards=1)
+    one = str(tmp_path / "m-00001-of-00001.gguf")
+    os.rename(files[0], one)
+    _check(one, ts, KV)
+    odd = str(tmp_path / "m-0000a-of-00002.gguf")
+    write_gguf(odd, ts, KV)
+    _check(odd, ts, KV)
 
 
 @pytest.mark.skipif(oracle.ref_gguf_lib() is None, reason="reference GGUF reader not built (no reference checkout)")
