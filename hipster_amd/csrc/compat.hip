@@ -154,6 +154,185 @@ int moe_q8_dispatch(int fmt, const void* W, const void* Wsh, size_t ebytes, cons
     }
 }
 
+// ---- grouped expert GEMM with q8 activations on the int8 matrix cores (Q4_K experts) ---------------
+// The arithmetic of the reference's moe_gemm (gemv.hip:804-953): per 32-weight sub-block the exact
+// integer dot C = sum q * xq, then acc += (d sc) xd C - (dmin m) xs in fp32, sub-blocks in K order.
+// Workgroup = (64 weight rows, tile); wave w owns rows n0 + 16w .. +15.  Per 256-weight block the pass's
+// tokens (at most 48 columns of the tile) are staged in LDS as int8 with their per-32 scales,
+// double-buffered (one barrier per block).  A sub-block is one v_mfma_i32_16x16x32_i8 per 16 tokens
+// with A = x (16 tokens x 32) and B = 32 weights x 16 rows: lane l supplies token l%16 and weight row
+// l%16, bytes k = 8(l/16)..+7 of the sub-block, and receives D[4(l/16) + r][l%16] -- four tokens of its
+// own weight row, whose sub-block scales it decoded from the block header it loaded itself.
+constexpr int kQmTok = 16, kQmMaxTok = 48, kQmRows = 64, kQmThreads = 256;
+
+struct QmLds {
+    uint2 x[2][8][4][kQmMaxTok];     // [buffer][sub-block][k quarter][token]: 8 bytes of x
+    float2 sd[2][8][kQmMaxTok];      // [buffer][sub-block][token]: {xd, xs}
+};
+
+struct QmArgs {
+    const uint8_t* W;                // routed experts (expert e at W + e * ebytes)
+    const uint8_t* Wsh;              // shared expert
+    size_t ebytes;
+    const qmm_moe_tile* tiles;       // blockIdx.y < ntiles: routed tiles; then the shared tiles
+    const qmm_moe_tile* stiles;
+    int ntiles;
+    const int* rowtab;
+    const int8_t* xq;
+    const float* xd;
+    const float* xs;
+    float* y;
+    int N, K;
+};
+
+// the x of block b for tokens [c0, c0 + 16 CB) of the tile (token c clamped to the last column) into
+// registers: thread t loads 16-byte piece t + 256 i (token p / 16, piece p % 16) and scale pair
+// t + 256 i (token p / 8, sub-block p % 8)
+template <int CB>
+struct QmXRegs { uint4 v[CB]; float2 sd[(CB * 128 + kQmThreads - 1) / kQmThreads]; };
+
+template <int CB>
+__device__ __forceinline__ void qm_x_load(const QmArgs& a, const qmm_moe_tile& tl, int c0, int ncl, int b, QmXRegs<CB>& R) {
+    const int nsb = a.K >> 5;
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+        const int p = (int)threadIdx.x + kQmThreads * i, c = p >> 4, part = p & 15;
+        const int k = tl.k0 + c0 + min(c, ncl - 1);
+        const size_t xr = (size_t)(a.rowtab ? a.rowtab[k] : k);
+        R.v[i] = *(const uint4*)(a.xq + xr * a.K + (size_t)b * 256 + 16 * part);
+    }
+#pragma unroll
+    for (int i = 0; i < (CB * 128 + kQmThreads - 1) / kQmThreads; ++i) {
+        const int p = min((int)threadIdx.x + kQmThreads * i, CB * 128 - 1), c = p >> 3, sb = p & 7;
+        const int k = tl.k0 + c0 + min(c, ncl - 1);
+        const size_t xr = (size_t)(a.rowtab ? a.rowtab[k] : k);
+        R.sd[i] = make_float2(a.xd[xr * nsb + (size_t)b * 8 + sb], a.xs[xr * nsb + (size_t)b * 8 + sb]);
+    }
+}
+
+template <int CB>
+__device__ __forceinline__ void qm_x_store(QmLds& L, int buf, const QmXRegs<CB>& R) {
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+        const int p = (int)threadIdx.x + kQmThreads * i, c = p >> 4, part = p & 15, sb = part >> 1, kq = 2 * (part & 1);
+        L.x[buf][sb][kq][c] = make_uint2(R.v[i].x, R.v[i].y);
+        L.x[buf][sb][kq + 1][c] = make_uint2(R.v[i].z, R.v[i].w);
+    }
+#pragma unroll
+    for (int i = 0; i < (CB * 128 + kQmThreads - 1) / kQmThreads; ++i) {
+        const int p = (int)threadIdx.x + kQmThreads * i;
+        if (p < CB * 128) L.sd[buf][p & 7][p >> 3] = R.sd[i];
+    }
+}
+
+struct QmW { uint4 hd; uint2 q[4]; };
+
+__device__ __forceinline__ void qm_w_load(const uint8_t* rp, int b, int kq, QmW& w) {
+    const uint8_t* blk = rp + (size_t)b * 144;
+    w.hd = *(const uint4*)blk;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w.q[j] = *(const uint2*)(blk + 16 + 32 * j + 8 * kq);
+}
+
+// one pass: tokens [c0, c0 + ncl) of the tile, ncl <= 16 CB, against the lane's weight row
+template <int CB>
+__device__ __forceinline__ void qm_pass(const QmArgs& a, const qmm_moe_tile& tl, const uint8_t* rp, int row, int c0, int ncl,
+                                        QmLds& L) {
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63, tok = lane & 15, kq = lane >> 4;
+    const int nb = a.K >> 8;
+    float acc[CB][4];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[cb][r] = 0.f;
+    QmXRegs<CB> R;
+    QmW w, wn;
+    qm_x_load<CB>(a, tl, c0, ncl, 0, R);
+    qm_w_load(rp, 0, kq, w);
+    __syncthreads();                                   // the previous pass's last reads of buffer 0 are done
+    qm_x_store<CB>(L, 0, R);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+        const int cur = b & 1;
+        if (b + 1 < nb) {                             // the next block's x and weights in flight during this one
+            qm_x_load<CB>(a, tl, c0, ncl, b + 1, R);
+            qm_w_load(rp, b + 1, kq, wn);
+        }
+        const float d = h2f(w.hd.x), dmin = h2f(w.hd.x >> 16);
+        const Q4kScaleBytes sbt = q4k_scale_bytes(w.hd.y, w.hd.z, w.hd.w);
+        uint2 q0 = w.q[0], q1 = w.q[1], q2 = w.q[2], q3 = w.q[3];
+        // a loop, not unrolled: one qs pair (two sub-blocks) per iteration keeps the register count low
+#pragma unroll 1
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+                const int sb = 2 * j + hi;
+                const float ws = d * (float)byte8(sbt.sc_lo, sbt.sc_hi, sb), wm = dmin * (float)byte8(sbt.m_lo, sbt.m_hi, sb);
+                const long wb = (long)(((uint64_t)((q0.y >> (4 * hi)) & 0x0f0f0f0fu) << 32) | (uint64_t)((q0.x >> (4 * hi)) & 0x0f0f0f0fu));
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const uint2 xv = L.x[cur][sb][kq][kQmTok * cb + tok];
+                    const long xa = (long)(((uint64_t)xv.y << 32) | (uint64_t)xv.x);
+                    const i32x4 z = {0, 0, 0, 0};
+                    const i32x4 C = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, wb, z, 0, 0, 0);
+                    const float4 s01 = *(const float4*)&L.sd[cur][sb][kQmTok * cb + 4 * kq];
+                    const float4 s23 = *(const float4*)&L.sd[cur][sb][kQmTok * cb + 4 * kq + 2];
+                    acc[cb][0] = __builtin_fmaf(-wm, s01.y, __builtin_fmaf(ws * s01.x, (float)C[0], acc[cb][0]));
+                    acc[cb][1] = __builtin_fmaf(-wm, s01.w, __builtin_fmaf(ws * s01.z, (float)C[1], acc[cb][1]));
+                    acc[cb][2] = __builtin_fmaf(-wm, s23.y, __builtin_fmaf(ws * s23.x, (float)C[2], acc[cb][2]));
+                    acc[cb][3] = __builtin_fmaf(-wm, s23.w, __builtin_fmaf(ws * s23.z, (float)C[3], acc[cb][3]));
+                }
+            }
+            q0 = q1;
+            q1 = q2;
+            q2 = q3;
+        }
+        if (b + 1 < nb) {
+            qm_x_store<CB>(L, cur ^ 1, R);
+            w = wn;
+        }
+        __syncthreads();
+    }
+    if (row < a.N) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int c = kQmTok * cb + 4 * kq + r;
+                if (c < ncl) a.y[(size_t)(tl.k0 + c0 + c) * a.N + row] = acc[cb][r];
+            }
+    }
+}
+
+__global__ void __launch_bounds__(kQmThreads) k_moe_gemm_q8_q4k(QmArgs a) {
+    __shared__ __align__(16) QmLds L;
+    const int ty = blockIdx.y;
+    const bool routed = ty < a.ntiles;
+    const qmm_moe_tile tl = routed ? a.tiles[ty] : a.stiles[ty - a.ntiles];
+    if (tl.ncols <= 0) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * kQmRows + 16 * wave + (lane & 15);
+    const uint8_t* base = routed && tl.expert >= 0 ? a.W + (size_t)tl.expert * a.ebytes : a.Wsh;
+    const uint8_t* rp = base + (size_t)min(row, a.N - 1) * (size_t)(a.K >> 8) * 144;
+    for (int c0 = 0; c0 < tl.ncols; c0 += kQmMaxTok) {
+        const int ncl = min(kQmMaxTok, tl.ncols - c0);
+        if (ncl <= kQmTok) qm_pass<1>(a, tl, rp, row, c0, ncl, L);
+        else if (ncl <= 2 * kQmTok) qm_pass<2>(a, tl, rp, row, c0, ncl, L);
+        else qm_pass<3>(a, tl, rp, row, c0, ncl, L);
+    }
+}
+
+int launch_moe_q8_q4k(const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles, int ntiles,
+                      const qmm_moe_tile* stiles, int nstiles, const int* rowtab, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+    if (ntiles + nstiles <= 0) return QMM_OK;
+    const QmArgs a = {(const uint8_t*)W, (const uint8_t*)Wsh, ebytes, tiles, stiles, ntiles, rowtab, x.q, x.d, x.s, y, N, K};
+    hipLaunchKernelGGL(k_moe_gemm_q8_q4k, dim3((unsigned)((N + kQmRows - 1) / kQmRows), (unsigned)(ntiles + nstiles)), dim3(kQmThreads),
+                       0, s, a);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
 // ---- Q8_K activations (gemv.hip:686-705): one scale per 256 weights, int16 sums per 32 ------------
 // q [ncol][K] int8, d [K/256][16] f32, bs [K/256][16][8] int16; workgroup (block b, column c):
 // d = amax/127 over the 256 values, q = rne(x * 127/amax) (0 when amax == 0), bs = sum of the 32 q.
@@ -268,9 +447,19 @@ int qmm_moe_gemm_q8(int fmt, int shared_fmt, const void* W, const void* Wsh, siz
         ct < 1 || ntiles > 65535 || nstiles > 65535)
         return QMM_ERR_SHAPE;
     hipStream_t s = (hipStream_t)stream;
-    int rc = moe_q8_dispatch(fmt, W, Wsh, ebytes, tiles, ntiles, rowtab, x, y, N, K, s);
-    if (rc != QMM_OK) return rc;
-    return moe_q8_dispatch(shared_fmt, Wsh, Wsh, 0, stiles, nstiles, rowtab, x, y, N, K, s);
+    // Q4_K tile lists run on the int8 matrix cores (routed and shared tiles in one launch when both are
+    // Q4_K); the other formats on the q8 GEMV units
+    const bool mr = fmt == QMM_Q4_K, ms = nstiles > 0 && shared_fmt == QMM_Q4_K;
+    if (mr || ms) {
+        const int rc = launch_moe_q8_q4k(W, Wsh, ebytes, tiles, mr ? ntiles : 0, stiles, ms ? nstiles : 0, rowtab, x, y, N, K, s);
+        if (rc != QMM_OK) return rc;
+    }
+    if (!mr) {
+        const int rc = moe_q8_dispatch(fmt, W, Wsh, ebytes, tiles, ntiles, rowtab, x, y, N, K, s);
+        if (rc != QMM_OK) return rc;
+    }
+    if (!ms) return moe_q8_dispatch(shared_fmt, Wsh, Wsh, 0, stiles, nstiles, rowtab, x, y, N, K, s);
+    return QMM_OK;
 }
 
 int qmm_quantize_x_q8k(const float* x, qmm_xq8k out, int ncol, int K, void* stream) {

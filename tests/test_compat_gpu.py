@@ -65,12 +65,15 @@ def _tiles(ids, maxc):
 
 @pytest.mark.parametrize("fmt,sfmt,N,K,T,n_exp,ct", [(synth.Q4_K, synth.Q4_K, 512, 2048, 96, 32, 1),
                                                       (synth.Q4_K, synth.Q8_0_SOA, 2048, 512, 64, 16, 3),
+                                                      (synth.Q4_K, synth.Q4_K, 200, 512, 40, 12, 4),
+                                                      (synth.Q8_0_SOA, synth.Q4_K, 192, 512, 30, 12, 2),
                                                       (synth.Q5_1_SOA, synth.Q5_1_SOA, 256, 640, 40, 12, 2),
                                                       (synth.Q5_K, synth.Q8_0_SOA, 640, 512, 33, 12, 1),
                                                       (synth.IQ4_XS, synth.IQ4_XS, 128, 768, 20, 10, 2),
                                                       (synth.Q8_0_SOA, synth.Q8_0_SOA, 200, 320, 17, 16, 1)])
 def test_moe_gemm_q8(gpu, fmt, sfmt, N, K, T, n_exp, ct):
-    """rows gathered by rowtab (gate/up) and in place (down, rowtab = NULL)"""
+    """rows gathered by rowtab (gate/up) and in place (down, rowtab = NULL); Q4_K tile lists run on the
+    int8 matrix cores (N = 200: a partial 64-row block; ct = 4: tiles of 64 columns, two passes)"""
     print(f"moe_gemm fmt={fmt}/{sfmt} N={N} K={K} T={T} E={n_exp} ct={ct}", flush=True)
     NE = 11
     assert n_exp >= 10                                   # top-10 routing
