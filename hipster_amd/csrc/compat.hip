@@ -164,6 +164,9 @@ int moe_q8_dispatch(int fmt, const void* W, const void* Wsh, size_t ebytes, cons
 // l%16, bytes k = 8(l/16)..+7 of the sub-block, and receives D[4(l/16) + r][l%16] -- four tokens of its
 // own weight row, whose sub-block scales it decoded from the block header it loaded itself.
 constexpr int kQmTok = 16, kQmMaxTok = 48, kQmRows = 64, kQmThreads = 256;
+#ifndef QMM_QM_RG
+#define QMM_QM_RG 2
+#endif
 
 struct QmLds {
     uint2 x[2][8][4][kQmMaxTok];     // [buffer][sub-block][k quarter][token]: 8 bytes of x
@@ -234,22 +237,26 @@ __device__ __forceinline__ void qm_w_load(const uint8_t* rp, int b, int kq, QmW&
     for (int j = 0; j < 4; ++j) w.q[j] = *(const uint2*)(blk + 16 + 32 * j + 8 * kq);
 }
 
-// one pass: tokens [c0, c0 + ncl) of the tile, ncl <= 16 CB, against the lane's weight row
-template <int CB>
-__device__ __forceinline__ void qm_pass(const QmArgs& a, const qmm_moe_tile& tl, const uint8_t* rp, int row, int c0, int ncl,
-                                        QmLds& L) {
+// one pass: tokens [c0, c0 + ncl) of the tile, ncl <= 16 CB, against the lane's RG weight rows (row
+// groups of 16: the x fragment of a sub-block feeds RG MFMAs)
+template <int CB, int RG>
+__device__ __forceinline__ void qm_pass(const QmArgs& a, const qmm_moe_tile& tl, const uint8_t* const (&rp)[RG], const int (&row)[RG],
+                                        int c0, int ncl, QmLds& L) {
     typedef int i32x4 __attribute__((ext_vector_type(4)));
     const int lane = threadIdx.x & 63, tok = lane & 15, kq = lane >> 4;
     const int nb = a.K >> 8;
-    float acc[CB][4];
+    float acc[CB][RG][4];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[cb][r] = 0.f;
+        for (int g = 0; g < RG; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[cb][g][r] = 0.f;
     QmXRegs<CB> R;
-    QmW w, wn;
+    QmW w[RG], wn[RG];
     qm_x_load<CB>(a, tl, c0, ncl, 0, R);
-    qm_w_load(rp, 0, kq, w);
+#pragma unroll
+    for (int g = 0; g < RG; ++g) qm_w_load(rp[g], 0, kq, w[g]);
     __syncthreads();                                   // the previous pass's last reads of buffer 0 are done
     qm_x_store<CB>(L, 0, R);
     __syncthreads();
@@ -257,54 +264,87 @@ __device__ __forceinline__ void qm_pass(const QmArgs& a, const qmm_moe_tile& tl,
         const int cur = b & 1;
         if (b + 1 < nb) {                             // the next block's x and weights in flight during this one
             qm_x_load<CB>(a, tl, c0, ncl, b + 1, R);
-            qm_w_load(rp, b + 1, kq, wn);
+#pragma unroll
+            for (int g = 0; g < RG; ++g) qm_w_load(rp[g], b + 1, kq, wn[g]);
         }
-        const float d = h2f(w.hd.x), dmin = h2f(w.hd.x >> 16);
-        const Q4kScaleBytes sbt = q4k_scale_bytes(w.hd.y, w.hd.z, w.hd.w);
-        uint2 q0 = w.q[0], q1 = w.q[1], q2 = w.q[2], q3 = w.q[3];
+        // per row group: d, dmin and the 8 scale / min bytes as 64-bit words, consumed two bytes (one pair)
+        // per iteration from the bottom
+        float d[RG], dmin[RG];
+        uint64_t scb[RG], mnb[RG];
+        uint2 q0[RG], q1[RG], q2[RG], q3[RG];
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+            d[g] = h2f(w[g].hd.x);
+            dmin[g] = h2f(w[g].hd.x >> 16);
+            const Q4kScaleBytes sbt = q4k_scale_bytes(w[g].hd.y, w[g].hd.z, w[g].hd.w);
+            scb[g] = ((uint64_t)sbt.sc_hi << 32) | sbt.sc_lo;
+            mnb[g] = ((uint64_t)sbt.m_hi << 32) | sbt.m_lo;
+            q0[g] = w[g].q[0]; q1[g] = w[g].q[1]; q2[g] = w[g].q[2]; q3[g] = w[g].q[3];
+        }
         // a loop, not unrolled: one qs pair (two sub-blocks) per iteration keeps the register count low
 #pragma unroll 1
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
             for (int hi = 0; hi < 2; ++hi) {
                 const int sb = 2 * j + hi;
-                const float ws = d * (float)byte8(sbt.sc_lo, sbt.sc_hi, sb), wm = dmin * (float)byte8(sbt.m_lo, sbt.m_hi, sb);
-                const long wb = (long)(((uint64_t)((q0.y >> (4 * hi)) & 0x0f0f0f0fu) << 32) | (uint64_t)((q0.x >> (4 * hi)) & 0x0f0f0f0fu));
+                float ws[RG], wm[RG];
+                long wb[RG];
+#pragma unroll
+                for (int g = 0; g < RG; ++g) {
+                    ws[g] = d[g] * (float)(((uint32_t)scb[g] >> (8 * hi)) & 0xffu);
+                    wm[g] = dmin[g] * (float)(((uint32_t)mnb[g] >> (8 * hi)) & 0xffu);
+                    wb[g] = (long)(((uint64_t)((q0[g].y >> (4 * hi)) & 0x0f0f0f0fu) << 32) | (uint64_t)((q0[g].x >> (4 * hi)) & 0x0f0f0f0fu));
+                }
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) {
                     const uint2 xv = L.x[cur][sb][kq][kQmTok * cb + tok];
                     const long xa = (long)(((uint64_t)xv.y << 32) | (uint64_t)xv.x);
-                    const i32x4 z = {0, 0, 0, 0};
-                    const i32x4 C = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, wb, z, 0, 0, 0);
                     const float4 s01 = *(const float4*)&L.sd[cur][sb][kQmTok * cb + 4 * kq];
                     const float4 s23 = *(const float4*)&L.sd[cur][sb][kQmTok * cb + 4 * kq + 2];
-                    acc[cb][0] = __builtin_fmaf(-wm, s01.y, __builtin_fmaf(ws * s01.x, (float)C[0], acc[cb][0]));
-                    acc[cb][1] = __builtin_fmaf(-wm, s01.w, __builtin_fmaf(ws * s01.z, (float)C[1], acc[cb][1]));
-                    acc[cb][2] = __builtin_fmaf(-wm, s23.y, __builtin_fmaf(ws * s23.x, (float)C[2], acc[cb][2]));
-                    acc[cb][3] = __builtin_fmaf(-wm, s23.w, __builtin_fmaf(ws * s23.z, (float)C[3], acc[cb][3]));
+#pragma unroll
+                    for (int g = 0; g < RG; ++g) {
+                        const i32x4 z = {0, 0, 0, 0};
+                        const i32x4 C = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, wb[g], z, 0, 0, 0);
+                        float* ac = acc[cb][g];
+                        ac[0] = __builtin_fmaf(-wm[g], s01.y, __builtin_fmaf(ws[g] * s01.x, (float)C[0], ac[0]));
+                        ac[1] = __builtin_fmaf(-wm[g], s01.w, __builtin_fmaf(ws[g] * s01.z, (float)C[1], ac[1]));
+                        ac[2] = __builtin_fmaf(-wm[g], s23.y, __builtin_fmaf(ws[g] * s23.x, (float)C[2], ac[2]));
+                        ac[3] = __builtin_fmaf(-wm[g], s23.w, __builtin_fmaf(ws[g] * s23.z, (float)C[3], ac[3]));
+                    }
                 }
             }
-            q0 = q1;
-            q1 = q2;
-            q2 = q3;
+#pragma unroll
+            for (int g = 0; g < RG; ++g) {
+                q0[g] = q1[g];
+                q1[g] = q2[g];
+                q2[g] = q3[g];
+                scb[g] >>= 16;
+                mnb[g] >>= 16;
+            }
         }
         if (b + 1 < nb) {
             qm_x_store<CB>(L, cur ^ 1, R);
-            w = wn;
+#pragma unroll
+            for (int g = 0; g < RG; ++g) w[g] = wn[g];
         }
         __syncthreads();
     }
-    if (row < a.N) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
+    for (int g = 0; g < RG; ++g)
+        if (row[g] < a.N) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int c = kQmTok * cb + 4 * kq + r;
-                if (c < ncl) a.y[(size_t)(tl.k0 + c0 + c) * a.N + row] = acc[cb][r];
-            }
-    }
+            for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int c = kQmTok * cb + 4 * kq + r;
+                    if (c < ncl) a.y[(size_t)(tl.k0 + c0 + c) * a.N + row[g]] = acc[cb][g][r];
+                }
+        }
 }
 
+// CBMAX: 16-token blocks of the widest pass (1 when every tile has at most 16 columns); RG row groups
+// of 16 per wave (a workgroup covers 64 RG weight rows)
+template <int CBMAX, int RG>
 __global__ void __launch_bounds__(kQmThreads) k_moe_gemm_q8_q4k(QmArgs a) {
     __shared__ __align__(16) QmLds L;
     const int ty = blockIdx.y;
@@ -312,23 +352,34 @@ __global__ void __launch_bounds__(kQmThreads) k_moe_gemm_q8_q4k(QmArgs a) {
     const qmm_moe_tile tl = routed ? a.tiles[ty] : a.stiles[ty - a.ntiles];
     if (tl.ncols <= 0) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = blockIdx.x * kQmRows + 16 * wave + (lane & 15);
     const uint8_t* base = routed && tl.expert >= 0 ? a.W + (size_t)tl.expert * a.ebytes : a.Wsh;
-    const uint8_t* rp = base + (size_t)min(row, a.N - 1) * (size_t)(a.K >> 8) * 144;
-    for (int c0 = 0; c0 < tl.ncols; c0 += kQmMaxTok) {
-        const int ncl = min(kQmMaxTok, tl.ncols - c0);
-        if (ncl <= kQmTok) qm_pass<1>(a, tl, rp, row, c0, ncl, L);
-        else if (ncl <= 2 * kQmTok) qm_pass<2>(a, tl, rp, row, c0, ncl, L);
-        else qm_pass<3>(a, tl, rp, row, c0, ncl, L);
+    int row[RG];
+    const uint8_t* rp[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+        row[g] = blockIdx.x * (kQmRows * RG) + 16 * (RG * wave + g) + (lane & 15);
+        rp[g] = base + (size_t)min(row[g], a.N - 1) * (size_t)(a.K >> 8) * 144;
+    }
+    constexpr int kPass = kQmTok * CBMAX;
+    for (int c0 = 0; c0 < tl.ncols; c0 += kPass) {
+        const int ncl = min(kPass, tl.ncols - c0);
+        if (CBMAX == 1 || ncl <= kQmTok) qm_pass<1, RG>(a, tl, rp, row, c0, ncl, L);
+        else if (CBMAX == 2 || ncl <= 2 * kQmTok) qm_pass<(CBMAX >= 2 ? 2 : 1), RG>(a, tl, rp, row, c0, ncl, L);
+        else qm_pass<(CBMAX >= 3 ? 3 : 1), RG>(a, tl, rp, row, c0, ncl, L);
     }
 }
 
 int launch_moe_q8_q4k(const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles, int ntiles,
-                      const qmm_moe_tile* stiles, int nstiles, const int* rowtab, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+                      const qmm_moe_tile* stiles, int nstiles, int ct, const int* rowtab, qmm_xq8 x, float* y, int N, int K,
+                      hipStream_t s) {
     if (ntiles + nstiles <= 0) return QMM_OK;
+    constexpr int RG = QMM_QM_RG;
     const QmArgs a = {(const uint8_t*)W, (const uint8_t*)Wsh, ebytes, tiles, stiles, ntiles, rowtab, x.q, x.d, x.s, y, N, K};
-    hipLaunchKernelGGL(k_moe_gemm_q8_q4k, dim3((unsigned)((N + kQmRows - 1) / kQmRows), (unsigned)(ntiles + nstiles)), dim3(kQmThreads),
-                       0, s, a);
+    const dim3 grid((unsigned)((N + kQmRows * RG - 1) / (kQmRows * RG)), (unsigned)(ntiles + nstiles));
+    // tiles hold at most 16 ct columns (the reference's tiling): passes of up to 48 columns
+    if (ct <= 1) hipLaunchKernelGGL((k_moe_gemm_q8_q4k<1, RG>), grid, dim3(kQmThreads), 0, s, a);
+    else if (ct == 2) hipLaunchKernelGGL((k_moe_gemm_q8_q4k<2, RG>), grid, dim3(kQmThreads), 0, s, a);
+    else hipLaunchKernelGGL((k_moe_gemm_q8_q4k<3, RG>), grid, dim3(kQmThreads), 0, s, a);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }
@@ -451,7 +502,7 @@ int qmm_moe_gemm_q8(int fmt, int shared_fmt, const void* W, const void* Wsh, siz
     // Q4_K); the other formats on the q8 GEMV units
     const bool mr = fmt == QMM_Q4_K, ms = nstiles > 0 && shared_fmt == QMM_Q4_K;
     if (mr || ms) {
-        const int rc = launch_moe_q8_q4k(W, Wsh, ebytes, tiles, mr ? ntiles : 0, stiles, ms ? nstiles : 0, rowtab, x, y, N, K, s);
+        const int rc = launch_moe_q8_q4k(W, Wsh, ebytes, tiles, mr ? ntiles : 0, stiles, ms ? nstiles : 0, ct, rowtab, x, y, N, K, s);
         if (rc != QMM_OK) return rc;
     }
     if (!mr) {
