@@ -974,6 +974,52 @@ int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, 
     }
 }
 
+// one run of nseg (<= 4) segments of format fmt sharing x: Q4_K on the matrix cores (16 columns per
+// launch) from g_mfma_min_ncol columns on, else the dot4 kernel (8 per launch); Q5_K, IQ4_XS, Q8_0_SOA
+// and Q5_1_SOA in one launch per 8 columns; Q6_K (both layouts) per segment
+int gemv_multi_run(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s) {
+    const int fmt = segs[0].fmt;
+    auto xcols = [&](int c0) {
+        return qmm_xq8{x.q + (size_t)c0 * K, x.d + (size_t)c0 * (K / 32), x.s + (size_t)c0 * (K / 32), nullptr};
+    };
+    if (fmt == QMM_Q4_K) {
+        int cpl = 16;                                         // columns per matrix-core launch
+        while (cpl > 1 && gemv_q4k_mfma_lds(K, cpl) > kMfmaLdsMax) cpl /= 2;
+        const bool mfma = ncol >= g_mfma_min_ncol && cpl >= 2;
+        const int step = mfma ? cpl : 8;
+        for (int c0 = 0; c0 < ncol; c0 += step) {
+            const int nc = ncol - c0 < step ? ncol - c0 : step;
+            const qmm_xq8 xc = xcols(c0);
+            qmm_gemv_seg sc[4];
+            for (int i = 0; i < nseg; ++i) {
+                sc[i] = segs[i];
+                sc[i].y = segs[i].y + (size_t)c0 * segs[i].N;
+            }
+            // a tail pass of fewer columns runs the dot4 kernel (the same bits)
+            const int e = mfma && nc >= g_mfma_min_ncol ? gemv_q4k_mfma(sc, nseg, xc, K, nc, s) : gemv_q4k_q8_multi(segs, nseg, xc, K, nc, c0, s);
+            if (e) return e;
+        }
+        return QMM_OK;
+    }
+    const bool fmt_multi = fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA;
+    for (int c0 = 0; c0 < ncol; c0 += 8) {
+        const int nc = ncol - c0 < 8 ? ncol - c0 : 8;
+        const qmm_xq8 xc = xcols(c0);
+        qmm_gemv_seg sc[4];
+        for (int i = 0; i < nseg; ++i) {
+            sc[i] = segs[i];
+            sc[i].y = segs[i].y + (size_t)c0 * segs[i].N;
+        }
+        if (fmt_multi) {
+            if (int e = gemv_fmt_dispatch_segs(fmt, sc, nseg, xc, K, nc, s)) return e;
+        } else {
+            for (int i = 0; i < nseg; ++i)
+                if (int e = gemv_q8_dispatch(fmt, sc[i].w, xc, sc[i].y, sc[i].N, K, nc, s)) return e;
+        }
+    }
+    return QMM_OK;
+}
+
 }  // namespace qmm
 
 using namespace qmm;
@@ -1045,42 +1091,13 @@ int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void
         if (segs[i].K != segs[0].K) return QMM_ERR_SHAPE;
     }
     const int K = segs[0].K;
-    bool all_q4k = true;
-    for (int i = 0; i < nseg; ++i) all_q4k = all_q4k && segs[i].fmt == QMM_Q4_K;
-    // columns per launch: 16 (8, 4 when x of 16 columns does not fit the LDS budget)
-    int cpl = 16;
-    while (cpl > 1 && gemv_q4k_mfma_lds(K, cpl) > kMfmaLdsMax) cpl /= 2;
-    if (all_q4k && ncol >= g_mfma_min_ncol && cpl >= 2) {      // every segment in one launch per cpl columns
-        for (int c0 = 0; c0 < ncol; c0 += cpl) {
-            const int nc = ncol - c0 < cpl ? ncol - c0 : cpl;
-            qmm_xq8 xc = {x.q + (size_t)c0 * K, x.d + (size_t)c0 * (K / 32), x.s + (size_t)c0 * (K / 32), nullptr};
-            qmm_gemv_seg sc[4];
-            for (int i = 0; i < nseg; ++i) {
-                sc[i] = segs[i];
-                sc[i].y = segs[i].y + (size_t)c0 * segs[i].N;
-            }
-            // a tail pass of fewer columns runs the dot4 kernel, all segments in one launch (the same bits)
-            const int e = nc >= g_mfma_min_ncol ? gemv_q4k_mfma(sc, nseg, xc, K, nc, (hipStream_t)stream)
-                                                : gemv_q4k_q8_multi(segs, nseg, xc, K, nc, c0, (hipStream_t)stream);
-            if (e) return e;
-        }
-        return QMM_OK;
-    }
-    if (all_q4k) {                                           // the dot4 kernel, all segments in one launch per 8 columns
-        for (int c0 = 0; c0 < ncol; c0 += 8) {
-            const int nc = ncol - c0 < 8 ? ncol - c0 : 8;
-            qmm_xq8 xc = {x.q + (size_t)c0 * K, x.d + (size_t)c0 * (K / 32), x.s + (size_t)c0 * (K / 32), nullptr};
-            if (int e = gemv_q4k_q8_multi(segs, nseg, xc, K, nc, c0, (hipStream_t)stream)) return e;
-        }
-        return QMM_OK;
-    }
-    for (int c0 = 0; c0 < ncol; c0 += 8) {
-        const int nc = ncol - c0 < 8 ? ncol - c0 : 8;
-        qmm_xq8 xc = {x.q + (size_t)c0 * K, x.d + (size_t)c0 * (K / 32), x.s + (size_t)c0 * (K / 32), nullptr};
-        for (int i = 0; i < nseg; ++i) {
-            const int e = gemv_q8_dispatch(segs[i].fmt, segs[i].w, xc, segs[i].y + (size_t)c0 * segs[i].N, segs[i].N, K, nc, (hipStream_t)stream);
-            if (e) return e;
-        }
+    // runs of consecutive segments of one format (at most 4, the reference's gemv_wmma grouping), each
+    // run in one launch per column pass; every row gets the arithmetic of its format's plain GEMV
+    for (int i0 = 0; i0 < nseg;) {
+        int i1 = i0 + 1;
+        while (i1 < nseg && segs[i1].fmt == segs[i0].fmt) ++i1;
+        if (int e = gemv_multi_run(segs + i0, i1 - i0, x, K, ncol, (hipStream_t)stream)) return e;
+        i0 = i1;
     }
     return QMM_OK;
 }

@@ -28,7 +28,7 @@ namespace qmm {
 extern int g_fmt_xlds;
 namespace {
 
-constexpr int kFmtBlock = 256, kFmtWaves = kFmtBlock / 64;
+constexpr int kFmtBlock = 256, kFmtWaves = kFmtBlock / 64, kFmtMaxSeg = 4;
 constexpr size_t kFmtXLds = 64 * 1024;   // bytes of LDS the plain GEMV may use for staged x
 
 // x of NCOL columns staged in LDS as [xq NCOL*K][xd NCOL*K/32][xs NCOL*K/32] (the layout of
@@ -62,16 +62,33 @@ struct FmtXFirst {
     }
 };
 
+// Up to four weights of one format sharing x (the reference's gemv_multi / gemv_wmma segments): the
+// workgroups of segment i are t0[i] .. t0[i+1]-1, each RPW rows per wave of that segment.
+struct FSegs {
+    const uint8_t* w[kFmtMaxSeg];
+    float* y[kFmtMaxSeg];
+    int N[kFmtMaxSeg];
+    int t0[kFmtMaxSeg + 1];
+    int nseg;
+};
+
 // XS: 0 = x read from global memory (L1) by every wave, 1 = staged in LDS before the weights are
 // loaded, 2 = staged in LDS from registers loaded ahead of the first weight loads (FmtXFirst).
-// The arithmetic is the same in all three, so are the results.
+// The arithmetic is the same in all three, so are the results; a row's arithmetic does not depend on
+// its segment or the other segments of the launch.
 template <int F, int NCOL, int NIT, int RPW, int XS>
-__global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
-                                                        const float* __restrict__ xd, const float* __restrict__ xs,
-                                                        float* __restrict__ y, int N, int K) {
+__global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(FSegs sg, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                        const float* __restrict__ xs, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < kFmtMaxSeg; ++i)
+        if (i < sg.nseg && (int)blockIdx.x >= sg.t0[i]) si = i;
+    const uint8_t* __restrict__ W = sg.w[si];
+    float* __restrict__ y = sg.y[si];
+    const int N = sg.N[si];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * kFmtWaves + wave) * RPW;
+    const int row0 = (((int)blockIdx.x - sg.t0[si]) * kFmtWaves + wave) * RPW;
     const int nsb = K / 32;
     XSrcQ8 xsrc[NCOL];
     float acc[RPW][NCOL];
@@ -221,11 +238,19 @@ int launch_moe_fmt(const qmm_moe_segs& a, int nseg, const int* ids, int nexp, qm
 }
 
 template <int F, int NCOL>
-int launch_fmt(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+int launch_fmt(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, hipStream_t s) {
     // rows per wave: 2 at one column (more waves in flight), 4 above (the shared x pays more), 2 for
     // Q5_K (its units hold 20 registers of raw weights)
     constexpr int RPW = (F == QMM_Q5_K || NCOL == 1) ? 2 : 4;
-    const int grid = (N + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
+    FSegs sg = {};
+    sg.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) {
+        sg.w[i] = (const uint8_t*)segs[i].w;
+        sg.y[i] = segs[i].y;
+        sg.N[i] = segs[i].N;
+        sg.t0[i + 1] = sg.t0[i] + (segs[i].N + kFmtWaves * RPW - 1) / (kFmtWaves * RPW);
+    }
+    const int grid = sg.t0[nseg];
     const int per_lane = (fmt_units<F>(K) + 63) / 64;
     // Where x comes from (measured at 17408 x 5120, M = 1..8): staged once per workgroup in LDS for
     // Q5_K and Q5_1_SOA at every width (Q5_K M = 4: 30.6 -> 23.6 us, M = 8: 52.5 -> 35.2 us), for
@@ -242,11 +267,11 @@ int launch_fmt(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) 
 #define QMM_FMTL(IV)                                                                                                     \
     do {                                                                                                                \
         if (xmode == 2) hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV, RPW, 2>), dim3(grid), dim3(kFmtBlock), xl, s,       \
-                                           (const uint8_t*)W, x.q, x.d, x.s, y, N, K);                                  \
+                                           sg, x.q, x.d, x.s, K);                                  \
         else if (xmode == 1) hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV, RPW, 1>), dim3(grid), dim3(kFmtBlock), xl, s,  \
-                                                (const uint8_t*)W, x.q, x.d, x.s, y, N, K);                             \
+                                                sg, x.q, x.d, x.s, K);                             \
         else hipLaunchKernelGGL((k_gemv_fmt<F, NCOL, IV, RPW, 0>), dim3(grid), dim3(kFmtBlock), 0, s,                   \
-                                (const uint8_t*)W, x.q, x.d, x.s, y, N, K);                                            \
+                                sg, x.q, x.d, x.s, K);                                            \
     } while (0)
     // units per lane and pass: all of them when they are few, else passes of two (registers: RPW
     // rows x NIT units of raw weights are live at once)
@@ -259,12 +284,12 @@ int launch_fmt(const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) 
 }
 
 template <int NCOL>
-int launch_fmt_ncol(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, hipStream_t s) {
+int launch_fmt_ncol(int fmt, const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, hipStream_t s) {
     switch (fmt) {
-        case QMM_Q5_K: return launch_fmt<QMM_Q5_K, NCOL>(W, x, y, N, K, s);
-        case QMM_IQ4_XS: return launch_fmt<QMM_IQ4_XS, NCOL>(W, x, y, N, K, s);
-        case QMM_Q8_0_SOA: return launch_fmt<QMM_Q8_0_SOA, NCOL>(W, x, y, N, K, s);
-        case QMM_Q5_1_SOA: return launch_fmt<QMM_Q5_1_SOA, NCOL>(W, x, y, N, K, s);
+        case QMM_Q5_K: return launch_fmt<QMM_Q5_K, NCOL>(segs, nseg, x, K, s);
+        case QMM_IQ4_XS: return launch_fmt<QMM_IQ4_XS, NCOL>(segs, nseg, x, K, s);
+        case QMM_Q8_0_SOA: return launch_fmt<QMM_Q8_0_SOA, NCOL>(segs, nseg, x, K, s);
+        case QMM_Q5_1_SOA: return launch_fmt<QMM_Q5_1_SOA, NCOL>(segs, nseg, x, K, s);
         default: return QMM_ERR_FORMAT;
     }
 }
@@ -273,18 +298,25 @@ int launch_fmt_ncol(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, h
 
 int g_fmt_xlds = 1;
 
-int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+// one launch for nseg (<= 4) segments of format fmt sharing x, ncol <= 8 columns
+int gemv_fmt_dispatch_segs(int fmt, const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s) {
+    if (nseg < 1 || nseg > kFmtMaxSeg) return QMM_ERR_SHAPE;
     switch (ncol) {
-        case 1: return launch_fmt_ncol<1>(fmt, W, x, y, N, K, s);
-        case 2: return launch_fmt_ncol<2>(fmt, W, x, y, N, K, s);
-        case 3: return launch_fmt_ncol<3>(fmt, W, x, y, N, K, s);
-        case 4: return launch_fmt_ncol<4>(fmt, W, x, y, N, K, s);
-        case 5: return launch_fmt_ncol<5>(fmt, W, x, y, N, K, s);
-        case 6: return launch_fmt_ncol<6>(fmt, W, x, y, N, K, s);
-        case 7: return launch_fmt_ncol<7>(fmt, W, x, y, N, K, s);
-        case 8: return launch_fmt_ncol<8>(fmt, W, x, y, N, K, s);
+        case 1: return launch_fmt_ncol<1>(fmt, segs, nseg, x, K, s);
+        case 2: return launch_fmt_ncol<2>(fmt, segs, nseg, x, K, s);
+        case 3: return launch_fmt_ncol<3>(fmt, segs, nseg, x, K, s);
+        case 4: return launch_fmt_ncol<4>(fmt, segs, nseg, x, K, s);
+        case 5: return launch_fmt_ncol<5>(fmt, segs, nseg, x, K, s);
+        case 6: return launch_fmt_ncol<6>(fmt, segs, nseg, x, K, s);
+        case 7: return launch_fmt_ncol<7>(fmt, segs, nseg, x, K, s);
+        case 8: return launch_fmt_ncol<8>(fmt, segs, nseg, x, K, s);
         default: return QMM_ERR_SHAPE;
     }
+}
+
+int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    const qmm_gemv_seg seg = {fmt, W, y, N, K};
+    return gemv_fmt_dispatch_segs(fmt, &seg, 1, x, K, ncol, s);
 }
 
 // routed format fmt, shared format sfmt (fmt, or Q8_0_SOA); fmt may be Q4_K only with a Q8_0_SOA

@@ -107,6 +107,36 @@ def test_gemv_multi_mixed_formats_equals_separate_calls(gpu):
         assert torch.equal(y, y1)
 
 
+@pytest.mark.parametrize("ncol", [1, 3, 8, 12])
+@pytest.mark.parametrize("layout", [((synth.Q5_K, 1024), (synth.Q5_K, 300), (synth.Q5_K, 17), (synth.IQ4_XS, 512)),
+                                    ((synth.IQ4_XS, 700), (synth.IQ4_XS, 64), (synth.Q8_0_SOA, 256), (synth.Q8_0_SOA, 130)),
+                                    ((synth.Q5_1_SOA, 96), (synth.Q5_1_SOA, 1000), (synth.Q5_1_SOA, 33), (synth.Q5_1_SOA, 512)),
+                                    ((synth.Q6_K_SOA, 256), (synth.Q6_K_SOA, 100), (synth.Q4_K, 512), (synth.Q4_K, 48))])
+def test_gemv_multi_same_format_runs(gpu, layout, ncol):
+    """Runs of consecutive same-format segments go out as one launch per column pass; every segment's
+    rows are bitwise its own gemv_q8 (the per-row arithmetic does not depend on the other segments)."""
+    K = 5120
+    print(f"gemv_multi runs {[f for f, _ in layout]} ncol={ncol}", flush=True)
+    x = synth.normal_f32(1400 + ncol, (ncol, K))
+    xb = q8_on_gpu(x)
+    segs, ref = [], []
+    for i, (fmt, N) in enumerate(layout):
+        W = dev(synth.matrix(1410 + 7 * i + fmt, fmt, N, K))
+        y = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+        y1 = torch.zeros((ncol, N), dtype=torch.float32, device="cuda")
+        for c0 in range(0, ncol, 8):
+            nc = min(8, ncol - c0)
+            xc = qmm.XQ8Buf(nc, K)
+            xc.q.copy_(xb.q[c0:c0 + nc]); xc.d.copy_(xb.d[c0:c0 + nc]); xc.s.copy_(xb.s[c0:c0 + nc])
+            y1c = torch.zeros((nc, N), dtype=torch.float32, device="cuda")
+            qmm.gemv_q8(fmt, W, xc, y1c, N, K, nc)
+            y1[c0:c0 + nc] = y1c
+        segs.append((fmt, W, y, N, K)); ref.append(y1)
+    qmm.gemv_multi(segs, xb, ncol)
+    for (_, _, y, _, _), y1 in zip(segs, ref):
+        assert torch.equal(y, y1)
+
+
 @pytest.mark.parametrize("fmt,K", [(synth.Q5_K, 5120), (synth.Q5_K, 17408), (synth.IQ4_XS, 5120), (synth.IQ4_XS, 2048),
                                    (synth.Q8_0_SOA, 5120), (synth.Q8_0_SOA, 640), (synth.Q5_1_SOA, 5120),
                                    (synth.Q5_1_SOA, 640), (synth.Q5_1_SOA, 96)])
