@@ -57,6 +57,7 @@ def q8_reference(fmt, W, N, K, x):
 
 
 SHAPES = [(synth.Q4_K, 17408, 5120), (synth.Q4_K, 1000, 256), (synth.Q4_K, 77, 2048), (synth.Q4_K, 5120, 17408),
+          (synth.Q4_K, 8192, 5120), (synth.Q4_K, 5120, 6144),        # config 1: QKV 5120 -> 6144+1024+1024, O 6144 -> 5120
           (synth.Q6_K, 5120, 17408), (synth.Q6_K, 333, 5120), (synth.Q6_K, 64, 768),
           (synth.Q6_K_SOA, 5120, 17408), (synth.Q6_K_SOA, 129, 512)]
 

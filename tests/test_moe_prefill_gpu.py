@@ -170,7 +170,8 @@ def test_moe_gemm_bf16_tile_size_invariant(gpu, N, K):
 def test_moe_prefill_config4_pipeline(gpu):
     """2048 tokens, hidden 2048, 512 Q4_K experts + shared, top-10 with the Zipf
     bias.  Device pipeline: route -> sort -> gate/up/silu (one launch) -> down -> combine; 12 sampled tokens
-    against the oracle's bf16 path (bf16 weights and activations, double accumulation)."""
+    against the oracle's bf16 path (bf16 weights and activations, double accumulation): every 8th token
+    and the edges (266 tokens)."""
     T, n_exp = 2048, 512
     Wg_h, Wu_h, Wd_h = (synth.experts(1420 + i, synth.Q4_K, n_exp, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
     Sg_h, Su_h, Sd_h = (synth.matrix(1425 + i, synth.Q4_K, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
@@ -193,8 +194,40 @@ def test_moe_prefill_config4_pipeline(gpu):
     y = torch.zeros((T, H), device="cuda")
     qmm.moe_combine_sorted(dn, w, kpos, y, T, NE, H)
     ids_h, w_h = host(ids), host(w)
-    toks = np.array([0, 1, 2, 100, 511, 777, 1000, 1024, 1500, 2000, 2046, 2047], np.int32)
+    toks = np.unique(np.concatenate([np.arange(0, T, 8), [1, 2, 511, 777, 1023, 1025, 1500, 2045, 2046, 2047]])).astype(np.int32)
     y_ref = oracle.moe_prefill_tokens(synth.Q4_K, Wg_h, Wu_h, Wd_h, Sg_h, Su_h, Sd_h, x_bits, ids_h, w_h, H, F, toks)
     err = rel_l2(host(y)[toks], y_ref)
-    print(f"config-4 MoE prefill, sampled tokens rel-L2 {err:.2e}", flush=True)
+    print(f"config-4 MoE prefill, {len(toks)} sampled tokens rel-L2 {err:.2e}", flush=True)
+    assert err <= 2e-3
+
+
+def test_moe_prefill_pipeline_every_token_against_oracle(gpu):
+    """The whole device pipeline (route, sort, gate/up/silu, down, combine) at 300 tokens over 64 Q4_K
+    experts + shared with the Zipf bias (small and full tiles, several tiles for the popular experts):
+    every token against the oracle's bf16 path."""
+    T, n_exp = 300, 64
+    Wg_h, Wu_h, Wd_h = (synth.experts(1460 + i, synth.Q4_K, n_exp, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
+    Sg_h, Su_h, Sd_h = (synth.matrix(1465 + i, synth.Q4_K, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
+    x_bits = synth.to_bf16_bits(synth.normal_f32(1470, (T, H)))
+    logits = synth.router_logits(1471, T, n_exp, 1.1)
+    Wg, Wu, Wd, Sg, Su, Sd = (dev(a) for a in (Wg_h, Wu_h, Wd_h, Sg_h, Su_h, Sd_h))
+    ids = torch.zeros((T, NE), dtype=torch.int32, device="cuda")
+    w = torch.zeros((T, NE), device="cuda")
+    qmm.moe_route_n(dev(logits), ids, w, T, n_exp, n_exp + 1, 10)
+    NS = T * NE
+    cap = qmm.moe_tiles_capacity(T, NE, n_exp)
+    kpos = torch.zeros(NS, dtype=torch.int32, device="cuda"); rowtok = torch.zeros(NS, dtype=torch.int32, device="cuda")
+    tiles = torch.zeros((cap, 3), dtype=torch.int32, device="cuda"); counts = torch.zeros(2, dtype=torch.int32, device="cuda")
+    qmm.moe_sort(ids, T, NE, n_exp, qmm.MOE_TILE_ROWS, kpos, rowtok, tiles, counts)
+    h = torch.zeros((NS, F), dtype=torch.bfloat16, device="cuda")
+    qmm.moe_gemm_gate_up_bf16(synth.Q4_K, synth.Q4_K, Wg, Sg, Wu, Su, Wg_h[0].nbytes, tiles, counts, cap, rowtok, bf16_dev(x_bits),
+                              h, F, H)
+    dn = torch.zeros((NS, H), device="cuda")
+    qmm.moe_gemm_bf16(synth.Q4_K, synth.Q4_K, Wd, Sd, Wd_h[0].nbytes, tiles, counts, cap, None, h, dn, H, F)
+    y = torch.zeros((T, H), device="cuda")
+    qmm.moe_combine_sorted(dn, w, kpos, y, T, NE, H)
+    toks = np.arange(T, dtype=np.int32)
+    y_ref = oracle.moe_prefill_tokens(synth.Q4_K, Wg_h, Wu_h, Wd_h, Sg_h, Su_h, Sd_h, x_bits, host(ids), host(w), H, F, toks)
+    err = rel_l2(host(y), y_ref)
+    print(f"MoE prefill T={T} E={n_exp}: every token rel-L2 {err:.2e}, tiles {host(counts).tolist()}", flush=True)
     assert err <= 2e-3
