@@ -50,7 +50,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-extra", action="store_true", help="skip the other BASELINE configurations")
     p.add_argument("--only-extra", choices=["activation_producers", "formats", "router", "dense_decode", "moe_decode", "moe_prefill",
-                                            "dense_prefill"],
+                                            "dense_prefill", "moe_uniform"],
                    default=None,
                    help="only run one of the extra measurements and print its JSON (for profiling it alone)")
     p.add_argument("--roofs", action="store_true",
@@ -485,6 +485,24 @@ def extra_cfg4(torch, tb):
     return out
 
 
+def extra_moe_uniform(torch):
+    """The gate/up grouped GEMM (with silu) on uniform 128-row tiles: 16 Q4_K experts of 1,280 rows each
+    (160 tiles), K = 2048, N = 2 x 512 -- the full-tile case of config 4 on its own, four launches."""
+    from hipster_amd import qmm, synth
+    H, F, T = 2048, 512, 2048
+    Wg = torch.from_numpy(synth.experts(5, synth.Q4_K, 16, F, H)).cuda()
+    Wu = torch.from_numpy(synth.experts(6, synth.Q4_K, 16, F, H)).cuda()
+    x = torch.randn((T, H), device="cuda").to(torch.bfloat16)
+    tiles = torch.tensor([[i // 10, 128 * i, 128] for i in range(160)], dtype=torch.int32, device="cuda")
+    counts = torch.tensor([160, 0], dtype=torch.int32, device="cuda")
+    rowtab = (torch.arange(20480, dtype=torch.int32, device="cuda") % T).contiguous()
+    h = torch.zeros((20480, F), dtype=torch.bfloat16, device="cuda")
+    gu = lambda: qmm.moe_gemm_gate_up_bf16(0, 0, Wg, Wg[0], Wu, Wu[0], Wg[0].numel(), tiles, counts, 160, rowtab, x, h, F, H)
+    us = graph_us(torch, [gu], reps=4)
+    flop = 2 * 20480 * 1024 * 2048
+    return {"gate_up_us": round(us, 1), "TFLOPS": round(flop / us / 1e6, 1), "tiles": 160, "rows_per_tile": 128}
+
+
 def host_threads():
     """All host cores this process may use, capped by the box's CPU share (OMP_NUM_THREADS, at most 16)."""
     try:
@@ -591,7 +609,7 @@ def main():
     if args.only_extra:
         fn = {"activation_producers": extra_act, "formats": extra_formats, "router": extra_router, "dense_decode": extra_cfg1,
               "moe_decode": lambda t: extra_cfg2(t, moe_tables(t)), "moe_prefill": lambda t: extra_cfg4(t, moe_tables(t)),
-              "dense_prefill": extra_cfg3}[args.only_extra]
+              "dense_prefill": extra_cfg3, "moe_uniform": extra_moe_uniform}[args.only_extra]
         print(json.dumps({args.only_extra: fn(torch)}), flush=True)
         return
     from hipster_amd import _lib
