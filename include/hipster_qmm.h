@@ -170,11 +170,12 @@ int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream
  * tpr in {0,1,2,4,8,16,32} and rpt in {0,1,2,3} for compatibility. */
 int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, int tpr, int rpt, void* stream);
 /* several weights sharing x (reference: gemv_multi, gemv.h:28, gemv.hip:1355-1369); up to 4
- * segments, all with the same K, any ncol.  When every segment is Q4_K all segments run in one launch:
- * per 16 columns on the int8 matrix cores from 4 columns on (the knob below), else per 8 columns on the
- * dot4 kernel; other formats run one launch per segment and 8 columns.  Results are bitwise those of qmm_gemv_q8 on each segment, and a Q4_K column's bits do
- * not depend on ncol (the matrix-core kernel adds the same values in the same order as the
- * one-column kernel). */
+ * segments, all with the same K, any ncol.  Each run of consecutive segments of one format is one launch
+ * per column pass (the grouping of the reference's gemv_wmma, gemv.hip:1313-1317): Q4_K per 16 columns
+ * on the int8 matrix cores from 4 columns on (the knob below), else per 8 columns on the dot4 kernel;
+ * Q5_K, IQ4_XS, Q8_0_SOA and Q5_1_SOA per 8 columns; Q6_K (both layouts) one launch per segment.
+ * Results are bitwise those of qmm_gemv_q8 on each segment, and a Q4_K column's bits do not depend on
+ * ncol (the matrix-core kernel adds the same values in the same order as the one-column kernel). */
 int qmm_gemv_multi(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int ncol, void* stream);
 /* Tuning knob (no reference counterpart, like the reference's bench knobs): Q4_K GEMV calls with at
  * least n columns use the matrix-core kernel (default 4; n > 16 keeps every call on the dot4
