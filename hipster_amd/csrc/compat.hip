@@ -501,7 +501,11 @@ int qmm_moe_gemm_q8(int fmt, int shared_fmt, const void* W, const void* Wsh, siz
     // Q4_K tile lists run on the int8 matrix cores (routed and shared tiles in one launch when both are
     // Q4_K); the other formats on the q8 GEMV units
     const bool mr = fmt == QMM_Q4_K, ms = nstiles > 0 && shared_fmt == QMM_Q4_K;
-    if (mr || ms) {
+    if (mr && ms && ntiles + nstiles > 65535) {              // one grid row per tile: two launches
+        int rc = launch_moe_q8_q4k(W, Wsh, ebytes, tiles, ntiles, stiles, 0, ct, rowtab, x, y, N, K, s);
+        if (rc == QMM_OK) rc = launch_moe_q8_q4k(W, Wsh, ebytes, tiles, 0, stiles, nstiles, ct, rowtab, x, y, N, K, s);
+        if (rc != QMM_OK) return rc;
+    } else if (mr || ms) {
         const int rc = launch_moe_q8_q4k(W, Wsh, ebytes, tiles, mr ? ntiles : 0, stiles, ms ? nstiles : 0, ct, rowtab, x, y, N, K, s);
         if (rc != QMM_OK) return rc;
     }

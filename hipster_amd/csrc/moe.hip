@@ -660,17 +660,22 @@ int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const
         nexp > kMaxSlots)
         return QMM_ERR_SHAPE;
     if (T > 64) return QMM_ERR_SHAPE;   // at most 64 columns (tokens) per expert in the dedup list
-    for (int g = 0; g < nseg; ++g)
-        if (!a->w[g] || !a->shared[g] || !a->y[g]) return QMM_ERR_NULL;
+    // a caller without a shared expert (the reference's bench_gemv gather) passes NULL shared matrices;
+    // in the routed format a negative id then reads expert 0, so no slot reads through NULL
+    qmm_moe_segs sg = *a;
+    for (int g = 0; g < nseg; ++g) {
+        if (!sg.shared[g] && shared_fmt == fmt) sg.shared[g] = sg.w[g];
+        if (!sg.w[g] || !sg.shared[g] || !sg.y[g]) return QMM_ERR_NULL;
+    }
     if (T == 0) return QMM_OK;
     hipStream_t s = (hipStream_t)stream;
-    if (a->slotw && nseg != 1) return QMM_ERR_ARG;
-    if (fmt != QMM_Q4_K || shared_fmt != QMM_Q4_K) return moe_fmt_dispatch(fmt, shared_fmt, a, nseg, ids, nexp, x, N, K, T, xrow_te, s);
-    if (a->slotw) {
-        return moe_lpr(K) == 8 ? launch_down<8>(*a, ids, nexp, x, N, K, T, s) : launch_down<16>(*a, ids, nexp, x, N, K, T, s);
+    if (sg.slotw && nseg != 1) return QMM_ERR_ARG;
+    if (fmt != QMM_Q4_K || shared_fmt != QMM_Q4_K) return moe_fmt_dispatch(fmt, shared_fmt, &sg, nseg, ids, nexp, x, N, K, T, xrow_te, s);
+    if (sg.slotw) {
+        return moe_lpr(K) == 8 ? launch_down<8>(sg, ids, nexp, x, N, K, T, s) : launch_down<16>(sg, ids, nexp, x, N, K, T, s);
     }
-    return moe_lpr(K) == 8 ? launch_gather<8>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s)
-                           : launch_gather<16>(*a, nseg, ids, nexp, x, N, K, T, xrow_te, s);
+    return moe_lpr(K) == 8 ? launch_gather<8>(sg, nseg, ids, nexp, x, N, K, T, xrow_te, s)
+                           : launch_gather<16>(sg, nseg, ids, nexp, x, N, K, T, xrow_te, s);
 }
 
 int qmm_moe_decode(int fmt, const void* Wg, const void* Wu, const void* Wd, size_t ebytes_gu, size_t ebytes_d, const void* Sg,

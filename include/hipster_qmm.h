@@ -246,7 +246,8 @@ int qmm_moe_router(const float* Wr, const float* x, float* logits, int* ids, flo
  * y[t][N] = sum_e slotw[te] * (W[ids[te]] . x[te]) summed in slot order (down + combine).
  * Formats as the reference's (gemv.hip:1386-1392): routed fmt Q4_K, Q5_K, IQ4_XS, Q8_0_SOA or Q5_1_SOA,
  * shared_fmt = fmt or Q8_0_SOA; K as for qmm_gemv_q8 (so the engine's K = 640 down projection runs
- * in the 32-weight formats); all-Q4_K also needs K <= 6144.  nexp <= 16; T <= 64.  Every slot's rows
+ * in the 32-weight formats); all-Q4_K also needs K <= 6144.  nexp <= 16; T <= 64.  a->shared[g] may be
+ * NULL when shared_fmt = fmt (a caller without a shared expert): negative ids then read expert 0.  Every slot's rows
  * are bitwise the plain GEMV of its expert, except Q4_K routed experts beside a Q8_0_SOA shared expert
  * (a different, equally exact, Q4_K decode). */
 int qmm_gemv_moe(int fmt, int shared_fmt, const qmm_moe_segs* a, int nseg, const int* ids, int nexp, qmm_xq8 x,

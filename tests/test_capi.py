@@ -133,6 +133,12 @@ def test_moe_argument_validation_without_device_work():
     assert L.qmm_gemv_moe(_lib.QMM_Q6_K_SOA, _lib.QMM_Q6_K_SOA, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 512, 1, 0, None) == -1
     assert L.qmm_gemv_moe(_lib.QMM_Q5_1_SOA, _lib.QMM_Q8_0_SOA, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 608, 1, 0, None) == -2
     assert L.qmm_gemv_moe(_lib.QMM_Q5_K, _lib.QMM_Q5_K, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 640, 1, 0, None) == -2
+    # no shared expert (NULL): accepted in the routed format (negative ids read expert 0), refused beside
+    # a Q8_0_SOA shared format; T = 0 runs nothing
+    segs.slotw = None
+    segs.shared[0] = None
+    assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q4_K, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 2048, 0, 0, None) == 0
+    assert L.qmm_gemv_moe(_lib.QMM_Q4_K, _lib.QMM_Q8_0_SOA, ctypes.byref(segs), 1, d, 11, _xq(16), 512, 2048, 0, 0, None) == -3
     assert L.qmm_moe_silu_quant(d, d, _xq(16), 4, 100, None) == -2
     assert L.qmm_moe_combine_sorted(d, d, None, d, 4, 11, 2048, None) == -3
 

@@ -108,6 +108,31 @@ def test_moe_gemm_q8(gpu, fmt, sfmt, N, K, T, n_exp, ct):
             assert max_rel_mag(got[sel], ref, mag) < TOL, (gather, e)
 
 
+def test_moe_gemm_q8_many_tiles(gpu):
+    """65535 routed + 2 shared Q4_K tiles: more grid rows than one launch holds, so the routed and
+    shared lists go in two launches; every row still matches its expert's q8 GEMV"""
+    N, K, T, ntl, nst = 64, 256, 8, 65535, 2
+    print(f"moe_gemm many tiles N={N} K={K} tiles={ntl}+{nst}", flush=True)
+    E = synth.experts(540, synth.Q4_K, 2, N, K)
+    S = synth.matrix(541, synth.Q4_K, N, K)
+    NS = ntl + nst
+    tl = np.stack([np.arange(ntl) % 2, np.arange(ntl), np.ones(ntl)], 1).astype(np.int32)
+    st = np.stack([np.full(nst, -1), ntl + np.arange(nst), np.ones(nst)], 1).astype(np.int32)
+    rowtab = (np.arange(NS) % T).astype(np.int32)
+    x = synth.normal_f32(542, (T, K))
+    y = torch.full((NS, N), np.nan, dtype=torch.float32, device="cuda")
+    eb = E.shape[1] if E.ndim == 2 else E[0].nbytes
+    qmm.moe_gemm(synth.Q4_K, synth.Q4_K, dev(E), dev(S), eb, dev(tl), ntl, dev(st), nst, 1, dev(rowtab),
+                 q8(x), y, N, K)
+    got = host(y)
+    xr = q8_dequant(x)
+    eid = np.concatenate([tl[:, 0], st[:, 0]])
+    for e in (-1, 0, 1):
+        sel = np.nonzero(eid == e)[0]
+        ref, mag = oracle.gemv_ref(synth.Q4_K, S if e < 0 else E[e], N, K, xr)
+        assert max_rel_mag(got[sel], ref[rowtab[sel]], mag[rowtab[sel]]) < TOL, e
+
+
 @pytest.mark.parametrize("ncol,K", [(1, 256), (5, 5120), (16, 2048)])
 def test_quantize_x_q8k_bit_exact(gpu, ncol, K):
     x = synth.normal_f32(530 + K, (ncol, K))

@@ -1,8 +1,8 @@
 """GPU end of the load path: weights written into a (sharded) GGUF v3 file, opened with the library's
 reader, put in the kernels' layout at load (the reference's to_lin, qwen4exp.cpp:34-65), uploaded and run
 through the decode GEMV, against the oracle on the same prepared weights (1e-5, the GEMV bar); and the
-reference's own MoE kernel validator (engine/bench/bench_moe.cpp, built by oracle/refpatch.py against
-this library) run on a synthetic GGUF expert tensor, its OK / MISMATCH verdict asserted."""
+reference's own kernel validators (engine/bench/bench_moe.cpp and bench_gemv.cpp, built by oracle/refpatch.py
+against this library) run on synthetic GGUF expert tensors, their OK / MISMATCH verdicts asserted."""
 import os
 import re
 import subprocess
@@ -88,3 +88,32 @@ def test_reference_bench_moe_validates(gpu, tmp_path, fmt, gt):
     assert r.returncode == 0
     lines = [ln for ln in r.stdout.splitlines() if "CT=" in ln]
     assert len(lines) == 3 and all(re.search(r"maxrel \S+ OK", ln) for ln in lines), lines
+
+
+BENCH_GEMV = os.path.join(ROOT, "oracle", "_ref", "bench_gemv")
+GEMV_LINE = re.compile(r"ncol=(\d+) tpr=\s*(\d+) rpt=(\d+): .* err_vs_ref=(\S+) (OK|MISMATCH)")
+
+
+@pytest.mark.skipif(not os.path.exists(BENCH_GEMV), reason="reference validator not built (needs the reference checkout)")
+@pytest.mark.parametrize("fmt,gt", [(synth.Q8_0, gguf.GType.Q8_0), (synth.Q5_1, gguf.GType.Q5_1)])
+def test_reference_bench_gemv_validates(gpu, tmp_path, fmt, gt):
+    """engine/bench/bench_gemv.cpp as the reference wrote it, on an expert tensor of the engine's K = 640
+    (rows repacked to SoA by the validator itself): every tpr / rpt configuration it runs at 1..8 columns
+    through gemv_q8, each checked on 64 sampled rows against its own CPU dequant . x (OK below 1e-5), then
+    its decode gather (gemv_moe, x rows per slot) timed.  The validator stops at the first call the
+    library refuses, so the count of lines is asserted too."""
+    E, N, K = 8, 512, 640
+    W = synth.blocks(synth.rng(630 + fmt), fmt, E * N * K // synth.BLOCK[fmt][0])
+    p = str(tmp_path / "e.gguf")
+    write_gguf(p, [("blk.0.ffn_down_exps.weight", gt, (K, N, E), W)])
+    print(f"bench_gemv fmt={fmt}", flush=True)
+    r = subprocess.run([BENCH_GEMV, p, "blk.0.ffn_down_exps.weight", "8", "q8"], capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    got = [GEMV_LINE.search(ln) for ln in r.stdout.splitlines() if "err_vs_ref" in ln]
+    # K % 256 != 0: the 3xx configurations are skipped; ncol 1 runs tpr 32..1 and 8/4 with rpt 3,
+    # ncol 2, 3, 4, 8 run tpr 32 and 4 and 4 with rpt 3
+    assert len(got) == 8 + 4 * 3 and all(got), r.stdout
+    assert all(m.group(5) == "OK" for m in got), r.stdout
+    assert "moe tpr= 1:" in r.stdout
