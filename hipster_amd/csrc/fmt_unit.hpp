@@ -274,18 +274,95 @@ template <> struct FmtUnit<QMM_Q6_K_SOA> {            // row = [ql K/2][qh K/4][
     }
 };
 
+// ---- where a unit's weight bytes are: the loaders of fmt_rows ----
+// FmtRowLoad: row `row` at W + row * rb in the format's own layout (every GEMV of the library).
+template <int F>
+struct FmtRowLoad {
+    static __device__ __forceinline__ void load(const uint8_t* W, int row, size_t rb, int K, int u, typename FmtUnit<F>::Raw& r) {
+        FmtUnit<F>::load(W + (size_t)row * rb, K, u, r);
+    }
+};
+// FmtIl8Load (Q4_K, Q5_K, IQ4_XS): the 8-row interleaved layout of the reference's layout experiment
+// (repack_interleave8, engine/kernels/gemv.hip:1442-1446): rows in groups of 8, a group's blocks
+// stored block-major, so block b of row r is block (r / 8) * 8 * nb + 8 b + r % 8 of W.  A block's own
+// bytes are unchanged: the format's load of unit u % (units per block) on that one block.
+template <int F>
+struct FmtIl8Load {
+    static __device__ __forceinline__ void load(const uint8_t* W, int row, size_t, int K, int u, typename FmtUnit<F>::Raw& r) {
+        static_assert(F == QMM_Q4_K || F == QMM_Q5_K || F == QMM_IQ4_XS, "block formats only");
+        constexpr int BB = F == QMM_Q4_K ? 144 : F == QMM_Q5_K ? 176 : 136, UPB = 256 / fmt_unit_weights<F>();
+        const int nb = K >> 8;
+        const uint8_t* blk = W + ((size_t)(row >> 3) * 8 * nb + (size_t)(u / UPB) * 8 + (row & 7)) * BB;
+        FmtUnit<F>::load(blk, 256, u % UPB, r);
+    }
+};
+// FmtIl16Load: the 16-row interleaved layout of the reference's matrix-core GEMV experiment
+// (repack_wmma_il, gemv.hip:1277-1303): rows in groups of 16 (the last padded with zero rows); per group
+// and 256-weight block, 16 x BB bytes G = W + ((row / 16) * nb + b) * 16 * BB hold the 16 rows' bytes
+// piece-major: 16-byte piece i of row r16 at G + 256 i + 16 r16 (IQ4_XS: 8-byte pieces at
+// G + 128 i + 8 r16; Q6_K_SOA: ql pieces 0..7, qh pieces at G + 2048, the 16 scale bytes at G + 3072, d at
+// G + 3328 + 2 r16; Q8_0_SOA: q pieces 0..15, the 8 sub-block d at G + 4096 + 16 r16).  Piece numbers are
+// the byte offsets in the row's own layout / 16.
+template <int F>
+struct FmtIl16Load {
+    static __device__ __forceinline__ size_t group(int row, int K, int b, int BB) {
+        return ((size_t)(row >> 4) * (K >> 8) + b) * 16 * BB;
+    }
+    static __device__ __forceinline__ void load(const uint8_t* W, int row, size_t, int K, int u, typename FmtUnit<F>::Raw& r) {
+        const int r16 = row & 15;
+        if constexpr (F == QMM_Q4_K) {                 // hd = piece 0, pair j: qs pieces 1 + 2j, 2 + 2j
+            const uint8_t* g = W + group(row, K, u >> 2, 144) + 16 * r16;
+            const int j = u & 3;
+            r.hd = ld16(g);
+            r.q0 = ld16(g + 256 * (1 + 2 * j));
+            r.q1 = ld16(g + 256 * (2 + 2 * j));
+        } else if constexpr (F == QMM_Q5_K) {          // hd, qh halves = pieces 0..2, pair j: 3 + 2j, 4 + 2j
+            const uint8_t* g = W + group(row, K, u >> 2, 176) + 16 * r16;
+            const int j = u & 3;
+            r.hd = ld16(g);
+            r.h0 = ld16(g + 256);
+            r.h1 = ld16(g + 512);
+            r.q0 = ld16(g + 256 * (3 + 2 * j));
+            r.q1 = ld16(g + 256 * (4 + 2 * j));
+        } else if constexpr (F == QMM_IQ4_XS) {        // 8-byte pieces: header 0, sub-block k: 1 + 2k, 2 + 2k
+            const uint8_t* g = W + group(row, K, u >> 3, 136) + 8 * r16;
+            const int k = u & 7;
+            r.hd = *(const uint2*)g;
+            const uint2 lo = *(const uint2*)(g + 128 * (1 + 2 * k)), hi = *(const uint2*)(g + 128 * (2 + 2 * k));
+            r.qs = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        } else if constexpr (F == QMM_Q6_K_SOA) {      // quarter (n, lh): ql pieces 4n + lh, + 2; qh 2n + lh
+            const uint8_t* g = W + group(row, K, u >> 2, 210);
+            const int n = (u >> 1) & 1, lh = u & 1;
+            r.a = ld16(g + 256 * (4 * n + lh) + 16 * r16);
+            r.b = ld16(g + 256 * (4 * n + lh + 2) + 16 * r16);
+            r.h = ld16(g + 2048 + 256 * (2 * n + lh) + 16 * r16);
+            const uint2 sc = *(const uint2*)(g + 3072 + 16 * r16 + 8 * n);
+            r.sc0 = sc.x;
+            r.sc1 = sc.y;
+            r.d = h2f(*(const uint16_t*)(g + 3328 + 2 * r16));
+        } else {                                       // Q8_0_SOA, sub-block s: q pieces 2s, 2s + 1
+            static_assert(F == QMM_Q8_0_SOA, "no 16-row interleaved layout for this format");
+            const uint8_t* g = W + group(row, K, u >> 3, 272);
+            const int sb = u & 7;
+            r.a = ld16(g + 256 * (2 * sb) + 16 * r16);
+            r.b = ld16(g + 256 * (2 * sb + 1) + 16 * r16);
+            r.d = *(const uint16_t*)(g + 4096 + 16 * r16 + 2 * sb);
+        }
+    }
+};
+
 // Lane-partial sums of RPW rows (row0..row0+RPW-1, clamped to N) x NCOL columns over units
 // [ub, ue): lane l takes units ub + l, ub + l + 64, ..., NIT at a time, every load of a pass issued
 // before its arithmetic.  xs[c] is column c's activation source; acc[r][c] is the lane's partial
 // (the caller reduces over the wave).  Rows of format F start rb bytes apart (0 = the format's own
-// row size for K).  pre() runs once, after the first pass's weight loads are issued and before its x
-// is read (a caller that stages x in LDS finishes the staging there, so its weights are already in
-// flight); FmtNoPre does nothing.
+// row size for K) unless the loader LD places them otherwise.  pre() runs once, after the first pass's
+// weight loads are issued and before its x is read (a caller that stages x in LDS finishes the staging
+// there, so its weights are already in flight); FmtNoPre does nothing.
 struct FmtNoPre {
     static constexpr bool active = false;
     __device__ __forceinline__ void operator()() const {}
 };
-template <int F, int NCOL, int NIT, int RPW, class XS, class Pre = FmtNoPre>
+template <int F, int NCOL, int NIT, int RPW, class XS, class Pre = FmtNoPre, class LD = FmtRowLoad<F>>
 __device__ __forceinline__ void fmt_rows(const uint8_t* __restrict__ W, int row0, int N, int K, const XS (&xs)[NCOL],
                                          float (&acc)[RPW][NCOL], int ub, int ue, size_t rb = 0, const Pre& pre = Pre()) {
 #pragma clang fp contract(off)
@@ -302,7 +379,7 @@ __device__ __forceinline__ void fmt_rows(const uint8_t* __restrict__ W, int row0
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
-            for (int i = 0; i < NIT; ++i) FU::load(W + (size_t)min(row0 + r, N - 1) * rb, K, min(base + lane + 64 * i, ue - 1), R[r][i]);
+            for (int i = 0; i < NIT; ++i) LD::load(W, min(row0 + r, N - 1), rb, K, min(base + lane + 64 * i, ue - 1), R[r][i]);
         if constexpr (Pre::active) {
             if (base == ub) {
                 __builtin_amdgcn_sched_barrier(0);

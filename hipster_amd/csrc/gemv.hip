@@ -1065,19 +1065,29 @@ int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int n
     if (!fmt_supported_q8(fmt)) return QMM_ERR_FORMAT;
     if (!W || !x.q || !x.d || !x.s || !y) return QMM_ERR_NULL;
     if (int e = check_gemv_shape(fmt, N, K)) return e;
+    // rpt 5 and rpt 4 with tpr 3 read the reference's experimental interleaved weight layouts
+    // (repack_interleave8, gemv.hip:1467-1472; repack_wmma_il, gemv_wmma mode 3)
+    if (rpt == 5) {
+        if (fmt != QMM_Q4_K && fmt != QMM_Q5_K && fmt != QMM_IQ4_XS) return QMM_ERR_FORMAT;
+        if (N % 8 != 0 || ncol < 1 || ncol > 8) return QMM_ERR_SHAPE;
+        return gemv_il_dispatch(8, fmt, W, x, y, N, K, ncol, (hipStream_t)stream);
+    }
+    if (rpt == 4 && tpr == 3) {
+        if (fmt != QMM_Q4_K && fmt != QMM_Q5_K && fmt != QMM_IQ4_XS && fmt != QMM_Q6_K_SOA && fmt != QMM_Q8_0_SOA)
+            return QMM_ERR_FORMAT;
+        if (K % 256 != 0 || ncol < 1 || ncol > 16) return QMM_ERR_SHAPE;
+        return gemv_il_dispatch(16, fmt, W, x, y, N, K, ncol, (hipStream_t)stream);
+    }
     // rpt 4 is the reference's route to its T-invariant WMMA GEMV (gemv.hip:1472-1475, up to 16
-    // columns), which every GEMV here already is; rpt 5 and rpt 4 with tpr 3 read its experimental
-    // interleaved weight layouts (repack_interleave8 / repack_wmma_il), which this library does not
-    // read: QMM_ERR_LAYOUT
-    if (rpt == 5 || (rpt == 4 && tpr == 3)) return QMM_ERR_LAYOUT;
+    // columns), which every GEMV here already is
     if (rpt == 4) {
         if (ncol < 1 || ncol > 16) return QMM_ERR_SHAPE;
         const qmm_gemv_seg seg = {fmt, W, y, N, K};
         return qmm_gemv_multi(&seg, 1, x, ncol, stream);
     }
+    // any other tpr / rpt: the reference's launch-shape knobs (its unlisted values fall to a default
+    // kernel, gemv.hip:1236-1242); the launch shape here follows the tensor shape
     if (ncol < 1 || ncol > 8) return QMM_ERR_SHAPE;
-    if (!(tpr == 0 || tpr == 1 || tpr == 2 || tpr == 4 || tpr == 8 || tpr == 16 || tpr == 32)) return QMM_ERR_ARG;
-    if (rpt < 0 || rpt > 3) return QMM_ERR_ARG;
     return gemv_q8_dispatch(fmt, W, x, y, N, K, ncol, (hipStream_t)stream);
 }
 
@@ -1106,7 +1116,7 @@ int qmm_gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int
     if (!W || !x || !y) return QMM_ERR_NULL;
     if (int e = check_gemv_shape(QMM_Q4_K, N, K)) return e;
     if (ncol < 1 || ncol > 8) return QMM_ERR_SHAPE;
-    if (!(tpr == 0 || tpr == 4 || tpr == 8 || tpr == 16 || tpr == 32)) return QMM_ERR_ARG;
+    (void)tpr;   // the reference's threads per row (its other values take its default, gemv.hip:1486-1489)
     hipStream_t s = (hipStream_t)stream;
     // pair kernel: columns in launches of at most g (what fits the LDS budget); every column gets
     // the same arithmetic whatever ncol is

@@ -123,6 +123,60 @@ __global__ void __launch_bounds__(kFmtBlock) k_gemv_fmt(FSegs sg, const int8_t* 
     }
 }
 
+// ---- the reference's interleaved weight layouts (its gemv_q8 rpt 5, and rpt 4 with tpr 3) ----
+// The format's own per-row arithmetic (fmt_rows), the loads placed by the layout's loader LD: two rows
+// per wave, x from global memory, NCOL columns per launch.
+template <int F, class LD, int NCOL>
+__global__ void __launch_bounds__(kFmtBlock) k_gemv_il(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                       const float* __restrict__ xd, const float* __restrict__ xs,
+                                                       float* __restrict__ y, int N, int K) {
+    constexpr int RPW = 2, NIT = 2;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = ((int)blockIdx.x * kFmtWaves + wave) * RPW;
+    const int nsb = K / 32;
+    XSrcQ8 xsrc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) xsrc[c] = XSrcQ8{xq + (size_t)c * K, xd + (size_t)c * nsb, xs + (size_t)c * nsb};
+    float acc[RPW][NCOL];
+    fmt_rows<F, NCOL, NIT, RPW, XSrcQ8, FmtNoPre, LD>(W, row0, N, K, xsrc, acc, 0, fmt_units<F>(K));
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) acc[r][c] = wave_sum(acc[r][c]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+            if (row0 + r < N) {
+#pragma unroll
+                for (int c = 0; c < NCOL; ++c) y[(size_t)c * N + row0 + r] = acc[r][c];
+            }
+    }
+}
+
+// columns in launches of 8, then 4, then the 1..3 left
+template <int F, class LD>
+int launch_il(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    const dim3 grid((unsigned)((N + kFmtWaves * 2 - 1) / (kFmtWaves * 2)));
+    const int nsb = K / 32;
+    for (int c0 = 0; c0 < ncol;) {
+        const int left = ncol - c0, nc = left >= 8 ? 8 : left >= 4 ? 4 : left;
+        const uint8_t* w = (const uint8_t*)W;
+        const int8_t* q = x.q + (size_t)c0 * K;
+        const float *d = x.d + (size_t)c0 * nsb, *sm = x.s + (size_t)c0 * nsb;
+        float* yc = y + (size_t)c0 * N;
+        switch (nc) {
+            case 1: hipLaunchKernelGGL((k_gemv_il<F, LD, 1>), grid, dim3(kFmtBlock), 0, s, w, q, d, sm, yc, N, K); break;
+            case 2: hipLaunchKernelGGL((k_gemv_il<F, LD, 2>), grid, dim3(kFmtBlock), 0, s, w, q, d, sm, yc, N, K); break;
+            case 3: hipLaunchKernelGGL((k_gemv_il<F, LD, 3>), grid, dim3(kFmtBlock), 0, s, w, q, d, sm, yc, N, K); break;
+            case 4: hipLaunchKernelGGL((k_gemv_il<F, LD, 4>), grid, dim3(kFmtBlock), 0, s, w, q, d, sm, yc, N, K); break;
+            default: hipLaunchKernelGGL((k_gemv_il<F, LD, 8>), grid, dim3(kFmtBlock), 0, s, w, q, d, sm, yc, N, K); break;
+        }
+        QMM_LAUNCH_CHECK();
+        c0 += nc;
+    }
+    return QMM_OK;
+}
+
 // ---- MoE decode for the formats above (reference: gemv_moe, gemv.h:44, gemv.hip:1385-1394) ----
 // Routed experts in format F, the shared expert in FS (F, or Q8_0_SOA as the reference allows).  A
 // slot's rows are computed by fmt_rows like the plain GEMV of its expert (same per-row order, so
@@ -317,6 +371,27 @@ int gemv_fmt_dispatch_segs(int fmt, const qmm_gemv_seg* segs, int nseg, qmm_xq8 
 int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
     const qmm_gemv_seg seg = {fmt, W, y, N, K};
     return gemv_fmt_dispatch_segs(fmt, &seg, 1, x, K, ncol, s);
+}
+
+// rows interleaved by 8 (rows = 8: Q4_K, Q5_K, IQ4_XS) or 16 (rows = 16: also Q6_K_SOA, Q8_0_SOA); shapes
+// checked by the caller (K % 256 == 0; N % 8 == 0 for 8)
+int gemv_il_dispatch(int rows, int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    if (rows == 8) {
+        switch (fmt) {
+            case QMM_Q4_K: return launch_il<QMM_Q4_K, FmtIl8Load<QMM_Q4_K>>(W, x, y, N, K, ncol, s);
+            case QMM_Q5_K: return launch_il<QMM_Q5_K, FmtIl8Load<QMM_Q5_K>>(W, x, y, N, K, ncol, s);
+            case QMM_IQ4_XS: return launch_il<QMM_IQ4_XS, FmtIl8Load<QMM_IQ4_XS>>(W, x, y, N, K, ncol, s);
+            default: return QMM_ERR_FORMAT;
+        }
+    }
+    switch (fmt) {
+        case QMM_Q4_K: return launch_il<QMM_Q4_K, FmtIl16Load<QMM_Q4_K>>(W, x, y, N, K, ncol, s);
+        case QMM_Q5_K: return launch_il<QMM_Q5_K, FmtIl16Load<QMM_Q5_K>>(W, x, y, N, K, ncol, s);
+        case QMM_IQ4_XS: return launch_il<QMM_IQ4_XS, FmtIl16Load<QMM_IQ4_XS>>(W, x, y, N, K, ncol, s);
+        case QMM_Q6_K_SOA: return launch_il<QMM_Q6_K_SOA, FmtIl16Load<QMM_Q6_K_SOA>>(W, x, y, N, K, ncol, s);
+        case QMM_Q8_0_SOA: return launch_il<QMM_Q8_0_SOA, FmtIl16Load<QMM_Q8_0_SOA>>(W, x, y, N, K, ncol, s);
+        default: return QMM_ERR_FORMAT;
+    }
 }
 
 // routed format fmt, shared format sfmt (fmt, or Q8_0_SOA); fmt may be Q4_K only with a Q8_0_SOA

@@ -260,6 +260,7 @@ inline int device_cu_count() {
 int launch_q4k_rows_gemm(const void* W, const uint16_t* A, float* D, int M, int N, int K, int ldd, int trows, hipStream_t s);
 // q8 GEMV of gemv_fmt.hip for QMM_Q5_K, QMM_IQ4_XS, QMM_Q8_0_SOA, QMM_Q5_1_SOA (ncol 1..8, K % 256 == 0)
 int gemv_fmt_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s);
+int gemv_il_dispatch(int rows, int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s);
 int gemv_fmt_dispatch_segs(int fmt, const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol, hipStream_t s);
 // prefill grouped GEMM (qmm_moe_gemm_bf16) for the formats other than all-Q4_K (moe_gemm_fmt.hip)
 int launch_moe_gemm_fmt(int fmt, int sfmt, const void* W, const void* Wsh, size_t ebytes, const qmm_moe_tile* tiles,

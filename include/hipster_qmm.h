@@ -35,8 +35,8 @@ enum {
     QMM_ERR_LAUNCH = -4,    /* the HIP runtime rejected the launch */
     QMM_ERR_WORKSPACE = -5, /* workspace missing or too small */
     QMM_ERR_ARG = -6,       /* other invalid argument (mode, tpr, alignment, ...) */
-    QMM_ERR_LAYOUT = -7,    /* a weight layout this library does not read (the reference's experimental
-                               interleaved layouts) */
+    QMM_ERR_LAYOUT = -7,    /* a weight layout this library does not read (kept for the ABI: every layout
+                               of the reference's call surface is read now) */
     QMM_ERR_IO = -8,        /* a GGUF file is missing, truncated, not GGUF v3 or has a tensor past its end */
     QMM_ERR_NOT_FOUND = -9, /* no tensor / key of that name in the GGUF */
     QMM_ERR_UNSUPPORTED = -10 /* an entry point of the reference's call surface that lies off the quantized
@@ -147,15 +147,14 @@ int qmm_repack_row_q5_1(const uint8_t* src, uint8_t* dst, int K);
 int qmm_repack_row_q5_0(const uint8_t* src, uint8_t* dst, int K);
 /* the reference's experimental 8-row block interleave (reference: repack_interleave8, gemv.h:21,
  * gemv.hip:1442-1447): block b of row r moves to ((r/8)*8*nb + b*8 + r%8) blocks; fmt Q4_K, Q5_K or
- * IQ4_XS, N % 8 == 0, K % 256 == 0.  Host only; the GEMVs here do not read this layout
- * (qmm_gemv_q8 with rpt 5 returns QMM_ERR_LAYOUT). */
+ * IQ4_XS, N % 8 == 0, K % 256 == 0.  Host only; qmm_gemv_q8 with rpt 5 reads this layout. */
 int qmm_repack_interleave8(int fmt, const uint8_t* src, uint8_t* dst, int N, int K);
 /* bytes of the reference's 16-row chunk-major layout (reference: wmma_il_bytes, gemv.h:37,
  * gemv.hip:1280): ceil(N/16) * (K/256) * 16 * block bytes (Q4_K 144, Q5_K 176, IQ4_XS 136, Q6_K_SOA 210,
  * Q8_0_SOA 272); 0 for other formats or K % 256 != 0 */
 size_t qmm_wmma_il_bytes(int fmt, int N, int K);
 /* that layout (reference: repack_wmma_il, gemv.h:38, gemv.hip:1281-1303), byte for byte; host only
- * (qmm_gemv_q8 with rpt 4, tpr 3 returns QMM_ERR_LAYOUT) */
+ * (qmm_gemv_q8 with rpt 4, tpr 3 reads it) */
 int qmm_repack_wmma_il(int fmt, const uint8_t* src, uint8_t* dst, int N, int K);
 
 /* ---- activation quantiser (reference: quantize_x_q8, gemv.h:10, gemv.hip:36-51,1333-1336) ----
@@ -166,8 +165,11 @@ int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream
  * y[c][n] = sum_k W[n][k] * x[c][k] for c < ncol (1..8).  fmt: every format of the call surface
  * (Q4_K, Q5_K, IQ4_XS, Q6_K, Q6_K_SOA, Q8_0_SOA, Q5_1_SOA); K % 256 == 0, or K % 64 for Q8_0_SOA and
  * K % 32 for Q5_1_SOA (32-weight blocks).  tpr/rpt are the reference's tuning knobs; this build picks its own launch shape from
- * the tensor shape only (never from ncol, which keeps the result T-invariant) and accepts any
- * tpr in {0,1,2,4,8,16,32} and rpt in {0,1,2,3} for compatibility. */
+ * the tensor shape only (never from ncol, which keeps the result T-invariant) and accepts any values,
+ * as the reference does, with the reference's three routes kept: rpt 4 = qmm_gemv_multi (ncol <= 16);
+ * rpt 5 = W in qmm_repack_interleave8's layout (Q4_K, Q5_K, IQ4_XS; N % 8 == 0); rpt 4 with tpr 3 = W
+ * in qmm_repack_wmma_il's layout (Q4_K, Q5_K, IQ4_XS, Q6_K_SOA, Q8_0_SOA; K % 256 == 0; ncol <= 16).
+ * The interleaved layouts give every row the arithmetic of its format's plain q8 GEMV (1e-5). */
 int qmm_gemv_q8(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, int tpr, int rpt, void* stream);
 /* several weights sharing x (reference: gemv_multi, gemv.h:28, gemv.hip:1355-1369); up to 4
  * segments, all with the same K, any ncol.  Each run of consecutive segments of one format is one launch
@@ -212,7 +214,8 @@ int qmm_gemv_q8k(const qmm_gemv_seg* segs, int nseg, qmm_xq8k x, int ncol, void*
  * fmt Q4_K, ncol <= 4, K <= 6144, K % 256 == 0. */
 int qmm_gemv_q8_f32x(int fmt, const void* W, const float* x, float* y, int N, int K, int ncol, void* stream);
 /* f32-activation Q4_K GEMV: acc += (d*sc)*sum(x*q) - (dmin*m)*sum(x) per sub-block
- * (reference: gemv_q4_K_f32, gemv.h:57, gemv.hip:1177-1216,1486-1489); ncol 1..8. */
+ * (reference: gemv_q4_K_f32, gemv.h:57, gemv.hip:1177-1216,1486-1489); ncol 1..8; tpr accepted and
+ * not used (any value, as the reference's). */
 int qmm_gemv_q4_K_f32(const void* W, const float* x, float* y, int N, int K, int ncol, int tpr, void* stream);
 
 /* ---- MoE decode ---- */

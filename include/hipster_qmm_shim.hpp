@@ -7,8 +7,8 @@
 //  - errors (unsupported format, bad shape, launch failure) throw std::runtime_error carrying the
 //    library's status string, where the reference calls abort() or misbehaves silently;
 //  - gemv_wmma / gemv_wmma_ok map onto the library's T-invariant GEMV (any ncol gives every column
-//    the same reduction order), so `mode` is accepted and ignored, except mode 3 (the experimental
-//    16-row interleaved layout), which this library does not read: it throws;
+//    the same reduction order), so `mode` is accepted and ignored, except mode 3 (weights in the
+//    experimental 16-row interleaved layout), which runs qmm_gemv_q8's reader of that layout per weight;
 //  - the experiment knobs g_persist_blocks, g_moe_tpr and g_moe_fake exist and are ignored (launch
 //    shapes here depend on the tensor shape only);
 //  - moe_gemm keeps its signature and q8 arithmetic on VALU kernels; the engine's fast prefill path
@@ -88,8 +88,10 @@ inline bool gemv_wmma_ok(const GemvSeg* segs, int nseg) {
     return true;
 }
 inline void gemv_wmma(const GemvSeg* segs, int nseg, XQ8 x, int ncol, int mode, hipStream_t s) {    // gemv.h:36
-    if (mode == 3) detail::ck(QMM_ERR_LAYOUT, "gemv_wmma");
-    gemv_multi(segs, nseg, x, ncol, s);
+    if (mode != 3) return gemv_multi(segs, nseg, x, ncol, s);
+    if (nseg < 1 || nseg > 4) detail::ck(QMM_ERR_SHAPE, "gemv_wmma");
+    for (int i = 0; i < nseg; ++i)   // weights repacked by repack_wmma_il: tpr 3, rpt 4 reads that layout
+        detail::ck(qmm_gemv_q8((int)segs[i].fmt, segs[i].w, to_c(x), segs[i].y, segs[i].N, segs[i].K, ncol, 3, 4, (void*)s), "gemv_wmma");
 }
 inline void quantize_x_q8k(const float* x, XQ8K out, int ncol, int K, hipStream_t s) {                // gemv.h:34
     detail::ck(qmm_quantize_x_q8k(x, to_c(out), ncol, K, (void*)s), "quantize_x_q8k");

@@ -99,8 +99,13 @@ def test_argument_validation_without_device_work():
     # null pointers
     assert L.qmm_gemv_q8(_lib.QMM_Q4_K, None, _xq(16), dummy, 16, 256, 1, 0, 1, None) == -3
     assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _lib.XQ8(0, 0, 0, 0), dummy, 16, 256, 1, 0, 1, None) == -3
-    # knobs
-    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 256, 1, 3, 1, None) == -6
+    # knobs: any tpr / rpt is accepted (as the reference's); the interleaved layouts' own limits
+    assert L.qmm_gemv_q8(_lib.QMM_Q6_K_SOA, dummy, _xq(16), dummy, 16, 512, 1, 0, 5, None) == -1     # rpt 5: block formats
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 12, 256, 1, 0, 5, None) == -2         # N % 8
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 256, 9, 0, 5, None) == -2         # 8 columns
+    assert L.qmm_gemv_q8(_lib.QMM_Q5_1_SOA, dummy, _xq(16), dummy, 16, 512, 1, 3, 4, None) == -1     # 16-row layout
+    assert L.qmm_gemv_q8(_lib.QMM_Q8_0_SOA, dummy, _xq(16), dummy, 16, 320, 1, 3, 4, None) == -2     # K % 256
+    assert L.qmm_gemv_q8(_lib.QMM_Q4_K, dummy, _xq(16), dummy, 16, 256, 17, 3, 4, None) == -2        # 16 columns
     assert L.qmm_quantize_x_q8(None, _xq(16), 1, 256, None) == -3
     assert L.qmm_quantize_x_q8(dummy, _xq(16), 1, 100, None) == -2
     assert L.qmm_gemv_q4_K_f32(dummy, dummy, dummy, 16, 200, 1, 0, None) == -2

@@ -8,6 +8,8 @@ working (compat.hip, gemm.hip), through the C ABI:
   q8k             quantize_x_q8k bit-exact against the oracle; gemv_wmma_q8k within 1e-5 of the double dot
   gemm_bf16_ld    strided operands give the bits of gemm_bf16 on contiguous copies
   gemv_q8 rpt 4   (the reference's route to its T-invariant GEMV) = gemv_multi, up to 16 columns
+  gemv_q8 layouts rpt 5 / rpt 4 + tpr 3 on the reference's interleaved weight layouts, within 1e-5 of the
+                  oracle on the row-major matrix
 """
 import numpy as np
 import pytest
@@ -185,8 +187,8 @@ def test_gemm_bf16_ld(gpu, M, N, K):
 
 
 def test_gemv_q8_rpt4_is_the_multi_gemv(gpu):
-    """rpt = 4 (the reference's route to gemv_wmma, up to 16 columns) gives the bits of gemv_multi; the
-    interleaved-layout routes (rpt 5; rpt 4 with tpr 3) are refused with QMM_ERR_LAYOUT."""
+    """rpt = 4 (the reference's route to gemv_wmma, up to 16 columns) gives the bits of gemv_multi; any
+    other tpr / rpt (the reference's launch knobs, unlisted values included) gives the plain GEMV's."""
     N, K = 4099, 5120
     W = dev(synth.matrix(550, synth.Q4_K, N, K))
     x = synth.normal_f32(551, (16, K))
@@ -197,6 +199,45 @@ def test_gemv_q8_rpt4_is_the_multi_gemv(gpu):
     qmm.gemv_multi([(synth.Q4_K, W, y2, N, K)], xb, 16)
     torch.cuda.synchronize()
     assert torch.equal(y, y2)
-    for tpr, rpt in ((3, 4), (4, 5)):
-        with pytest.raises(qmm.QmmError, match="LAYOUT"):
-            qmm.gemv_q8(synth.Q4_K, W, xb, y, N, K, 1, tpr=tpr, rpt=rpt)
+    for tpr, rpt in ((0, 1), (3, 1), (7, 3), (64, 0)):
+        qmm.gemv_q8(synth.Q4_K, W, xb, y, N, K, 8, tpr=tpr, rpt=rpt)
+        qmm.gemv_q8(synth.Q4_K, W, xb, y2, N, K, 8)
+        torch.cuda.synchronize()
+        assert torch.equal(y[:8], y2[:8]), (tpr, rpt)
+
+
+IL_CASES = [(8, synth.Q4_K, 4104, 5120), (8, synth.Q5_K, 520, 2048), (8, synth.IQ4_XS, 264, 1024),
+            (16, synth.Q4_K, 4099, 5120), (16, synth.Q5_K, 300, 2048), (16, synth.IQ4_XS, 257, 1024),
+            (16, synth.Q6_K_SOA, 130, 5120), (16, synth.Q8_0_SOA, 100, 2560)]
+
+
+@pytest.mark.parametrize("rows,fmt,N,K", IL_CASES)
+def test_gemv_q8_interleaved_layouts(gpu, rows, fmt, N, K):
+    """The reference's experimental layouts (rpt 5: repack_interleave8, 8 rows; rpt 4 with tpr 3:
+    repack_wmma_il, 16 rows, N padded): the repacked bytes uploaded, every row within 1e-5 of the
+    oracle's q8 GEMV on the row-major matrix, at column counts that take one and several launches
+    (8, then 4, then the rest); the 32-weight-unit formats give the bits of their plain GEMV."""
+    print(f"gemv_q8 layout rows={rows} fmt={fmt} N={N} K={K}", flush=True)
+    Wr = synth.matrix(560 + fmt + rows, fmt, N, K)
+    Wil = qmm.repack_interleave8(fmt, Wr, N, K) if rows == 8 else qmm.repack_wmma_il(fmt, Wr, N, K)
+    tpr, rpt = (0, 5) if rows == 8 else (3, 4)
+    ncols = (1, 5, 8) if rows == 8 else (1, 11, 16)
+    x = synth.normal_f32(561 + K, (16, K))
+    xb = q8(x)
+    xr = q8_dequant(x)
+    ref, mag = oracle.gemv_ref(fmt, Wr, N, K, xr)
+    Wd = dev(Wil)
+    for ncol in ncols:
+        y = torch.full((ncol, N), np.nan, dtype=torch.float32, device="cuda")
+        qmm.gemv_q8(fmt, Wd, xb, y, N, K, ncol, tpr=tpr, rpt=rpt)
+        got = host(y)
+        assert max_rel_mag(got, ref[:ncol], mag[:ncol]) < TOL, ncol
+    if fmt in (synth.Q5_K, synth.IQ4_XS, synth.Q8_0_SOA):
+        yp = torch.zeros((8, N), dtype=torch.float32, device="cuda")
+        qmm.gemv_q8(fmt, dev(Wr), xb, yp, N, K, 8)
+        y = torch.zeros((8, N), dtype=torch.float32, device="cuda")
+        qmm.gemv_q8(fmt, Wd, xb, y, N, K, 8, tpr=tpr, rpt=rpt)
+        torch.cuda.synchronize()
+        assert torch.equal(y, yp)
+    with pytest.raises(qmm.QmmError):          # the layouts' formats only
+        qmm.gemv_q8(synth.Q5_1_SOA, Wd, xb, y, N, K, 1, tpr=tpr, rpt=rpt)
