@@ -44,9 +44,10 @@ constexpr int kMaxSlots = 16;      // slots per token
 // denominator is the xor-butterfly sum of e over each 32 consecutive experts (experts 32g..32g+31 are
 // the 32 lanes of half g & 1 of value j = g >> 1), then those group sums added in order; p = e / sum;
 // the top-k by p with ties to the lower id; weights p / (the selected p summed in selection order);
-// slot k is the shared expert: id -1, weight sigmoid(logit[nexp]).  Each round takes the wave max of
-// the lanes' best untaken p (DPP on the bits as integers), finds the lane holding it with one ballot
-// and, only when several lanes hold that value, the lowest id among them.
+// slot k is the shared expert: id -1, weight sigmoid(logit[nexp]).  Each lane sorts its candidates once
+// (best first); each round takes the wave max of the lanes' first candidates (DPP on the bits of p as
+// integers), finds the lane holding it with one ballot and, only when several lanes hold that value,
+// the lowest id among them; that lane drops its first candidate.
 
 // one DPP step of a wave max / min (lanes without a source see the neutral value)
 template <int CTRL, int ROWS>
@@ -80,10 +81,21 @@ __device__ __forceinline__ int wave_min64(int v) {
 }
 
 constexpr int kRouteMaxK = 16, kRouteMaxExp = 1024;
+// LDS of one routing wave (64-bit words): the 64 lane heads, the candidates (at most topk lanes x 16
+// entries), the topk selections in rank order
+constexpr int kRouteLdsWords = 64 + kRouteMaxK * 16 + kRouteMaxK;
 
-// one wave routes the token whose logits start at l: ids / weights of its topk + 1 slots to idt / wt
+// (p bits, id) as one unsigned 64-bit key whose order is the selection order: higher p first (the bits
+// of p as a signed int, offset to unsigned: every p >= 0 above a missing expert's -inf), then the
+// lower id
+__device__ __forceinline__ uint64_t route_key(int pbits, int id) {
+    return ((uint64_t)((uint32_t)pbits ^ 0x80000000u) << 32) | (uint32_t)(0xffffffffu - (uint32_t)id);
+}
+
+// one wave routes the token whose logits start at l: ids / weights of its topk + 1 slots to idt / wt;
+// lds: kRouteLdsWords words of LDS private to this wave
 template <int VPL>
-__device__ __forceinline__ void route_token(const float* __restrict__ l, int nexp, int topk, int* idt, float* wt) {
+__device__ __forceinline__ void route_token(const float* __restrict__ l, int nexp, int topk, int* idt, float* wt, uint64_t* lds) {
     const int lane = threadIdx.x & 63;
     float v[VPL];
 #pragma unroll
@@ -107,42 +119,63 @@ __device__ __forceinline__ void route_token(const float* __restrict__ l, int nex
         sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs[j]), 0));
         sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gs[j]), 32));
     }
-    // p of a taken expert becomes -1 (below every p >= 0), a missing one is -inf
-    float p[VPL];
+    // Top-k without sequential rounds.  Every expert's key (route_key of p = e / sum); the lane's best
+    // key is its head.  The topk-th best head theta bounds the selection: the topk best keys are all >=
+    // theta and lie in the topk lanes whose heads are >= theta.  So: rank the 64 heads against each
+    // other, take theta, gather the keys >= theta (at most topk x VPL), rank them against each other;
+    // rank r < topk is selection r.  The same selections and order as taking the best key topk times.
+    uint64_t key[VPL], head = 0;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) p[j] = lane + 64 * j < nexp ? e[j] / sum : -INFINITY;
-    float bv = p[0];
-    int bj = 0;
+    for (int j = 0; j < VPL; ++j) {
+        key[j] = route_key(__float_as_int(lane + 64 * j < nexp ? e[j] / sum : -INFINITY), lane + 64 * j);
+        head = key[j] > head ? key[j] : head;
+    }
+    uint64_t* const heads = lds;
+    uint64_t* const cand = lds + 64;
+    uint64_t* const sel = lds + 64 + kRouteMaxK * 16;
+    heads[lane] = head;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    int hr[4] = {0, 0, 0, 0};                            // four independent counts (no add chain)
 #pragma unroll
-    for (int j = 1; j < VPL; ++j)
-        if (p[j] > bv) { bv = p[j]; bj = j; }            // strict: ties keep the lower id
+    for (int m = 0; m < 64; m += 2) {
+        const ulonglong2 h = *(const ulonglong2*)(heads + m);
+        hr[(m >> 1) & 3] += (h.x > head) + (h.y > head);
+    }
+    const int hrank = (hr[0] + hr[1]) + (hr[2] + hr[3]);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(hrank == topk - 1);   // exactly one lane
+    const int tl = __builtin_ctzll(hit);
+    const uint64_t theta = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(head >> 32), tl) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)head, tl);
+    int nc = 0;                                          // wave-uniform candidate count
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const bool c = key[j] >= theta;
+        const uint64_t b = __builtin_amdgcn_ballot_w64(c);
+        if (c) cand[nc + __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0))] = key[j];
+        nc += __builtin_popcountll(b);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (int c0 = 0; c0 < nc; c0 += 64) {                // candidate c0 + lane: its rank among all nc
+        const int ci = c0 + lane;
+        const uint64_t mine = cand[min(ci, nc - 1)];
+        int r0 = 0, r1 = 0;
+        int m = 0;
+        for (; m + 1 < nc; m += 2) {
+            r0 += cand[m] > mine;
+            r1 += cand[m + 1] > mine;
+        }
+        if (m < nc) r0 += cand[m] > mine;
+        const int r = r0 + r1;
+        if (ci < nc && r < topk) sel[r] = mine;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float psel = 0.f, wsum = 0.f;
     int isel = 0;
-    // the round's max on the bits of p as signed ints: every p >= 0 orders as its float (and beats
-    // the negative marks of taken or missing experts, whose order among themselves never matters:
-    // an untaken expert with p >= 0 is always left)
-    for (int r = 0; r < topk; ++r) {
-        const int mb = wave_imax64(__float_as_int(bv));
-        const float m = __int_as_float(mb);
-        const uint64_t hit = __builtin_amdgcn_ballot_w64(__float_as_int(bv) == mb);
-        int wl;
-        if (__builtin_popcountll(hit) == 1) {
-            wl = __builtin_ctzll(hit);
-        } else {                                         // a tie across lanes: the lowest id wins
-            wl = wave_min64(__float_as_int(bv) == mb ? lane + 64 * bj : 0x7fffffff) & 63;
-        }
-        const int wj = __builtin_amdgcn_readlane(bj, wl);
-        if (lane == r) { psel = m; isel = wl + 64 * wj; }
-        wsum += m;                                       // selection order
-        if (lane == wl) {
-#pragma unroll
-            for (int j = 0; j < VPL; ++j)
-                if (j == wj) p[j] = -1.f;
-            bv = p[0]; bj = 0;
-#pragma unroll
-            for (int j = 1; j < VPL; ++j)
-                if (p[j] > bv) { bv = p[j]; bj = j; }
-        }
+    for (int r = 0; r < topk; ++r) {                     // the selected p summed in selection order
+        const uint64_t k = sel[r];
+        const float pr = __uint_as_float((uint32_t)(k >> 32) ^ 0x80000000u);
+        if (lane == r) { psel = pr; isel = (int)(0xffffffffu - (uint32_t)k); }
+        wsum += pr;
     }
     if (lane < topk) { idt[lane] = isel; wt[lane] = psel / wsum; }
     if (lane == topk) { idt[topk] = -1; wt[topk] = 1.f / (1.f + __expf(-gate)); }
@@ -151,9 +184,11 @@ __device__ __forceinline__ void route_token(const float* __restrict__ l, int nex
 template <int VPL>
 __global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ logits, int* __restrict__ ids,
                                                    float* __restrict__ w, int T, int nexp, int stride, int topk) {
+    __shared__ uint64_t lds[4][kRouteLdsWords];
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;                                  // wave-uniform
-    route_token<VPL>(logits + (size_t)t * stride, nexp, topk, ids + (size_t)t * (topk + 1), w + (size_t)t * (topk + 1));
+    route_token<VPL>(logits + (size_t)t * stride, nexp, topk, ids + (size_t)t * (topk + 1), w + (size_t)t * (topk + 1),
+                     lds[threadIdx.x >> 6]);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -320,7 +355,8 @@ __device__ __forceinline__ void gu_rows(const Q4kPairs<I> (&A)[8 / (64 / LPR)], 
     }
 }
 
-// ROUTE false: the ids come from ids_out (k_moe_route ran before), nothing is routed or written there
+// ROUTE true (T = 1 only): wave 0 routes the token while the others stage x; ROUTE false: the ids come
+// from ids_out (k_moe_route ran before), nothing is routed or written there
 template <int LPR, int I, int VPL, bool ROUTE>
 __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs a, const float* __restrict__ logits, int stride,
                                                                   int nexp_total, int topk, int T, int* __restrict__ ids_out,
@@ -334,6 +370,7 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
     __shared__ int s_cols[64 + kMaxCols];
     __shared__ int s_n, s_dup;
     __shared__ float s_gu[2][32][kDecMaxTok];
+    __shared__ uint64_t s_route[ROUTE ? kRouteLdsWords : 1];   // routed here only at T = 1: one routing wave
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nexp = topk + 1, nslot = T * nexp;
     // x of the T tokens in the pair layout of stage_gather, token c at c * 5H/4
     auto stage = [&](int first, int step) {
@@ -349,14 +386,10 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
         }
     };
     const int e = blockIdx.y, rb = blockIdx.x;
-    if constexpr (ROUTE) {
-        if (wave < T) route_token<VPL>(logits + (size_t)wave * stride, nexp_total, topk, s_ids + wave * nexp, s_w + wave * nexp);
-        else stage(tid - 64 * T, 64 * (kGuWaves - T));
+    if constexpr (ROUTE) {                                   // T = 1 (the launcher routes here only then)
+        if (wave == 0) route_token<VPL>(logits, nexp_total, topk, s_ids, s_w, s_route);
+        else stage(tid - 64, 64 * (kGuWaves - 1));
         __syncthreads();
-        if (T == kGuWaves) {                                 // every wave routed: stage now
-            stage(tid, 64 * kGuWaves);
-            __syncthreads();
-        }
         if (rb == 0 && e == 0 && tid < nslot) {
             ids_out[tid] = s_ids[tid];
             w_out[tid] = s_w[tid];
@@ -367,10 +400,14 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
         __syncthreads();
     }
     const int id = s_ids[e];
-    if (tid < 64) moe_slot_columns(s_ids, nslot, e, id, s_cols, &s_n, &s_dup);
-    __syncthreads();
-    if (s_dup) return;                                       // an earlier slot computes this expert
-    const int seg = wave >> 2, ncols = min(s_n, kMaxCols);     // at most T <= 8: a token holds an expert once
+    int ncols = 1;
+    if constexpr (!ROUTE) {
+        if (tid < 64) moe_slot_columns(s_ids, nslot, e, id, s_cols, &s_n, &s_dup);
+        __syncthreads();
+        if (s_dup) return;                                   // an earlier slot computes this expert
+        ncols = min(s_n, kMaxCols);                          // at most T <= 8: a token holds an expert once
+    }   // routed here (T = 1): the token's slots hold distinct experts, slot e is the one column
+    const int seg = wave >> 2;
     constexpr int RPW = 64 / LPR, NP = 8 / RPW;              // rows per wave pass; passes for the wave's 8 rows
     const int nb = H >> 8, ntask = 4 * nb, t = lane & (LPR - 1), j = t & 3;
     const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[seg] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[seg];
@@ -381,10 +418,16 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
         q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, F - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[p]);
     }
     const int rbase = (wave & 3) * 8 + lane / LPR;
-    switch (ncols) {
+    if constexpr (ROUTE) {
+        const int col0[1] = {e};
+        gu_rows<1, LPR, I>(A, smem, col0, nexp, H, t, j, ntask, rbase, s_gu[seg]);
+        if (tid == 0) s_cols[0] = e;
+    } else {
+        switch (ncols) {
 #define QMM_GU(NCV) case NCV: gu_rows<NCV, LPR, I>(A, smem, s_cols, nexp, H, t, j, ntask, rbase, s_gu[seg]); break;
-        QMM_GU(1) QMM_GU(2) QMM_GU(3) QMM_GU(4) QMM_GU(5) QMM_GU(6) QMM_GU(7) QMM_GU(8)
+            QMM_GU(1) QMM_GU(2) QMM_GU(3) QMM_GU(4) QMM_GU(5) QMM_GU(6) QMM_GU(7) QMM_GU(8)
 #undef QMM_GU
+        }
     }
     __syncthreads();
     if (tid < 32 * ncols) {                                  // one half-wave per column: its slot's q8 block
@@ -401,7 +444,9 @@ __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __r
                                            Stage stage) {
     constexpr int RPW = 64 / LPR, SPW = kMaxSlots / 4;
     __shared__ float vres[kMaxSlots][RPW];
+    __shared__ float sw[kMaxSlots];
     const int tok = blockIdx.y, tid = threadIdx.x;
+    if (tid < nexp) sw[tid] = a.slotw[tok * nexp + tid];   // read now, used after the barriers below
     const int lane = tid & 63, wave = tid >> 6, t = lane & (LPR - 1), j = t & 3;
     const int nb = K >> 8, ntask = 4 * nb;
     const int rloc = lane / LPR, row = blockIdx.x * RPW + rloc;
@@ -434,7 +479,7 @@ __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __r
     __syncthreads();
     if (tid < RPW && blockIdx.x * RPW + tid < N) {
         float acc = 0.f;
-        for (int e = 0; e < nexp; ++e) acc += a.slotw[tok * nexp + e] * vres[e][tid];
+        for (int e = 0; e < nexp; ++e) acc += sw[e] * vres[e][tid];
         a.y[0][(size_t)tok * N + blockIdx.x * RPW + tid] = acc;
     }
 }

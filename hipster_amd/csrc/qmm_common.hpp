@@ -143,16 +143,10 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 
 // ---- half-wave (32-lane) butterflies ----
 // ds_swizzle in bit mode (offset[15] = 0: and_mask 0x1f, or_mask 0, xor_mask O) reads lane l^O
-// within each group of 32 lanes without touching LDS memory.  After the five steps O = 16..1
-// every lane of the half-wave holds the same value: the pairwise tree that pairs lane l with
-// l^16 first, then l^8, ..., l^1 (addition commutes, so both partners compute the same sum).
+// within each group of 32 lanes without touching LDS memory.
 template <int O>
 __device__ __forceinline__ float swz_xor(float v) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (O << 10) | 0x1f));
-}
-__device__ __forceinline__ float hw32_sum(float v) {
-    v += swz_xor<16>(v); v += swz_xor<8>(v); v += swz_xor<4>(v); v += swz_xor<2>(v); v += swz_xor<1>(v);
-    return v;
 }
 // Reductions whose result does not depend on the order (max, integer sum) over 8 or 32 lanes, on the
 // VALU instead of the LDS pipe: DPP quad_perm [1,0,3,2] and [2,3,0,1] (lanes l^1, l^2), row_half_mirror
@@ -166,6 +160,23 @@ __device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+constexpr int kDppQuadReverse = 0x1B, kDppRor8 = 0x128;
+
+// The 32-lane sum as the pairwise tree that pairs lane l with l^16 first, then l^8, l^4, l^2, l^1
+// (every lane of the half-wave ends with the same value; addition commutes, so both partners of a
+// step compute the same sum), with the partners read on the VALU: l^16 from v_permlane16_swap of the
+// value with itself (one result holds row r, the other row r^1: their sum is the step), l^8 by a
+// rotation of the 16-lane row by 8, l^4 as (l^7)^3 (row_half_mirror, then the reversed quad), l^2 and
+// l^1 by quad permutes.  The same partners as the xor swizzles, so the same bits.
+__device__ __forceinline__ float hw32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    v += dpp_f<kDppRor8>(v);
+    v += dpp_f<kDppQuadReverse>(dpp_f<kDppHalfMirror>(v));
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppXor1>(v);
+    return v;
+}
 
 __device__ __forceinline__ float g8_max(float v) {
     v = fmaxf(v, dpp_f<kDppXor1>(v)); v = fmaxf(v, dpp_f<kDppXor2>(v));
