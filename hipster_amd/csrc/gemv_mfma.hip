@@ -267,9 +267,10 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
 // repeated).  A row 4t + s is token t against unit s alone (its x of group g in the lanes of group
 // q = s, zeros elsewhere), so D[4t + s][j] is the exact integer isum of unit s, group g, and lane
 // (j, q) receives D[4q + v][j], v = 0..3: token q (q + 4 in the second token block), units 0..3.
-// A workgroup is 16 rows x 4 waves; wave w takes blocks b = w + 4m, whose units 4b + v belong to the
-// unit kernel's lanes 4w + v + 16k, k = m % 4, in the same order: acc[k][v] is lane (4w + v + 16k)'s
-// partial sum.  The 64 partials of each (row, token) meet in LDS in the butterfly's association order.
+// A workgroup is 16 rows x kQ6MWaves waves (W); wave w takes blocks b = w + Wm, whose units 4b + v belong
+// to the unit kernel's lanes 4w + v + 4Wk, k = m % (16 / W), in the same order: acc[k][v] is lane
+// (4w + v + 4Wk)'s partial sum.  The 64 partials of each (row, token) meet in LDS in the butterfly's
+// association order.
 struct Q6MBlk {
     uint4 a, b, h;      // the lane's unit: 16 bytes of ql run A, of run B and of qh
     uint4 sc;           // the block's 16 scale bytes
@@ -334,6 +335,8 @@ __device__ __forceinline__ void q6m_compute(const Q6MBlk& B, const uint4 (&X)[NT
 }
 
 constexpr int kQ6MWaves = 4;
+constexpr int kQ6MParts = 16 / kQ6MWaves;   // partial sums per lane and unit position
+constexpr int kQ6MUnroll = kQ6MParts < 2 ? 2 : kQ6MParts;   // blocks per loop pass: the 2-block ring and acc[m % kQ6MParts]
 constexpr int kQ6MScaleRegs = 8;      // x-scale float4 per thread loaded ahead of the weights
 
 // LDS: x scales [ncol][K/32] float, after the main loop reused for the partials [64][4 NT][16] float
@@ -376,7 +379,7 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
 #pragma unroll
     for (int r = 0; r < kQ6MScaleRegs; ++r) sv[r] = ((const float4*)xd)[min(tid + 64 * kQ6MWaves * r, nx4 - 1)];
     __builtin_amdgcn_sched_barrier(0);
-    const int nm = (nb - wave + kQ6MWaves - 1) / kQ6MWaves;  // blocks b = wave + 4m of this wave (may be 0)
+    const int nm = (nb - wave + kQ6MWaves - 1) / kQ6MWaves;  // blocks b = wave + W m of this wave (may be 0)
     auto blk = [&](int m) { return min(wave + kQ6MWaves * min(m, max(nm - 1, 0)), nb - 1); };
     // two blocks in flight (weights three blocks ahead measured no faster); every load unconditional
     // (clamped block), so the wait counts stay exact
@@ -389,9 +392,9 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
     for (int r = 0; r < kQ6MScaleRegs; ++r)                 // no branch: a clamped item stores its own value
         ((float4*)sxd)[min(tid + 64 * kQ6MWaves * r, nx4 - 1)] = sv[r];
     lds_barrier();
-    float acc[4][4][NT];
+    float acc[kQ6MParts][4][NT];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < kQ6MParts; ++k)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
 #pragma unroll
@@ -401,25 +404,25 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
     int m0 = 0;
     do {                                                     // wave-uniform
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < kQ6MUnroll; ++k) {
             const int m = m0 + k;
-            q6m_compute<NT>(R[k & 1], X[k & 1], blk(m), q, sxd, nsb, ncol, m < nm, acc[k]);
+            q6m_compute<NT>(R[k & 1], X[k & 1], blk(m), q, sxd, nsb, ncol, m < nm, acc[k % kQ6MParts]);
             // the refill stays right here: the scheduler would otherwise move the ring's loads next to
             // their uses and drain the queue
             __builtin_amdgcn_sched_barrier(0);
             q6m_load<NT>(R[k & 1], X[k & 1], qlp, qhp, scp, dp, rx, xo, blk(m + 2));
             __builtin_amdgcn_sched_barrier(0);
         }
-        m0 += 4;
+        m0 += kQ6MUnroll;
     } while (m0 < nm);
     lds_barrier();                                           // every wave is done with the x scales
     float* part = (float*)smem;                              // [slot l][token][row]
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < kQ6MParts; ++k)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
 #pragma unroll
-            for (int i = 0; i < NT; ++i) part[((4 * wave + v + 16 * k) * NS + 4 * i + q) * 16 + j] = acc[k][v][i];
+            for (int i = 0; i < NT; ++i) part[((4 * wave + v + 4 * kQ6MWaves * k) * NS + 4 * i + q) * 16 + j] = acc[k][v][i];
     lds_barrier();
     for (int e = tid; e < 16 * ncol; e += 64 * kQ6MWaves) {
         const int orow = e & 15, oc = e >> 4;
