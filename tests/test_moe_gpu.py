@@ -152,8 +152,11 @@ def test_gemv_moe_down_combine_matches_oracle(gpu):
 
 def test_moe_decode_t_invariant_and_end_to_end(gpu):
     """Full decode MoE on device (route -> gate|up -> silu q8 -> down+combine) for T = 8, and each
-    token again alone: bitwise equal.  End to end against the oracle's own pipeline within 1e-3
-    (its silu uses the host libm exp, which can flip a q8 rounding of h)."""
+    token again alone: bitwise equal.  Each stage against the oracle on the previous stage's device
+    output: gate and up rows within 1e-5 (on the device's ids), h within one q8 quantum of the oracle's
+    silu * up of the device's g and u, down + combine within 1e-5 (on the device's h).  End to end
+    against the oracle's own pipeline within 1e-3 (its silu uses the host libm exp, which can flip a
+    q8 rounding of h, and the down projection carries that flip)."""
     n_exp, T, nexp = 64, 8, 11
     Wg_h, Wu_h, Wd_h = experts(1230, n_exp, F, H), experts(1231, n_exp, F, H), experts(1232, n_exp, H, F)
     Sg_h, Su_h, Sd_h = (synth.matrix(1233 + i, synth.Q4_K, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
@@ -171,13 +174,24 @@ def test_moe_decode_t_invariant_and_end_to_end(gpu):
         qmm.moe_silu_quant(g, u, hq, Tn * nexp, F)
         y = torch.zeros((Tn, H), device="cuda")
         qmm.gemv_moe(synth.Q4_K, synth.Q4_K, [W[2]], [W[5]], [y], Wd_h[0].nbytes, ids, nexp, hq, H, F, Tn, True, slotw=w)
-        return host(y), host(ids), host(w)
+        return host(y), host(ids), host(w), (host(g), host(u), host(hq.q), host(hq.d))
 
-    yT, idsT, wT = run(x, logits)
+    yT, idsT, wT, (gT, uT, hqT, hdT) = run(x, logits)
     for t in range(T):
-        y1, _, _ = run(x[t:t + 1], logits[t:t + 1])
+        y1, _, _, _ = run(x[t:t + 1], logits[t:t + 1])
         assert np.array_equal(y1[0].view(np.uint32), yT[t].view(np.uint32)), t
-    _, _, _, y_ref = oracle.moe_decode(synth.Q4_K, Wg_h, Wu_h, Wd_h, Sg_h, Su_h, Sd_h, x, idsT, wT, H, F)
+    g_ref, u_ref, _, y_ref = oracle.moe_decode(synth.Q4_K, Wg_h, Wu_h, Wd_h, Sg_h, Su_h, Sd_h, x, idsT, wT, H, F)
+    for r in range(T * nexp):
+        assert rel_l2(gT[r], g_ref[r]) <= 1e-5 and rel_l2(uT[r], u_ref[r]) <= 1e-5, r
+    gc, uc = np.ascontiguousarray(gT), np.ascontiguousarray(uT)
+    h_ref = np.empty_like(gc)
+    oracle.lib().qo_silu_mul(oracle._ptr(gc), oracle._ptr(uc), gc.size, oracle._ptr(h_ref))
+    hq_ref, hd_ref, _ = oracle.quantize_x_q8(h_ref)
+    assert np.abs(hqT.reshape(-1).astype(np.int32) - hq_ref.reshape(-1).astype(np.int32)).max() <= 1
+    np.testing.assert_allclose(hdT.reshape(-1), hd_ref.reshape(-1), rtol=1e-5)
+    _, y_chain = oracle.moe_down_q8(synth.Q4_K, Wd_h, Sd_h, hqT, hdT, idsT, wT, H, F)
+    for t in range(T):
+        assert rel_l2(yT[t], y_chain[t]) <= 1e-5, t
     assert rel_l2(yT, y_ref) <= 1e-3
 
 
