@@ -11,7 +11,8 @@
 //    experimental 16-row interleaved layout), which runs qmm_gemv_q8's reader of that layout per weight;
 //  - the experiment knobs g_persist_blocks, g_moe_tpr and g_moe_fake exist and are ignored (launch
 //    shapes here depend on the tensor shape only);
-//  - moe_gemm keeps its signature and q8 arithmetic on VALU kernels; the engine's fast prefill path
+//  - moe_gemm keeps its signature and q8 arithmetic (Q4_K tiles on the int8 matrix cores, the other
+//    formats on the VALU); the engine's fast prefill path
 //    is moe_sort + moe_gemm_gate_up_bf16 + moe_gemm_bf16 (bf16 MFMA);
 //  - BlasLt::gemm runs the library's own bf16 MFMA GEMM (no hipBLASLt, no autotune, no workspace);
 //  - fn::moe_combine_sorted takes the row width from the hidden size E of the caller's model: the
