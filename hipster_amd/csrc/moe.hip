@@ -436,13 +436,16 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
     }
 }
 
-// the down projection of one token's slots: wave w takes the slots e = w, w + 4, ... (at most
-// kMaxSlots / 4 of them); their weight rows are loaded before the caller stages x (stage(), then a
-// barrier), per-slot row results go to LDS and lane r of wave 0 sums row r over the slots in order
-template <int LPR, int I, typename Stage>
+// the down projection of one token's slots: wave w of DW takes the slots e = w, w + DW, ... (at most
+// kMaxSlots / DW of them); their weight rows are loaded before the caller stages x (stage(), then a
+// barrier), per-slot row results go to LDS and lane r of wave 0 sums row r over the slots in order.
+// A slot's row is one wave's work whatever the wave count, so the results do not depend on it: 8
+// waves at one token (the slots' latency chains side by side: 14.7 against 15.5 us for the T = 1 decode
+// step), 4 from two tokens on (more workgroups, fewer idle waves).
+template <int LPR, int I, int DW, typename Stage>
 __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __restrict__ ids, int nexp, uint8_t* smem, int N, int K,
                                            Stage stage) {
-    constexpr int RPW = 64 / LPR, SPW = kMaxSlots / 4;
+    constexpr int RPW = 64 / LPR, SPW = kMaxSlots / DW;
     __shared__ float vres[kMaxSlots][RPW];
     __shared__ float sw[kMaxSlots];
     const int tok = blockIdx.y, tid = threadIdx.x;
@@ -453,7 +456,7 @@ __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __r
     Q4kPairs<I> A[SPW];
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
-        const int e = wave + 4 * i;
+        const int e = wave + DW * i;
         if (e < nexp) {                                  // wave-uniform
             const int id = ids[tok * nexp + e];
             const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[0] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[0];
@@ -466,7 +469,7 @@ __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __r
     const bool exact = (ntask % LPR) == 0;
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
-        const int e = wave + 4 * i;
+        const int e = wave + DW * i;
         if (e < nexp) {
             XPairSrc<true> xs[1] = {XPairSrc<true>{smem + (size_t)e * (K + (K >> 2)), nullptr, nullptr, K}};
             float acc[1] = {0.f};
@@ -488,13 +491,13 @@ __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __r
 // Down projection + weighted combine: grid = (row blocks of 64/LPR rows, tokens), down_slots over
 // the token's slot rows of q8 x.
 
-template <int LPR, int I>
-__global__ void __launch_bounds__(256) k_gemv_moe_down_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
+template <int LPR, int I, int DW>
+__global__ void __launch_bounds__(64 * DW) k_gemv_moe_down_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
                                                            const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                            const float* __restrict__ xsum, int N, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tok = blockIdx.y;
-    down_slots<LPR, I>(a, ids, nexp, smem, N, K, [&] {   // the nexp slot rows of this token
+    down_slots<LPR, I, DW>(a, ids, nexp, smem, N, K, [&] {   // the nexp slot rows of this token
         int xrow[kMaxSlots];
 #pragma unroll
         for (int e = 0; e < kMaxSlots; ++e) xrow[e] = tok * nexp + min(e, nexp - 1);
@@ -560,7 +563,11 @@ int launch_down(const qmm_moe_segs& a, const int* ids, int nexp, qmm_xq8 x, int 
     const dim3 grid((N + (64 / LPR) - 1) / (64 / LPR), T);
     const size_t lds = (size_t)nexp * (K + K / 4);
     if (lds > kDecDownLds) return QMM_ERR_SHAPE;
-#define QMM_D(IV) case IV: hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV>), grid, dim3(256), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K); break;
+#define QMM_D(IV)                                                                                                   \
+    case IV:                                                                                                        \
+        if (T == 1) hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV, 8>), grid, dim3(512), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K); \
+        else hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV, 4>), grid, dim3(256), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K);       \
+        break;
     switch (iters) {
         QMM_D(1) QMM_D(2) QMM_D(3) QMM_D(4) QMM_D(5) QMM_D(6)
         default: return QMM_ERR_SHAPE;
