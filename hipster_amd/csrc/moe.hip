@@ -92,6 +92,16 @@ __device__ __forceinline__ uint64_t route_key(int pbits, int id) {
     return ((uint64_t)((uint32_t)pbits ^ 0x80000000u) << 32) | (uint32_t)(0xffffffffu - (uint32_t)id);
 }
 
+// r[q & 3] += how many of the 16 keys at ks (LDS, 16-byte aligned) exceed mine: eight 16-byte reads in
+// flight before the comparisons, so one LDS latency covers 16 keys
+__device__ __forceinline__ void route_count16(const uint64_t* ks, uint64_t mine, int (&r)[4]) {
+    ulonglong2 h[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) h[q] = *(const ulonglong2*)(ks + 2 * q);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) r[q & 3] += (h[q].x > mine) + (h[q].y > mine);
+}
+
 // one wave routes the token whose logits start at l: ids / weights of its topk + 1 slots to idt / wt;
 // lds: kRouteLdsWords words of LDS private to this wave
 template <int VPL>
@@ -137,10 +147,7 @@ __device__ __forceinline__ void route_token(const float* __restrict__ l, int nex
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     int hr[4] = {0, 0, 0, 0};                            // four independent counts (no add chain)
 #pragma unroll
-    for (int m = 0; m < 64; m += 2) {
-        const ulonglong2 h = *(const ulonglong2*)(heads + m);
-        hr[(m >> 1) & 3] += (h.x > head) + (h.y > head);
-    }
+    for (int m = 0; m < 64; m += 16) route_count16(heads + m, head, hr);
     const int hrank = (hr[0] + hr[1]) + (hr[2] + hr[3]);
     const uint64_t hit = __builtin_amdgcn_ballot_w64(hrank == topk - 1);   // exactly one lane
     const int tl = __builtin_ctzll(hit);
@@ -158,14 +165,11 @@ __device__ __forceinline__ void route_token(const float* __restrict__ l, int nex
     for (int c0 = 0; c0 < nc; c0 += 64) {                // candidate c0 + lane: its rank among all nc
         const int ci = c0 + lane;
         const uint64_t mine = cand[min(ci, nc - 1)];
-        int r0 = 0, r1 = 0;
+        int rc[4] = {0, 0, 0, 0};
         int m = 0;
-        for (; m + 1 < nc; m += 2) {
-            r0 += cand[m] > mine;
-            r1 += cand[m + 1] > mine;
-        }
-        if (m < nc) r0 += cand[m] > mine;
-        const int r = r0 + r1;
+        for (; m + 16 <= nc; m += 16) route_count16(cand + m, mine, rc);
+        for (; m < nc; ++m) rc[m & 3] += cand[m] > mine;
+        const int r = (rc[0] + rc[1]) + (rc[2] + rc[3]);
         if (ci < nc && r < topk) sel[r] = mine;
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -184,7 +188,7 @@ __device__ __forceinline__ void route_token(const float* __restrict__ l, int nex
 template <int VPL>
 __global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ logits, int* __restrict__ ids,
                                                    float* __restrict__ w, int T, int nexp, int stride, int topk) {
-    __shared__ uint64_t lds[4][kRouteLdsWords];
+    __shared__ __align__(16) uint64_t lds[4][kRouteLdsWords];   // 16-byte reads of the heads (2688 B per wave)
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;                                  // wave-uniform
     route_token<VPL>(logits + (size_t)t * stride, nexp, topk, ids + (size_t)t * (topk + 1), w + (size_t)t * (topk + 1),
@@ -370,7 +374,6 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
     __shared__ int s_cols[64 + kMaxCols];
     __shared__ int s_n, s_dup;
     __shared__ float s_gu[2][32][kDecMaxTok];
-    __shared__ uint64_t s_route[ROUTE ? kRouteLdsWords : 1];   // routed here only at T = 1: one routing wave
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nexp = topk + 1, nslot = T * nexp;
     // x of the T tokens in the pair layout of stage_gather, token c at c * 5H/4
     auto stage = [&](int first, int step) {
@@ -387,6 +390,7 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
     };
     const int e = blockIdx.y, rb = blockIdx.x;
     if constexpr (ROUTE) {                                   // T = 1 (the launcher routes here only then)
+        __shared__ __align__(16) uint64_t s_route[kRouteLdsWords];
         if (wave == 0) route_token<VPL>(logits, nexp_total, topk, s_ids, s_w, s_route);
         else stage(tid - 64, 64 * (kGuWaves - 1));
         __syncthreads();
