@@ -17,8 +17,8 @@
 // column's arithmetic is the same whatever the number of columns (T-invariant, bitwise).
 //
 // Down projection with slot weights: y[t][n] = sum_e slotw[t,e] * (W_{ids[t,e]} . x[t*nexp+e]).
-// The 4 waves of a workgroup split the slots of one token; the per-slot row results meet in LDS
-// and one lane per row adds them in slot order (deterministic, no atomics).
+// The waves of a workgroup (8 at one token, 4 from two on) split the slots of one token; the per-slot
+// row results meet in LDS and one lane per row adds them in slot order (deterministic, no atomics).
 #include "q4k_pair.hpp"
 #include "qmm_common.hpp"
 
@@ -44,10 +44,9 @@ constexpr int kMaxSlots = 16;      // slots per token
 // denominator is the xor-butterfly sum of e over each 32 consecutive experts (experts 32g..32g+31 are
 // the 32 lanes of half g & 1 of value j = g >> 1), then those group sums added in order; p = e / sum;
 // the top-k by p with ties to the lower id; weights p / (the selected p summed in selection order);
-// slot k is the shared expert: id -1, weight sigmoid(logit[nexp]).  Each lane sorts its candidates once
-// (best first); each round takes the wave max of the lanes' first candidates (DPP on the bits of p as
-// integers), finds the lane holding it with one ballot and, only when several lanes hold that value,
-// the lowest id among them; that lane drops its first candidate.
+// slot k is the shared expert: id -1, weight sigmoid(logit[nexp]).  The top-k is found by ranks, not
+// by k sequential argmax rounds (route_token): (p, id) packed as one 64-bit key, a threshold from the
+// ranks of the lanes' best keys, then the keys at or above it ranked against each other in LDS.
 
 // one DPP step of a wave max / min (lanes without a source see the neutral value)
 template <int CTRL, int ROWS>
@@ -260,6 +259,61 @@ __device__ __forceinline__ void stage_gather(uint8_t* lds, const int8_t* __restr
     }
 }
 
+// v / d for 0 <= v < 2^20, d >= 1, rd = 1 / d within a few ulp: the float quotient is then within 1/4
+// of v / d, so its truncation is off by at most one, which the two integer checks correct
+__device__ __forceinline__ int div_small(int v, int d, float rd) {
+    int c = (int)((float)v * rd);
+    c += (c + 1) * d <= v;
+    c -= c * d > v;
+    return c;
+}
+
+// stage_gather in two halves, for the x rows row0 .. row0 + nc - 1 of a workgroup whose x items
+// (nc * (K/16 + K/64) 16-byte pieces) fit NR per thread: load() issues every piece into registers at
+// once, store() writes them where stage_gather does.  A caller loads first and stores after its weight
+// loads are issued, so the x latency overlaps its ids -> weights chain (loads retire in issue order:
+// the stores wait for x only).  No branches: every thread loads two 8-byte halves per item (an item
+// past the last is the last again, stored twice with the same bytes), so the compiler's wait counts
+// stay exact.
+template <int NR>
+struct GatherRegs {
+    uint2 lo[NR], hi[NR];
+    // item v: q piece u of row c (v = c * nu + u) below nq, else the (d, s) pair piece p of row c
+    // (v - nq = c * kq + p); off = its LDS offset
+    __device__ __forceinline__ static void item(int v, int K, int nc, int& c, int& u, bool& isq) {
+        const int nu = K >> 4, kq = K >> 6, nq = nc * nu;
+        isq = v < nq;
+        const int d = isq ? nu : kq, w = isq ? v : v - nq;
+        c = div_small(w, d, __builtin_amdgcn_rcpf((float)d));
+        u = w - c * d;
+    }
+    __device__ __forceinline__ void load(const int8_t* __restrict__ xq, const float* __restrict__ xd, const float* __restrict__ xsum,
+                                         int row0, int nc, int K) {
+        const int n = nc * ((K >> 4) + (K >> 6)), nsb = K >> 5;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            int c, u;
+            bool isq;
+            item(min((int)threadIdx.x + (int)blockDim.x * r, n - 1), K, nc, c, u, isq);
+            const int8_t* pq = xq + (size_t)(row0 + c) * K + (size_t)u * 16;
+            const size_t ps = (size_t)(row0 + c) * nsb + 2 * u;
+            lo[r] = *(const uint2*)(isq ? (const void*)pq : (const void*)(xd + ps));
+            hi[r] = *(const uint2*)(isq ? (const void*)(pq + 8) : (const void*)(xsum + ps));
+        }
+    }
+    __device__ __forceinline__ void store(uint8_t* lds, int nc, int K) const {
+        const int n = nc * ((K >> 4) + (K >> 6)), kq = K >> 6;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            int c, u;
+            bool isq;
+            item(min((int)threadIdx.x + (int)blockDim.x * r, n - 1), K, nc, c, u, isq);
+            const size_t off = (size_t)c * (K + (K >> 2)) + (isq ? (size_t)((u & 3) * kq + (u >> 2)) * 16 : (size_t)K + (size_t)u * 16);
+            *(uint4*)(lds + off) = make_uint4(lo[r].x, lo[r].y, hi[r].x, hi[r].y);
+        }
+    }
+};
+
 // the gather of slot te's expert for the columns s_cols[0..ncols) (after the dedup): weights of
 // expert id (segment seg), x rows xrow_te ? slot : slot / nexp
 template <int LPR, int I>
@@ -446,28 +500,31 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
 // A slot's row is one wave's work whatever the wave count, so the results do not depend on it: 8
 // waves at one token (the slots' latency chains side by side: 14.7 against 15.5 us for the T = 1 decode
 // step), 4 from two tokens on (more workgroups, fewer idle waves).
-template <int LPR, int I, int DW, typename Stage>
+template <int LPR, int I, int DW, typename Pre, typename Stage>
 __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __restrict__ ids, int nexp, uint8_t* smem, int N, int K,
-                                           Stage stage) {
+                                           Pre pre, Stage stage) {
     constexpr int RPW = 64 / LPR, SPW = kMaxSlots / DW;
     __shared__ float vres[kMaxSlots][RPW];
     __shared__ float sw[kMaxSlots];
     const int tok = blockIdx.y, tid = threadIdx.x;
-    if (tid < nexp) sw[tid] = a.slotw[tok * nexp + tid];   // read now, used after the barriers below
-    const int lane = tid & 63, wave = tid >> 6, t = lane & (LPR - 1), j = t & 3;
+    pre();                                               // x loads that need no ids, if the caller has them
+    __builtin_amdgcn_sched_barrier(0);
+    const float swv = a.slotw[tok * nexp + min(tid, nexp - 1)];   // read now, stored after the weight loads
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), t = lane & (LPR - 1), j = t & 3;
     const int nb = K >> 8, ntask = 4 * nb;
     const int rloc = lane / LPR, row = blockIdx.x * RPW + rloc;
     Q4kPairs<I> A[SPW];
+    // every wave loads SPW slots' rows, a slot past the last being the last again (not computed): loads
+    // on every path keep the wait before the x stores from covering the weights
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
-        const int e = wave + DW * i;
-        if (e < nexp) {                                  // wave-uniform
-            const int id = ids[tok * nexp + e];
-            const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[0] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[0];
-            q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, N - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[i]);
-        }
+        const int id = ids[tok * nexp + min(wave + DW * i, nexp - 1)];   // wave-uniform: a scalar load
+        const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[0] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[0];
+        q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, N - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[i]);
     }
+    __builtin_amdgcn_sched_barrier(0);
     stage();
+    if (tid < nexp) sw[tid] = swv;
     __syncthreads();
     const Q4kPairDecode dc(j);
     const bool exact = (ntask % LPR) == 0;
@@ -495,18 +552,26 @@ __device__ __forceinline__ void down_slots(const qmm_moe_segs& a, const int* __r
 // Down projection + weighted combine: grid = (row blocks of 64/LPR rows, tokens), down_slots over
 // the token's slot rows of q8 x.
 
-template <int LPR, int I, int DW>
+// XF: the token's x pieces (nexp * (K/16 + K/64) of 16 bytes) fit the kDownXItems a workgroup holds in
+// registers (launch_down checks): they are loaded before the slot ids, their latency off the chain
+// ids -> weights
+constexpr int kDownXItems = 512;
+template <int LPR, int I, int DW, bool XF>
 __global__ void __launch_bounds__(64 * DW) k_gemv_moe_down_q4k(qmm_moe_segs a, const int* __restrict__ ids, int nexp,
                                                            const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                            const float* __restrict__ xsum, int N, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tok = blockIdx.y;
-    down_slots<LPR, I, DW>(a, ids, nexp, smem, N, K, [&] {   // the nexp slot rows of this token
+    if constexpr (XF) {                                  // the nexp slot rows of this token: tok * nexp + e
+        GatherRegs<kDownXItems / (64 * DW)> g;
+        down_slots<LPR, I, DW>(a, ids, nexp, smem, N, K, [&] { g.load(xq, xd, xsum, tok * nexp, nexp, K); },
+                               [&] { g.store(smem, nexp, K); });
+    } else {
         int xrow[kMaxSlots];
 #pragma unroll
         for (int e = 0; e < kMaxSlots; ++e) xrow[e] = tok * nexp + min(e, nexp - 1);
-        stage_gather(smem, xq, xd, xsum, xrow, nexp, K);
-    });
+        down_slots<LPR, I, DW>(a, ids, nexp, smem, N, K, [] {}, [&] { stage_gather(smem, xq, xd, xsum, xrow, nexp, K); });
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -567,10 +632,16 @@ int launch_down(const qmm_moe_segs& a, const int* ids, int nexp, qmm_xq8 x, int 
     const dim3 grid((N + (64 / LPR) - 1) / (64 / LPR), T);
     const size_t lds = (size_t)nexp * (K + K / 4);
     if (lds > kDecDownLds) return QMM_ERR_SHAPE;
-#define QMM_D(IV)                                                                                                   \
-    case IV:                                                                                                        \
-        if (T == 1) hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV, 8>), grid, dim3(512), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K); \
-        else hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV, 4>), grid, dim3(256), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K);       \
+    const bool xf = (size_t)nexp * (K / 16 + K / 64) <= (size_t)kDownXItems;
+#define QMM_D(IV)                                                                                                      \
+    case IV:                                                                                                           \
+        if (T == 1) {                                                                                                  \
+            if (xf) hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV, 8, true>), grid, dim3(512), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K);  \
+            else hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV, 8, false>), grid, dim3(512), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K);  \
+        } else {                                                                                                       \
+            if (xf) hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV, 4, true>), grid, dim3(256), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K);  \
+            else hipLaunchKernelGGL((k_gemv_moe_down_q4k<LPR, IV, 4, false>), grid, dim3(256), lds, s, a, ids, nexp, x.q, x.d, x.s, N, K);  \
+        }                                                                                                              \
         break;
     switch (iters) {
         QMM_D(1) QMM_D(2) QMM_D(3) QMM_D(4) QMM_D(5) QMM_D(6)
