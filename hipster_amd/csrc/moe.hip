@@ -414,8 +414,13 @@ __device__ __forceinline__ void gu_rows(const Q4kPairs<I> (&A)[8 / (64 / LPR)], 
 }
 
 // ROUTE true (T = 1 only): wave 0 routes the token while the others stage x; ROUTE false: the ids come
-// from ids_out (k_moe_route ran before), nothing is routed or written there
-template <int LPR, int I, int VPL, bool ROUTE>
+// from ids_out (k_moe_route ran before), nothing is routed or written there.  XF (ROUTE false, the
+// tokens' x fits kGuXItems 16-byte pieces): x and the slot ids are loaded into registers first, then
+// the slot's expert rows (its id by a scalar load), and only then are x and the ids stored to LDS and
+// the dedup run, so the x latency and the dedup overlap the weight loads (a slot that turns out to be a
+// duplicate drops rows that the slot computing its expert loads as well)
+constexpr int kGuXItems = 1536;
+template <int LPR, int I, int VPL, bool ROUTE, bool XF>
 __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs a, const float* __restrict__ logits, int stride,
                                                                   int nexp_total, int topk, int T, int* __restrict__ ids_out,
                                                                   float* __restrict__ w_out, const int8_t* __restrict__ xq,
@@ -428,7 +433,9 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
     __shared__ int s_cols[64 + kMaxCols];
     __shared__ int s_n, s_dup;
     __shared__ float s_gu[2][32][kDecMaxTok];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nexp = topk + 1, nslot = T * nexp;
+    // the wave index uniform (readfirstlane), so that the segment's base pointer is a scalar load that
+    // does not wait for the vector loads issued before it
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, nexp = topk + 1, nslot = T * nexp;
     // x of the T tokens in the pair layout of stage_gather, token c at c * 5H/4
     auto stage = [&](int first, int step) {
         const int nu = H >> 4, kq = H >> 6, nsb = H >> 5;
@@ -442,7 +449,20 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
             *(float4*)(smem + (size_t)c * (H + (H >> 2)) + (size_t)H + (size_t)pp * 16) = make_float4(dd.x, dd.y, ss.x, ss.y);
         }
     };
+    static_assert(!(ROUTE && XF), "x ahead of the ids only without routing");
     const int e = blockIdx.y, rb = blockIdx.x;
+    const int seg = wave >> 2;
+    constexpr int RPW = 64 / LPR, NP = 8 / RPW;              // rows per wave pass; passes for the wave's 8 rows
+    const int nb = H >> 8, ntask = 4 * nb, t = lane & (LPR - 1), j = t & 3;
+    Q4kPairs<I> A[NP];
+    auto load_rows = [&](int id) {                           // this wave's 8 rows of expert id (gate or up)
+        const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[seg] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[seg];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const int row = rb * 32 + (wave & 3) * 8 + p * RPW + lane / LPR;
+            q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, F - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[p]);
+        }
+    };
     if constexpr (ROUTE) {                                   // T = 1 (the launcher routes here only then)
         __shared__ __align__(16) uint64_t s_route[kRouteLdsWords];
         if (wave == 0) route_token<VPL>(logits, nexp_total, topk, s_ids, s_w, s_route);
@@ -452,6 +472,16 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
             ids_out[tid] = s_ids[tid];
             w_out[tid] = s_w[tid];
         }
+    } else if constexpr (XF) {
+        GatherRegs<kGuXItems / (64 * kGuWaves)> g;
+        g.load(xq, xd, xsum, 0, T, H);
+        const int idv = ids_out[min(tid, nslot - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        load_rows(ids_out[e]);                               // e is uniform: a scalar load
+        __builtin_amdgcn_sched_barrier(0);
+        g.store(smem, T, H);
+        if (tid < nslot) s_ids[tid] = idv;
+        __syncthreads();
     } else {
         if (tid < nslot) s_ids[tid] = ids_out[tid];
         stage(tid, 64 * kGuWaves);
@@ -465,16 +495,7 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
         if (s_dup) return;                                   // an earlier slot computes this expert
         ncols = min(s_n, kMaxCols);                          // at most T <= 8: a token holds an expert once
     }   // routed here (T = 1): the token's slots hold distinct experts, slot e is the one column
-    const int seg = wave >> 2;
-    constexpr int RPW = 64 / LPR, NP = 8 / RPW;              // rows per wave pass; passes for the wave's 8 rows
-    const int nb = H >> 8, ntask = 4 * nb, t = lane & (LPR - 1), j = t & 3;
-    const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[seg] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[seg];
-    Q4kPairs<I> A[NP];
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        const int row = rb * 32 + (wave & 3) * 8 + p * RPW + lane / LPR;
-        q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, F - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[p]);
-    }
+    if constexpr (!XF) load_rows(id);
     const int rbase = (wave & 3) * 8 + lane / LPR;
     if constexpr (ROUTE) {
         const int col0[1] = {e};
@@ -659,13 +680,18 @@ int launch_decode_gu_q8(const qmm_moe_segs& a, const float* logits, int stride, 
     const int iters = (H / 256 * 4 + LPR - 1) / LPR;
     const dim3 grid(F / 32, T * (topk + 1));
     const size_t lds = (size_t)T * (H + H / 4);
+    const bool xf = (size_t)T * (H / 16 + H / 64) <= (size_t)kGuXItems;
+    // without routing the kernel does not use VPL: one instance (VPL 1) serves every expert count
 #define QMM_G(IV) case IV:                                                                                                   \
         if (T == 1)                                                                                                          \
-            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL, true>), grid, dim3(64 * kGuWaves), lds, s, a, logits, stride,  \
-                               nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                              \
+            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL, true, false>), grid, dim3(64 * kGuWaves), lds, s, a, logits,   \
+                               stride, nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                      \
+        else if (xf)                                                                                                         \
+            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, 1, false, true>), grid, dim3(64 * kGuWaves), lds, s, a, logits,     \
+                               stride, nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                      \
         else                                                                                                                 \
-            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL, false>), grid, dim3(64 * kGuWaves), lds, s, a, logits, stride, \
-                               nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                              \
+            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, 1, false, false>), grid, dim3(64 * kGuWaves), lds, s, a, logits,    \
+                               stride, nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                      \
         break;
     switch (iters) {
         QMM_G(1) QMM_G(2) QMM_G(3) QMM_G(4) QMM_G(5) QMM_G(6)
