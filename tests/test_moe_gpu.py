@@ -232,14 +232,18 @@ def test_moe_combine_sorted(gpu):
     assert np.array_equal(host(ybuf[1:]).reshape(T, E).view(np.uint32), host(y).view(np.uint32))
 
 
-@pytest.mark.parametrize("T,n_exp", [(1, 512), (4, 512), (8, 512), (3, 40)])
-def test_moe_decode_step_bitwise(gpu, T, n_exp):
+# (T, n_exp, H, F): config 2 at T = 1 / 4 / 8, a small expert table, and a wider shape (H 4096, F 1024) whose
+# tokens' x no longer fits the registers the two launches load it into ahead of the expert rows (both
+# launches then stage x after their ids, the other code path)
+@pytest.mark.parametrize("T,n_exp,H,F", [(1, 512, H, F), (4, 512, H, F), (8, 512, H, F), (3, 40, H, F), (8, 16, 4096, 1024),
+                                         (1, 16, 4096, 1024)])
+def test_moe_decode_step_bitwise(gpu, T, n_exp, H, F):
     """qmm_moe_decode (routing, each distinct expert's gate|up rows once for its slots and silu*up -> q8 in
     the first launch, the q8 down projection in the second) against the four-launch sequence of separate calls
     on the same inputs: ids, weights, y and the workspace's q8 of h bit for bit.  Then y against the
     oracle's down projection + combine fed with the device's q8 h and routing (1e-5: every stage after the
     device exp of silu pinned)."""
-    print(f"moe_decode T={T} n_exp={n_exp}", flush=True)
+    print(f"moe_decode T={T} n_exp={n_exp} H={H} F={F}", flush=True)
     nexp = 11
     Wg_h, Wu_h, Wd_h = experts(1260, n_exp, F, H), experts(1261, n_exp, F, H), experts(1262, n_exp, H, F)
     Sg_h, Su_h, Sd_h = (synth.matrix(1263 + i, synth.Q4_K, *s) for i, s in enumerate(((F, H), (F, H), (H, F))))
