@@ -396,7 +396,7 @@ def extra_cfg2(torch, tb):
         ws = torch.zeros(qmm.moe_decode_ws_bytes(T, 10, F) // 4, device="cuda")
         y2 = torch.zeros((T, H), device="cuda")
 
-        def fused(r):      # the same step in two launches (routing in the gather, silu -> q8 in the down staging)
+        def fused(r):      # the same step in two launches (routing at T = 1, gate|up and silu -> q8; then down + combine)
             return lambda: qmm.moe_decode(synth.Q4_K, tb["Wg"], tb["Wu"], tb["Wd"], tb["Wg"][0].numel(), tb["Wd"][0].numel(), tb["Sg"],
                                           tb["Su"], tb["Sd"], lg[r], 513, 512, 10, xb, T, H, F, ids[r], w[r], ws, y2)
         us = graph_us(torch, [fused(r) for r in range(R)], reps=2) / R

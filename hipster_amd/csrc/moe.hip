@@ -382,17 +382,24 @@ constexpr size_t kDecDownLds = 64 * 1024;   // dynamic LDS budget of the decode 
 // The step's first launch (T <= 8): workgroup (32-row block rb, slot e) routes the T tokens (wave t
 // routes token t, route_token: the arithmetic of k_moe_route) while the other waves stage the tokens'
 // x; then, if e is the first slot holding its expert (the gather's dedup, moe_slot_columns), it
-// computes rows rb*32..rb*32+31 of that expert's gate (waves 0-3) and up (waves 4-7) projections for
+// computes rows rb*32..rb*32+31 of that expert's gate (the first half of the waves) and up (the second
+// half) projections for
 // every slot holding it (the columns, in slot order) with the gather's per-row arithmetic (q4k pairs
 // over LPR lanes per row: the same floats as k_gemv_moe_q4k), meets them in LDS and writes, one
 // half-wave per column, h = silu(g) * u quantised per 32 (half_wave_quant32: the q8 bits of
 // k_moe_silu_quant).  The second launch is the plain q8 down projection (k_gemv_moe_down_q4k).
-constexpr int kGuWaves = 8;
+// Waves per workgroup.  At T = 1 (routing inside) LPR: each wave computes 64 / LPR rows in one pass
+// (its 64 lanes are that many rows of LPR lanes), the shortest chain after the routing (T = 1 step
+// 13.7 -> 13.4 us on one box against 8 waves at LPR 16); from two tokens on 8, each wave 8 rows in
+// 8 / (64 / LPR) passes (16 waves measured 0.5-1.5 us slower at T = 4 and 8).  A row's arithmetic is
+// the same either way.
+template <int LPR, bool ROUTE>
+constexpr int gu_waves() { return ROUTE ? LPR : 8; }
 
-template <int NC, int LPR, int I>
-__device__ __forceinline__ void gu_rows(const Q4kPairs<I> (&A)[8 / (64 / LPR)], const uint8_t* smem, const int* cols, int nexp, int H,
+template <int NC, int LPR, int I, int NP>
+__device__ __forceinline__ void gu_rows(const Q4kPairs<I> (&A)[NP], const uint8_t* smem, const int* cols, int nexp, int H,
                                         int t, int j, int ntask, int rbase, float (*s_g)[kDecMaxTok]) {
-    constexpr int RPW = 64 / LPR, NP = 8 / RPW;
+    constexpr int RPW = 64 / LPR;
     XPairSrc<true> xs[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) xs[c] = XPairSrc<true>{smem + (size_t)(cols[c] / nexp) * (H + (H >> 2)), nullptr, nullptr, H};
@@ -421,7 +428,7 @@ __device__ __forceinline__ void gu_rows(const Q4kPairs<I> (&A)[8 / (64 / LPR)], 
 // duplicate drops rows that the slot computing its expert loads as well)
 constexpr int kGuXItems = 1536;
 template <int LPR, int I, int VPL, bool ROUTE, bool XF>
-__global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs a, const float* __restrict__ logits, int stride,
+__global__ void __launch_bounds__((64 * gu_waves<LPR, ROUTE>())) k_moe_route_gu_q8(qmm_moe_segs a, const float* __restrict__ logits, int stride,
                                                                   int nexp_total, int topk, int T, int* __restrict__ ids_out,
                                                                   float* __restrict__ w_out, const int8_t* __restrict__ xq,
                                                                   const float* __restrict__ xd, const float* __restrict__ xsum,
@@ -433,6 +440,7 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
     __shared__ int s_cols[64 + kMaxCols];
     __shared__ int s_n, s_dup;
     __shared__ float s_gu[2][32][kDecMaxTok];
+    constexpr int GW = gu_waves<LPR, ROUTE>();
     // the wave index uniform (readfirstlane), so that the segment's base pointer is a scalar load that
     // does not wait for the vector loads issued before it
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, nexp = topk + 1, nslot = T * nexp;
@@ -451,29 +459,29 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
     };
     static_assert(!(ROUTE && XF), "x ahead of the ids only without routing");
     const int e = blockIdx.y, rb = blockIdx.x;
-    const int seg = wave >> 2;
-    constexpr int RPW = 64 / LPR, NP = 8 / RPW;              // rows per wave pass; passes for the wave's 8 rows
+    // GW / 2 waves per segment (gate, up), RW rows per wave in NP passes of RPW rows
+    constexpr int RPW = 64 / LPR, RW = 64 / GW, NP = RW / RPW;
+    static_assert(NP >= 1 && NP * RPW == RW, "a wave's rows are whole passes");
+    const int seg = wave / (GW / 2), rbase = (wave % (GW / 2)) * RW + lane / LPR;
     const int nb = H >> 8, ntask = 4 * nb, t = lane & (LPR - 1), j = t & 3;
     Q4kPairs<I> A[NP];
-    auto load_rows = [&](int id) {                           // this wave's 8 rows of expert id (gate or up)
+    auto load_rows = [&](int id) {                           // this wave's rows of expert id (gate or up)
         const uint8_t* wbase = id >= 0 ? (const uint8_t*)a.w[seg] + (size_t)id * a.ebytes : (const uint8_t*)a.shared[seg];
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const int row = rb * 32 + (wave & 3) * 8 + p * RPW + lane / LPR;
-            q4k_load_pairs<I, LPR>(wbase + (size_t)min(row, F - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[p]);
-        }
+        for (int p = 0; p < NP; ++p)
+            q4k_load_pairs<I, LPR>(wbase + (size_t)min(rb * 32 + rbase + p * RPW, F - 1) * ((size_t)nb * 144), t, j, ntask, 0, A[p]);
     };
     if constexpr (ROUTE) {                                   // T = 1 (the launcher routes here only then)
         __shared__ __align__(16) uint64_t s_route[kRouteLdsWords];
         if (wave == 0) route_token<VPL>(logits, nexp_total, topk, s_ids, s_w, s_route);
-        else stage(tid - 64, 64 * (kGuWaves - 1));
+        else stage(tid - 64, 64 * (GW - 1));
         __syncthreads();
         if (rb == 0 && e == 0 && tid < nslot) {
             ids_out[tid] = s_ids[tid];
             w_out[tid] = s_w[tid];
         }
     } else if constexpr (XF) {
-        GatherRegs<kGuXItems / (64 * kGuWaves)> g;
+        GatherRegs<(kGuXItems + 64 * GW - 1) / (64 * GW)> g;
         g.load(xq, xd, xsum, 0, T, H);
         const int idv = ids_out[min(tid, nslot - 1)];
         __builtin_amdgcn_sched_barrier(0);
@@ -484,7 +492,7 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
         __syncthreads();
     } else {
         if (tid < nslot) s_ids[tid] = ids_out[tid];
-        stage(tid, 64 * kGuWaves);
+        stage(tid, 64 * GW);
         __syncthreads();
     }
     const int id = s_ids[e];
@@ -496,14 +504,13 @@ __global__ void __launch_bounds__(64 * kGuWaves) k_moe_route_gu_q8(qmm_moe_segs 
         ncols = min(s_n, kMaxCols);                          // at most T <= 8: a token holds an expert once
     }   // routed here (T = 1): the token's slots hold distinct experts, slot e is the one column
     if constexpr (!XF) load_rows(id);
-    const int rbase = (wave & 3) * 8 + lane / LPR;
     if constexpr (ROUTE) {
         const int col0[1] = {e};
-        gu_rows<1, LPR, I>(A, smem, col0, nexp, H, t, j, ntask, rbase, s_gu[seg]);
+        gu_rows<1, LPR, I, NP>(A, smem, col0, nexp, H, t, j, ntask, rbase, s_gu[seg]);
         if (tid == 0) s_cols[0] = e;
     } else {
         switch (ncols) {
-#define QMM_GU(NCV) case NCV: gu_rows<NCV, LPR, I>(A, smem, s_cols, nexp, H, t, j, ntask, rbase, s_gu[seg]); break;
+#define QMM_GU(NCV) case NCV: gu_rows<NCV, LPR, I, NP>(A, smem, s_cols, nexp, H, t, j, ntask, rbase, s_gu[seg]); break;
             QMM_GU(1) QMM_GU(2) QMM_GU(3) QMM_GU(4) QMM_GU(5) QMM_GU(6) QMM_GU(7) QMM_GU(8)
 #undef QMM_GU
         }
@@ -684,13 +691,13 @@ int launch_decode_gu_q8(const qmm_moe_segs& a, const float* logits, int stride, 
     // without routing the kernel does not use VPL: one instance (VPL 1) serves every expert count
 #define QMM_G(IV) case IV:                                                                                                   \
         if (T == 1)                                                                                                          \
-            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL, true, false>), grid, dim3(64 * kGuWaves), lds, s, a, logits,   \
+            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, VPL, true, false>), grid, dim3(64 * gu_waves<LPR, true>()), lds, s, a, logits,   \
                                stride, nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                      \
         else if (xf)                                                                                                         \
-            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, 1, false, true>), grid, dim3(64 * kGuWaves), lds, s, a, logits,     \
+            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, 1, false, true>), grid, dim3(64 * gu_waves<LPR, false>()), lds, s, a, logits,     \
                                stride, nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                      \
         else                                                                                                                 \
-            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, 1, false, false>), grid, dim3(64 * kGuWaves), lds, s, a, logits,    \
+            hipLaunchKernelGGL((k_moe_route_gu_q8<LPR, IV, 1, false, false>), grid, dim3(64 * gu_waves<LPR, false>()), lds, s, a, logits,    \
                                stride, nexp_total, topk, T, ids, w, x.q, x.d, x.s, F, H, h.q, h.d, h.s);                      \
         break;
     switch (iters) {
