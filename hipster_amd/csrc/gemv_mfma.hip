@@ -128,11 +128,14 @@ __host__ __device__ inline size_t gemv_q4k_mfma_main_lds(int K, int mv) {
     const size_t scales = (size_t)(K / 64) * (4 * mv) * 16, parts = (size_t)16 * (4 * mv) * 16 * 4;
     return scales > parts ? scales : parts;
 }
-// x staged in LDS (XL) for ncol <= 4 and ncol * K <= kXlMax: token c at c * (K + 64) (the 64-byte skew
+// x staged in LDS (XL) for ncol <= 8 and ncol * K <= xl_max(MV): token c at c * (K + 64) (the 64-byte skew
 // spreads the tokens over the banks), then 256 bytes of zeros read by the empty token slots; staged
-// by kXlRegs 16-byte pieces per thread, loaded before the first weights
-constexpr int kXlRegs = 8;
-constexpr int kXlMax = 256 * 16 * kXlRegs;
+// by xl_regs(MV) 16-byte pieces per thread, loaded before the first weights: 8 up to 4 columns, 10 (all
+// of 8 columns at K = 5120) for 5..8 (10 at 4 columns measured 0.8 us slower at 17408 x 5120: 106
+// against 94 VGPRs; x in LDS at 5..8 columns: 20.8-21.4 -> 20.1-20.4 us, config-1 layer at M = 8
+// 100.7 -> 99.4 us)
+__host__ __device__ constexpr int xl_regs(int mv) { return mv == 1 ? 8 : 10; }
+__host__ __device__ constexpr int xl_max(int mv) { return 256 * 16 * xl_regs(mv); }
 __host__ __device__ inline size_t gemv_q4k_mfma_xl_bytes(int K, int ncol) { return (size_t)ncol * (K + 64) + 256; }
 
 // grid = all 16-row tiles of all segments, 256 threads; LDS: x pair scales [K/64][4 MV] float4, after
@@ -182,10 +185,11 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
     // exact for these small integers), loaded (clamped) ahead of the weights as well
     const int nxq = XL ? ncol * (K >> 4) : 1;
     const float inv_kq = 1.f / (float)(K >> 4);
-    uint4 xv[XL ? kXlRegs : 1];
+    constexpr int XR = XL ? xl_regs(MV) : 1;
+    uint4 xv[XR];
     if constexpr (XL) {
 #pragma unroll
-        for (int u = 0; u < kXlRegs; ++u) xv[u] = ld16(xq + (size_t)min(tid + 256 * u, nxq - 1) * 16);
+        for (int u = 0; u < XR; ++u) xv[u] = ld16(xq + (size_t)min(tid + 256 * u, nxq - 1) * 16);
     }
     // every load below is unconditional (block indices clamped to the last block): with the same
     // loads on every path the wait counts stay exact and each prefetch stays in flight
@@ -203,7 +207,7 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
     }
     if constexpr (XL) {
 #pragma unroll
-        for (int u = 0; u < kXlRegs; ++u) {               // no branch: a clamped piece stores its own value
+        for (int u = 0; u < XR; ++u) {                    // no branch: a clamped piece stores its own value
             const int e = min(tid + 256 * u, nxq - 1), c = (int)(((float)e + 0.5f) * inv_kq), o = e - c * (K >> 4);
             *(uint4*)(xlds + c * kp + 16 * o) = xv[u];
         }
@@ -444,8 +448,8 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
 }
 }  // namespace
 
-// x in LDS: up to 4 columns whose x fits the staging registers
-static bool gemv_q4k_mfma_xl(int K, int ncol) { return ncol <= 4 && ncol * K <= kXlMax; }
+// x in LDS: up to 8 columns whose x fits the staging registers
+static bool gemv_q4k_mfma_xl(int K, int ncol) { return ncol <= 8 && ncol * K <= xl_max(ncol <= 4 ? 1 : 2); }
 
 size_t gemv_q4k_mfma_lds(int K, int ncol) {
     const int mv = ncol <= 4 ? 1 : ncol <= 8 ? 2 : 4;
@@ -478,7 +482,12 @@ int gemv_q4k_mfma(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol
             else
                 hipLaunchKernelGGL((k_gemv_q4k_mfma<1, false>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol);
             break;
-        case 2: hipLaunchKernelGGL((k_gemv_q4k_mfma<2, false>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
+        case 2:
+            if (gemv_q4k_mfma_xl(K, ncol))
+                hipLaunchKernelGGL((k_gemv_q4k_mfma<2, true>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol);
+            else
+                hipLaunchKernelGGL((k_gemv_q4k_mfma<2, false>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol);
+            break;
         default: hipLaunchKernelGGL((k_gemv_q4k_mfma<4, false>), grid, dim3(256), lds, s, sg, x.q, x.d, x.s, K, ncol); break;
     }
     QMM_LAUNCH_CHECK();
