@@ -88,6 +88,7 @@ SIGNATURES = {
     "qmm_gemv_q8k": (c_int, [ctypes.POINTER(GemvSeg), c_int, XQ8K, c_int, c_vp]),
     "qmm_set_gemv_mfma_min_ncol": (c_int, [c_int]),
     "qmm_set_gemv_q6k_mfma_min_ncol": (c_int, [c_int]),
+    "qmm_set_gemv_q80_mfma_min_ncol": (c_int, [c_int]),
     "qmm_set_gemv_fmt_xlds": (c_int, [c_int]),
     "qmm_moe_route": (c_int, [c_vp, c_vp, c_vp, c_int, c_vp]),
     "qmm_moe_route_n": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),

@@ -950,8 +950,14 @@ int g_mfma_min_ncol = 4;
 // Q6_K_SOA calls with at least this many columns (and at most 8) run on the matrix cores (measured at
 // 5120 x 17408: 2 columns 26.5 us on the dot4 kernel against 33, 3 columns 35 against 33, 4 43 against 33)
 int g_q6_mfma_min_ncol = 3;
+// Q8_0_SOA calls with at least this many columns (and at most 8) run on the matrix cores (measured at
+// 17408 x 5120: 25.0-25.3 us at any column count; the dot4 kernel 24.2-24.7 at 3 columns, 26.8 at 4,
+// 35.0 at 8)
+int g_q80_mfma_min_ncol = 4;
 
 int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    if (fmt == QMM_Q8_0_SOA && ncol >= g_q80_mfma_min_ncol && gemv_q80_mfma_fits(K, ncol) && ((uintptr_t)x.d & 7) == 0)
+        return gemv_q80_mfma(W, x, y, N, K, ncol, s);
     if (fmt == QMM_Q5_K || fmt == QMM_IQ4_XS || fmt == QMM_Q8_0_SOA || fmt == QMM_Q5_1_SOA)
         return gemv_fmt_dispatch(fmt, W, x, y, N, K, ncol, s);
     if (fmt == QMM_Q4_K && ncol >= g_mfma_min_ncol && ncol <= 16 && gemv_q4k_mfma_lds(K, ncol) <= kMfmaLdsMax) {
@@ -1035,6 +1041,12 @@ int qmm_set_gemv_mfma_min_ncol(int n) {
 int qmm_set_gemv_q6k_mfma_min_ncol(int n) {
     const int prev = g_q6_mfma_min_ncol;
     g_q6_mfma_min_ncol = n < 1 ? 1 : n;
+    return prev;
+}
+
+int qmm_set_gemv_q80_mfma_min_ncol(int n) {
+    const int prev = g_q80_mfma_min_ncol;
+    g_q80_mfma_min_ncol = n < 1 ? 1 : n;
     return prev;
 }
 

@@ -446,6 +446,159 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
         y[(size_t)oc * N + row0 + orow] = a[0] + a[1];
     }
 }
+
+// ------------------------------------------------------------------------------------------
+// Q8_0_SOA GEMV for 2..8 columns on the int8 matrix cores, bitwise the unit kernel of gemv_fmt.hip
+// (k_gemv_fmt with FmtUnit<QMM_Q8_0_SOA>: lane l of a row's wave adds (d * xd) * isum of the 32-weight
+// sub-blocks l, l + 64, ... in that order, and the 64 partial sums meet in the xor butterfly 32, 16, 8,
+// 4, 2, 1).  Row = [qs K][d K/32 x f16] (the engine's load-time SoA repack of Q8_0).
+//
+// v_mfma_i32_16x16x64_i8 over one 64-byte chunk c (sub-blocks 2c, 2c + 1) of 16 weight rows and up to
+// 8 tokens: lane (j, q) = (l % 16, l / 16) supplies as B column j the chunk bytes 16q..16q+15 of
+// weight row j (half q & 1 of sub-block q >> 1), and as A row j -- token j >> 1 against sub-block j & 1
+// alone -- that token's x bytes at the same chunk offset when q >> 1 == j & 1, zeros elsewhere (an
+// offset past the end of x).  So D[2t + s][j] is the exact isum of sub-block 2c + s of row j with token
+// t, and lane (j, q) receives D[4q + v][j]: token 2q + (v >> 1), sub-block 2c + (v & 1).  Wave w of
+// kQ8MWaves (4) takes chunks c = w + 4i; sub-block 2c + s belongs to the unit kernel's lane
+// (2c + s) % 64 = 2w + s + 8 (i % 8), so acc[i % 8][v] is that lane's partial sum, its sub-blocks
+// added in the same order.  The 64 partials of each (row, token) meet in LDS in the butterfly's order.
+constexpr int kQ8MWaves = 4;
+constexpr int kQ8MRing = 8;          // weight pieces in flight per lane
+constexpr int kQ8MScaleRegs = 8;     // x-scale pairs per thread, staged ahead of the weights
+constexpr int kQ8MXRegs = 10;        // 16-byte x pieces per thread, staged ahead of the weights
+constexpr int kQ8MDRegs = 8;         // dwords of the tile's d per thread, staged ahead of the weights
+
+// LDS: x [ncol][K + 64] bytes (the skew spreads the tokens over the banks) and 16 zero bytes (the A
+// pieces of the lanes that hold no x), the tile's d [16][K/16 + 4] bytes, the x scales [ncol][K/32]
+// float; after the main loop the partials [64][8][16] float from offset 0
+__host__ __device__ inline size_t gemv_q80_mfma_x_bytes(int K, int ncol) { return (size_t)ncol * (K + 64) + 16; }
+__host__ __device__ inline size_t gemv_q80_mfma_d_bytes(int K) { return (size_t)16 * (K / 16 + 4); }
+__host__ __device__ inline size_t gemv_q80_mfma_lds(int K, int ncol) {
+    const size_t st = gemv_q80_mfma_x_bytes(K, ncol) + gemv_q80_mfma_d_bytes(K) + (size_t)ncol * (K / 32) * 4;
+    const size_t parts = (size_t)64 * 8 * 16 * 4;
+    return st > parts ? st : parts;
+}
+
+__device__ __forceinline__ void q8m_compute(uint4 w, const uint8_t* xa, int xs, int c, int q, const uint8_t* da, const float* sxd, int nsb,
+                                            int ncol, bool live, float (&acc)[4]) {
+#pragma clang fp contract(off)
+    const uint4 xv = *(const uint4*)(xa + xs * c);
+    const uint32_t dd = *(const uint32_t*)(da + 4 * c);
+    const i32x4 a = {(int)xv.x, (int)xv.y, (int)xv.z, (int)xv.w}, b = {(int)w.x, (int)w.y, (int)w.z, (int)w.w};
+    const i32x4 z = {0, 0, 0, 0};
+    const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, z, 0, 0, 0);
+    const float d0 = h2f(dd), d1 = h2f(dd >> 16);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int t = min(2 * q + (v >> 1), ncol - 1), sb = 2 * c + (v & 1);
+        const float val = ((v & 1) ? d1 : d0) * sxd[t * nsb + sb] * (float)D[v];
+        acc[v] += live ? val : 0.f;
+    }
+}
+
+__global__ void __launch_bounds__(64 * kQ8MWaves) k_gemv_q80_mfma(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                                const float* __restrict__ xd, float* __restrict__ y, int N, int K,
+                                                                int ncol) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nsb = K >> 5, nch = K >> 6, kp = K + 64, drs = (K >> 4) + 4;
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, q = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: a scalar chunk loop
+    const int row0 = blockIdx.x * 16;
+    const size_t rb = (size_t)K + (size_t)(K >> 4);
+    const uint8_t* rp = W + (size_t)min(row0 + j, N - 1) * rb;
+    uint8_t* const xl = smem;
+    uint8_t* const dl = smem + gemv_q80_mfma_x_bytes(K, ncol);
+    float* const sxd = (float*)(dl + gemv_q80_mfma_d_bytes(K));
+    // staged ahead of the weights (loads retire in issue order, so the LDS stores wait for them only),
+    // every item clamped to the last one (a clamped item stores its own bytes again): x scales, x, d
+    const int nx2 = ncol * (nsb >> 1), nxq = ncol * (K >> 4), ndq = 16 * (K >> 6);
+    const float rk = __builtin_amdgcn_rcpf((float)(K >> 4)), rd = __builtin_amdgcn_rcpf((float)(K >> 6));
+    float2 sv[kQ8MScaleRegs];
+    uint4 xv[kQ8MXRegs];
+    uint32_t dv[kQ8MDRegs];
+#pragma unroll
+    for (int r = 0; r < kQ8MScaleRegs; ++r) sv[r] = ((const float2*)xd)[min(tid + 64 * kQ8MWaves * r, nx2 - 1)];
+#pragma unroll
+    for (int r = 0; r < kQ8MXRegs; ++r) xv[r] = ld16(xq + (size_t)min(tid + 64 * kQ8MWaves * r, nxq - 1) * 16);
+#pragma unroll
+    for (int r = 0; r < kQ8MDRegs; ++r) {                   // dword e: row e / (K/64), K/64 dwords per row
+        const int e = min(tid + 64 * kQ8MWaves * r, ndq - 1), rr = div_small(e, K >> 6, rd);
+        dv[r] = *(const uint32_t*)(W + (size_t)min(row0 + rr, N - 1) * rb + K + (size_t)(e - rr * (K >> 6)) * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int nm = (nch - wave + kQ8MWaves - 1) / kQ8MWaves;    // chunks c = wave + W m of this wave (may be 0)
+    auto chk = [&](int m) { return min(wave + kQ8MWaves * min(m, max(nm - 1, 0)), nch - 1); };
+    // every weight load unconditional (clamped chunk), so the wait counts stay exact
+    uint4 R[kQ8MRing];
+#pragma unroll
+    for (int r = 0; r < kQ8MRing; ++r) R[r] = ld16_a4(rp + 64 * (size_t)chk(r) + 16 * q);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < kQ8MScaleRegs; ++r) ((float2*)sxd)[min(tid + 64 * kQ8MWaves * r, nx2 - 1)] = sv[r];
+#pragma unroll
+    for (int r = 0; r < kQ8MXRegs; ++r) {
+        const int e = min(tid + 64 * kQ8MWaves * r, nxq - 1), c = div_small(e, K >> 4, rk);
+        *(uint4*)(xl + c * kp + 16 * (e - c * (K >> 4))) = xv[r];
+    }
+#pragma unroll
+    for (int r = 0; r < kQ8MDRegs; ++r) {
+        const int e = min(tid + 64 * kQ8MWaves * r, ndq - 1), rr = div_small(e, K >> 6, rd);
+        *(uint32_t*)(dl + rr * drs + 4 * (e - rr * (K >> 6))) = dv[r];
+    }
+    if (tid == 0) *(uint4*)(xl + ncol * kp) = make_uint4(0, 0, 0, 0);
+    lds_barrier();
+    // the lane's A piece: token j >> 1 at chunk offset 16q when q >> 1 == j & 1, else the zero bytes
+    const int t = j >> 1;
+    const bool xa_on = (q >> 1) == (j & 1) && t < ncol;
+    const uint8_t* const xa = xa_on ? xl + t * kp + 16 * q : xl + ncol * kp;
+    const int xs = xa_on ? 64 : 0;
+    const uint8_t* const da = dl + j * drs;
+    float acc[8][4];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[k][v] = 0.f;
+    // at least one pass: a loop that might not run would let the compiler sink the ring's loads past
+    // the barrier into its entry
+    int m0 = 0;
+    do {                                                     // wave-uniform
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int m = m0 + k;
+            q8m_compute(R[k % kQ8MRing], xa, xs, chk(m), q, da, sxd, nsb, ncol, m < nm, acc[k]);
+            // the refill stays right here: the scheduler would otherwise move the ring's loads next to
+            // their uses and drain the queue
+            __builtin_amdgcn_sched_barrier(0);
+            R[k % kQ8MRing] = ld16_a4(rp + 64 * (size_t)chk(m + kQ8MRing) + 16 * q);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        m0 += 8;
+    } while (m0 < nm);
+    lds_barrier();                                           // every wave is done with the staged x, d and scales
+    float* part = (float*)smem;                              // [unit-kernel lane L][token][row]
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[((2 * wave + (v & 1) + 8 * k) * 8 + 2 * q + (v >> 1)) * 16 + j] = acc[k][v];
+    lds_barrier();
+    for (int e = tid; e < 16 * ncol; e += 64 * kQ8MWaves) {
+        const int orow = e & 15, oc = e >> 4;
+        if (row0 + orow >= N) continue;
+        // the association order of the butterfly over the 64 lanes of the unit kernel's row wave
+        float a[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) a[u] = part[(u * 8 + oc) * 16 + orow] + part[((u + 32) * 8 + oc) * 16 + orow];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) a[u] = a[u] + a[u + 16];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] = a[u] + a[u + 8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = a[u] + a[u + 4];
+        a[0] = a[0] + a[2];
+        a[1] = a[1] + a[3];
+        y[(size_t)oc * N + row0 + orow] = a[0] + a[1];
+    }
+}
 }  // namespace
 
 // x in LDS: up to 8 columns whose x fits the staging registers
@@ -506,6 +659,23 @@ int gemv_q6k_mfma(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hi
         hipLaunchKernelGGL(k_gemv_q6k_mfma<1>, grid, dim3(64 * kQ6MWaves), lds, s, (const uint8_t*)W, x.q, x.d, y, N, K, ncol);
     else
         hipLaunchKernelGGL(k_gemv_q6k_mfma<2>, grid, dim3(64 * kQ6MWaves), lds, s, (const uint8_t*)W, x.q, x.d, y, N, K, ncol);
+    QMM_LAUNCH_CHECK();
+    return QMM_OK;
+}
+
+// the shapes whose x, d and x scales the kernel stages in one pass
+bool gemv_q80_mfma_fits(int K, int ncol) {
+    return ncol >= 1 && ncol <= 8 && K >= 64 && K % 64 == 0 && (size_t)ncol * (K / 64) <= (size_t)64 * kQ8MWaves * kQ8MScaleRegs &&
+           (size_t)ncol * (K / 16) <= (size_t)64 * kQ8MWaves * kQ8MXRegs && (size_t)K / 4 <= (size_t)64 * kQ8MWaves * kQ8MDRegs;
+}
+
+// ncol (1..8) columns of q8 x against a Q8_0_SOA matrix (gemv_q80_mfma_fits, x.d 8-byte aligned),
+// bitwise the unit kernel's columns
+int gemv_q80_mfma(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
+    if (!gemv_q80_mfma_fits(K, ncol) || N < 1 || ((uintptr_t)x.d & 7)) return QMM_ERR_SHAPE;
+    const size_t lds = gemv_q80_mfma_lds(K, ncol);
+    const dim3 grid((unsigned)((N + 15) / 16));
+    hipLaunchKernelGGL(k_gemv_q80_mfma, grid, dim3(64 * kQ8MWaves), lds, s, (const uint8_t*)W, x.q, x.d, y, N, K, ncol);
     QMM_LAUNCH_CHECK();
     return QMM_OK;
 }

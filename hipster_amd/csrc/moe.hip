@@ -259,15 +259,6 @@ __device__ __forceinline__ void stage_gather(uint8_t* lds, const int8_t* __restr
     }
 }
 
-// v / d for 0 <= v < 2^20, d >= 1, rd = 1 / d within a few ulp: the float quotient is then within 1/4
-// of v / d, so its truncation is off by at most one, which the two integer checks correct
-__device__ __forceinline__ int div_small(int v, int d, float rd) {
-    int c = (int)((float)v * rd);
-    c += (c + 1) * d <= v;
-    c -= c * d > v;
-    return c;
-}
-
 // stage_gather in two halves, for the x rows row0 .. row0 + nc - 1 of a workgroup whose x items
 // (nc * (K/16 + K/64) 16-byte pieces) fit NR per thread: load() issues every piece into registers at
 // once, store() writes them where stage_gather does.  A caller loads first and stores after its weight

@@ -65,6 +65,15 @@ __device__ __forceinline__ uint32_t iq4_levels4(uint32_t nib) {
 // Q6_K: 6-bit values (0..63, one per byte) -> signed q-32 per byte without carries between bytes.
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
+// v / d for 0 <= v < 2^20, d >= 1, rd = 1 / d within a few ulp: the float quotient is then within 1/4
+// of v / d, so its truncation is off by at most one, which the two integer checks correct
+__device__ __forceinline__ int div_small(int v, int d, float rd) {
+    int c = (int)((float)v * rd);
+    c += (c + 1) * d <= v;
+    c -= c * d > v;
+    return c;
+}
+
 // LDS byte address of a pointer into __shared__ memory
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -289,6 +298,13 @@ extern int g_mfma_min_ncol;
 // 16-byte aligned x scales)
 int gemv_q6k_mfma(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s);
 extern int g_q6_mfma_min_ncol;
+// Q8_0_SOA GEMV of 1..8 columns on the int8 matrix cores (gemv_mfma.hip), bitwise the unit kernel;
+// the dispatch sends Q8_0_SOA calls of at least g_q80_mfma_min_ncol columns there when the kernel stages
+// their x, d and x scales in one pass (gemv_q80_mfma_fits: ncol * K <= 40960, K <= 8192, K % 64 == 0)
+// and the x scales are 8-byte aligned
+int gemv_q80_mfma(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s);
+bool gemv_q80_mfma_fits(int K, int ncol);
+extern int g_q80_mfma_min_ncol;
 
 // the MoE decode step of qmm_moe_decode (moe.hip): argument checks, and the two launches with the gate /
 // up rows in gu (2 * T * (topk + 1) * F floats)

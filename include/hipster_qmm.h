@@ -164,8 +164,9 @@ int qmm_quantize_x_q8(const float* x, qmm_xq8 out, int ncol, int K, void* stream
 /* ---- decode GEMV, int8 activations (reference: gemv_q8, gemv.h:25, gemv.hip:1466-1485) ----
  * y[c][n] = sum_k W[n][k] * x[c][k] for c < ncol (1..8).  fmt: every format of the call surface
  * (Q4_K, Q5_K, IQ4_XS, Q6_K, Q6_K_SOA, Q8_0_SOA, Q5_1_SOA); K % 256 == 0, or K % 64 for Q8_0_SOA and
- * K % 32 for Q5_1_SOA (32-weight blocks).  tpr/rpt are the reference's tuning knobs; this build picks its own launch shape from
- * the tensor shape only (never from ncol, which keeps the result T-invariant) and accepts any values,
+ * K % 32 for Q5_1_SOA (32-weight blocks).  tpr/rpt are the reference's tuning knobs; this build picks its own launch shape (Q4_K,
+ * Q6_K_SOA and Q8_0_SOA run on the int8 matrix cores from a few columns on, the knobs below; every
+ * kernel adds a column's values in the same order, so its bits do not depend on ncol) and accepts any values,
  * as the reference does, with the reference's three routes kept: rpt 4 = qmm_gemv_multi (ncol <= 16);
  * rpt 5 = W in qmm_repack_interleave8's layout (Q4_K, Q5_K, IQ4_XS; N % 8 == 0); rpt 4 with tpr 3 = W
  * in qmm_repack_wmma_il's layout (Q4_K, Q5_K, IQ4_XS, Q6_K_SOA, Q8_0_SOA; K % 256 == 0; ncol <= 16).
@@ -187,6 +188,10 @@ int qmm_set_gemv_mfma_min_ncol(int n);
  * ncol * K <= 262144, x.d 16-byte aligned) use the int8 matrix-core kernel (default 3; n > 8 keeps
  * every call on the dot4 kernels).  Returns the previous value.  Results are the same bits either way. */
 int qmm_set_gemv_q6k_mfma_min_ncol(int n);
+/* Tuning knob (no reference counterpart): Q8_0_SOA GEMV calls of n..8 columns (ncol * K <= 40960,
+ * K <= 8192, x.d 8-byte aligned) use the int8 matrix-core kernel (default 4; n > 8 keeps every call on the dot4
+ * kernels).  Returns the previous value.  Results are the same bits either way. */
+int qmm_set_gemv_q80_mfma_min_ncol(int n);
 /* Tuning knob (no reference counterpart): the Q5_K / IQ4_XS / Q8_0_SOA / Q5_1_SOA GEMV stages x once
  * per workgroup in LDS where that measured faster (on = 1, the default; needs K % 128 == 0 and the
  * columns' x within 64 KiB) or always reads it from global memory (0).  Returns the previous value.

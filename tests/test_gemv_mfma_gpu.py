@@ -166,3 +166,69 @@ def test_q6k_matrix_cores_large_k_falls_back(gpu):
     with q6_min_ncol(1):
         got = q6_gemv(Wd, xb, N, K, 8)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+class q80_min_ncol:
+    """qmm_set_gemv_q80_mfma_min_ncol for the duration of a block"""
+
+    def __init__(self, n):
+        self.n = n
+
+    def __enter__(self):
+        self.prev = _lib.lib().qmm_set_gemv_q80_mfma_min_ncol(self.n)
+
+    def __exit__(self, *a):
+        _lib.lib().qmm_set_gemv_q80_mfma_min_ncol(self.prev)
+
+
+def q80_gemv(Wd, xb, N, K, ncol):
+    y = torch.full((ncol, N), float("nan"), dtype=torch.float32, device="cuda")
+    qmm.gemv_q8(synth.Q8_0_SOA, Wd, xb, y, N, K, ncol)
+    torch.cuda.synchronize()
+    return host(y)
+
+
+@pytest.mark.parametrize("N,K", [(17408, 5120), (129, 64), (515, 2048), (77, 1088), (1000, 5120), (40, 8192)])
+def test_q80_matrix_cores_bitwise_dot4(gpu, N, K):
+    """Q8_0_SOA on the int8 matrix cores (forced from one column on) against the dot4 kernels (the
+    matrix cores switched off): every column bitwise equal, ncol 1..8; rows not a multiple of 16, one
+    64-weight chunk (three of the four waves have none), chunk counts not a multiple of 4 or of 32, 8
+    columns at K = 5120 (the most x the kernel stages) and the largest K it takes (8192: matrix cores up
+    to 5 columns, the dot4 kernels above)"""
+    print(f"q8_0 mfma vs dot4 N={N} K={K}", flush=True)
+    Wd = dev(synth.matrix(750 + N, synth.Q8_0_SOA, N, K))
+    xb = q8_on_gpu(synth.normal_f32(751, (8, K)))
+    for ncol in range(1, 9):
+        with q80_min_ncol(9):
+            ref = q80_gemv(Wd, xb, N, K, ncol)
+        with q80_min_ncol(1):
+            got = q80_gemv(Wd, xb, N, K, ncol)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), ncol
+
+
+def test_q80_matrix_cores_against_oracle(gpu):
+    """the matrix-core Q8_0_SOA GEMV at 2, 5 and 8 columns against the oracle within the GEMV bar"""
+    N, K = 333, 5120
+    W = synth.matrix(760, synth.Q8_0_SOA, N, K)
+    x = synth.normal_f32(761, (8, K))
+    q, d, _ = oracle.quantize_x_q8(x)
+    ref, mag = oracle.gemv_ref(synth.Q8_0_SOA, W, N, K, oracle.q8_to_f32(q, d))
+    xb = q8_on_gpu(x)
+    Wd = dev(W)
+    with q80_min_ncol(1):
+        for ncol in (2, 5, 8):
+            y = q80_gemv(Wd, xb, N, K, ncol)
+            assert rel_l2(y, ref[:ncol]) <= 1e-5
+            assert max_rel_mag(y, ref[:ncol], mag[:ncol]) < 1e-5
+
+
+def test_q80_matrix_cores_large_k_falls_back(gpu):
+    """K above what the kernel stages (8192) runs the dot4 kernels: the same bits"""
+    N, K = 64, 32768
+    Wd = dev(synth.matrix(770, synth.Q8_0_SOA, N, K))
+    xb = q8_on_gpu(synth.normal_f32(771, (8, K)))
+    with q80_min_ncol(9):
+        ref = q80_gemv(Wd, xb, N, K, 8)
+    with q80_min_ncol(1):
+        got = q80_gemv(Wd, xb, N, K, 8)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
