@@ -965,7 +965,7 @@ int gemv_q8_dispatch(int fmt, const void* W, qmm_xq8 x, float* y, int N, int K, 
         return gemv_q4k_mfma(&seg, 1, x, K, ncol, s);
     }
     if (fmt == QMM_Q6_K_SOA && ncol >= g_q6_mfma_min_ncol && ncol <= 8 && K >= 512 && K % 512 == 0 &&
-        (size_t)ncol * K <= 262144 && ((uintptr_t)x.d & 15) == 0)
+        gemv_q6k_mfma_fits(K, ncol) && ((uintptr_t)x.d & 15) == 0)
         return gemv_q6k_mfma(W, x, y, N, K, ncol, s);
     switch (ncol) {
         case 1: return launch_gemv_q8_ncol<1>(fmt, W, x, y, N, K, s);

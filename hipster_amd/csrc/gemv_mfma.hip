@@ -277,18 +277,14 @@ __global__ void __launch_bounds__(256) k_gemv_q4k_mfma(MSegs sg, const int8_t* _
 // association order.
 struct Q6MBlk {
     uint4 a, b, h;      // the lane's unit: 16 bytes of ql run A, of run B and of qh
-    uint4 sc;           // the block's 16 scale bytes
-    uint32_t d;         // the block's f16 d
 };
 
 template <int NT>
-__device__ __forceinline__ void q6m_load(Q6MBlk& B, uint4 (&X)[NT][4], const uint8_t* qlp, const uint8_t* qhp, const uint8_t* scp,
-                                         const uint16_t* dp, __amdgpu_buffer_rsrc_t rx, const uint32_t (&xo)[NT], int b) {
+__device__ __forceinline__ void q6m_load(Q6MBlk& B, uint4 (&X)[NT][4], const uint8_t* qlp, const uint8_t* qhp,
+                                         __amdgpu_buffer_rsrc_t rx, const uint32_t (&xo)[NT], int b) {
     B.a = ld16_a4(qlp + b * 128);
     B.b = ld16_a4(qlp + b * 128 + 32);
     B.h = ld16_a4(qhp + b * 64);
-    B.sc = ld16_a4(scp + b * 16);
-    B.d = dp[b];
 #pragma unroll
     for (int i = 0; i < NT; ++i)
 #pragma unroll
@@ -297,7 +293,8 @@ __device__ __forceinline__ void q6m_load(Q6MBlk& B, uint4 (&X)[NT][4], const uin
 
 // the block's unit values for the lane's tokens q + 4i added to acc[v][i] (live = false adds +0)
 template <int NT>
-__device__ __forceinline__ void q6m_compute(const Q6MBlk& B, const uint4 (&X)[NT][4], int b, int q, const float* sxd, int nsb,
+__device__ __forceinline__ void q6m_compute(const Q6MBlk& B, const uint4 (&X)[NT][4], int b, int q, const uint8_t* scl, const uint16_t* dl,
+                                            const float* sxd, int nsb,
                                             int ncol, bool live, float (&acc)[4][NT]) {
     const uint32_t aw[4] = {B.a.x, B.a.y, B.a.z, B.a.w}, bw[4] = {B.b.x, B.b.y, B.b.z, B.b.w};
     const uint32_t hw[4] = {B.h.x, B.h.y, B.h.z, B.h.w};
@@ -309,8 +306,9 @@ __device__ __forceinline__ void q6m_compute(const Q6MBlk& B, const uint4 (&X)[NT
         bop[2][w] = (int)q6_signed(((aw[w] >> 4) & 0x0f0f0f0fu) | (hw[w] & 0x30303030u));
         bop[3][w] = (int)q6_signed(((bw[w] >> 4) & 0x0f0f0f0fu) | ((hw[w] >> 2) & 0x30303030u));
     }
-    const float d = h2f(B.d);
-    const uint32_t scw[4] = {B.sc.x, B.sc.y, B.sc.z, B.sc.w};
+    const float d = h2f(dl[b]);                           // the row's staged d and scales of block b
+    const uint4 sc = *(const uint4*)(scl + 16 * b);
+    const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
         i32x4 c[4];
@@ -342,11 +340,17 @@ constexpr int kQ6MWaves = 4;
 constexpr int kQ6MParts = 16 / kQ6MWaves;   // partial sums per lane and unit position
 constexpr int kQ6MUnroll = kQ6MParts < 2 ? 2 : kQ6MParts;   // blocks per loop pass: the 2-block ring and acc[m % kQ6MParts]
 constexpr int kQ6MScaleRegs = 8;      // x-scale float4 per thread loaded ahead of the weights
+constexpr int kQ6MScRegs = 5;         // 16-byte pieces of the tile's block scales per thread, staged ahead of the weights
+constexpr int kQ6MDRegs = 3;          // dwords of the tile's block d per thread, staged ahead of the weights
 
-// LDS: x scales [ncol][K/32] float, after the main loop reused for the partials [64][4 NT][16] float
+// LDS: x scales [ncol][K/32] float, the tile's block scales [16][K/16 + 16] bytes and d [16][K/256 + 2]
+// f16; after the main loop the partials [64][4 NT][16] float from offset 0
+__host__ __device__ inline size_t gemv_q6k_mfma_sc_row(int K) { return (size_t)K / 16 + 16; }
+__host__ __device__ inline size_t gemv_q6k_mfma_d_row(int K) { return (size_t)K / 256 + 2; }   // f16 elements
 __host__ __device__ inline size_t gemv_q6k_mfma_lds(int K, int ncol) {
-    const size_t xs = (size_t)ncol * (K / 32) * 4, parts = (size_t)64 * (ncol <= 4 ? 4 : 8) * 16 * 4;
-    return xs > parts ? xs : parts;
+    const size_t st = (size_t)ncol * (K / 32) * 4 + 16 * gemv_q6k_mfma_sc_row(K) + 16 * gemv_q6k_mfma_d_row(K) * 2;
+    const size_t parts = (size_t)64 * (ncol <= 4 ? 4 : 8) * 16 * 4;
+    return st > parts ? st : parts;
 }
 
 template <int NT>
@@ -363,8 +367,6 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
     const int un = q >> 1, ulh = q & 1;                      // the lane's unit (n, lh) = q of each block
     const uint8_t* qlp = rp + 64 * un + 16 * ulh;
     const uint8_t* qhp = rp + (size_t)nb * 128 + 32 * un + 16 * ulh;
-    const uint8_t* scp = rp + (size_t)nb * 192;
-    const uint16_t* dp = (const uint16_t*)(rp + (size_t)nb * 208);
     // A source: token 4i + (j >> 2) against unit s = j & 3 of the block, from the lanes of group q = s
     // only (an offset past the end of x reads zeros)
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, ncol * K, 0x00020000);
@@ -382,6 +384,26 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
     float4 sv[kQ6MScaleRegs];
 #pragma unroll
     for (int r = 0; r < kQ6MScaleRegs; ++r) sv[r] = ((const float4*)xd)[min(tid + 64 * kQ6MWaves * r, nx4 - 1)];
+    // the tile's block scales (nb 16-byte pieces per row) and d (nb / 2 dwords per row), staged the same
+    // way, so the main loop loads weights and x only
+    uint8_t* const scl = (uint8_t*)(sxd + (size_t)ncol * nsb);
+    uint16_t* const dlds = (uint16_t*)(scl + 16 * gemv_q6k_mfma_sc_row(K));
+    const int scrs = (int)gemv_q6k_mfma_sc_row(K), drs = (int)gemv_q6k_mfma_d_row(K);
+    const size_t rbytes = (size_t)nb * 210;
+    const int nsc = 16 * nb, ndw = 16 * (nb >> 1);
+    const float rnb = __builtin_amdgcn_rcpf((float)nb), rnh = __builtin_amdgcn_rcpf((float)(nb >> 1));
+    uint4 scv[kQ6MScRegs];
+    uint32_t dv[kQ6MDRegs];
+#pragma unroll
+    for (int r = 0; r < kQ6MScRegs; ++r) {                 // piece e: row e / nb, block e % nb
+        const int e = min(tid + 64 * kQ6MWaves * r, nsc - 1), rr = div_small(e, nb, rnb);
+        scv[r] = ld16_a4(W + (size_t)min(row0 + rr, N - 1) * rbytes + (size_t)nb * 192 + (size_t)(e - rr * nb) * 16);
+    }
+#pragma unroll
+    for (int r = 0; r < kQ6MDRegs; ++r) {                  // dword e: row e / (nb/2), blocks 2 (e % (nb/2)) + 0, 1
+        const int e = min(tid + 64 * kQ6MWaves * r, ndw - 1), rr = div_small(e, nb >> 1, rnh);
+        dv[r] = *(const uint32_t*)(W + (size_t)min(row0 + rr, N - 1) * rbytes + (size_t)nb * 208 + (size_t)(e - rr * (nb >> 1)) * 4);
+    }
     __builtin_amdgcn_sched_barrier(0);
     const int nm = (nb - wave + kQ6MWaves - 1) / kQ6MWaves;  // blocks b = wave + W m of this wave (may be 0)
     auto blk = [&](int m) { return min(wave + kQ6MWaves * min(m, max(nm - 1, 0)), nb - 1); };
@@ -389,13 +411,25 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
     // (clamped block), so the wait counts stay exact
     Q6MBlk R[2];
     uint4 X[2][NT][4];
-    q6m_load<NT>(R[0], X[0], qlp, qhp, scp, dp, rx, xo, blk(0));
-    q6m_load<NT>(R[1], X[1], qlp, qhp, scp, dp, rx, xo, blk(1));
+    q6m_load<NT>(R[0], X[0], qlp, qhp, rx, xo, blk(0));
+    q6m_load<NT>(R[1], X[1], qlp, qhp, rx, xo, blk(1));
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < kQ6MScaleRegs; ++r)                 // no branch: a clamped item stores its own value
         ((float4*)sxd)[min(tid + 64 * kQ6MWaves * r, nx4 - 1)] = sv[r];
+#pragma unroll
+    for (int r = 0; r < kQ6MScRegs; ++r) {
+        const int e = min(tid + 64 * kQ6MWaves * r, nsc - 1), rr = div_small(e, nb, rnb);
+        *(uint4*)(scl + rr * scrs + 16 * (e - rr * nb)) = scv[r];
+    }
+#pragma unroll
+    for (int r = 0; r < kQ6MDRegs; ++r) {
+        const int e = min(tid + 64 * kQ6MWaves * r, ndw - 1), rr = div_small(e, nb >> 1, rnh);
+        *(uint32_t*)(dlds + rr * drs + 2 * (e - rr * (nb >> 1))) = dv[r];
+    }
     lds_barrier();
+    const uint8_t* const scr = scl + j * scrs;            // the lane's row
+    const uint16_t* const dr = dlds + j * drs;
     float acc[kQ6MParts][4][NT];
 #pragma unroll
     for (int k = 0; k < kQ6MParts; ++k)
@@ -410,11 +444,11 @@ __global__ void __launch_bounds__(64 * kQ6MWaves) k_gemv_q6k_mfma(const uint8_t*
 #pragma unroll
         for (int k = 0; k < kQ6MUnroll; ++k) {
             const int m = m0 + k;
-            q6m_compute<NT>(R[k & 1], X[k & 1], blk(m), q, sxd, nsb, ncol, m < nm, acc[k % kQ6MParts]);
+            q6m_compute<NT>(R[k & 1], X[k & 1], blk(m), q, scr, dr, sxd, nsb, ncol, m < nm, acc[k % kQ6MParts]);
             // the refill stays right here: the scheduler would otherwise move the ring's loads next to
             // their uses and drain the queue
             __builtin_amdgcn_sched_barrier(0);
-            q6m_load<NT>(R[k & 1], X[k & 1], qlp, qhp, scp, dp, rx, xo, blk(m + 2));
+            q6m_load<NT>(R[k & 1], X[k & 1], qlp, qhp, rx, xo, blk(m + 2));
             __builtin_amdgcn_sched_barrier(0);
         }
         m0 += kQ6MUnroll;
@@ -647,11 +681,17 @@ int gemv_q4k_mfma(const qmm_gemv_seg* segs, int nseg, qmm_xq8 x, int K, int ncol
     return QMM_OK;
 }
 
-// ncol (1..8) columns of q8 x against a Q6_K_SOA matrix (K % 512 == 0, 512 <= K, ncol * K <= 262144),
+// the shapes whose x scales, block scales and d the Q6_K_SOA kernel stages in one pass
+bool gemv_q6k_mfma_fits(int K, int ncol) {
+    return (size_t)ncol * (K / 128) <= (size_t)64 * kQ6MWaves * kQ6MScaleRegs && (size_t)16 * (K / 256) <= (size_t)64 * kQ6MWaves * kQ6MScRegs &&
+           (size_t)8 * (K / 256) <= (size_t)64 * kQ6MWaves * kQ6MDRegs;
+}
+
+// ncol (1..8) columns of q8 x against a Q6_K_SOA matrix (K % 512 == 0, 512 <= K, gemv_q6k_mfma_fits),
 // bitwise the unit kernel's columns
 int gemv_q6k_mfma(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s) {
     if (ncol < 1 || ncol > 8 || K < 512 || K % 512 || N < 1) return QMM_ERR_SHAPE;
-    if ((size_t)ncol * (K / 128) > (size_t)64 * kQ6MWaves * kQ6MScaleRegs) return QMM_ERR_SHAPE;   // x scales in one pass
+    if (!gemv_q6k_mfma_fits(K, ncol)) return QMM_ERR_SHAPE;   // x scales, block scales and d in one staging pass
     const size_t lds = gemv_q6k_mfma_lds(K, ncol);
     if (lds > kMfmaLdsMax) return QMM_ERR_SHAPE;
     const dim3 grid((unsigned)((N + 15) / 16));

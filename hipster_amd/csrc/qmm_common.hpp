@@ -297,6 +297,7 @@ extern int g_mfma_min_ncol;
 // the dispatch sends Q6_K_SOA calls of at least g_q6_mfma_min_ncol columns there (K % 512 == 0,
 // 16-byte aligned x scales)
 int gemv_q6k_mfma(const void* W, qmm_xq8 x, float* y, int N, int K, int ncol, hipStream_t s);
+bool gemv_q6k_mfma_fits(int K, int ncol);     // its one-pass staging of x scales, block scales and d (K <= 20480)
 extern int g_q6_mfma_min_ncol;
 // Q8_0_SOA GEMV of 1..8 columns on the int8 matrix cores (gemv_mfma.hip), bitwise the unit kernel;
 // the dispatch sends Q8_0_SOA calls of at least g_q80_mfma_min_ncol columns there when the kernel stages
